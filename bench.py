@@ -1,0 +1,211 @@
+#!/usr/bin/env python3
+"""Benchmark of the quantized decode hot path on one MI355X.
+
+Workload (the metric's isolated-matvec configuration): y = W x with fp32
+x ~ N(0,1) of length 4096 and weights N(0, 0.02) quantized to Q8_0 and Q4_0,
+shapes 4096x4096 and 11008x4096, batch 1.  One step = one matvec of each of
+the four (format, shape) cases.  Each case cycles through a pool of distinct
+weight copies larger than the 256 MB Infinity Cache, so every launch streams
+its weights from HBM.  The K timed steps run case by case, each case's K
+launches captured in one HIP graph and bracketed by HIP events on the stream
+they run on; `value` is the total algorithmic bytes of all K steps over the
+total timed time.
+
+Algorithmic bytes per launch = weight bytes + 4*K (x) + 4*N (y).
+
+    python bench.py [--gpus 1] [--steps 1000] [--warmup 50] [--cpu-seconds 12]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "Q4/Q8 decode tok/s at batch 1 & 128; qmatvec achieved HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
+POOL_BYTES = 320 << 20  # > 256 MB MALL
+CASES = [("q8_0", 10, 4096, 4096), ("q8_0", 10, 11008, 4096), ("q4_0", 20, 4096, 4096), ("q4_0", 20, 11008, 4096)]
+
+
+def row_bytes(dt, k):
+    return (k // 32) * (36 if dt == 10 else 18)
+
+
+def alg_bytes(dt, n, k):
+    return n * row_bytes(dt, k) + 4 * k + 4 * n
+
+
+def cpu_baseline(cases_host, budget_s):
+    """The reference's own scalar matvec (oracle/_ref, compiled from the
+    reference sources) on this host, one thread; falls back to the oracle's
+    restatement when the reference build is absent."""
+    from oracle import pyoracle as po
+    R = po.ref()
+    kind = "reference" if R is not None else "port"
+    per = budget_s / len(cases_host)
+    tot_bytes, tot_time, parts = 0, 0.0, []
+    for (name, dt, n, k, wq, x) in cases_host:
+        y = np.zeros(n, np.float32)
+        it, t0 = 0, time.perf_counter()
+        while True:
+            if R is not None:
+                R.ref_matvec_q(wq.ctypes.data, dt, 32, n, k, x.ctypes.data_as(po._fp), y.ctypes.data_as(po._fp))
+            else:
+                po.lib().or_matvec_q(wq.ctypes.data, dt, 32, n, k, x.ctypes.data_as(po._fp), y.ctypes.data_as(po._fp))
+            it += 1
+            dt_s = time.perf_counter() - t0
+            if dt_s >= per:
+                break
+        tot_bytes += it * alg_bytes(dt, n, k)
+        tot_time += dt_s
+        parts.append(f"{name} {n}x{k}: {it} iters")
+    cpu = platform.processor() or platform.machine()
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                cpu = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"value": round(tot_bytes / tot_time / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
+            "sample": "; ".join(parts) + f" of dispatch_matvec_q (scalar x86 path), single thread, {tot_time:.1f} s, "
+                      f"host CPU: {cpu}"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=1000)
+    ap.add_argument("--warmup", type=int, default=50)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--rows-per-wave", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
+              "(the decode path shards by sequence across GPUs, see DESIGN.md)", file=sys.stderr)
+        sys.exit(2)
+
+    import qraf_amd
+    from qraf_amd._lib import call
+    from qraf_amd.backend import DeviceBuffer, Event, Graph, Stream
+
+    qraf_amd.backend.backend_init(0)
+    if args.rows_per_wave:
+        call("qraf_hip_set_matvec_rows_per_wave", args.rows_per_wave)
+    stream = Stream()
+    rng = np.random.default_rng(2024)
+    x_host = rng.standard_normal(4096).astype(np.float32)
+
+    cases = []
+    for (name, dt, n, k) in CASES:
+        wbytes = n * row_bytes(dt, k)
+        copies = max(2, math.ceil(POOL_BYTES / wbytes))
+        pool = DeviceBuffer(copies * wbytes)
+        seed_stream = qraf_amd.lib.qraf_hip_name_hash(f"bench.{name}.{n}x{k}".encode())
+        call("qraf_hip_gen_weights_dev", pool.ptr, dt, n * k, 2024, seed_stream, 0.02, stream.h)
+        for c in range(1, copies):
+            call("qraf_hip_memcpy_d2d", pool.ptr + c * wbytes, pool.ptr, wbytes, stream.h)
+        x = DeviceBuffer.from_array(x_host)
+        y = DeviceBuffer(n * 4)
+        cases.append(dict(name=name, dt=dt, n=n, k=k, wbytes=wbytes, copies=copies, pool=pool, x=x, y=y))
+    stream.synchronize()
+
+    def launch(c, i):
+        call("qraf_hip_matvec_q_dev", c["pool"].ptr + (i % c["copies"]) * c["wbytes"], c["dt"], 32, c["n"], c["k"],
+             c["x"].ptr, c["y"].ptr, stream.h)
+
+    # warmup (eager)
+    for i in range(args.warmup):
+        for c in cases:
+            launch(c, i)
+    stream.synchronize()
+
+    # capture K launches per case; timed region = the four graph launches
+    graphs = []
+    for c in cases:
+        g = Graph(stream)
+        with g:
+            for i in range(args.steps):
+                launch(c, args.warmup + i)
+        graphs.append(g)
+    for g in graphs:  # one untimed replay so graph upload is out of the timed region
+        g.launch()
+    stream.synchronize()
+    ev = [Event() for _ in range(len(cases) + 1)]
+    call("qraf_hip_device_synchronize")
+    ev[0].record(stream)
+    for i, g in enumerate(graphs):
+        g.launch()
+        ev[i + 1].record(stream)
+    stream.synchronize()
+    call("qraf_hip_device_synchronize")
+    per_case = []
+    total_ms, total_bytes = 0.0, 0
+    for i, c in enumerate(cases):
+        ms = ev[i].elapsed_ms(ev[i + 1])
+        b = alg_bytes(c["dt"], c["n"], c["k"])
+        us = ms * 1e3 / args.steps
+        per_case.append({"case": f"{c['name']} {c['n']}x{c['k']}", "us_per_launch": round(us, 3),
+                         "alg_bytes": b, "GB_s": round(b / (us * 1e-6) / 1e9, 1),
+                         "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                         "pool_copies": c["copies"]})
+        total_ms += ms
+        total_bytes += b * args.steps
+    value = total_bytes / (total_ms * 1e-3) / 1e9
+
+    # cache-resident reference point (same weight copy every launch), labelled as such
+    cache_res = []
+    for c in cases:
+        g = Graph(stream)
+        with g:
+            for i in range(200):
+                call("qraf_hip_matvec_q_dev", c["pool"].ptr, c["dt"], 32, c["n"], c["k"], c["x"].ptr, c["y"].ptr,
+                     stream.h)
+        g.launch()
+        stream.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        g.launch()
+        e1.record(stream)
+        us = e0.elapsed_ms(e1) * 1e3 / 200
+        cache_res.append({"case": f"{c['name']} {c['n']}x{c['k']}", "GB_s": round(
+            alg_bytes(c["dt"], c["n"], c["k"]) / (us * 1e-6) / 1e9, 1)})
+        g.destroy()
+
+    dom = max(per_case, key=lambda p: p["us_per_launch"])  # dominant kernel: longest launch
+    roofline = {"bound": "hbm", "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                "frac": round(dom["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
+                "kernel": "qmv_q8_kernel" if dom["case"].startswith("q8") else "qmv_q4_kernel",
+                "case": dom["case"], "alg_bytes_per_launch": dom["alg_bytes"]}
+
+    cpu = None
+    if not args.no_cpu:
+        hosts = []
+        for c in cases:
+            wq = DeviceBuffer.download(c["pool"], np.uint8, c["wbytes"])
+            hosts.append((c["name"], c["dt"], c["n"], c["k"], wq, x_host))
+        cpu = cpu_baseline(hosts, args.cpu_seconds)
+
+    out = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 5), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+           "config": {"workload": "isolated quantized matvec, batch 1: fp32 x[4096] times Q8_0 and Q4_0 weights "
+                                  "4096x4096 and 11008x4096 (N(0,0.02), repo quantizer), one launch per case per "
+                                  "step, weights rotating through >320 MB pools per case",
+                      "cases": [p["case"] for p in per_case]},
+           "per_case": per_case, "cache_resident": cache_res, "roofline": roofline, "cpu_baseline": cpu}
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

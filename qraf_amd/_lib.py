@@ -1,0 +1,97 @@
+"""ctypes binding of libqraf_hip.so (include/qraf_hip.h).
+
+The library is loaded from this package directory only.  There is no CPU
+fallback: if the shared object is missing or fails to load, importing
+qraf_amd raises.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+PKG = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PKG, "libqraf_hip.so")
+
+OK = 0
+ERR_INVALID, ERR_DTYPE, ERR_HIP, ERR_NOMEM, ERR_STATE = -1, -2, -3, -4, -5
+F32, F16, Q8_0, Q4_0 = 0, 1, 10, 20
+
+vp = C.c_void_p
+fp = C.POINTER(C.c_float)
+u32p = C.POINTER(C.c_uint32)
+i32p = C.POINTER(C.c_int32)
+
+# name -> (restype, argtypes); every function returns int status unless noted
+SIGNATURES = {
+    "qraf_hip_last_error": (C.c_char_p, []),
+    "qraf_hip_version": (C.c_char_p, []),
+    "qraf_hip_init": (C.c_int, [C.c_int]),
+    "qraf_hip_device_count": (C.c_int, [C.POINTER(C.c_int)]),
+    "qraf_hip_malloc": (C.c_int, [C.POINTER(vp), C.c_uint64]),
+    "qraf_hip_free": (C.c_int, [vp]),
+    "qraf_hip_memcpy_h2d": (C.c_int, [vp, vp, C.c_uint64]),
+    "qraf_hip_memcpy_d2h": (C.c_int, [vp, vp, C.c_uint64]),
+    "qraf_hip_memcpy_d2d": (C.c_int, [vp, vp, C.c_uint64, vp]),
+    "qraf_hip_memset": (C.c_int, [vp, C.c_int, C.c_uint64]),
+    "qraf_hip_stream_create": (C.c_int, [C.POINTER(vp)]),
+    "qraf_hip_stream_destroy": (C.c_int, [vp]),
+    "qraf_hip_stream_synchronize": (C.c_int, [vp]),
+    "qraf_hip_device_synchronize": (C.c_int, []),
+    "qraf_hip_event_create": (C.c_int, [C.POINTER(vp)]),
+    "qraf_hip_event_destroy": (C.c_int, [vp]),
+    "qraf_hip_event_record": (C.c_int, [vp, vp]),
+    "qraf_hip_event_elapsed_ms": (C.c_int, [vp, vp, fp]),
+    "qraf_hip_graph_begin": (C.c_int, [vp]),
+    "qraf_hip_graph_end": (C.c_int, [vp, C.POINTER(vp)]),
+    "qraf_hip_graph_launch": (C.c_int, [vp, vp]),
+    "qraf_hip_graph_destroy": (C.c_int, [vp]),
+    "qraf_hip_register_weights": (C.c_int, [vp, C.c_uint64]),
+    "qraf_hip_unregister_weights": (C.c_int, [vp]),
+    "qraf_hip_matvec_q": (C.c_int, [vp, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, fp, fp]),
+    "qraf_hip_matvec_f32": (C.c_int, [fp, fp, fp, C.c_uint32, C.c_uint32]),
+    "qraf_hip_dot_f32": (C.c_int, [fp, fp, C.c_int, fp]),
+    "qraf_hip_rms_norm": (C.c_int, [fp, fp, C.c_int, C.c_float]),
+    "qraf_hip_softmax": (C.c_int, [fp, C.c_int]),
+    "qraf_hip_silu": (C.c_int, [fp, C.c_int]),
+    "qraf_hip_add": (C.c_int, [fp, fp, C.c_int]),
+    "qraf_hip_mul": (C.c_int, [fp, fp, C.c_int]),
+    "qraf_hip_scale": (C.c_int, [fp, C.c_float, C.c_int]),
+    "qraf_hip_matvec_q_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp]),
+    "qraf_hip_matvec_f32_dev": (C.c_int, [vp, vp, vp, C.c_uint32, C.c_uint32, vp]),
+    "qraf_hip_set_matvec_rows_per_wave": (C.c_int, [C.c_int]),
+    "qraf_hip_quantize_dev": (C.c_int, [vp, C.c_uint64, C.c_uint32, vp, vp]),
+    "qraf_hip_gen_weights_dev": (C.c_int, [vp, C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, vp]),
+    "qraf_hip_name_hash": (C.c_uint64, [C.c_char_p]),
+}
+
+
+class HipError(RuntimeError):
+    def __init__(self, fn, code, msg):
+        super().__init__(f"{fn} -> {code}: {msg}")
+        self.code = code
+
+
+def _load():
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run `python qraf_amd/build.py` (no CPU fallback exists)")
+    lib = C.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        f = getattr(lib, name)
+        f.restype = res
+        f.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def check(fn_name, rc):
+    if rc != OK:
+        msg = lib.qraf_hip_last_error()
+        raise HipError(fn_name, rc, msg.decode() if msg else "")
+    return rc
+
+
+def call(name, *args):
+    """Call `name` and raise HipError on a nonzero status."""
+    return check(name, getattr(lib, name)(*args))

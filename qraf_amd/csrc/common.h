@@ -1,0 +1,60 @@
+// common.h -- shared definitions for the gfx950 QRAF decode library.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/qraf_hip.h"
+
+namespace qraf_hip {
+
+// QRAF dtype codes (reference include/core/types.h:27-39).
+constexpr uint32_t DT_F32 = 0, DT_F16 = 1, DT_Q8_0 = 10, DT_Q4_0 = 20;
+
+// Sets the calling thread's last-error string and returns `code`.
+int set_error(int code, const char* fmt, ...);
+void clear_error();
+
+#define QH_CHECK_HIP(expr)                                                              \
+    do {                                                                                \
+        hipError_t e_ = (expr);                                                         \
+        if (e_ != hipSuccess)                                                           \
+            return ::qraf_hip::set_error(QRAF_HIP_ERR_HIP, "%s failed: %s (%s:%d)", #expr, \
+                                         hipGetErrorString(e_), __FILE__, __LINE__);     \
+    } while (0)
+
+#define QH_REQUIRE(cond, code, ...)                                  \
+    do {                                                             \
+        if (!(cond)) return ::qraf_hip::set_error(code, __VA_ARGS__); \
+    } while (0)
+
+// Bytes of one quantized block (reference quantize.cpp:107, :146).
+__host__ __device__ inline size_t q_block_bytes(uint32_t dtype, int bs) {
+    if (dtype == DT_Q8_0) return 4 + (size_t)bs;
+    if (dtype == DT_Q4_0) return 2 + (size_t)(bs / 2);
+    return 0;
+}
+// Bytes of one weight row of in_dim elements (reference backend.cpp:137-140, :166-169).
+__host__ __device__ inline size_t q_row_bytes(uint32_t dtype, int bs, uint32_t in_dim) {
+    return ((size_t)(in_dim + bs - 1) / bs) * q_block_bytes(dtype, bs);
+}
+
+// Kernel launchers (device pointers; stream-ordered; no synchronisation).
+int launch_matvec_q(const void* W, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x,
+                    float* y, hipStream_t s);
+int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s);
+int set_matvec_rows_per_wave(int r);
+int launch_rms_norm(float* x, const float* w, int n, float eps, hipStream_t s);
+int launch_softmax(float* x, int n, hipStream_t s);
+int launch_dot(const float* a, const float* b, int n, float* out, hipStream_t s);
+// op: 0 silu, 1 add, 2 mul, 3 scale
+int launch_ew(int op, float* x, const float* y, float sc, int n, hipStream_t s);
+
+// Library default stream of the current device (created by qraf_hip_init).
+hipStream_t default_stream();
+inline hipStream_t as_stream(void* s) { return s ? (hipStream_t)s : default_stream(); }
+
+}  // namespace qraf_hip

@@ -1,0 +1,178 @@
+"""GPU parity of the Q8_0/Q4_0 matvec and the op-level dispatch mirror
+against the oracle (oracle/oracle.c) on the same seeded inputs.
+
+Tolerance for every matvec output row i (floating point; the GPU sums in a
+different order than the reference's sequential loop):
+    |y_gpu[i] - y_oracle[i]| <= 2 * (K + 2) * 2^-24 * sum_j |w_ij * x_j|
+i.e. twice the classical worst-case bound of a K-term fp32 dot product, which
+both implementations satisfy with respect to the exact value.  A dropped
+block, a wrong scale or a swapped nibble overshoots it by orders of magnitude.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+
+FP = C.POINTER(C.c_float)
+
+
+def quantize_rows(dt, w, n, k, bs=32):
+    if k % bs == 0:
+        return po.quantize(dt, w, bs)
+    return np.concatenate([po.quantize(dt, w[i * k:(i + 1) * k], bs) for i in range(n)])
+
+
+def dequant_rows(dt, wq, n, k, bs=32):
+    rb = len(wq) // n
+    return np.stack([po.dequantize(dt, wq[i * rb:(i + 1) * rb], k, bs) for i in range(n)])
+
+
+def tol_rows(dt, wq, n, k, x, bs=32):
+    W = dequant_rows(dt, wq, n, k, bs).astype(np.float64)
+    if dt == po.Q4_0 and k % 2:  # reference ignores the odd tail element
+        W[:, -1] = 0
+    return 2.0 * (k + 2) * 2.0 ** -24 * (np.abs(W) @ np.abs(x.astype(np.float64))) + 1e-30
+
+
+def check(y, y_ref, tol):
+    err = np.abs(y.astype(np.float64) - y_ref.astype(np.float64))
+    bad = np.nonzero(err > tol)[0]
+    assert bad.size == 0, f"{bad.size} rows out of tolerance, first {bad[:5]}: err {err[bad[:5]]} tol {tol[bad[:5]]}"
+
+
+SHAPES = [
+    # (N, K, bs): BASELINE matvec shapes, SmolLM2-135M and Qwen2.5-3B projection shapes, ragged cases
+    (4096, 4096, 32), (11008, 4096, 32),
+    (576, 576, 32), (192, 576, 32), (1536, 576, 32), (576, 1536, 32), (49152, 576, 32),
+    (2048, 2048, 32), (256, 2048, 32), (11008, 2048, 32), (2048, 11008, 32),
+    (1, 64, 32), (7, 100, 32), (13, 31, 32), (33, 96, 32), (5, 45, 8), (9, 19, 4), (3, 4000, 16),
+]
+
+
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("shape", SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_matvec_q_vs_oracle(hip, dt, shape):
+    n, k, bs = shape
+    print(f"matvec dt={dt} N={n} K={k} bs={bs}", flush=True)
+    rng = np.random.default_rng(n * 131 + k * 7 + dt)
+    w = (rng.standard_normal(n * k) * 0.02).astype(np.float32)
+    wq = quantize_rows(dt, w, n, k, bs)
+    x = rng.standard_normal(k).astype(np.float32)
+    y_ref = po.matvec_q(wq, dt, n, k, x, bs)
+    y = np.zeros(n, np.float32)
+    hip.backend.dispatch_matvec_q(wq, wq.nbytes, dt, bs, n, k, x, y)
+    check(y, y_ref, tol_rows(dt, wq, n, k, x, bs))
+
+
+@pytest.mark.parametrize("rows", [1, 2, 4, 8])
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+def test_matvec_rows_per_wave_variants(hip, rows, dt):
+    n, k = 1000, 2048
+    rng = np.random.default_rng(rows)
+    wq = po.quantize(dt, (rng.standard_normal(n * k) * 0.02).astype(np.float32))
+    x = rng.standard_normal(k).astype(np.float32)
+    y_ref = po.matvec_q(wq, dt, n, k, x)
+    y = np.zeros(n, np.float32)
+    hip.lib.qraf_hip_set_matvec_rows_per_wave(rows)
+    try:
+        hip.backend.dispatch_matvec_q(wq, 0, dt, 32, n, k, x, y)
+    finally:
+        hip.lib.qraf_hip_set_matvec_rows_per_wave(4)
+    check(y, y_ref, tol_rows(dt, wq, n, k, x))
+
+
+def test_matvec_golden_fixtures(hip):
+    from tests.conftest import golden
+    g = golden("matvec.npz")
+    for key in [f[2:] for f in g.files if f.startswith("w_")]:
+        dt, n, k, bs = (int(v) for v in key.split("_"))
+        y = np.zeros(n, np.float32)
+        hip.backend.dispatch_matvec_q(g["w_" + key], 0, dt, bs, n, k, g["x_" + key], y)
+        check(y, g["y_" + key], tol_rows(dt, g["w_" + key], n, k, g["x_" + key], bs))
+    y = np.zeros(40, np.float32)
+    hip.backend.dispatch_matvec_opt(np.ascontiguousarray(g["f32_W"]), g["f32_x"], y, 40, 96)
+    tol = 2 * 98 * 2.0 ** -24 * (np.abs(g["f32_W"]).astype(np.float64) @ np.abs(g["f32_x"]))
+    check(y, g["f32_y"], tol)
+
+
+def test_matvec_unaligned_and_registered(hip):
+    n, k = 300, 4096
+    rng = np.random.default_rng(11)
+    for dt in (po.Q8_0, po.Q4_0):
+        wq = po.quantize(dt, (rng.standard_normal(n * k) * 0.02).astype(np.float32))
+        x = rng.standard_normal(k).astype(np.float32)
+        y_ref = po.matvec_q(wq, dt, n, k, x)
+        tol = tol_rows(dt, wq, n, k, x)
+        # weights at an odd address take the general kernel
+        buf = np.zeros(wq.nbytes + 3, np.uint8)
+        buf[1:1 + wq.nbytes] = wq
+        y = np.zeros(n, np.float32)
+        hip.backend.dispatch_matvec_q(buf[1:], 0, dt, 32, n, k, x, y)
+        check(y, y_ref, tol)
+        # registered (HBM-resident) weights give the same bits as uploaded ones
+        y2 = np.zeros(n, np.float32)
+        hip.backend.dispatch_matvec_q(wq, 0, dt, 32, n, k, x, y2)
+        hip.backend.register_weights(wq)
+        y3 = np.zeros(n, np.float32)
+        hip.backend.dispatch_matvec_q(wq, 0, dt, 32, n, k, x, y3)
+        hip.backend.unregister_weights(wq)
+        assert np.array_equal(y2.view(np.uint32), y3.view(np.uint32))
+
+
+def test_matvec_device_level_matches_op_level(hip):
+    from qraf_amd.backend import DeviceBuffer
+    n, k = 2048, 11008
+    rng = np.random.default_rng(12)
+    for dt in (po.Q8_0, po.Q4_0):
+        wq = po.quantize(dt, (rng.standard_normal(n * k) * 0.02).astype(np.float32))
+        x = rng.standard_normal(k).astype(np.float32)
+        y = np.zeros(n, np.float32)
+        hip.backend.dispatch_matvec_q(wq, 0, dt, 32, n, k, x, y)
+        dw, dx, dy = DeviceBuffer.from_array(wq), DeviceBuffer.from_array(x), DeviceBuffer(n * 4)
+        hip._lib.call("qraf_hip_matvec_q_dev", dw.ptr, dt, 32, n, k, dx.ptr, dy.ptr, None)
+        hip._lib.call("qraf_hip_stream_synchronize", None)
+        assert np.array_equal(dy.download(np.float32, n).view(np.uint32), y.view(np.uint32))
+
+
+def test_matvec_error_codes(hip):
+    x = np.ones(64, np.float32)
+    y = np.zeros(4, np.float32)
+    with pytest.raises(hip.HipError) as e:
+        hip.backend.dispatch_matvec_q(np.zeros(300, np.uint8), 0, 7, 32, 4, 64, x, y)
+    assert e.value.code == -2
+
+
+def test_elementwise_ops_vs_oracle(hip):
+    rng = np.random.default_rng(13)
+    L = po.lib()
+    for n in (576, 2048, 3000):
+        x = (rng.standard_normal(n) * 3).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+        a, b = x.copy(), x.copy()
+        L.or_rms_norm(a.ctypes.data_as(FP), w.ctypes.data_as(FP), n, 1e-5)
+        hip.backend.dispatch_rms_norm(b, w, n, 1e-5)
+        np.testing.assert_allclose(b, a, rtol=2e-6, atol=1e-7)
+        a, b = x.copy(), x.copy()
+        L.or_softmax(a.ctypes.data_as(FP), n)
+        hip.backend.dispatch_softmax(b, n)
+        np.testing.assert_allclose(b, a, rtol=1e-5, atol=1e-9)
+        a, b = x.copy(), x.copy()
+        L.or_silu(a.ctypes.data_as(FP), n)
+        hip.backend.dispatch_silu(b, n)
+        np.testing.assert_allclose(b, a, rtol=4e-7, atol=1e-30)
+        y = rng.standard_normal(n).astype(np.float32)
+        b = x.copy()
+        hip.backend.dispatch_add(b, y, n)
+        assert np.array_equal(b, x + y)
+        b = x.copy()
+        hip.backend.dispatch_mul(b, y, n)
+        assert np.array_equal(b, x * y)
+        b = x.copy()
+        hip.backend.dispatch_scale(b, 0.37, n)
+        assert np.array_equal(b, x * np.float32(0.37))
+        d = hip.backend.dispatch_dot_f32(x, y, n)
+        assert abs(d - float(np.dot(x.astype(np.float64), y))) <= 2 * n * 2.0 ** -24 * float(np.abs(x * y).sum())
