@@ -89,6 +89,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--rows-per-wave", type=int, default=0)
+    ap.add_argument("--kernel", type=int, default=0, help="matvec kernel: 0 auto, 1 one-shot, 2 persistent")
+    ap.add_argument("--wgs-per-cu", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -100,8 +102,7 @@ def main():
     from qraf_amd.backend import DeviceBuffer, Event, Graph, Stream
 
     qraf_amd.backend.backend_init(0)
-    if args.rows_per_wave:
-        call("qraf_hip_set_matvec_rows_per_wave", args.rows_per_wave)
+    call("qraf_hip_set_matvec_tuning", args.kernel, args.rows_per_wave, args.wgs_per_cu)
     stream = Stream()
     rng = np.random.default_rng(2024)
     x_host = rng.standard_normal(4096).astype(np.float32)

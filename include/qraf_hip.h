@@ -108,8 +108,10 @@ int qraf_hip_matvec_q_dev(const void* w, uint32_t dtype, uint32_t block_size, ui
                           uint32_t in_dim, const float* x, float* y, void* stream);
 int qraf_hip_matvec_f32_dev(const float* W, const float* x, float* y, uint32_t out_dim,
                             uint32_t in_dim, void* stream);
-/* Tuning knob of the batch-1 kernel: rows per wave (1, 2, 4 or 8). */
-int qraf_hip_set_matvec_rows_per_wave(int rows);
+/* Tuning of the batch-1 kernel (process-wide): kernel 0 = automatic,
+ * 1 = one-shot, 2 = persistent streaming; rows per wave 0 (automatic), 1, 2,
+ * 4 or 8; workgroups per CU for the persistent kernel (0 = automatic). */
+int qraf_hip_set_matvec_tuning(int kernel, int rows, int wgs_per_cu);
 
 /* quantize_q8_0 / quantize_q4_0 (quantize.cpp:105-183) on the device, block
  * size 32, bit-exact with the reference: `count` fp32 values -> `dst` in the

@@ -395,6 +395,8 @@ int qraf_hip_matvec_f32_dev(const float* W, const float* x, float* y, uint32_t o
     return launch_matvec_f32(W, x, y, out_dim, in_dim, as_stream(stream));
 }
 
-int qraf_hip_set_matvec_rows_per_wave(int rows) { return set_matvec_rows_per_wave(rows); }
+int qraf_hip_set_matvec_tuning(int kernel, int rows, int wgs_per_cu) {
+    return set_matvec_tuning(kernel, rows, wgs_per_cu);
+}
 
 }  // extern "C"

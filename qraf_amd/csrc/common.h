@@ -46,7 +46,7 @@ __host__ __device__ inline size_t q_row_bytes(uint32_t dtype, int bs, uint32_t i
 int launch_matvec_q(const void* W, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x,
                     float* y, hipStream_t s);
 int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s);
-int set_matvec_rows_per_wave(int r);
+int set_matvec_tuning(int kernel, int rows, int wgs_per_cu);
 int launch_rms_norm(float* x, const float* w, int n, float eps, hipStream_t s);
 int launch_softmax(float* x, int n, hipStream_t s);
 int launch_dot(const float* a, const float* b, int n, float* out, hipStream_t s);

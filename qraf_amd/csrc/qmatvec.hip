@@ -66,50 +66,207 @@ __device__ __forceinline__ float wave_reduce_rows(float (&acc)[R], int lane, int
 
 // ----------------------------------------------------------------------------
 // Fast path: block_size 32, 4-byte aligned rows, staged x fits in LDS.
+//
+// Latency hiding: the first unit's weights are requested before x is staged,
+// and every iteration requests the next unit's weights before it computes the
+// current one, so each wave keeps two units x R rows of loads in flight.
 // ----------------------------------------------------------------------------
 template <int R>
-__global__ __launch_bounds__(WG) void qmv_q8_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes,
-                                                   int N, int K, int nb, const float* __restrict__ x,
-                                                   float* __restrict__ y) {
+struct Units {
+    uint32_t s[R];
+    u32x4a4 a[R], b[R];
+};
+
+template <int R>
+__device__ __forceinline__ void load_units(Units<R>& w, const uint8_t* const (&rowp)[R], int u) {
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const uint8_t* p = rowp[r] + (size_t)u * 36;
+        w.s[r] = *(const uint32_t*)p;
+        w.a[r] = *(const u32x4a4*)(p + 4);
+        w.b[r] = *(const u32x4a4*)(p + 20);
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void q8_compute(const Units<R>& w, const float* xs, float (&acc)[R]) {
+    const f32x4* xv = (const f32x4*)xs;
+    f32x4 xr[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) xr[j] = xv[j];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float bs = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t d = j < 4 ? w.a[r][j] : w.b[r][j - 4];
+#pragma unroll
+            for (int k = 0; k < 4; k++) bs = __builtin_fmaf((float)(int8_t)(d >> (8 * k)), xr[j][k], bs);
+        }
+        acc[r] = __builtin_fmaf(bs, __builtin_bit_cast(float, w.s[r]), acc[r]);
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void q4_compute(const Units<R>& w, const float* xu, float (&acc)[R]) {
+    f32x4 xe[8], xo[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        xe[j] = ((const f32x4*)xu)[j];
+        xo[j] = ((const f32x4*)(xu + 36))[j];
+    }
+    const float se8 = 8.f * xu[32], so8 = 8.f * xu[36 + 32];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        // unit dwords: s = 0, a = 1..4, b = 5..8
+        uint32_t dw[9] = {w.s[r], w.a[r][0], w.a[r][1], w.a[r][2], w.a[r][3], w.b[r][0], w.b[r][1], w.b[r][2], w.b[r][3]};
+        float be = 0.f, bo = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+            uint32_t ne = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2);  // even block, nibble bytes 4k..4k+3
+            uint32_t no = dw[5 + k];                                         // odd block, nibble bytes 4k..4k+3
+            uint32_t elo = ne & 0x0F0F0F0Fu, ehi = (ne >> 4) & 0x0F0F0F0Fu;
+            uint32_t olo = no & 0x0F0F0F0Fu, ohi = (no >> 4) & 0x0F0F0F0Fu;
+            asm volatile("" : "+v"(elo), "+v"(ehi), "+v"(olo), "+v"(ohi));  // keep v_cvt_f32_ubyteN selection
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                be = __builtin_fmaf((float)((elo >> (8 * q)) & 0xFFu), xe[2 * k][q], be);
+                be = __builtin_fmaf((float)((ehi >> (8 * q)) & 0xFFu), xe[2 * k + 1][q], be);
+                bo = __builtin_fmaf((float)((olo >> (8 * q)) & 0xFFu), xo[2 * k][q], bo);
+                bo = __builtin_fmaf((float)((ohi >> (8 * q)) & 0xFFu), xo[2 * k + 1][q], bo);
+            }
+        }
+        const float se = half_bits_to_float(dw[0]), so = half_bits_to_float(dw[4] >> 16);
+        acc[r] = __builtin_fmaf(be - se8, se, acc[r]);
+        acc[r] = __builtin_fmaf(bo - so8, so, acc[r]);
+    }
+}
+
+template <int FMT>
+__device__ __forceinline__ void stage_x(float* sx, const float* __restrict__ x, int K, int nb) {
+    if (FMT == 8) {
+        // thread t stages elements 4t..4t+3 (one float4, inside one block)
+        for (int i = threadIdx.x * 4; i < nb * 32; i += WG * 4) {
+            f32x4 v;
+            if (i + 3 < K && ((((uintptr_t)x) & 15) == 0)) {
+                v = *(const f32x4*)(x + i);
+            } else {
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = (i + e < K) ? x[i + e] : 0.f;
+            }
+            *(f32x4*)(sx + (i >> 5) * XS8 + (i & 31)) = v;
+        }
+    } else {
+        // thread t stages elements 8t..8t+7 (even ones then odd ones) and the
+        // four threads of a block reduce its sum.  Keff drops the odd tail
+        // element the reference never reads (quantize.cpp:227).
+        const int Keff = K & ~1;
+        const int nthr = nb * 4;  // 8 elements per thread
+        for (int base = 0; base < nthr; base += WG) {
+            const int t = base + threadIdx.x;
+            const int i = t * 8;
+            float v[8];
+            if (t < nthr && i + 7 < Keff && ((((uintptr_t)x) & 15) == 0)) {
+                f32x4 a = *(const f32x4*)(x + i), b = *(const f32x4*)(x + i + 4);
+                v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
+                v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) v[e] = (t < nthr && i + e < Keff) ? x[i + e] : 0.f;
+            }
+            float part = ((v[0] + v[2]) + (v[4] + v[6])) + ((v[1] + v[3]) + (v[5] + v[7]));
+            part += __shfl_xor(part, 1);
+            part += __shfl_xor(part, 2);
+            if (t < nthr) {
+                const int blk = i >> 5, g = (i & 31) >> 3;
+                float* dst = sx + (blk >> 1) * XS4 + (blk & 1) * 36;
+                *(f32x4*)(dst + g * 8) = f32x4{v[0], v[2], v[4], v[6]};
+                *(f32x4*)(dst + g * 8 + 4) = f32x4{v[1], v[3], v[5], v[7]};
+                if ((t & 3) == 0) dst[32] = part;
+            }
+        }
+    }
+}
+
+// FMT 8: unit = one Q8_0 block; FMT 4: unit = a pair of Q4_0 blocks.
+template <int FMT, int R>
+__global__ __launch_bounds__(WG) void qmv_stream_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
+                                                     int K, int nb, const float* __restrict__ x,
+                                                     float* __restrict__ y) {
     extern __shared__ __align__(16) float sx[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * R;
+    const int U = FMT == 8 ? nb : nb >> 1;
 
-    for (int i = threadIdx.x; i < nb * 32; i += WG) sx[(i >> 5) * XS8 + (i & 31)] = (i < K) ? x[i] : 0.f;
+    const uint8_t* rowp[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) rowp[r] = W + (size_t)min(row0 + r, N - 1) * row_bytes;
+
+    // Loads are unconditional, with the unit index clamped into the row, so
+    // they never sit in a divergent branch (whose join would force a full
+    // vmcnt wait); clamped duplicates re-read bytes already in flight.
+    Units<R> b0, b1;
+    load_units<R>(b0, rowp, min(lane, U - 1));  // in flight while x is staged
+
+    stage_x<FMT>(sx, x, K, nb);
     __syncthreads();
 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.f;
 
+    // Two-deep ping-pong pipeline: unit u+64 is requested before unit u is used.
+    for (int u = lane; u < U; u += 128) {
+        load_units<R>(b1, rowp, min(u + 64, U - 1));
+        if (FMT == 8) q8_compute<R>(b0, sx + u * XS8, acc);
+        else q4_compute<R>(b0, sx + u * XS4, acc);
+        if (u + 64 >= U) break;
+        load_units<R>(b0, rowp, min(u + 128, U - 1));
+        if (FMT == 8) q8_compute<R>(b1, sx + (u + 64) * XS8, acc);
+        else q4_compute<R>(b1, sx + (u + 64) * XS4, acc);
+    }
+    int rr;
+    float v = wave_reduce_rows<R>(acc, lane, &rr);
+    if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = v;
+}
+
+// ----------------------------------------------------------------------------
+// One-shot kernel (J <= 8 units per lane per row): every wave requests all
+// R x J units it will use at entry, before x is staged, so the whole matrix is
+// in flight almost at once; staging x (float4 loads) overlaps those loads.
+// This is the main path: for the shapes of the decode path the kernel is a
+// few microseconds long, and a load -> use -> load chain per wave would pay
+// the HBM latency several times.
+// ----------------------------------------------------------------------------
+template <int FMT, int R, int J>
+__global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
+                                                        int K, int nb, const float* __restrict__ x,
+                                                        float* __restrict__ y) {
+    extern __shared__ __align__(16) float sx[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * 4 + wave) * R;
+    const int U = FMT == 8 ? nb : nb >> 1;
+
     const uint8_t* rowp[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rowp[r] = W + (size_t)min(row0 + r, N - 1) * row_bytes;
 
-    for (int u = lane; u < nb; u += 64) {
-        uint32_t s[R];
-        u32x4a4 a[R], b[R];
+    Units<R> w[J];
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint8_t* p = rowp[r] + (size_t)u * 36;
-            s[r] = *(const uint32_t*)p;
-            a[r] = *(const u32x4a4*)(p + 4);
-            b[r] = *(const u32x4a4*)(p + 20);
-        }
-        const f32x4* xv = (const f32x4*)(sx + u * XS8);
-        f32x4 xr[8];
+    for (int j = 0; j < J; j++) load_units<R>(w[j], rowp, min(lane + 64 * j, U - 1));
+
+    stage_x<FMT>(sx, x, K, nb);
+    __syncthreads();
+
+    float acc[R];
 #pragma unroll
-        for (int j = 0; j < 8; j++) xr[j] = xv[j];
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            float bs = 0.f;
-#pragma unroll
-            for (int j = 0; j < 8; j++) {
-                uint32_t d = j < 4 ? a[r][j] : b[r][j - 4];
-#pragma unroll
-                for (int k = 0; k < 4; k++) bs = __builtin_fmaf((float)(int8_t)(d >> (8 * k)), xr[j][k], bs);
-            }
-            acc[r] = __builtin_fmaf(bs, __builtin_bit_cast(float, s[r]), acc[r]);
+    for (int j = 0; j < J; j++) {
+        const int u = lane + 64 * j;
+        if (u < U) {
+            if (FMT == 8) q8_compute<R>(w[j], sx + u * XS8, acc);
+            else q4_compute<R>(w[j], sx + u * XS4, acc);
         }
     }
     int rr;
@@ -117,84 +274,76 @@ __global__ __launch_bounds__(WG) void qmv_q8_kernel(const uint8_t* __restrict__ 
     if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = v;
 }
 
-template <int R>
-__global__ __launch_bounds__(WG) void qmv_q4_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes,
-                                                   int N, int K, int nb, const float* __restrict__ x,
-                                                   float* __restrict__ y) {
+// ----------------------------------------------------------------------------
+// Persistent streaming kernel: a grid of a few workgroups per CU; each WG
+// stages x once, then each wave walks its share of (row group, unit column)
+// steps with a two-deep ping-pong prefetch.  Waves drift out of phase, so
+// one wave's dequantise-and-FMA work overlaps other waves' loads.
+// ----------------------------------------------------------------------------
+template <int FMT, int R>
+__global__ __launch_bounds__(WG) void qmv_persist_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
+                                                        int K, int nb, const float* __restrict__ x,
+                                                        float* __restrict__ y) {
     extern __shared__ __align__(16) float sx[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * 4 + wave) * R;
-    const int U = nb >> 1;
-    // The reference drops the last element of an odd-length final block
-    // (quantize.cpp:227 iterates this_block/2 pairs): stage it as zero.
-    const int Keff = K & ~1;
+    const int U = FMT == 8 ? nb : nb >> 1;
+    const int J = (U + 63) >> 6;
+    const int ngroups = (N + R - 1) / R;
+    const int gw = blockIdx.x * 4 + wave, nw = gridDim.x * 4;
+    const int my_groups = gw < ngroups ? (ngroups - 1 - gw) / nw + 1 : 0;
+    const int n_it = my_groups * J;
 
-    for (int i = threadIdx.x; i < nb * 32; i += WG) {
-        int blk = i >> 5;
-        sx[(blk >> 1) * XS4 + (blk & 1) * 36 + q4_slot(i & 31)] = (i < Keff) ? x[i] : 0.f;
+    // step it -> row group gw + (it / J) * nw, unit column it % J
+    auto rows_of = [&](int it, const uint8_t* (&rp)[R]) {
+        const int g = gw + (it / J) * nw;
+#pragma unroll
+        for (int r = 0; r < R; r++) rp[r] = W + (size_t)min(g * R + r, N - 1) * row_bytes;
+    };
+    auto unit_of = [&](int it) { return min(lane + 64 * (it % J), U - 1); };
+
+    Units<R> b0, b1;
+    const uint8_t* rp0[R];
+    const uint8_t* rp1[R];
+    if (n_it > 0) {
+        rows_of(0, rp0);
+        load_units<R>(b0, rp0, unit_of(0));
     }
+    stage_x<FMT>(sx, x, K, nb);
     __syncthreads();
-    for (int blk = threadIdx.x; blk < nb; blk += WG) {
-        const float* p = sx + (blk >> 1) * XS4 + (blk & 1) * 36;
-        float t = 0.f;
-        for (int e = 0; e < 32; e++) t += p[e];
-        sx[(blk >> 1) * XS4 + (blk & 1) * 36 + 32] = t;
-    }
-    __syncthreads();
+    if (n_it == 0) return;
 
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) acc[r] = 0.f;
-    const uint8_t* rowp[R];
-#pragma unroll
-    for (int r = 0; r < R; r++) rowp[r] = W + (size_t)min(row0 + r, N - 1) * row_bytes;
 
-    for (int u = lane; u < U; u += 64) {
-        uint32_t d0[R];
-        u32x4a4 a[R], b[R];
+    auto finish = [&](int it) {  // after the last unit column of a row group
+        const int g = gw + (it / J) * nw;
+        int rr;
+        float v = wave_reduce_rows<R>(acc, lane, &rr);
+        if ((lane & (64 / R - 1)) == 0 && g * R + rr < N) y[g * R + rr] = v;
 #pragma unroll
-        for (int r = 0; r < R; r++) {
-            const uint8_t* p = rowp[r] + (size_t)u * 36;
-            d0[r] = *(const uint32_t*)p;
-            a[r] = *(const u32x4a4*)(p + 4);
-            b[r] = *(const u32x4a4*)(p + 20);
+        for (int r = 0; r < R; r++) acc[r] = 0.f;
+    };
+    auto compute = [&](const Units<R>& b, int it) {
+        const int u = lane + 64 * (it % J);
+        if (u < U) {
+            if (FMT == 8) q8_compute<R>(b, sx + u * XS8, acc);
+            else q4_compute<R>(b, sx + u * XS4, acc);
         }
-        const float* xu = sx + u * XS4;
-        f32x4 xe[8], xo[8];
-#pragma unroll
-        for (int j = 0; j < 8; j++) {
-            xe[j] = ((const f32x4*)xu)[j];
-            xo[j] = ((const f32x4*)(xu + 36))[j];
-        }
-        const float se8 = 8.f * xu[32], so8 = 8.f * xu[36 + 32];
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            // a = dwords 1..4, b = dwords 5..8 of the unit
-            uint32_t dw[9] = {d0[r], a[r][0], a[r][1], a[r][2], a[r][3], b[r][0], b[r][1], b[r][2], b[r][3]};
-            float be = 0.f, bo = 0.f;
-#pragma unroll
-            for (int k = 0; k < 4; k++) {
-                uint32_t ne = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2);  // even block bytes 4k..4k+3
-                uint32_t no = dw[5 + k];                                         // odd block bytes 4k..4k+3
-                uint32_t elo = ne & 0x0F0F0F0Fu, ehi = (ne >> 4) & 0x0F0F0F0Fu;
-                uint32_t olo = no & 0x0F0F0F0Fu, ohi = (no >> 4) & 0x0F0F0F0Fu;
-                asm volatile("" : "+v"(elo), "+v"(ehi), "+v"(olo), "+v"(ohi));
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    be = __builtin_fmaf((float)((elo >> (8 * q)) & 0xFFu), xe[2 * k][q], be);
-                    be = __builtin_fmaf((float)((ehi >> (8 * q)) & 0xFFu), xe[2 * k + 1][q], be);
-                    bo = __builtin_fmaf((float)((olo >> (8 * q)) & 0xFFu), xo[2 * k][q], bo);
-                    bo = __builtin_fmaf((float)((ohi >> (8 * q)) & 0xFFu), xo[2 * k + 1][q], bo);
-                }
-            }
-            float se = half_bits_to_float(dw[0]), so = half_bits_to_float(dw[4] >> 16);
-            acc[r] = __builtin_fmaf(be - se8, se, acc[r]);
-            acc[r] = __builtin_fmaf(bo - so8, so, acc[r]);
-        }
+        if (it % J == J - 1) finish(it);
+    };
+
+    for (int it = 0; it < n_it; it += 2) {
+        const int i1 = min(it + 1, n_it - 1);
+        rows_of(i1, rp1);
+        load_units<R>(b1, rp1, unit_of(i1));
+        compute(b0, it);
+        if (it + 1 >= n_it) break;
+        const int i2 = min(it + 2, n_it - 1);
+        rows_of(i2, rp0);
+        load_units<R>(b0, rp0, unit_of(i2));
+        compute(b1, it + 1);
     }
-    int rr;
-    float v = wave_reduce_rows<R>(acc, lane, &rr);
-    if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = v;
 }
 
 // ----------------------------------------------------------------------------
@@ -264,29 +413,70 @@ __global__ __launch_bounds__(WG) void mv_f32_kernel(const float* __restrict__ W,
 // ----------------------------------------------------------------------------
 // Launchers
 // ----------------------------------------------------------------------------
-static int g_rows_per_wave = 4;  // tunable: 1, 2, 4 or 8
+static int g_rows_per_wave = 0;  // 0: automatic; else 1, 2, 4 or 8
+static int g_kernel = 0;         // 0: automatic, 1: one-shot, 2: persistent streaming
+static int g_wgs_per_cu = 0;     // persistent grid size per CU (0: automatic)
 
-int set_matvec_rows_per_wave(int r) {
-    QH_REQUIRE(r == 1 || r == 2 || r == 4 || r == 8, QRAF_HIP_ERR_INVALID, "rows per wave must be 1, 2, 4 or 8");
+int set_matvec_tuning(int kernel, int r, int wgs_per_cu) {
+    QH_REQUIRE(r == 0 || r == 1 || r == 2 || r == 4 || r == 8, QRAF_HIP_ERR_INVALID,
+               "rows per wave must be 0 (auto), 1, 2, 4 or 8");
+    QH_REQUIRE(kernel >= 0 && kernel <= 2, QRAF_HIP_ERR_INVALID, "kernel must be 0, 1 or 2");
+    QH_REQUIRE(wgs_per_cu >= 0 && wgs_per_cu <= 16, QRAF_HIP_ERR_INVALID, "workgroups per CU must be 0..16");
     g_rows_per_wave = r;
+    g_kernel = kernel;
+    g_wgs_per_cu = wgs_per_cu;
     return QRAF_HIP_OK;
 }
 
-template <int R>
-static int launch_fast(uint32_t dtype, const uint8_t* W, size_t rb, int N, int K, int nb, const float* x, float* y,
-                       size_t lds, hipStream_t s) {
-    dim3 grid((N + 4 * R - 1) / (4 * R));
-    if (dtype == DT_Q8_0) {
-        if (lds > 65536) QH_CHECK_HIP(hipFuncSetAttribute((const void*)qmv_q8_kernel<R>,
-                                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL(qmv_q8_kernel<R>, grid, dim3(WG), lds, s, W, (uint32_t)rb, N, K, nb, x, y);
-    } else {
-        if (lds > 65536) QH_CHECK_HIP(hipFuncSetAttribute((const void*)qmv_q4_kernel<R>,
-                                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-        hipLaunchKernelGGL(qmv_q4_kernel<R>, grid, dim3(WG), lds, s, W, (uint32_t)rb, N, K, nb, x, y);
+static int cu_count() {
+    static int n = 0;
+    if (!n) {
+        int d = 0;
+        hipDeviceProp_t p;
+        if (hipGetDevice(&d) == hipSuccess && hipGetDeviceProperties(&p, d) == hipSuccess) n = p.multiProcessorCount;
+        if (n <= 0) n = 256;
     }
-    QH_CHECK_HIP(hipGetLastError());
-    return QRAF_HIP_OK;
+    return n;
+}
+
+typedef void (*qmv_fn)(const uint8_t*, uint32_t, int, int, int, const float*, float*);
+
+template <int FMT, int R, int J>
+static qmv_fn oneshot_if_valid() {
+    if constexpr (R * J <= 8) return qmv_oneshot_kernel<FMT, R, J>;
+    else return nullptr;
+}
+
+template <int FMT, int R>
+static qmv_fn pick_oneshot(int J) {
+    switch (J) {
+        case 1: return oneshot_if_valid<FMT, R, 1>();
+        case 2: return oneshot_if_valid<FMT, R, 2>();
+        case 3: return oneshot_if_valid<FMT, R, 3>();
+        case 4: return oneshot_if_valid<FMT, R, 4>();
+        case 5: return oneshot_if_valid<FMT, R, 5>();
+        case 6: return oneshot_if_valid<FMT, R, 6>();
+        case 7: return oneshot_if_valid<FMT, R, 7>();
+        case 8: return oneshot_if_valid<FMT, R, 8>();
+        default: return nullptr;
+    }
+}
+
+template <int FMT>
+static qmv_fn pick_kernel(int R, int J) {
+    if (J <= 8) {
+        switch (R) {
+            case 1: return pick_oneshot<FMT, 1>(J);
+            case 2: return pick_oneshot<FMT, 2>(J);
+            case 4: return pick_oneshot<FMT, 4>(J);
+            default: return pick_oneshot<FMT, 8>(J);
+        }
+    }
+    switch (R) {
+        case 1: return qmv_stream_kernel<FMT, 1>;
+        case 2: return qmv_stream_kernel<FMT, 2>;
+        default: return qmv_stream_kernel<FMT, 4>;
+    }
 }
 
 int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x, float* y,
@@ -302,12 +492,45 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
     const bool fast = bs == 32 && (((uintptr_t)W) & 3) == 0 && (dtype == DT_Q8_0 || (nb % 2) == 0) &&
                       lds <= 160 * 1024 && rb <= 0xFFFFFFFFu;
     if (fast) {
-        switch (g_rows_per_wave) {
-            case 1: return launch_fast<1>(dtype, W, rb, (int)N, (int)K, nb, x, y, lds, s);
-            case 2: return launch_fast<2>(dtype, W, rb, (int)N, (int)K, nb, x, y, lds, s);
-            case 8: return launch_fast<8>(dtype, W, rb, (int)N, (int)K, nb, x, y, lds, s);
-            default: return launch_fast<4>(dtype, W, rb, (int)N, (int)K, nb, x, y, lds, s);
+        const int U = dtype == DT_Q8_0 ? nb : nb / 2;
+        const int J = (U + 63) / 64;
+        // Automatic choice (measured on MI355X with weights streamed from HBM):
+        // the persistent kernel for large matrices (R=1 / 4 WGs per CU for Q8,
+        // R=2 / 2 WGs per CU for Q4), the one-shot kernel when there are fewer
+        // than 4 row groups per wave slot.
+        int kern = g_kernel;
+        if (kern == 0) kern = (N >= 8192 && J <= 8) ? 2 : 1;
+        if (kern == 2 || J > 8) {
+            const int R = g_rows_per_wave ? min(g_rows_per_wave, 4) : (dtype == DT_Q8_0 ? 1 : 2);
+            const int ngroups = (int)((N + R - 1) / R);
+            const int per_cu = g_wgs_per_cu ? g_wgs_per_cu : (dtype == DT_Q8_0 ? 4 : 2);
+            const int grid = max(1, min((ngroups + 3) / 4, per_cu * cu_count()));
+            qmv_fn k = nullptr;
+            if (dtype == DT_Q8_0) k = R == 1 ? qmv_persist_kernel<8, 1> : R == 2 ? qmv_persist_kernel<8, 2> : qmv_persist_kernel<8, 4>;
+            else k = R == 1 ? qmv_persist_kernel<4, 1> : R == 2 ? qmv_persist_kernel<4, 2> : qmv_persist_kernel<4, 4>;
+            if (lds > 65536)
+                QH_CHECK_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+            hipLaunchKernelGGL(k, dim3(grid), dim3(WG), lds, s, W, (uint32_t)rb, (int)N, (int)K, nb, x, y);
+            QH_CHECK_HIP(hipGetLastError());
+            return QRAF_HIP_OK;
         }
+        int R = g_rows_per_wave;
+        if (R == 0) {
+            // as many rows per wave as the register budget allows (R*J <= 8),
+            // but keep at least ~256 workgroups so every CU streams
+            R = 8;
+            while (R > 1 && (R * J > 8 || (N + 4 * R - 1) / (4 * R) < 256)) R >>= 1;
+        } else if (J <= 8) {
+            while (R > 1 && R * J > 8) R >>= 1;
+        }
+        qmv_fn k = dtype == DT_Q8_0 ? pick_kernel<8>(R, J) : pick_kernel<4>(R, J);
+        QH_REQUIRE(k, QRAF_HIP_ERR_INVALID, "no matvec kernel for R=%d J=%d", R, J);
+        if (lds > 65536)
+            QH_CHECK_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+        hipLaunchKernelGGL(k, dim3((N + 4 * R - 1) / (4 * R)), dim3(WG), lds, s, W, (uint32_t)rb, (int)N, (int)K, nb,
+                           x, y);
+        QH_CHECK_HIP(hipGetLastError());
+        return QRAF_HIP_OK;
     }
     hipLaunchKernelGGL(qmv_generic_kernel, dim3((N + 3) / 4), dim3(WG), 0, s, W, dtype, bs, rb, (int)N, (int)K, x, y);
     QH_CHECK_HIP(hipGetLastError());

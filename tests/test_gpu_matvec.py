@@ -68,20 +68,22 @@ def test_matvec_q_vs_oracle(hip, dt, shape):
     check(y, y_ref, tol_rows(dt, wq, n, k, x, bs))
 
 
-@pytest.mark.parametrize("rows", [1, 2, 4, 8])
+@pytest.mark.parametrize("kernel,rows,wgs", [(1, 1, 0), (1, 2, 0), (1, 4, 0), (1, 8, 0), (2, 1, 4), (2, 2, 2),
+                                             (2, 4, 1), (2, 2, 8)])
 @pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
-def test_matvec_rows_per_wave_variants(hip, rows, dt):
-    n, k = 1000, 2048
-    rng = np.random.default_rng(rows)
+@pytest.mark.parametrize("k", [2048, 11008])
+def test_matvec_kernel_variants(hip, kernel, rows, wgs, dt, k):
+    n = 1000
+    rng = np.random.default_rng(rows + k)
     wq = po.quantize(dt, (rng.standard_normal(n * k) * 0.02).astype(np.float32))
     x = rng.standard_normal(k).astype(np.float32)
     y_ref = po.matvec_q(wq, dt, n, k, x)
     y = np.zeros(n, np.float32)
-    hip.lib.qraf_hip_set_matvec_rows_per_wave(rows)
+    hip.lib.qraf_hip_set_matvec_tuning(kernel, rows, wgs)
     try:
         hip.backend.dispatch_matvec_q(wq, 0, dt, 32, n, k, x, y)
     finally:
-        hip.lib.qraf_hip_set_matvec_rows_per_wave(4)
+        hip.lib.qraf_hip_set_matvec_tuning(0, 0, 0)
     check(y, y_ref, tol_rows(dt, wq, n, k, x))
 
 
