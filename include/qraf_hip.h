@@ -127,6 +127,127 @@ int qraf_hip_gen_weights_dev(void* dst, uint32_t dtype, uint64_t count, uint64_t
 /* FNV-1a of a tensor name (format.h:296-303); returns the hash itself. */
 uint64_t qraf_hip_name_hash(const char* name);
 
+/* ------------------------------------------- ragged paged decode attention */
+
+/* Workspace bytes for qraf_hip_paged_attention_dev.  The workspace must be
+ * zero-filled once after allocation; the kernels leave it ready for the next
+ * call (its first bytes are per-sequence merge counters). */
+uint64_t qraf_hip_attention_workspace_bytes(int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads,
+                                            int32_t head_dim, int32_t max_ctx);
+/* The score / softmax / weighted-sum loops of attention_forward
+ * (attention.cpp:122-150) for a ragged batch of n_seqs sequences that each
+ * attend with one query token:
+ *   q        [n_seqs][n_heads][head_dim] f32, RoPE already applied
+ *   k_cache, v_cache  [num_pages][n_kv_heads][page_size][head_dim], F32 or F16
+ *   page_table [n_seqs][max_pages_per_seq] physical page of logical page j
+ *   ctx_lens [n_seqs] positions attended (1 <= ctx <= max_ctx), on the device
+ *   out      [n_seqs][n_heads][head_dim] f32
+ * Query head h reads KV head h / (n_heads / n_kv_heads) (attention.cpp:127);
+ * scale is 1/sqrt(head_dim) in the reference (attention.cpp:122).
+ * head_dim 64 or 128 with n_heads / n_kv_heads in {1,2,3,4,6,8,12,16}, or
+ * head_dim 16 or 32 with n_heads / n_kv_heads in {1,2,4,8}. */
+int qraf_hip_paged_attention_dev(const float* q, const void* k_cache, const void* v_cache, uint32_t kv_dtype,
+                                 const int32_t* page_table, int32_t max_pages_per_seq, const int32_t* ctx_lens,
+                                 int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                 int32_t page_size, float scale, int32_t max_ctx, float* out, void* workspace,
+                                 uint64_t workspace_bytes, void* stream);
+/* RoPE angle table, RopeCache::init (ops.cpp:179-193) computed on the host
+ * with the host libm: table[pos*head_dim + i] = cos(pos*f_i),
+ * table[pos*head_dim + i + 1] = sin(pos*f_i), f_i = 1/powf(theta, i/head_dim)
+ * for even i < head_dim; `table` holds max_pos*head_dim floats. */
+int qraf_hip_rope_table_host(int32_t max_pos, int32_t head_dim, float rope_theta, float* table);
+/* Bias add + interleaved-pair RoPE + cache store for one new token per
+ * sequence (attention.cpp:100-119, ops.cpp:158-177): qkv [n_seqs][(H+2Hkv)*hd]
+ * rows of the fused q|k|v projection, bias the matching F32 vector or NULL,
+ * rope_table a device copy of the qraf_hip_rope_table_host table covering
+ * every position; writes rotated q to q_out [n_seqs][H*hd] and rotated k, v at
+ * positions[s] into the paged cache. */
+int qraf_hip_rope_append_dev(const float* qkv, const float* bias, int32_t n_seqs, int32_t n_heads,
+                             int32_t n_kv_heads, int32_t head_dim, const int32_t* positions, const float* rope_table,
+                             float* q_out, void* k_cache, void* v_cache, uint32_t kv_dtype, const int32_t* page_table,
+                             int32_t max_pages_per_seq, int32_t page_size, void* stream);
+
+/* ------------------------------------------------- batched quantized GEMM */
+
+/* Split fp32 activations into bf16 planes x = hi + lo + r, |r| <= 2^-17 |x|
+ * (round-to-nearest-even at both steps), the operand form of
+ * qraf_hip_qgemm_dev.  rows x cols elements, row-major. */
+int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int32_t rows, int32_t cols,
+                            void* stream);
+/* dispatch_matvec_q (backend.cpp:131-199) for `batch` activation rows at
+ * once on the matrix cores: y[m][i] = dot(row_i(w), x[m]) (+ add[m][i] when add
+ * is not NULL), m < batch <= 128, i < out_dim.  w: Q8_0 (4-byte aligned) or
+ * Q4_0 (2-byte aligned), block size 32, in_dim a multiple of 32; x given as the hi/lo planes of
+ * qraf_hip_split_bf16_dev (16-byte aligned).  Error bound per output:
+ * (2^-17 + (in_dim+2) 2^-24) sum_k |w_k x_k|. */
+int qraf_hip_qgemm_dev(const void* w, uint32_t dtype, uint32_t block_size, uint32_t out_dim, uint32_t in_dim,
+                       const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, float* y, const float* add,
+                       void* stream);
+
+/* ------------------------------------------------------------- engine */
+
+/* The model hyper-parameters the reference reads from the QRAF config block
+ * (loader.cpp:151-177, types.h:97-124).  num_kv_heads 0 means num_heads;
+ * head_dim = hidden_size / num_heads (16, 32, 64 or 128). */
+typedef struct qraf_model_config {
+    uint32_t vocab_size, hidden_size, num_layers, num_heads, num_kv_heads, intermediate_size, max_seq_len;
+    float rope_theta, rms_norm_eps;
+} qraf_model_config;
+
+/* Engine resources.  kv_dtype F32 (0, the reference's KVCache) or F16;
+ * page_size tokens per KV page (0 -> 16, must divide 256); max_batch rows
+ * per step (0 -> 1, at most 128); num_pages KV pages per layer (0 -> enough
+ * for max_batch sequences of min(max_seq_len, 8192) positions). */
+typedef struct qraf_engine_options {
+    uint32_t kv_dtype, page_size, max_batch, num_pages;
+} qraf_engine_options;
+
+typedef struct qraf_engine qraf_engine;
+
+int qraf_engine_create(const qraf_model_config* config, const qraf_engine_options* options, qraf_engine** engine);
+int qraf_engine_destroy(qraf_engine* engine);
+/* Transformer::init weight binding (transformer.cpp:96-126, :310-400) for
+ * one tensor, by the reference's names: model.embed_tokens.weight,
+ * lm_head.weight (absent: tied to the embedding), model.norm.weight,
+ * model.layers.<l>.{self_attn.{q,k,v,o}_proj.weight, self_attn.{q,k,v}_proj.bias,
+ * mlp.{gate,up,down}_proj.weight, input_layernorm.weight,
+ * post_attention_layernorm.weight}.  Shapes follow the reference's
+ * [out, in] orientation; data is host memory, copied to HBM.  Quantized
+ * tensors need block size 32; biases that are not F32 are ignored and the
+ * four attention (three MLP) matrices of a layer must share one dtype, as in
+ * the reference; other names are ignored. */
+int qraf_engine_set_tensor(qraf_engine* engine, const char* name, uint32_t dtype, uint32_t block_size,
+                           const uint32_t* shape, uint32_t ndim, const void* data, uint64_t bytes);
+/* All weights synthetic, generated on the device: every tensor N(0, 0.02)
+ * from qraf_hip_gen_weights_dev with stream = qraf_hip_name_hash(name),
+ * norms 1, optional F32 q/k/v biases, lm_head unless tied. */
+int qraf_engine_generate_weights(qraf_engine* engine, uint32_t weight_dtype, uint32_t embed_dtype,
+                                 uint32_t head_dtype, int32_t tied, int32_t qkv_bias, uint64_t seed);
+/* Checks that every tensor the forward pass reads is present. */
+int qraf_engine_finalize(qraf_engine* engine);
+
+/* Sequences own KV pages; positions are added in order (pos <= length). */
+int qraf_engine_seq_create(qraf_engine* engine, int32_t* seq_id);
+int qraf_engine_seq_release(qraf_engine* engine, int32_t seq_id);
+int qraf_engine_seq_length(qraf_engine* engine, int32_t seq_id, int32_t* length);
+int qraf_engine_free_pages(qraf_engine* engine, int32_t* free_pages);
+
+/* One batched decode step: row i feeds token tokens[i] at position
+ * positions[i] of sequence seq_ids[i] (a sequence may own several rows, in
+ * increasing position order: chunked prefill).  Rows with want_logits[i] != 0
+ * (all rows when want_logits is NULL) get logits, written compactly in row
+ * order to logits [k][vocab] and/or their argmax (Sampler::argmax,
+ * sampler.cpp:25-35) to next_tokens [k]; either output may be NULL.
+ * QRAF_HIP_ERR_NOMEM when the KV page pool cannot hold the new positions (no
+ * state changes in that case).  The reference has no batched call: this is
+ * Transformer::forward (transformer.cpp:573-639) for many sequences at once. */
+int qraf_engine_step(qraf_engine* engine, int32_t n_rows, const int32_t* seq_ids, const uint32_t* tokens,
+                     const int32_t* positions, const uint8_t* want_logits, float* logits, uint32_t* next_tokens);
+/* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)
+ * on the engine's default sequence, and Transformer::reset() (:641-643). */
+int qraf_engine_forward(qraf_engine* engine, uint32_t token, int32_t pos, float* logits);
+int qraf_engine_reset(qraf_engine* engine);
+
 #ifdef __cplusplus
 }
 #endif

@@ -62,7 +62,45 @@ SIGNATURES = {
     "qraf_hip_quantize_dev": (C.c_int, [vp, C.c_uint64, C.c_uint32, vp, vp]),
     "qraf_hip_gen_weights_dev": (C.c_int, [vp, C.c_uint32, C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, vp]),
     "qraf_hip_name_hash": (C.c_uint64, [C.c_char_p]),
+    "qraf_hip_attention_workspace_bytes": (C.c_uint64, [C.c_int32] * 5),
+    "qraf_hip_paged_attention_dev": (C.c_int, [vp, vp, vp, C.c_uint32, vp, C.c_int32, vp] + [C.c_int32] * 5 +
+                                     [C.c_float, C.c_int32, vp, vp, C.c_uint64, vp]),
+    "qraf_hip_split_bf16_dev": (C.c_int, [vp, vp, vp, C.c_int32, C.c_int32, vp]),
+    "qraf_hip_qgemm_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp,
+                                     vp]),
+    "qraf_hip_rope_table_host": (C.c_int, [C.c_int32, C.c_int32, C.c_float, fp]),
+    "qraf_hip_rope_append_dev": (C.c_int, [vp, vp] + [C.c_int32] * 4 + [vp, vp, vp, vp, vp, C.c_uint32, vp,
+                                                                       C.c_int32, C.c_int32, vp]),
 }
+
+
+class ModelConfig(C.Structure):
+    """qraf_model_config (include/qraf_hip.h)."""
+    _fields_ = [(n, C.c_uint32) for n in ("vocab_size", "hidden_size", "num_layers", "num_heads", "num_kv_heads",
+                                          "intermediate_size", "max_seq_len")] + [
+        ("rope_theta", C.c_float), ("rms_norm_eps", C.c_float)]
+
+
+class EngineOptions(C.Structure):
+    """qraf_engine_options (include/qraf_hip.h)."""
+    _fields_ = [(n, C.c_uint32) for n in ("kv_dtype", "page_size", "max_batch", "num_pages")]
+
+
+SIGNATURES.update({
+    "qraf_engine_create": (C.c_int, [C.POINTER(ModelConfig), C.POINTER(EngineOptions), C.POINTER(vp)]),
+    "qraf_engine_destroy": (C.c_int, [vp]),
+    "qraf_engine_set_tensor": (C.c_int, [vp, C.c_char_p, C.c_uint32, C.c_uint32, u32p, C.c_uint32, vp, C.c_uint64]),
+    "qraf_engine_generate_weights": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32, C.c_int32,
+                                               C.c_uint64]),
+    "qraf_engine_finalize": (C.c_int, [vp]),
+    "qraf_engine_seq_create": (C.c_int, [vp, i32p]),
+    "qraf_engine_seq_release": (C.c_int, [vp, C.c_int32]),
+    "qraf_engine_seq_length": (C.c_int, [vp, C.c_int32, i32p]),
+    "qraf_engine_free_pages": (C.c_int, [vp, i32p]),
+    "qraf_engine_step": (C.c_int, [vp, C.c_int32, i32p, u32p, i32p, C.POINTER(C.c_uint8), fp, u32p]),
+    "qraf_engine_forward": (C.c_int, [vp, C.c_uint32, C.c_int32, fp]),
+    "qraf_engine_reset": (C.c_int, [vp]),
+})
 
 
 class HipError(RuntimeError):

@@ -4,7 +4,9 @@
 
 Every csrc/*.hip file is compiled to an object in parallel and the objects
 are linked into qraf_amd/libqraf_hip.so.  Packed-FP32 instruction selection
-is disabled for all device code (-target-feature -packed-fp32-ops).
+is disabled for all device code (-target-feature -packed-fp32-ops), and no
+multiply-add is contracted into an FMA unless the source asks for one
+(-ffp-contract=off): unfused products round like the reference's scalar code.
 """
 from __future__ import annotations
 
@@ -22,7 +24,7 @@ OBJ = os.path.join(PKG, "_build")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 ARCH = os.environ.get("QRAF_HIP_ARCH", "gfx950")
-FLAGS = ["-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}", "-Xclang", "-target-feature",
+FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", f"--offload-arch={ARCH}", "-Xclang", "-target-feature",
          "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument", "-I", os.path.join(ROOT, "include")]
 
 

@@ -43,15 +43,31 @@ __host__ __device__ inline size_t q_row_bytes(uint32_t dtype, int bs, uint32_t i
 }
 
 // Kernel launchers (device pointers; stream-ordered; no synchronisation).
+// add (optional, may alias y): y[i] = dot(row_i, x) + add[i]
 int launch_matvec_q(const void* W, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x,
-                    float* y, hipStream_t s);
-int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s);
+                    float* y, hipStream_t s, const float* add = nullptr);
+int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s,
+                      const float* add = nullptr);
 int set_matvec_tuning(int kernel, int rows, int wgs_per_cu);
 int launch_rms_norm(float* x, const float* w, int n, float eps, hipStream_t s);
 int launch_softmax(float* x, int n, hipStream_t s);
 int launch_dot(const float* a, const float* b, int n, float* out, hipStream_t s);
 // op: 0 silu, 1 add, 2 mul, 3 scale
 int launch_ew(int op, float* x, const float* y, float sc, int n, hipStream_t s);
+
+int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s);
+int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
+                 float* Y, const float* add, hipStream_t s);
+size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx);
+int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv_dtype, const int32_t* page_table,
+                     int max_pages, const int32_t* ctx, int n, int H, int Hkv, int hd, int page_size, float scale,
+                     int max_ctx, float* out, void* ws, size_t ws_bytes, hipStream_t st);
+int launch_rope_append(const float* qkv, const float* bias, int n, int H, int Hkv, int hd, const int32_t* pos,
+                       const float* rope, float* q_out, void* kc, void* vc, uint32_t kv_dtype,
+                       const int32_t* page_table, int max_pages, int page_size, hipStream_t st);
+int launch_gen_weights(void* dst, uint32_t dtype, uint64_t count, uint64_t seed, uint64_t stream_id, float stddev,
+                       hipStream_t s);
+int launch_quantize(const float* src, uint64_t count, uint32_t dtype, void* dst, hipStream_t s);
 
 // Library default stream of the current device (created by qraf_hip_init).
 hipStream_t default_stream();

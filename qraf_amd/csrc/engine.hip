@@ -1,0 +1,756 @@
+// engine.hip -- device-resident decode engine for LLaMA/Qwen2-family QRAF models.
+//
+// The MI355X counterpart of Transformer::init / forward / reset
+// (reference transformer.cpp:310-439, :573-643, transformer.h:55-90) with
+// the one API extension a continuous batch needs: a step that advances
+// several sequences at once, each with its own token and position.
+//
+// Weights are uploaded (or generated) once into HBM, in the reference's
+// block layout, with two layout-only changes that let one launch serve
+// several reference matvecs: the q, k and v projection rows are stored
+// back to back (one [q_dim + 2 kv_dim] x hidden matrix), and the gate and up
+// projection rows are interleaved (row 2i = gate_i, row 2i+1 = up_i), so
+// SiLU(gate) * up (attention.cpp:172-180) pairs neighbouring outputs.
+//
+// KV cache: a pool of pages per layer, [num_pages][Hkv][page_size][head_dim]
+// (f32 or f16); sequences own page lists handed out by a host-side free list.
+// Each step: embedding row, then per layer RMSNorm -> fused QKV projection
+// -> bias + RoPE + page append -> ragged paged attention -> O projection with
+// the residual add in its epilogue -> RMSNorm -> gate/up projection ->
+// SiLU-gate -> down projection with the residual add; final RMSNorm, LM head
+// for the rows that want logits, argmax on the device.  Batch 1 runs on the
+// streaming matvec, larger batches on the matrix-core GEMM.
+#include <math.h>
+#include <string.h>
+
+#include <algorithm>
+#include <string>
+#include <vector>
+
+#include "common.h"
+
+namespace qraf_hip {
+
+// ---------------------------------------------------------------- kernels
+
+// embedding row of token tok[s] (load_tensor_f32 + Tensor::row,
+// transformer.cpp:34-39, :577): dequantised values (f32)q * scale
+__global__ void embed_kernel(const uint8_t* __restrict__ emb, uint32_t dtype, int bs, int D,
+                             const int32_t* __restrict__ tok, float* __restrict__ h) {
+    const int s = blockIdx.x;
+    const size_t row = (size_t)tok[s];
+    for (int i = threadIdx.x; i < D; i += blockDim.x) {
+        const size_t e = row * D + i;
+        float v;
+        if (dtype == DT_F32) {
+            v = ((const float*)emb)[e];
+        } else if (dtype == DT_F16) {
+            v = (float)((const _Float16*)emb)[e];
+        } else {
+            const size_t b = e / bs, w = e % bs;
+            const uint8_t* p = emb + b * q_block_bytes(dtype, bs);
+            if (dtype == DT_Q8_0) {
+                const float sc = __builtin_bit_cast(float, (uint32_t)p[0] | ((uint32_t)p[1] << 8) |
+                                                               ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24));
+                v = __fmul_rn((float)(int8_t)p[4 + w], sc);
+            } else {
+                const float sc = (float)__builtin_bit_cast(_Float16, (uint16_t)(p[0] | (p[1] << 8)));
+                const uint8_t q = p[2 + w / 2];
+                v = __fmul_rn((float)((int)((w & 1) ? (q >> 4) : (q & 15)) - 8), sc);
+            }
+        }
+        h[(size_t)s * D + i] = v;
+    }
+}
+
+// rms_norm_inplace (ops.cpp:107-118) of `rows` rows, one workgroup per row
+__global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restrict__ x, const float* __restrict__ w,
+                                                          int D, float eps, float* __restrict__ out,
+                                                          const int32_t* __restrict__ row_map) {
+    __shared__ float red[4];
+    const int s = blockIdx.x;
+    const float* xr = x + (size_t)(row_map ? row_map[s] : s) * D;
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < D; i += 256) ss = __builtin_fmaf(xr[i], xr[i], ss);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float r = 1.0f / sqrtf(ss / (float)D + eps);
+    for (int i = threadIdx.x; i < D; i += 256) out[(size_t)s * D + i] = __fmul_rn(__fmul_rn(xr[i], r), w[i]);
+}
+
+// silu_inplace then mul_inplace (attention.cpp:177-178) on interleaved gate/up rows
+__global__ void silu_gate_kernel(const float* __restrict__ gu, int F, int n, float* __restrict__ act) {
+    const size_t total = (size_t)n * F;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const size_t s = i / F, j = i % F;
+        const float g = gu[s * 2 * F + 2 * j], u = gu[s * 2 * F + 2 * j + 1];
+        act[i] = __fmul_rn(g / (1.0f + expf(-g)), u);
+    }
+}
+
+// Sampler::argmax (sampler.cpp:25-35): strict '>', lowest index wins ties
+__global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restrict__ logits, int V,
+                                                         uint32_t* __restrict__ out) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+    const float* l = logits + (size_t)blockIdx.x * V;
+    // each thread scans its strided indices in increasing order: its first
+    // value seeds the running maximum, then only strictly larger values win
+    float best = -INFINITY;
+    int bi = V;  // sentinel: no index seen yet
+    for (int i = threadIdx.x; i < V; i += 256) {
+        const float v = l[i];
+        if (bi == V || v > best) {
+            best = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(best, o);
+        const int oi = __shfl_xor(bi, o);
+        if (ov > best || (ov == best && oi < bi)) {
+            best = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = best;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 4; w++)
+            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
+                best = sv[w];
+                bi = si[w];
+            }
+        out[blockIdx.x] = (uint32_t)(bi == V ? 0 : bi);
+    }
+}
+
+__global__ void fill_kernel(float* p, float v, size_t n) {
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
+}
+
+// compact rows: dst[j] = src[rows[j]] (D floats each)
+__global__ void gather_rows_kernel(const float* __restrict__ src, const int32_t* __restrict__ rows, int D,
+                                   float* __restrict__ dst) {
+    const int j = blockIdx.x;
+    for (int i = threadIdx.x; i < D; i += blockDim.x) dst[(size_t)j * D + i] = src[(size_t)rows[j] * D + i];
+}
+
+}  // namespace qraf_hip
+
+// ---------------------------------------------------------------- engine
+
+using namespace qraf_hip;
+
+struct qraf_engine {
+    qraf_model_config c{};
+    qraf_engine_options o{};
+    int hd = 0, qd = 0, kvd = 0, qkvd = 0, capacity = 0, max_pages = 0;
+    hipStream_t stream = nullptr;
+    bool finalized = false;
+
+    struct Layer {
+        uint8_t* wqkv = nullptr;
+        uint8_t* wo = nullptr;
+        uint8_t* wgu = nullptr;
+        uint8_t* wd = nullptr;
+        float* bqkv = nullptr;
+        float* an = nullptr;
+        float* fn = nullptr;
+        uint32_t dt_attn = 0xFFFFFFFFu, dt_mlp = 0xFFFFFFFFu;
+        uint32_t have = 0;  // bit per tensor
+        bool has_bias = false;
+    };
+    std::vector<Layer> layers;
+    uint8_t* embed = nullptr;
+    uint32_t dt_embed = 0xFFFFFFFFu;
+    uint8_t* head = nullptr;
+    uint32_t dt_head = 0xFFFFFFFFu;
+    float* onorm = nullptr;
+    std::vector<void*> allocs;
+
+    // KV pool and pages
+    uint8_t* kpool = nullptr;
+    uint8_t* vpool = nullptr;
+    size_t layer_kv_bytes = 0;
+    std::vector<int32_t> free_pages;
+    struct Seq {
+        bool live = false;
+        int len = 0;
+        std::vector<int32_t> pages;
+    };
+    std::vector<Seq> seqs;
+    int32_t default_seq = -1;
+
+    // activations (max_batch rows)
+    float *h = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *gu = nullptr, *act = nullptr,
+          *logits = nullptr, *xhead = nullptr, *rope = nullptr;
+    uint16_t *xh = nullptr, *xl = nullptr;
+    uint32_t* amax = nullptr;
+    int32_t* d_in = nullptr;  // tokens | positions | ctx | logit rows | page table rows
+    int32_t* h_in = nullptr;  // pinned staging of the same
+    uint32_t* h_amax = nullptr;
+    void* attn_ws = nullptr;
+    size_t attn_ws_bytes = 0;
+    size_t in_words = 0;
+};
+
+static int ealloc(qraf_engine* e, void** p, size_t bytes) {
+    hipError_t r = hipMalloc(p, bytes ? bytes : 16);
+    if (r == hipErrorOutOfMemory)
+        return set_error(QRAF_HIP_ERR_NOMEM, "engine: out of device memory (%zu bytes)", bytes);
+    QH_CHECK_HIP(r);
+    e->allocs.push_back(*p);
+    return QRAF_HIP_OK;
+}
+
+#define QH_TRY(expr)                        \
+    do {                                    \
+        int rc_ = (expr);                   \
+        if (rc_ != QRAF_HIP_OK) return rc_; \
+    } while (0)
+
+static size_t dt_row_bytes(uint32_t dt, uint32_t cols) {
+    if (dt == DT_F32) return (size_t)cols * 4;
+    if (dt == DT_F16) return (size_t)cols * 2;
+    return q_row_bytes(dt, 32, cols);
+}
+
+enum {
+    T_Q = 1, T_K = 2, T_V = 4, T_O = 8, T_G = 16, T_U = 32, T_D = 64, T_AN = 128, T_FN = 256,
+    T_ALL = 511
+};
+
+// parse "model.layers.<l>.<rest>"
+static bool layer_name(const char* name, int* l, const char** rest) {
+    const char* pre = "model.layers.";
+    if (strncmp(name, pre, strlen(pre)) != 0) return false;
+    const char* p = name + strlen(pre);
+    char* end = nullptr;
+    long v = strtol(p, &end, 10);
+    if (end == p || *end != '.') return false;
+    *l = (int)v;
+    *rest = end + 1;
+    return true;
+}
+
+// host dequantisation of a norm vector (load_tensor_f32, transformer.cpp:34-39)
+static int host_to_f32(uint32_t dt, const void* data, uint64_t bytes, uint32_t n, std::vector<float>& out) {
+    out.assign(n, 0.f);
+    if (dt == DT_F32) {
+        QH_REQUIRE(bytes >= (uint64_t)n * 4, QRAF_HIP_ERR_INVALID, "tensor too small");
+        memcpy(out.data(), data, (size_t)n * 4);
+        return QRAF_HIP_OK;
+    }
+    return set_error(QRAF_HIP_ERR_DTYPE, "norm weights must be F32 (got dtype %u)", dt);
+}
+
+extern "C" {
+
+int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* opt, qraf_engine** out) {
+    clear_error();
+    QH_REQUIRE(cfg && out, QRAF_HIP_ERR_INVALID, "engine: null argument");
+    *out = nullptr;
+    const qraf_model_config& c = *cfg;
+    QH_REQUIRE(c.vocab_size && c.hidden_size && c.num_layers && c.num_heads && c.intermediate_size,
+               QRAF_HIP_ERR_INVALID, "engine: empty dimension in the model config");
+    const uint32_t kvh = c.num_kv_heads ? c.num_kv_heads : c.num_heads;  // types.h:123
+    QH_REQUIRE(c.hidden_size % c.num_heads == 0 && c.num_heads % kvh == 0, QRAF_HIP_ERR_INVALID,
+               "engine: heads do not divide hidden size / kv heads");
+    const int hd = (int)(c.hidden_size / c.num_heads);  // types.h:122
+    QH_REQUIRE(hd == 16 || hd == 32 || hd == 64 || hd == 128, QRAF_HIP_ERR_INVALID,
+               "engine: head_dim %d (16, 32, 64 or 128 supported)", hd);
+    QH_REQUIRE(c.hidden_size % 32 == 0 && c.intermediate_size % 32 == 0, QRAF_HIP_ERR_INVALID,
+               "engine: hidden and intermediate sizes must be multiples of 32");
+    qraf_engine_options o = opt ? *opt : qraf_engine_options{};
+    if (!o.kv_dtype) o.kv_dtype = DT_F32;
+    if (o.kv_dtype != DT_F32 && o.kv_dtype != DT_F16) return set_error(QRAF_HIP_ERR_DTYPE, "engine: KV dtype %u", o.kv_dtype);
+    if (!o.page_size) o.page_size = 16;
+    if (!o.max_batch) o.max_batch = 1;
+    QH_REQUIRE(o.max_batch <= 128, QRAF_HIP_ERR_INVALID, "engine: max_batch %u > 128", o.max_batch);
+    QH_REQUIRE(o.page_size <= 256 && (256 % o.page_size) == 0, QRAF_HIP_ERR_INVALID,
+               "engine: page_size must divide 256");
+
+    qraf_engine* e = new qraf_engine();
+    e->c = c;
+    e->c.num_kv_heads = kvh;
+    e->hd = hd;
+    e->qd = (int)c.num_heads * hd;
+    e->kvd = (int)kvh * hd;
+    e->qkvd = e->qd + 2 * e->kvd;
+    e->capacity = (int)std::min(c.max_seq_len ? c.max_seq_len : 2048u, 8192u);  // transformer.cpp:425-428
+    e->max_pages = (e->capacity + (int)o.page_size - 1) / (int)o.page_size;
+    if (!o.num_pages) o.num_pages = o.max_batch * (uint32_t)e->max_pages;
+    e->o = o;
+    e->layers.resize(c.num_layers);
+    auto fail = [&](int rc) {
+        for (void* p : e->allocs) hipFree(p);
+        if (e->h_in) hipHostFree(e->h_in);
+        if (e->h_amax) hipHostFree(e->h_amax);
+        if (e->stream) hipStreamDestroy(e->stream);
+        delete e;
+        return rc;
+    };
+    if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
+        return fail(set_error(QRAF_HIP_ERR_HIP, "engine: stream creation failed"));
+    const int B = (int)o.max_batch, D = (int)c.hidden_size, F = (int)c.intermediate_size, V = (int)c.vocab_size;
+    const size_t kv_elem = o.kv_dtype == DT_F16 ? 2 : 4;
+    e->layer_kv_bytes = (size_t)o.num_pages * kvh * o.page_size * hd * kv_elem;
+    int rc = QRAF_HIP_OK;
+#define A(ptr, bytes)                                           \
+    if ((rc = ealloc(e, (void**)&(ptr), (bytes))) != QRAF_HIP_OK) \
+        return fail(rc);
+    A(e->kpool, e->layer_kv_bytes * c.num_layers);
+    A(e->vpool, e->layer_kv_bytes * c.num_layers);
+    A(e->h, (size_t)B * D * 4);
+    A(e->xn, (size_t)B * D * 4);
+    A(e->xhead, (size_t)B * D * 4);
+    A(e->qkv, (size_t)B * e->qkvd * 4);
+    A(e->q, (size_t)B * e->qd * 4);
+    A(e->att, (size_t)B * e->qd * 4);
+    A(e->gu, (size_t)B * 2 * F * 4);
+    A(e->act, (size_t)B * F * 4);
+    A(e->logits, (size_t)B * V * 4);
+    const size_t kmax = std::max({(size_t)D, (size_t)F, (size_t)e->qd});
+    A(e->xh, (size_t)B * kmax * 2 + 64);
+    A(e->xl, (size_t)B * kmax * 2 + 64);
+    A(e->amax, (size_t)B * 4);
+    e->in_words = (size_t)B * (4 + e->max_pages);
+    A(e->d_in, e->in_words * 4);
+    e->attn_ws_bytes = attn_workspace_bytes(B, (int)c.num_heads, (int)kvh, hd, e->capacity);
+    A(e->attn_ws, e->attn_ws_bytes);
+    A(e->rope, (size_t)e->capacity * hd * 4);
+#undef A
+    if (hipMemset(e->attn_ws, 0, e->attn_ws_bytes) != hipSuccess ||
+        hipHostMalloc((void**)&e->h_in, e->in_words * 4, hipHostMallocDefault) != hipSuccess ||
+        hipHostMalloc((void**)&e->h_amax, (size_t)B * 4, hipHostMallocDefault) != hipSuccess)
+        return fail(set_error(QRAF_HIP_ERR_HIP, "engine: workspace set-up failed"));
+    // RoPE table from the host libm (RopeCache::init, ops.cpp:179-193)
+    {
+        std::vector<float> tab((size_t)e->capacity * hd);
+        qraf_hip_rope_table_host(e->capacity, hd, c.rope_theta, tab.data());
+        if (hipMemcpy(e->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
+            return fail(set_error(QRAF_HIP_ERR_HIP, "engine: rope table upload failed"));
+    }
+    e->free_pages.resize(o.num_pages);
+    for (uint32_t i = 0; i < o.num_pages; i++) e->free_pages[i] = (int32_t)(o.num_pages - 1 - i);
+    *out = e;
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_destroy(qraf_engine* e) {
+    if (!e) return QRAF_HIP_OK;
+    hipStreamSynchronize(e->stream);
+    for (void* p : e->allocs) hipFree(p);
+    if (e->h_in) hipHostFree(e->h_in);
+    if (e->h_amax) hipHostFree(e->h_amax);
+    hipStreamDestroy(e->stream);
+    delete e;
+    return QRAF_HIP_OK;
+}
+
+// Bind one tensor by its reference name (transformer.cpp:96-126, :310-400).
+int qraf_engine_set_tensor(qraf_engine* e, const char* name, uint32_t dtype, uint32_t block_size, const uint32_t* shape,
+                           uint32_t ndim, const void* data, uint64_t bytes) {
+    clear_error();
+    QH_REQUIRE(e && name && data && shape && ndim >= 1, QRAF_HIP_ERR_INVALID, "set_tensor: null argument");
+    QH_REQUIRE(!e->finalized, QRAF_HIP_ERR_STATE, "set_tensor: engine already finalized");
+    QH_REQUIRE(dtype == DT_F32 || dtype == DT_F16 || dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE,
+               "set_tensor %s: unsupported dtype %u", name, dtype);
+    QH_REQUIRE(dtype == DT_F32 || dtype == DT_F16 || block_size == 0 || block_size == 32, QRAF_HIP_ERR_DTYPE,
+               "set_tensor %s: quant block size %u (32 supported)", name, block_size);
+    const qraf_model_config& c = e->c;
+    const uint32_t D = c.hidden_size, F = c.intermediate_size;
+    const uint32_t rows = shape[0], cols = ndim > 1 ? shape[1] : 1;
+    auto need = [&](uint32_t r, uint32_t cc) -> int {
+        QH_REQUIRE(rows == r && (ndim == 1 ? cc == 1 : cols == cc), QRAF_HIP_ERR_INVALID,
+                   "set_tensor %s: shape [%u, %u], expected [%u, %u]", name, rows, cols, r, cc);
+        QH_REQUIRE(bytes >= (uint64_t)r * dt_row_bytes(dtype, cc), QRAF_HIP_ERR_INVALID,
+                   "set_tensor %s: %llu bytes, expected %zu", name, (unsigned long long)bytes,
+                   (size_t)r * dt_row_bytes(dtype, cc));
+        return QRAF_HIP_OK;
+    };
+    auto upload = [&](void* dst, const void* src, size_t n) -> int {
+        QH_CHECK_HIP(hipMemcpy(dst, src, n, hipMemcpyHostToDevice));
+        return QRAF_HIP_OK;
+    };
+    auto ensure = [&](uint8_t** p, size_t n) -> int {
+        if (!*p) QH_TRY(ealloc(e, (void**)p, n));
+        return QRAF_HIP_OK;
+    };
+
+    if (!strcmp(name, "model.embed_tokens.weight")) {
+        QH_TRY(need(c.vocab_size, D));
+        const size_t n = (size_t)c.vocab_size * dt_row_bytes(dtype, D);
+        QH_REQUIRE(!e->embed || e->dt_embed == dtype, QRAF_HIP_ERR_STATE, "embedding dtype changed");
+        QH_TRY(ensure(&e->embed, n));
+        e->dt_embed = dtype;
+        return upload(e->embed, data, n);
+    }
+    if (!strcmp(name, "lm_head.weight")) {
+        QH_TRY(need(c.vocab_size, D));
+        const size_t n = (size_t)c.vocab_size * dt_row_bytes(dtype, D);
+        QH_REQUIRE(!e->head || e->dt_head == dtype, QRAF_HIP_ERR_STATE, "lm_head dtype changed");
+        QH_TRY(ensure(&e->head, n));
+        e->dt_head = dtype;
+        return upload(e->head, data, n);
+    }
+    if (!strcmp(name, "model.norm.weight")) {
+        QH_TRY(need(D, 1));
+        std::vector<float> f;
+        QH_TRY(host_to_f32(dtype, data, bytes, D, f));
+        QH_TRY(ensure((uint8_t**)&e->onorm, (size_t)D * 4));
+        return upload(e->onorm, f.data(), (size_t)D * 4);
+    }
+    int l;
+    const char* rest;
+    if (!layer_name(name, &l, &rest) || l < 0 || l >= (int)c.num_layers)
+        return QRAF_HIP_OK;  // tensors the LLaMA path does not read are ignored, as by the reference
+    qraf_engine::Layer& L = e->layers[l];
+    const uint32_t qd = e->qd, kvd = e->kvd;
+    struct {
+        const char* n;
+        int bit;
+        uint32_t r, cc;
+        int group;  // 0 attention matrix, 1 mlp matrix, 2 bias, 3 norm
+        uint32_t off;  // row offset (matrices) / element offset (biases)
+    } tab[] = {
+        {"self_attn.q_proj.weight", T_Q, qd, D, 0, 0},         {"self_attn.k_proj.weight", T_K, kvd, D, 0, qd},
+        {"self_attn.v_proj.weight", T_V, kvd, D, 0, qd + kvd}, {"self_attn.o_proj.weight", T_O, D, qd, 0, 0},
+        {"mlp.gate_proj.weight", T_G, F, D, 1, 0},             {"mlp.up_proj.weight", T_U, F, D, 1, 1},
+        {"mlp.down_proj.weight", T_D, D, F, 1, 0},             {"self_attn.q_proj.bias", 0, qd, 1, 2, 0},
+        {"self_attn.k_proj.bias", 0, kvd, 1, 2, qd},           {"self_attn.v_proj.bias", 0, kvd, 1, 2, qd + kvd},
+        {"input_layernorm.weight", T_AN, D, 1, 3, 0},          {"post_attention_layernorm.weight", T_FN, D, 1, 3, 1},
+    };
+    for (auto& t : tab) {
+        if (strcmp(rest, t.n)) continue;
+        if (t.group == 2) {  // biases: F32 only, others silently dropped (transformer.cpp:45-50)
+            if (dtype != DT_F32) return QRAF_HIP_OK;
+            QH_REQUIRE(rows == t.r && bytes >= (uint64_t)t.r * 4, QRAF_HIP_ERR_INVALID, "set_tensor %s: bad shape", name);
+            if (!L.bqkv) {
+                QH_TRY(ensure((uint8_t**)&L.bqkv, (size_t)e->qkvd * 4));
+                QH_CHECK_HIP(hipMemset(L.bqkv, 0, (size_t)e->qkvd * 4));
+            }
+            L.has_bias = true;
+            return upload(L.bqkv + t.off, data, (size_t)t.r * 4);
+        }
+        if (t.group == 3) {
+            QH_TRY(need(t.r, 1));
+            std::vector<float> f;
+            QH_TRY(host_to_f32(dtype, data, bytes, D, f));
+            float** dst = t.off ? &L.fn : &L.an;
+            QH_TRY(ensure((uint8_t**)dst, (size_t)D * 4));
+            L.have |= t.bit;
+            return upload(*dst, f.data(), (size_t)D * 4);
+        }
+        QH_TRY(need(t.r, t.cc));
+        QH_REQUIRE(dtype != DT_F16, QRAF_HIP_ERR_DTYPE, "set_tensor %s: F16 projection weights are not supported", name);
+        // one dtype per group (AttentionWeights / MLPWeights carry a single dtype)
+        uint32_t& gdt = t.group == 0 ? L.dt_attn : L.dt_mlp;
+        QH_REQUIRE(gdt == 0xFFFFFFFFu || gdt == dtype, QRAF_HIP_ERR_DTYPE,
+                   "set_tensor %s: dtype %u differs from the other matrices of its group (%u)", name, dtype, gdt);
+        const size_t rb = dt_row_bytes(dtype, t.cc);
+        const size_t n = (size_t)t.r * rb;
+        if (t.bit == T_Q || t.bit == T_K || t.bit == T_V) {
+            if (L.wqkv && gdt != dtype) return set_error(QRAF_HIP_ERR_STATE, "dtype changed");
+            QH_TRY(ensure(&L.wqkv, (size_t)e->qkvd * rb));
+            gdt = dtype;
+            L.have |= t.bit;
+            return upload(L.wqkv + (size_t)t.off * rb, data, n);
+        }
+        if (t.bit == T_O) {
+            QH_TRY(ensure(&L.wo, n));
+            gdt = dtype;
+            L.have |= t.bit;
+            return upload(L.wo, data, n);
+        }
+        if (t.bit == T_D) {
+            QH_TRY(ensure(&L.wd, n));
+            gdt = dtype;
+            L.have |= t.bit;
+            return upload(L.wd, data, n);
+        }
+        // gate / up: interleave rows (row 2i = gate_i, 2i+1 = up_i)
+        QH_TRY(ensure(&L.wgu, 2 * n));
+        gdt = dtype;
+        L.have |= t.bit;
+        QH_CHECK_HIP(hipMemcpy2D(L.wgu + (size_t)t.off * rb, 2 * rb, data, rb, rb, t.r, hipMemcpyHostToDevice));
+        return QRAF_HIP_OK;
+    }
+    return QRAF_HIP_OK;  // unknown per-layer tensor: not read by the LLaMA path
+}
+
+// Synthetic weights generated on the device with the repository's generator
+// (same names, seed and per-tensor streams as the test oracle's model).
+int qraf_engine_generate_weights(qraf_engine* e, uint32_t wdtype, uint32_t embed_dtype, uint32_t head_dtype,
+                                 int32_t tied, int32_t qkv_bias, uint64_t seed) {
+    clear_error();
+    QH_REQUIRE(e && !e->finalized, QRAF_HIP_ERR_STATE, "generate_weights: engine finalized or null");
+    auto ok_dt = [](uint32_t d) { return d == DT_F32 || d == DT_Q8_0 || d == DT_Q4_0; };
+    QH_REQUIRE(ok_dt(wdtype) && ok_dt(embed_dtype) && (tied || ok_dt(head_dtype)), QRAF_HIP_ERR_DTYPE,
+               "generate_weights: unsupported dtype");
+    const qraf_model_config& c = e->c;
+    const uint32_t D = c.hidden_size, F = c.intermediate_size;
+    hipStream_t s = e->stream;
+    auto gen = [&](const std::string& nm, uint8_t* dst, uint32_t dt, size_t count) -> int {
+        return launch_gen_weights(dst, dt, count, seed, qraf_hip_name_hash(nm.c_str()), 0.02f, s);
+    };
+    auto fill1 = [&](float* p, size_t n) -> int {
+        hipLaunchKernelGGL(fill_kernel, dim3(64), dim3(256), 0, s, p, 1.0f, n);
+        QH_CHECK_HIP(hipGetLastError());
+        return QRAF_HIP_OK;
+    };
+    e->dt_embed = embed_dtype;
+    QH_TRY(ealloc(e, (void**)&e->embed, (size_t)c.vocab_size * dt_row_bytes(embed_dtype, D)));
+    QH_TRY(gen("model.embed_tokens.weight", e->embed, embed_dtype, (size_t)c.vocab_size * D));
+    const size_t rbD = dt_row_bytes(wdtype, D), rbF = dt_row_bytes(wdtype, F), rbQ = dt_row_bytes(wdtype, e->qd);
+    uint8_t* tmp = nullptr;
+    QH_TRY(ealloc(e, (void**)&tmp, std::max((size_t)F * rbD, (size_t)e->qd * 4)));
+    for (uint32_t l = 0; l < c.num_layers; l++) {
+        qraf_engine::Layer& L = e->layers[l];
+        const std::string pre = "model.layers." + std::to_string(l) + ".";
+        L.dt_attn = L.dt_mlp = wdtype;
+        QH_TRY(ealloc(e, (void**)&L.wqkv, (size_t)e->qkvd * rbD));
+        QH_TRY(gen(pre + "self_attn.q_proj.weight", L.wqkv, wdtype, (size_t)e->qd * D));
+        QH_TRY(gen(pre + "self_attn.k_proj.weight", L.wqkv + (size_t)e->qd * rbD, wdtype, (size_t)e->kvd * D));
+        QH_TRY(gen(pre + "self_attn.v_proj.weight", L.wqkv + (size_t)(e->qd + e->kvd) * rbD, wdtype,
+                   (size_t)e->kvd * D));
+        QH_TRY(ealloc(e, (void**)&L.wo, (size_t)D * rbQ));
+        QH_TRY(gen(pre + "self_attn.o_proj.weight", L.wo, wdtype, (size_t)D * e->qd));
+        if (qkv_bias) {
+            QH_TRY(ealloc(e, (void**)&L.bqkv, (size_t)e->qkvd * 4));
+            QH_TRY(gen(pre + "self_attn.q_proj.bias", (uint8_t*)L.bqkv, DT_F32, e->qd));
+            QH_TRY(gen(pre + "self_attn.k_proj.bias", (uint8_t*)(L.bqkv + e->qd), DT_F32, e->kvd));
+            QH_TRY(gen(pre + "self_attn.v_proj.bias", (uint8_t*)(L.bqkv + e->qd + e->kvd), DT_F32, e->kvd));
+            L.has_bias = true;
+        }
+        QH_TRY(ealloc(e, (void**)&L.wgu, (size_t)2 * F * rbD));
+        QH_TRY(gen(pre + "mlp.gate_proj.weight", tmp, wdtype, (size_t)F * D));
+        QH_CHECK_HIP(hipMemcpy2DAsync(L.wgu, 2 * rbD, tmp, rbD, rbD, F, hipMemcpyDeviceToDevice, s));
+        QH_TRY(gen(pre + "mlp.up_proj.weight", tmp, wdtype, (size_t)F * D));
+        QH_CHECK_HIP(hipMemcpy2DAsync(L.wgu + rbD, 2 * rbD, tmp, rbD, rbD, F, hipMemcpyDeviceToDevice, s));
+        QH_TRY(ealloc(e, (void**)&L.wd, (size_t)D * rbF));
+        QH_TRY(gen(pre + "mlp.down_proj.weight", L.wd, wdtype, (size_t)D * F));
+        QH_TRY(ealloc(e, (void**)&L.an, (size_t)D * 4));
+        QH_TRY(ealloc(e, (void**)&L.fn, (size_t)D * 4));
+        QH_TRY(fill1(L.an, D));
+        QH_TRY(fill1(L.fn, D));
+        L.have = T_ALL;
+    }
+    QH_TRY(ealloc(e, (void**)&e->onorm, (size_t)D * 4));
+    QH_TRY(fill1(e->onorm, D));
+    if (!tied) {
+        e->dt_head = head_dtype;
+        QH_TRY(ealloc(e, (void**)&e->head, (size_t)c.vocab_size * dt_row_bytes(head_dtype, D)));
+        QH_TRY(gen("lm_head.weight", e->head, head_dtype, (size_t)c.vocab_size * D));
+    }
+    QH_CHECK_HIP(hipStreamSynchronize(s));
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_finalize(qraf_engine* e) {
+    clear_error();
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "finalize: null engine");
+    QH_REQUIRE(e->embed, QRAF_HIP_ERR_STATE, "finalize: model.embed_tokens.weight missing");
+    QH_REQUIRE(e->onorm, QRAF_HIP_ERR_STATE, "finalize: model.norm.weight missing");
+    for (size_t l = 0; l < e->layers.size(); l++)
+        QH_REQUIRE(e->layers[l].have == T_ALL, QRAF_HIP_ERR_STATE, "finalize: layer %zu incomplete (mask %x)", l,
+                   e->layers[l].have);
+    e->finalized = true;
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_seq_create(qraf_engine* e, int32_t* id) {
+    clear_error();
+    QH_REQUIRE(e && id, QRAF_HIP_ERR_INVALID, "seq_create: null argument");
+    for (size_t i = 0; i < e->seqs.size(); i++)
+        if (!e->seqs[i].live) {
+            e->seqs[i].live = true;
+            e->seqs[i].len = 0;
+            *id = (int32_t)i;
+            return QRAF_HIP_OK;
+        }
+    e->seqs.push_back({});
+    e->seqs.back().live = true;
+    *id = (int32_t)e->seqs.size() - 1;
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_seq_release(qraf_engine* e, int32_t id) {
+    clear_error();
+    QH_REQUIRE(e && id >= 0 && id < (int32_t)e->seqs.size() && e->seqs[id].live, QRAF_HIP_ERR_INVALID,
+               "seq_release: unknown sequence %d", id);
+    qraf_engine::Seq& sq = e->seqs[id];
+    for (int32_t p : sq.pages) e->free_pages.push_back(p);
+    sq.pages.clear();
+    sq.len = 0;
+    sq.live = false;
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_seq_length(qraf_engine* e, int32_t id, int32_t* len) {
+    QH_REQUIRE(e && len && id >= 0 && id < (int32_t)e->seqs.size() && e->seqs[id].live, QRAF_HIP_ERR_INVALID,
+               "seq_length: unknown sequence %d", id);
+    *len = e->seqs[id].len;
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_free_pages(qraf_engine* e, int32_t* n) {
+    QH_REQUIRE(e && n, QRAF_HIP_ERR_INVALID, "free_pages: null argument");
+    *n = (int32_t)e->free_pages.size();
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const uint32_t* tokens,
+                     const int32_t* positions, const uint8_t* want_logits, float* logits, uint32_t* next_tokens) {
+    clear_error();
+    QH_REQUIRE(e && seq_ids && tokens && positions, QRAF_HIP_ERR_INVALID, "step: null argument");
+    QH_REQUIRE(e->finalized, QRAF_HIP_ERR_STATE, "step: engine not finalized");
+    QH_REQUIRE(n > 0 && n <= (int32_t)e->o.max_batch, QRAF_HIP_ERR_INVALID, "step: %d rows (max_batch %u)", n,
+               e->o.max_batch);
+    const qraf_model_config& c = e->c;
+    const int ps = (int)e->o.page_size, MP = e->max_pages;
+    // validate, and count the pages each sequence needs (before allocating any)
+    std::vector<std::pair<int32_t, int>> target;  // (sequence, pages after this step)
+    int need_pages = 0;
+    for (int i = 0; i < n; i++) {
+        const int32_t id = seq_ids[i], p = positions[i];
+        QH_REQUIRE(id >= 0 && id < (int32_t)e->seqs.size() && e->seqs[id].live, QRAF_HIP_ERR_INVALID,
+                   "step: unknown sequence %d", id);
+        QH_REQUIRE(tokens[i] < c.vocab_size, QRAF_HIP_ERR_INVALID, "Token %u >= vocab %u", tokens[i], c.vocab_size);
+        QH_REQUIRE(p >= 0 && p < e->capacity, QRAF_HIP_ERR_INVALID, "step: position %d outside the cache (%d)", p,
+                   e->capacity);
+        // rows of one sequence add positions without gaps (earlier rows count)
+        int len = e->seqs[id].len;
+        for (int j = 0; j < i; j++)
+            if (seq_ids[j] == id) len = std::max(len, positions[j] + 1);
+        QH_REQUIRE(p <= len, QRAF_HIP_ERR_INVALID, "step: sequence %d position %d skips past its length %d", id, p,
+                   len);
+        auto it = std::find_if(target.begin(), target.end(), [&](const std::pair<int32_t, int>& t) { return t.first == id; });
+        if (it == target.end()) {
+            target.push_back({id, (int)e->seqs[id].pages.size()});
+            it = target.end() - 1;
+        }
+        it->second = std::max(it->second, p / ps + 1);
+    }
+    for (auto& t : target) need_pages += t.second - (int)e->seqs[t.first].pages.size();
+    QH_REQUIRE(need_pages <= (int)e->free_pages.size(), QRAF_HIP_ERR_NOMEM,
+               "step: KV page pool exhausted (%d pages needed, %zu free)", need_pages, e->free_pages.size());
+    int n_logit_rows = 0;
+    int32_t* tok = e->h_in;
+    int32_t* pos = tok + n;
+    int32_t* ctx = pos + n;
+    int32_t* lrows = ctx + n;
+    int32_t* ptab = lrows + n;
+    for (int i = 0; i < n; i++) {
+        qraf_engine::Seq& sq = e->seqs[seq_ids[i]];
+        while ((int)sq.pages.size() < positions[i] / ps + 1) {
+            sq.pages.push_back(e->free_pages.back());
+            e->free_pages.pop_back();
+        }
+        sq.len = std::max(sq.len, positions[i] + 1);
+        tok[i] = (int32_t)tokens[i];
+        pos[i] = positions[i];
+        ctx[i] = positions[i] + 1;
+        if (!want_logits || want_logits[i]) lrows[n_logit_rows++] = i;
+        for (int j = 0; j < MP; j++) ptab[(size_t)i * MP + j] = j < (int)sq.pages.size() ? sq.pages[j] : 0;
+    }
+    hipStream_t s = e->stream;
+    const size_t words = (size_t)n * (4 + MP);
+    QH_CHECK_HIP(hipMemcpyAsync(e->d_in, e->h_in, words * 4, hipMemcpyHostToDevice, s));
+    const int32_t* d_tok = e->d_in;
+    const int32_t* d_pos = d_tok + n;
+    const int32_t* d_ctx = d_pos + n;
+    const int32_t* d_lrows = d_ctx + n;
+    const int32_t* d_ptab = d_lrows + n;
+
+    const int D = (int)c.hidden_size, F = (int)c.intermediate_size, V = (int)c.vocab_size;
+    const int H = (int)c.num_heads, Hkv = (int)c.num_kv_heads, hd = e->hd;
+    const float scale = 1.0f / sqrtf((float)hd);  // attention.cpp:122
+
+    // y[n][N] = x[n][K] * W^T (+ add): matvec at batch 1, else the matrix-core GEMM
+    auto proj = [&](const uint8_t* W, uint32_t dt, int N, int K, const float* x, int rows, float* y,
+                    const float* add) -> int {
+        if (dt == DT_F32) {
+            for (int r = 0; r < rows; r++)
+                QH_TRY(launch_matvec_f32((const float*)W, x + (size_t)r * K, y + (size_t)r * N, N, K, s,
+                                         add ? add + (size_t)r * N : nullptr));
+            return QRAF_HIP_OK;
+        }
+        if (rows == 1) return launch_matvec_q(W, dt, 32, N, K, x, y, s, add);
+        QH_TRY(launch_split_bf16(x, e->xh, e->xl, rows, K, 0, nullptr, s));
+        return launch_qgemm(W, dt, 32, N, K, e->xh, e->xl, rows, y, add, s);
+    };
+
+    hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, 32, D, d_tok, e->h);
+    QH_CHECK_HIP(hipGetLastError());
+    for (uint32_t l = 0; l < c.num_layers; l++) {
+        qraf_engine::Layer& L = e->layers[l];
+        uint8_t* kc = e->kpool + (size_t)l * e->layer_kv_bytes;
+        uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;
+        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.an, D, c.rms_norm_eps, e->xn,
+                           nullptr);
+        QH_TRY(proj(L.wqkv, L.dt_attn, e->qkvd, D, e->xn, n, e->qkv, nullptr));
+        QH_TRY(launch_rope_append(e->qkv, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
+                                  e->o.kv_dtype, d_ptab, MP, ps, s));
+        QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale, e->capacity,
+                                e->att, e->attn_ws, e->attn_ws_bytes, s));
+        QH_TRY(proj(L.wo, L.dt_attn, D, e->qd, e->att, n, e->h, e->h));  // + residual (transformer.cpp:593)
+        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.fn, D, c.rms_norm_eps, e->xn,
+                           nullptr);
+        QH_TRY(proj(L.wgu, L.dt_mlp, 2 * F, D, e->xn, n, e->gu, nullptr));
+        if (n == 1 || L.dt_mlp == DT_F32) {
+            hipLaunchKernelGGL(silu_gate_kernel, dim3(std::min((n * F + 255) / 256, 4096)), dim3(256), 0, s, e->gu, F,
+                               n, e->act);
+            QH_TRY(proj(L.wd, L.dt_mlp, D, F, e->act, n, e->h, e->h));  // + residual (transformer.cpp:601)
+        } else {
+            QH_TRY(launch_split_bf16(e->gu, e->xh, e->xl, n, F, 1, nullptr, s));  // SiLU-gate fused into the split
+            QH_TRY(launch_qgemm(L.wd, L.dt_mlp, 32, D, F, e->xh, e->xl, n, e->h, e->h, s));
+        }
+    }
+    QH_CHECK_HIP(hipGetLastError());
+    if (n_logit_rows > 0 && (logits || next_tokens)) {
+        // final norm of the rows that want logits (transformer.cpp:605), then the head
+        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n_logit_rows), dim3(256), 0, s, e->h, e->onorm, D,
+                           c.rms_norm_eps, e->xhead, d_lrows);
+        const uint8_t* W = e->head ? e->head : e->embed;  // tied head reads the embedding (transformer.cpp:392-400)
+        const uint32_t dt = e->head ? e->dt_head : e->dt_embed;
+        QH_TRY(proj(W, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
+        hipLaunchKernelGGL(argmax_rows_kernel, dim3(n_logit_rows), dim3(256), 0, s, e->logits, V, e->amax);
+        QH_CHECK_HIP(hipGetLastError());
+        if (logits)
+            QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_rows * V * 4, hipMemcpyDeviceToHost, s));
+        if (next_tokens)
+            QH_CHECK_HIP(hipMemcpyAsync(next_tokens, e->amax, (size_t)n_logit_rows * 4, hipMemcpyDeviceToHost, s));
+    }
+    QH_CHECK_HIP(hipStreamSynchronize(s));
+    return QRAF_HIP_OK;
+}
+
+// Transformer::forward(token, pos) on the engine's default sequence.
+int qraf_engine_forward(qraf_engine* e, uint32_t token, int32_t pos, float* logits) {
+    clear_error();
+    QH_REQUIRE(e && logits, QRAF_HIP_ERR_INVALID, "forward: null argument");
+    if (e->default_seq < 0) QH_TRY(qraf_engine_seq_create(e, &e->default_seq));
+    return qraf_engine_step(e, 1, &e->default_seq, &token, &pos, nullptr, logits, nullptr);
+}
+
+// Transformer::reset(): the default sequence forgets its cache.
+int qraf_engine_reset(qraf_engine* e) {
+    clear_error();
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "reset: null engine");
+    if (e->default_seq >= 0) {
+        QH_TRY(qraf_engine_seq_release(e, e->default_seq));
+        e->default_seq = -1;
+    }
+    return QRAF_HIP_OK;
+}
+
+}  // extern "C"

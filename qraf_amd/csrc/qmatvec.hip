@@ -192,7 +192,7 @@ __device__ __forceinline__ void stage_x(float* sx, const float* __restrict__ x, 
 template <int FMT, int R>
 __global__ __launch_bounds__(WG) void qmv_stream_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
                                                      int K, int nb, const float* __restrict__ x,
-                                                     float* __restrict__ y) {
+                                                     float* __restrict__ y, const float* __restrict__ add) {
     extern __shared__ __align__(16) float sx[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * R;
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(WG) void qmv_stream_kernel(const uint8_t* __restric
     }
     int rr;
     float v = wave_reduce_rows<R>(acc, lane, &rr);
-    if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = v;
+    if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = add ? v + add[row0 + rr] : v;
 }
 
 // ----------------------------------------------------------------------------
@@ -241,7 +241,7 @@ __global__ __launch_bounds__(WG) void qmv_stream_kernel(const uint8_t* __restric
 template <int FMT, int R, int J>
 __global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
                                                         int K, int nb, const float* __restrict__ x,
-                                                        float* __restrict__ y) {
+                                                        float* __restrict__ y, const float* __restrict__ add) {
     extern __shared__ __align__(16) float sx[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * R;
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restri
     }
     int rr;
     float v = wave_reduce_rows<R>(acc, lane, &rr);
-    if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = v;
+    if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = add ? v + add[row0 + rr] : v;
 }
 
 // ----------------------------------------------------------------------------
@@ -283,7 +283,7 @@ __global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restri
 template <int FMT, int R>
 __global__ __launch_bounds__(WG) void qmv_persist_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
                                                         int K, int nb, const float* __restrict__ x,
-                                                        float* __restrict__ y) {
+                                                        float* __restrict__ y, const float* __restrict__ add) {
     extern __shared__ __align__(16) float sx[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int U = FMT == 8 ? nb : nb >> 1;
@@ -320,7 +320,7 @@ __global__ __launch_bounds__(WG) void qmv_persist_kernel(const uint8_t* __restri
         const int g = gw + (it / J) * nw;
         int rr;
         float v = wave_reduce_rows<R>(acc, lane, &rr);
-        if ((lane & (64 / R - 1)) == 0 && g * R + rr < N) y[g * R + rr] = v;
+        if ((lane & (64 / R - 1)) == 0 && g * R + rr < N) y[g * R + rr] = add ? v + add[g * R + rr] : v;
 #pragma unroll
         for (int r = 0; r < R; r++) acc[r] = 0.f;
     };
@@ -353,7 +353,8 @@ __global__ __launch_bounds__(WG) void qmv_persist_kernel(const uint8_t* __restri
 // ----------------------------------------------------------------------------
 __global__ __launch_bounds__(WG) void qmv_generic_kernel(const uint8_t* __restrict__ W, uint32_t dtype,
                                                         int bs, size_t row_bytes, int N, int K,
-                                                        const float* __restrict__ x, float* __restrict__ y) {
+                                                        const float* __restrict__ x, float* __restrict__ y,
+                                                        const float* __restrict__ add) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= N) return;
@@ -381,13 +382,13 @@ __global__ __launch_bounds__(WG) void qmv_generic_kernel(const uint8_t* __restri
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m);
-    if (lane == 0) y[row] = part;
+    if (lane == 0) y[row] = add ? part + add[row] : part;
 }
 
 // f32 weights (reference dispatch_matvec_opt, backend.cpp:62-105; used for F32
 // projection weights and the tied f32 lm_head).  One wave per row, float4 loads.
 __global__ __launch_bounds__(WG) void mv_f32_kernel(const float* __restrict__ W, const float* __restrict__ x,
-                                                   float* __restrict__ y, int N, int K) {
+                                                   float* __restrict__ y, int N, int K, const float* __restrict__ add) {
     const int lane = threadIdx.x & 63;
     const int row = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (row >= N) return;
@@ -407,7 +408,7 @@ __global__ __launch_bounds__(WG) void mv_f32_kernel(const float* __restrict__ W,
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) part += __shfl_xor(part, m);
-    if (lane == 0) y[row] = part;
+    if (lane == 0) y[row] = add ? part + add[row] : part;
 }
 
 // ----------------------------------------------------------------------------
@@ -439,7 +440,7 @@ static int cu_count() {
     return n;
 }
 
-typedef void (*qmv_fn)(const uint8_t*, uint32_t, int, int, int, const float*, float*);
+typedef void (*qmv_fn)(const uint8_t*, uint32_t, int, int, int, const float*, float*, const float*);
 
 template <int FMT, int R, int J>
 static qmv_fn oneshot_if_valid() {
@@ -480,7 +481,7 @@ static qmv_fn pick_kernel(int R, int J) {
 }
 
 int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x, float* y,
-                    hipStream_t s) {
+                    hipStream_t s, const float* add) {
     QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "unsupported weight dtype %u", dtype);
     QH_REQUIRE(bs > 0 && bs <= 4096, QRAF_HIP_ERR_INVALID, "bad block size %d", bs);
     QH_REQUIRE(K > 0 && N > 0, QRAF_HIP_ERR_INVALID, "empty matvec (%u x %u)", N, K);
@@ -510,7 +511,7 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
             else k = R == 1 ? qmv_persist_kernel<4, 1> : R == 2 ? qmv_persist_kernel<4, 2> : qmv_persist_kernel<4, 4>;
             if (lds > 65536)
                 QH_CHECK_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-            hipLaunchKernelGGL(k, dim3(grid), dim3(WG), lds, s, W, (uint32_t)rb, (int)N, (int)K, nb, x, y);
+            hipLaunchKernelGGL(k, dim3(grid), dim3(WG), lds, s, W, (uint32_t)rb, (int)N, (int)K, nb, x, y, add);
             QH_CHECK_HIP(hipGetLastError());
             return QRAF_HIP_OK;
         }
@@ -528,18 +529,20 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
         if (lds > 65536)
             QH_CHECK_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL(k, dim3((N + 4 * R - 1) / (4 * R)), dim3(WG), lds, s, W, (uint32_t)rb, (int)N, (int)K, nb,
-                           x, y);
+                           x, y, add);
         QH_CHECK_HIP(hipGetLastError());
         return QRAF_HIP_OK;
     }
-    hipLaunchKernelGGL(qmv_generic_kernel, dim3((N + 3) / 4), dim3(WG), 0, s, W, dtype, bs, rb, (int)N, (int)K, x, y);
+    hipLaunchKernelGGL(qmv_generic_kernel, dim3((N + 3) / 4), dim3(WG), 0, s, W, dtype, bs, rb, (int)N, (int)K, x, y,
+                       add);
     QH_CHECK_HIP(hipGetLastError());
     return QRAF_HIP_OK;
 }
 
-int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s) {
+int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s,
+                      const float* add) {
     QH_REQUIRE(W && x && y && N > 0 && K > 0, QRAF_HIP_ERR_INVALID, "bad f32 matvec arguments");
-    hipLaunchKernelGGL(mv_f32_kernel, dim3((N + 3) / 4), dim3(WG), 0, s, W, x, y, (int)N, (int)K);
+    hipLaunchKernelGGL(mv_f32_kernel, dim3((N + 3) / 4), dim3(WG), 0, s, W, x, y, (int)N, (int)K, add);
     QH_CHECK_HIP(hipGetLastError());
     return QRAF_HIP_OK;
 }

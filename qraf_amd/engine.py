@@ -1,0 +1,299 @@
+"""Host-side mirror of the reference's engine API over the HIP C ABI.
+
+    Transformer      Transformer::init / forward / reset (transformer.h:55-90)
+    InferenceEngine  InferenceEngine::generate_tokens (inference.cpp:68-159), greedy
+    BatchScheduler   the continuous-batching contract of batch_scheduler.h:54-283:
+                     requests queue, are admitted into max_batch slots as others
+                     finish, and retire on EOS or max_tokens; every active
+                     request advances one token per step, all in one batched
+                     device step
+
+Sampling is greedy (temperature 0, Sampler::argmax, sampler.cpp:25-35) with
+the reference's repetition penalty (sampler.cpp:37-49).  With penalty 1 the
+argmax runs on the device and only token ids cross PCIe; otherwise the logits
+are copied back and penalised on the host before the argmax, as the
+reference does.
+"""
+from __future__ import annotations
+
+import ctypes as C
+from collections import deque
+from dataclasses import dataclass, field
+
+import numpy as np
+
+from ._lib import F16, F32, Q4_0, Q8_0, EngineOptions, ModelConfig, call, fp, i32p, lib, u32p
+
+__all__ = ["Engine", "Transformer", "InferenceEngine", "BatchScheduler", "Request", "model_config"]
+
+
+def model_config(vocab, hidden, layers, heads, kv_heads, inter, max_seq=2048, rope_theta=1e4, eps=1e-5):
+    return ModelConfig(vocab, hidden, layers, heads, kv_heads, inter, max_seq, rope_theta, eps)
+
+
+class Engine:
+    """qraf_engine: device-resident weights, paged KV cache, batched steps."""
+
+    def __init__(self, config: ModelConfig, kv_dtype=F32, page_size=16, max_batch=1, num_pages=0):
+        self.config = config
+        self.max_batch = max_batch
+        opt = EngineOptions(kv_dtype, page_size, max_batch, num_pages)
+        h = C.c_void_p()
+        call("qraf_engine_create", C.byref(config), C.byref(opt), C.byref(h))
+        self.h = h.value
+        self.vocab = config.vocab_size
+
+    def close(self):
+        if getattr(self, "h", None):
+            lib.qraf_engine_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def set_tensor(self, name: str, dtype: int, shape, data: np.ndarray, block_size: int = 32):
+        data = np.ascontiguousarray(data)
+        sh = np.ascontiguousarray(shape, dtype=np.uint32)
+        call("qraf_engine_set_tensor", self.h, name.encode(), dtype, block_size, sh.ctypes.data_as(u32p), sh.size,
+             data.ctypes.data, data.nbytes)
+
+    def generate_weights(self, weight_dtype, embed_dtype, head_dtype, tied, qkv_bias, seed):
+        call("qraf_engine_generate_weights", self.h, weight_dtype, embed_dtype, head_dtype, int(tied), int(qkv_bias),
+             seed)
+
+    def finalize(self):
+        call("qraf_engine_finalize", self.h)
+
+    def seq_create(self) -> int:
+        i = C.c_int32()
+        call("qraf_engine_seq_create", self.h, C.byref(i))
+        return i.value
+
+    def seq_release(self, seq_id: int):
+        call("qraf_engine_seq_release", self.h, seq_id)
+
+    def seq_length(self, seq_id: int) -> int:
+        i = C.c_int32()
+        call("qraf_engine_seq_length", self.h, seq_id, C.byref(i))
+        return i.value
+
+    def free_pages(self) -> int:
+        i = C.c_int32()
+        call("qraf_engine_free_pages", self.h, C.byref(i))
+        return i.value
+
+    def step(self, seq_ids, tokens, positions, want_logits=None, logits=False, argmax=True):
+        """One batched step.  Returns (logits [k][vocab] or None, next tokens [k] or None)
+        for the k rows that want logits (all rows by default)."""
+        sid = np.ascontiguousarray(seq_ids, dtype=np.int32)
+        tok = np.ascontiguousarray(tokens, dtype=np.uint32)
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        n = sid.size
+        if want_logits is None:
+            k, wl = n, None
+        else:
+            wl = np.ascontiguousarray(want_logits, dtype=np.uint8)
+            k = int(np.count_nonzero(wl))
+        lg = np.empty((k, self.vocab), np.float32) if logits else None
+        nx = np.empty(k, np.uint32) if argmax else None
+        call("qraf_engine_step", self.h, n, sid.ctypes.data_as(i32p), tok.ctypes.data_as(u32p),
+             pos.ctypes.data_as(i32p), wl.ctypes.data_as(C.POINTER(C.c_uint8)) if wl is not None else None,
+             lg.ctypes.data_as(fp) if lg is not None else None, nx.ctypes.data_as(u32p) if nx is not None else None)
+        return lg, nx
+
+
+class Transformer:
+    """Transformer::init / forward / reset (transformer.h:55-90) on the GPU."""
+
+    def __init__(self, engine: Engine):
+        self.engine = engine
+        self._logits = np.empty(engine.vocab, np.float32)
+
+    @classmethod
+    def from_tensors(cls, config: ModelConfig, tensors, kv_dtype=F32, max_batch=1, num_pages=0, page_size=16):
+        """tensors: iterable of (name, dtype, shape, bytes ndarray) as a QRAF
+        model exposes them (TensorView, loader.h:12-27)."""
+        e = Engine(config, kv_dtype=kv_dtype, max_batch=max_batch, num_pages=num_pages, page_size=page_size)
+        for name, dt, shape, data in tensors:
+            e.set_tensor(name, dt, shape, data)
+        e.finalize()
+        return cls(e)
+
+    @classmethod
+    def synthetic(cls, config: ModelConfig, weight_dtype, seed, embed_dtype=None, head_dtype=None, tied=False,
+                  qkv_bias=False, kv_dtype=F32, max_batch=1, num_pages=0, page_size=16):
+        e = Engine(config, kv_dtype=kv_dtype, max_batch=max_batch, num_pages=num_pages, page_size=page_size)
+        e.generate_weights(weight_dtype, weight_dtype if embed_dtype is None else embed_dtype,
+                           weight_dtype if head_dtype is None else head_dtype, tied, qkv_bias, seed)
+        e.finalize()
+        return cls(e)
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        out = np.empty(self.engine.vocab, np.float32)
+        call("qraf_engine_forward", self.engine.h, int(token), int(pos), out.ctypes.data_as(fp))
+        return out
+
+    def reset(self):
+        call("qraf_engine_reset", self.engine.h)
+
+
+def apply_repetition_penalty(logits: np.ndarray, recent, penalty: float):
+    """Sampler::apply_repetition_penalty (sampler.cpp:37-49), once per occurrence."""
+    if penalty == 1.0:
+        return
+    p = np.float32(penalty)
+    n = logits.shape[0]
+    for t in recent:
+        if t >= n:
+            continue
+        v = logits[t]
+        logits[t] = v / p if v > 0 else v * p
+
+
+def argmax(logits: np.ndarray) -> int:
+    """Sampler::argmax: numpy's argmax also returns the lowest index of the max."""
+    return int(np.argmax(logits))
+
+
+class InferenceEngine:
+    """InferenceEngine::generate_tokens (inference.cpp:68-159), greedy."""
+
+    def __init__(self, transformer: Transformer, eos_token: int | None = 2):
+        self.transformer = transformer
+        self.eos = eos_token  # tokenizer.h:62 default when the file has no tokenizer
+
+    def generate_tokens(self, prompt_tokens, max_tokens=256, repetition_penalty=1.1, stop_tokens=()):
+        if len(prompt_tokens) == 0:
+            raise ValueError("empty prompt")
+        tf = self.transformer
+        stops = set(stop_tokens) | ({self.eos} if self.eos is not None else set())
+        tf.reset()
+        logits = None
+        for i, t in enumerate(prompt_tokens):
+            logits = tf.forward(t, i)
+        pos = len(prompt_tokens)
+        recent = list(prompt_tokens)
+        out = []
+        for _ in range(max_tokens):
+            apply_repetition_penalty(logits, recent, repetition_penalty)
+            nxt = argmax(logits)
+            if nxt in stops:
+                break
+            out.append(nxt)
+            recent.append(nxt)
+            logits = tf.forward(nxt, pos)
+            pos += 1
+        return out
+
+
+@dataclass
+class Request:
+    """BatchRequest (batch_scheduler.h:23-37)."""
+    id: int
+    prompt: list
+    max_tokens: int
+    penalty: float = 1.0
+    eos: int | None = None
+    generated: list = field(default_factory=list)
+    state: str = "QUEUED"  # QUEUED -> PREFILLING -> DECODING -> DONE
+    seq: int = -1
+    next_prompt: int = 0
+
+
+class BatchScheduler:
+    """Continuous batching over one Engine (batch_scheduler.h:54-283 contract).
+
+    Each step admits queued requests into free slots (max_batch), then feeds
+    every active request one token: the next prompt token while PREFILLING,
+    the last generated token while DECODING.  A request whose last prompt
+    token was just fed, or that is decoding, gets its next token from this
+    step's logits; it retires on EOS or after max_tokens generated tokens and
+    frees its KV pages for the next admission.  Every request's token stream
+    equals an independent greedy decode of its prompt (the reference's
+    scheduler runs requests one at a time over one shared cache, F3 in the
+    survey, so it offers no batched numerics to mirror)."""
+
+    def __init__(self, engine: Engine, max_batch: int | None = None):
+        self.engine = engine
+        self.max_batch = max_batch or engine.max_batch
+        self.pending = deque()
+        self.active = []
+        self.done = []
+        self._next_id = 1
+        self.steps = 0
+        self.rows = 0
+
+    def submit(self, prompt_tokens, max_tokens, repetition_penalty=1.0, eos=None) -> int:
+        if len(prompt_tokens) == 0:
+            raise ValueError("empty prompt")
+        r = Request(self._next_id, list(prompt_tokens), max_tokens, repetition_penalty, eos)
+        self._next_id += 1
+        self.pending.append(r)
+        return r.id
+
+    def _admit(self):
+        while self.pending and len(self.active) < self.max_batch:
+            r = self.pending.popleft()
+            r.seq = self.engine.seq_create()
+            r.state = "PREFILLING"
+            self.active.append(r)
+
+    def _finish(self, r):
+        r.state = "DONE"
+        self.engine.seq_release(r.seq)
+        self.done.append(r)
+
+    def step(self) -> bool:
+        """One scheduler iteration (process_step, batch_scheduler.h:239-273)."""
+        self._admit()
+        if not self.active:
+            return False
+        rows = []  # (request, token, position, wants logits)
+        for r in self.active:
+            if r.state == "PREFILLING":
+                i = r.next_prompt
+                rows.append((r, r.prompt[i], i, i == len(r.prompt) - 1))
+            else:
+                pos = len(r.prompt) + len(r.generated) - 1
+                rows.append((r, r.generated[-1], pos, True))
+        want = np.array([w for (_, _, _, w) in rows], np.uint8)
+        need_host = any(r.penalty != 1.0 for (r, _, _, w) in rows if w)
+        lg, nx = self.engine.step([r.seq for (r, _, _, _) in rows], [t for (_, t, _, _) in rows],
+                                  [p for (_, _, p, _) in rows], want_logits=want, logits=need_host,
+                                  argmax=not need_host)
+        self.steps += 1
+        self.rows += len(rows)
+        k = 0
+        retire = []
+        for (r, tok, pos, w) in rows:
+            if r.state == "PREFILLING":
+                r.next_prompt += 1
+                if r.next_prompt == len(r.prompt):
+                    r.state = "DECODING"
+            if not w:
+                continue
+            if need_host:
+                l = lg[k]
+                apply_repetition_penalty(l, r.prompt + r.generated, r.penalty)
+                t = argmax(l)
+            else:
+                t = int(nx[k])
+            k += 1
+            if (r.eos is not None and t == r.eos) or len(r.generated) >= r.max_tokens:
+                retire.append(r)
+                continue
+            r.generated.append(t)
+            if len(r.generated) >= r.max_tokens:
+                retire.append(r)
+        for r in retire:
+            self.active.remove(r)
+            self._finish(r)
+        return True
+
+    def run(self):
+        while self.step():
+            pass
+        return self.done

@@ -1,0 +1,84 @@
+"""GPU parity of the batched Q8_0/Q4_0 GEMM (matrix cores) against the
+oracle's dispatch_matvec_q applied to every batch row.
+
+Tolerance per output (floating point): the GEMM's activation split leaves
+|r| <= 2^-17 |x| per element and both sides accumulate in fp32, so
+    |y_gpu - y_oracle| <= (2^-17 + 2 (K + 2) 2^-24) sum_k |w_k x_k|.
+"""
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+
+pytestmark = pytest.mark.gpu
+
+
+def run_gemm(hip, wq, dt, N, K, X, add=None):
+    from qraf_amd.backend import DeviceBuffer
+    call = hip._lib.call
+    M = X.shape[0]
+    dw, dx = DeviceBuffer.from_array(wq), DeviceBuffer.from_array(X)
+    dh, dl = DeviceBuffer(M * K * 2), DeviceBuffer(M * K * 2)
+    dy = DeviceBuffer(M * N * 4)
+    da = DeviceBuffer.from_array(add) if add is not None else None
+    call("qraf_hip_split_bf16_dev", dx.ptr, dh.ptr, dl.ptr, M, K, None)
+    call("qraf_hip_qgemm_dev", dw.ptr, dt, 32, N, K, dh.ptr, dl.ptr, M, dy.ptr, da.ptr if da else None, None)
+    call("qraf_hip_stream_synchronize", None)
+    return dy.download(np.float32, M * N).reshape(M, N), dh.download(np.uint16, M * K), dl.download(np.uint16, M * K)
+
+
+def check(Y, wq, dt, N, K, X, add=None):
+    W = po.dequantize(dt, wq, N * K).reshape(N, K).astype(np.float64)
+    absw = np.abs(W)
+    for m in range(X.shape[0]):
+        y_ref = po.matvec_q(wq, dt, N, K, X[m]).astype(np.float64)
+        if add is not None:
+            y_ref = y_ref + add[m]
+        tol = (2.0 ** -17 + 2 * (K + 2) * 2.0 ** -24) * (absw @ np.abs(X[m].astype(np.float64))) + 1e-30
+        if add is not None:
+            tol += 2.0 ** -23 * np.abs(y_ref)
+        err = np.abs(Y[m] - y_ref)
+        assert np.all(err <= tol), f"row {m}: max err {err.max():.3e}, worst ratio {(err / tol).max():.3f}"
+
+
+CASES = [
+    # (N, K, batch): Qwen2.5-3B projection shapes at the continuous-batch sizes, ragged cases
+    (2048, 2048, 128), (256, 2048, 64), (11008, 2048, 32), (2048, 11008, 8),
+    (2560, 2048, 17), (100, 64, 1), (65, 96, 3), (1000, 576, 100), (576, 1536, 16),
+]
+
+
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("case", CASES, ids=lambda c: "x".join(map(str, c)))
+def test_qgemm_vs_oracle(hip, dt, case):
+    N, K, M = case
+    print(f"qgemm dt={dt} N={N} K={K} M={M}", flush=True)
+    rng = np.random.default_rng(N + K + M + dt)
+    wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    Y, _, _ = run_gemm(hip, wq, dt, N, K, X)
+    check(Y, wq, dt, N, K, X)
+
+
+def test_qgemm_residual_epilogue(hip):
+    rng = np.random.default_rng(5)
+    N, K, M = 2048, 2048, 40
+    wq = po.quantize(po.Q8_0, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    add = rng.standard_normal((M, N)).astype(np.float32)
+    Y, _, _ = run_gemm(hip, wq, po.Q8_0, N, K, X, add)
+    check(Y, wq, po.Q8_0, N, K, X, add)
+
+
+def test_split_bf16_reconstruction(hip):
+    rng = np.random.default_rng(6)
+    X = (rng.standard_normal((7, 4096)) * np.exp(rng.uniform(-30, 30, (7, 4096)))).astype(np.float32)
+    X[0, :4] = [0.0, -0.0, 1.0, -3.0]
+    _, h, l = run_gemm(hip, np.zeros(36 * 4096 // 32, np.uint8), po.Q8_0, 1, 4096, X)
+    hi = (h.astype(np.uint32) << 16).view(np.float32).reshape(X.shape).astype(np.float64)
+    lo = (l.astype(np.uint32) << 16).view(np.float32).reshape(X.shape).astype(np.float64)
+    assert np.all(np.abs(hi + lo - X) <= 2.0 ** -17 * np.abs(X))
+    # hi is the round-to-nearest-even bf16 of x
+    ref_hi = X.view(np.uint32).astype(np.uint64)
+    ref_hi = ((ref_hi + 0x7FFF + ((ref_hi >> 16) & 1)) >> 16).astype(np.uint16)
+    assert np.array_equal(h.reshape(X.shape), ref_hi)
