@@ -1,19 +1,30 @@
 #!/usr/bin/env python3
 """Benchmark of the quantized decode hot path on one MI355X.
 
-Workload (the metric's isolated-matvec configuration): y = W x with fp32
-x ~ N(0,1) of length 4096 and weights N(0, 0.02) quantized to Q8_0 and Q4_0,
-shapes 4096x4096 and 11008x4096, batch 1.  One step = one matvec of each of
-the four (format, shape) cases.  Each case cycles through a pool of distinct
-weight copies larger than the 256 MB Infinity Cache, so every launch streams
-its weights from HBM.  The K timed steps run case by case, each case's K
-launches captured in one HIP graph and bracketed by HIP events on the stream
-they run on; `value` is the total algorithmic bytes of all K steps over the
-total timed time.
+Headline workload (the metric's isolated-matvec configuration): y = W x with
+fp32 x ~ N(0,1) of length 4096 and weights N(0, 0.02) quantized to Q8_0 and
+Q4_0, shapes 4096x4096 and 11008x4096, batch 1.  One step = one matvec of
+each of the four (format, shape) cases.  Each case cycles through a pool of
+distinct weight copies larger than the 256 MB Infinity Cache, so every launch
+streams its weights from HBM.  The K timed steps run case by case, each
+case's K launches captured in one HIP graph and bracketed by HIP events on
+the stream they run on; `value` is the total algorithmic bytes of all K steps
+over the total timed time.  Algorithmic bytes per launch = weight bytes +
+4*K (x) + 4*N (y).
 
-Algorithmic bytes per launch = weight bytes + 4*K (x) + 4*N (y).
+The same JSON line also reports the other configurations of the metric:
+  decode_b1    SmolLM2-135M architecture, Q8_0, batch 1: seeded 32-token
+               prompt, 128 greedy tokens (decode-only and prefill+decode tok/s)
+  decode_b128  Qwen2.5-3B architecture, Q4_0, tied head, QKV bias, fp16 KV
+               pages: 128 concurrent sequences, prompts U[16,512], outputs
+               U[64,256], new requests admitted as others finish; aggregate
+               generated tok/s
+  gemm         batched Q-GEMM, B in {8,32,64,128}, Qwen2.5-3B projection shapes
+  attention    ragged paged decode attention: 128 sequences, context U[128,4096],
+               16 q / 2 kv heads, head_dim 128, fp16 K/V
+All weights are synthetic (N(0,0.02), generated and quantized on the GPU).
 
-    python bench.py [--gpus 1] [--steps 1000] [--warmup 50] [--cpu-seconds 12]
+    python bench.py [--gpus 1] [--steps 1000] [--warmup 50] [--cpu-seconds 12] [--only matvec,gemm,...]
 """
 from __future__ import annotations
 
@@ -31,23 +42,125 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 METRIC = "Q4/Q8 decode tok/s at batch 1 & 128; qmatvec achieved HBM GB/s vs peak"
-HBM_PEAK_GBS = 8000.0  # MI355X published HBM3E bandwidth
-POOL_BYTES = 320 << 20  # > 256 MB MALL
-CASES = [("q8_0", 10, 4096, 4096), ("q8_0", 10, 11008, 4096), ("q4_0", 20, 4096, 4096), ("q4_0", 20, 11008, 4096)]
+HBM_PEAK_GBS = 8000.0      # MI355X published HBM3E bandwidth
+POOL_BYTES = 320 << 20     # > 256 MB MALL
+Q8, Q4, F32, F16 = 10, 20, 0, 1
+MV_CASES = [("q8_0", Q8, 4096, 4096), ("q8_0", Q8, 11008, 4096), ("q4_0", Q4, 4096, 4096), ("q4_0", Q4, 11008, 4096)]
+GEMM_SHAPES = [(2048, 2048), (256, 2048), (11008, 2048), (2048, 11008)]
 
 
 def row_bytes(dt, k):
-    return (k // 32) * (36 if dt == 10 else 18)
+    return (k // 32) * (36 if dt == Q8 else 18)
 
 
-def alg_bytes(dt, n, k):
-    return n * row_bytes(dt, k) + 4 * k + 4 * n
+def mv_bytes(dt, n, k, b=1):
+    return n * row_bytes(dt, k) + 4 * b * k + 4 * b * n
 
 
-def cpu_baseline(cases_host, budget_s):
+def host_cpu():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def graph_time_us(rt, body, iters):
+    """Capture `iters` calls of body(i) in one graph; replay once untimed, then
+    time one replay with events on the stream; microseconds per call."""
+    stream, Graph, Event = rt["stream"], rt["Graph"], rt["Event"]
+    g = Graph(stream)
+    with g:
+        for i in range(iters):
+            body(i)
+    g.launch()
+    stream.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(stream)
+    g.launch()
+    e1.record(stream)
+    us = e0.elapsed_ms(e1) * 1e3 / iters
+    g.destroy()
+    return us
+
+
+# --------------------------------------------------------------------------- matvec (headline)
+
+def bench_matvec(args, rt):
+    call, DeviceBuffer, Event, Graph, stream, lib = (rt[k] for k in ("call", "DeviceBuffer", "Event", "Graph", "stream",
+                                                                     "lib"))
+    rng = np.random.default_rng(2024)
+    x_host = rng.standard_normal(4096).astype(np.float32)
+    cases = []
+    for (name, dt, n, k) in MV_CASES:
+        wbytes = n * row_bytes(dt, k)
+        copies = max(2, math.ceil(POOL_BYTES / wbytes))
+        pool = DeviceBuffer(copies * wbytes)
+        sid = lib.qraf_hip_name_hash(f"bench.{name}.{n}x{k}".encode())
+        call("qraf_hip_gen_weights_dev", pool.ptr, dt, n * k, 2024, sid, 0.02, stream.h)
+        for c in range(1, copies):
+            call("qraf_hip_memcpy_d2d", pool.ptr + c * wbytes, pool.ptr, wbytes, stream.h)
+        cases.append(dict(name=name, dt=dt, n=n, k=k, wbytes=wbytes, copies=copies, pool=pool,
+                          x=DeviceBuffer.from_array(x_host), y=DeviceBuffer(n * 4)))
+    stream.synchronize()
+
+    def launch(c, i):
+        call("qraf_hip_matvec_q_dev", c["pool"].ptr + (i % c["copies"]) * c["wbytes"], c["dt"], 32, c["n"], c["k"],
+             c["x"].ptr, c["y"].ptr, stream.h)
+
+    for i in range(args.warmup):
+        for c in cases:
+            launch(c, i)
+    stream.synchronize()
+    graphs = []
+    for c in cases:
+        g = Graph(stream)
+        with g:
+            for i in range(args.steps):
+                launch(c, args.warmup + i)
+        graphs.append(g)
+    for g in graphs:  # one untimed replay: graph upload stays out of the timed region
+        g.launch()
+    stream.synchronize()
+    ev = [Event() for _ in range(len(cases) + 1)]
+    call("qraf_hip_device_synchronize")
+    ev[0].record(stream)
+    for i, g in enumerate(graphs):
+        g.launch()
+        ev[i + 1].record(stream)
+    stream.synchronize()
+    call("qraf_hip_device_synchronize")
+    per_case, total_ms, total_bytes = [], 0.0, 0
+    for i, c in enumerate(cases):
+        ms = ev[i].elapsed_ms(ev[i + 1])
+        b = mv_bytes(c["dt"], c["n"], c["k"])
+        us = ms * 1e3 / args.steps
+        per_case.append({"case": f"{c['name']} {c['n']}x{c['k']}", "us_per_launch": round(us, 3), "alg_bytes": b,
+                         "GB_s": round(b / (us * 1e-6) / 1e9, 1),
+                         "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "pool_copies": c["copies"]})
+        total_ms += ms
+        total_bytes += b * args.steps
+    for g in graphs:
+        g.destroy()
+    # cache-resident reference point (same weight copy every launch), labelled as such
+    cache_res = []
+    for c in cases:
+        us = graph_time_us(rt, lambda i: call("qraf_hip_matvec_q_dev", c["pool"].ptr, c["dt"], 32, c["n"], c["k"],
+                                              c["x"].ptr, c["y"].ptr, stream.h), 200)
+        cache_res.append({"case": f"{c['name']} {c['n']}x{c['k']}",
+                          "GB_s": round(mv_bytes(c["dt"], c["n"], c["k"]) / (us * 1e-6) / 1e9, 1)})
+    hosts = [(c["name"], c["dt"], c["n"], c["k"], c["pool"].download(np.uint8, c["wbytes"]), x_host) for c in cases]
+    for c in cases:
+        c["pool"].free()
+    return total_bytes / (total_ms * 1e-3) / 1e9, total_ms, per_case, cache_res, hosts
+
+
+def cpu_baseline_matvec(cases_host, budget_s):
     """The reference's own scalar matvec (oracle/_ref, compiled from the
-    reference sources) on this host, one thread; falls back to the oracle's
-    restatement when the reference build is absent."""
+    reference sources) on this host, one thread; the oracle's restatement
+    when the reference build is absent."""
     from oracle import pyoracle as po
     R = po.ref()
     kind = "reference" if R is not None else "port"
@@ -62,24 +175,188 @@ def cpu_baseline(cases_host, budget_s):
             else:
                 po.lib().or_matvec_q(wq.ctypes.data, dt, 32, n, k, x.ctypes.data_as(po._fp), y.ctypes.data_as(po._fp))
             it += 1
-            dt_s = time.perf_counter() - t0
-            if dt_s >= per:
+            el = time.perf_counter() - t0
+            if el >= per:
                 break
-        tot_bytes += it * alg_bytes(dt, n, k)
-        tot_time += dt_s
+        tot_bytes += it * mv_bytes(dt, n, k)
+        tot_time += el
         parts.append(f"{name} {n}x{k}: {it} iters")
-    cpu = platform.processor() or platform.machine()
-    try:
-        for line in open("/proc/cpuinfo"):
-            if line.startswith("model name"):
-                cpu = line.split(":", 1)[1].strip()
-                break
-    except OSError:
-        pass
     return {"value": round(tot_bytes / tot_time / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": kind,
-            "sample": "; ".join(parts) + f" of dispatch_matvec_q (scalar x86 path), single thread, {tot_time:.1f} s, "
-                      f"host CPU: {cpu}"}
+            "sample": "; ".join(parts) + f" of dispatch_matvec_q (the scalar x86 path), one thread, {tot_time:.1f} s, "
+                      f"host CPU {host_cpu()}"}
 
+
+# --------------------------------------------------------------------------- batched GEMM
+
+def bench_gemm(args, rt):
+    call, DeviceBuffer, stream, lib = rt["call"], rt["DeviceBuffer"], rt["stream"], rt["lib"]
+    rng = np.random.default_rng(7)
+    out = []
+    for dt, fmt in ((Q8, "q8_0"), (Q4, "q4_0")):
+        for (n, k) in GEMM_SHAPES:
+            wbytes = n * row_bytes(dt, k)
+            copies = max(2, math.ceil(POOL_BYTES / wbytes))
+            pool = DeviceBuffer(copies * wbytes)
+            call("qraf_hip_gen_weights_dev", pool.ptr, dt, n * k, 7, lib.qraf_hip_name_hash(b"bench.gemm"), 0.02,
+                 stream.h)
+            for c in range(1, copies):
+                call("qraf_hip_memcpy_d2d", pool.ptr + c * wbytes, pool.ptr, wbytes, stream.h)
+            for b in (8, 32, 64, 128):
+                dx = DeviceBuffer.from_array(rng.standard_normal((b, k)).astype(np.float32))
+                xh, xl, y = DeviceBuffer(b * k * 2), DeviceBuffer(b * k * 2), DeviceBuffer(b * n * 4)
+                call("qraf_hip_split_bf16_dev", dx.ptr, xh.ptr, xl.ptr, b, k, stream.h)
+                us = graph_time_us(rt, lambda i: call("qraf_hip_qgemm_dev", pool.ptr + (i % copies) * wbytes, dt, 32,
+                                                      n, k, xh.ptr, xl.ptr, b, y.ptr, None, stream.h), 100)
+                by, fl = mv_bytes(dt, n, k, b), 2.0 * b * n * k
+                out.append({"case": f"{fmt} {n}x{k} B={b}", "us": round(us, 2),
+                            "GB_s": round(by / (us * 1e-6) / 1e9, 1), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 2)})
+            pool.free()
+    return out
+
+
+# --------------------------------------------------------------------------- attention
+
+def bench_attention(args, rt):
+    call, DeviceBuffer, stream, lib = rt["call"], rt["DeviceBuffer"], rt["stream"], rt["lib"]
+    rng = np.random.default_rng(2024)
+    n, H, Hkv, hd, ps, max_ctx = 128, 16, 2, 128, 16, 4096
+    ctxs = rng.integers(128, max_ctx + 1, n).astype(np.int32)
+    max_pages = max_ctx // ps
+    num_pages = int(sum((c + ps - 1) // ps for c in ctxs))
+    table = np.zeros((n, max_pages), np.int32)
+    perm = rng.permutation(num_pages).astype(np.int32)
+    k = 0
+    for s, c in enumerate(ctxs):
+        m = (c + ps - 1) // ps
+        table[s, :m] = perm[k:k + m]
+        k += m
+    kv_words = num_pages * Hkv * ps * hd // 2  # fp16 pages, filled with N(0,1) bit patterns of f32 pairs
+    K, V = DeviceBuffer(kv_words * 4), DeviceBuffer(kv_words * 4)
+    Kh = rng.standard_normal(kv_words * 2).astype(np.float16)
+    K.upload(Kh)
+    V.upload(rng.standard_normal(kv_words * 2).astype(np.float16))
+    q = DeviceBuffer.from_array(rng.standard_normal((n, H * hd)).astype(np.float32))
+    dt_, dc = DeviceBuffer.from_array(table), DeviceBuffer.from_array(ctxs)
+    out = DeviceBuffer(n * H * hd * 4)
+    wsb = lib.qraf_hip_attention_workspace_bytes(n, H, Hkv, hd, max_ctx)
+    ws = DeviceBuffer(wsb)
+    ws.zero()
+    us = graph_time_us(rt, lambda i: call("qraf_hip_paged_attention_dev", q.ptr, K.ptr, V.ptr, F16, dt_.ptr, max_pages,
+                                          dc.ptr, n, H, Hkv, hd, ps, np.float32(1 / math.sqrt(hd)), max_ctx, out.ptr,
+                                          ws.ptr, wsb, stream.h), 50)
+    by = int(ctxs.sum()) * Hkv * hd * 2 * 2 + 2 * n * H * hd * 4
+    return {"us": round(us, 2), "sum_ctx": int(ctxs.sum()), "alg_bytes": by, "GB_s": round(by / (us * 1e-6) / 1e9, 1),
+            "frac_hbm_peak": round(by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+
+# --------------------------------------------------------------------------- decode, batch 1
+
+SMOL = dict(vocab=49152, hidden=576, layers=30, heads=9, kv_heads=3, inter=1536, max_seq=2048, rope_theta=1e5,
+            eps=1e-5)
+
+
+def smol_bytes_per_token(ctx):
+    """Weights + KV read per decode token of the SmolLM2-135M architecture in Q8_0."""
+    D, F, L, V, kvd = 576, 1536, 30, 49152, 192
+    layer = (D + 2 * kvd) * row_bytes(Q8, D) + D * row_bytes(Q8, D) + 2 * F * row_bytes(Q8, D) + D * row_bytes(Q8, F)
+    return L * layer + V * row_bytes(Q8, D) + int(ctx * L * 2 * kvd * 4)
+
+
+def bench_decode_b1(args, rt):
+    from qraf_amd.engine import Engine, model_config
+    cfg = model_config(*(SMOL[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq",
+                                           "rope_theta", "eps")))
+    e = Engine(cfg, kv_dtype=F32, max_batch=1)
+    e.generate_weights(Q8, Q8, Q8, False, False, 1)
+    e.finalize()
+    prompt = np.random.default_rng(1).integers(0, SMOL["vocab"], 32).tolist()
+    n_gen = 128
+
+    def run():
+        s = e.seq_create()
+        t0 = time.perf_counter()
+        nx = None
+        for i, t in enumerate(prompt):
+            _, nx = e.step([s], [t], [i], want_logits=[1 if i == len(prompt) - 1 else 0])
+        t1 = time.perf_counter()
+        toks = [int(nx[0])]
+        pos = len(prompt)
+        while len(toks) < n_gen:
+            _, nx = e.step([s], [toks[-1]], [pos])
+            toks.append(int(nx[0]))
+            pos += 1
+        t2 = time.perf_counter()
+        e.seq_release(s)
+        return t1 - t0, t2 - t1, toks
+
+    run()  # warm-up
+    pre, dec, toks = run()
+    steps = n_gen - 1  # the first token comes from the prefill's logits
+    gbs = steps * smol_bytes_per_token(len(prompt) + steps / 2) / dec / 1e9
+    e.close()
+    return {"model": "SmolLM2-135M architecture, Q8_0 weights, f32 KV pages, random init", "prompt": len(prompt),
+            "generated": n_gen, "decode_tok_s": round(steps / dec, 1), "ms_per_token": round(dec / steps * 1e3, 3),
+            "prefill_plus_decode_tok_s": round(n_gen / (pre + dec), 1), "decode_GB_s": round(gbs, 1),
+            "first_tokens": toks[:8]}
+
+
+def cpu_decode_b1(n_tokens=8):
+    """SmolLM2-135M-architecture Q8 decode with the reference's own
+    InferenceEngine (oracle/_ref) on this host: 8-token prompt + 8 tokens."""
+    import tempfile
+    from oracle import pyoracle as po
+    if po.ref() is None:
+        return None
+    m = po.Model(po.make_config(wdtype=Q8, **SMOL), 1)
+    path = os.path.join(tempfile.mkdtemp(), "smol.qraf")
+    m.write_qraf(path)
+    m.close()
+    eng = po.RefEngine(path)
+    prompt = [po.lib().or_gen_token(1, i, SMOL["vocab"]) for i in range(8)]
+    toks, ms = eng.generate(prompt, n_tokens, 1.0)
+    eng.close()
+    os.remove(path)
+    return {"value": round(len(toks) / (ms / 1e3), 3),
+            "unit": "tok/s, generated / (prefill + decode) as inference.cpp:150-153 reports", "cores": 1,
+            "kind": "reference", "sample": f"8-token prompt + {len(toks)} greedy tokens via "
+                                           f"InferenceEngine::generate_tokens, {ms / 1e3:.1f} s, host CPU {host_cpu()}"}
+
+
+# --------------------------------------------------------------------------- decode, batch 128
+
+QWEN = dict(vocab=151936, hidden=2048, layers=36, heads=16, kv_heads=2, inter=11008, max_seq=1024, rope_theta=1e6,
+            eps=1e-6)
+
+
+def bench_decode_b128(args, rt):
+    from qraf_amd.engine import BatchScheduler, Engine, model_config
+    cfg = model_config(*(QWEN[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq",
+                                           "rope_theta", "eps")))
+    e = Engine(cfg, kv_dtype=F16, max_batch=128)
+    e.generate_weights(Q4, Q4, Q4, True, True, 3)
+    e.finalize()
+    rng = np.random.default_rng(3)
+    warm = BatchScheduler(e, max_batch=128)
+    for _ in range(4):
+        warm.submit(rng.integers(0, QWEN["vocab"], 16).tolist(), 4)
+    warm.run()
+    sched = BatchScheduler(e, max_batch=128)
+    for _ in range(args.requests):
+        plen, olen = int(rng.integers(16, 513)), int(rng.integers(64, 257))
+        sched.submit(rng.integers(0, QWEN["vocab"], plen).tolist(), olen)
+    t0 = time.perf_counter()
+    done = sched.run()
+    el = time.perf_counter() - t0
+    gen = sum(len(r.generated) for r in done)
+    e.close()
+    return {"model": "Qwen2.5-3B architecture, Q4_0 weights, tied head, QKV bias, fp16 KV pages, random init",
+            "requests": args.requests, "max_concurrent": 128, "generated_tokens": gen, "steps": sched.steps,
+            "rows_processed": sched.rows, "wall_s": round(el, 3), "generated_tok_s": round(gen / el, 1),
+            "rows_per_s": round(sched.rows / el, 1), "ms_per_step": round(el / sched.steps * 1e3, 3),
+            "note": "prompt tokens are fed one per step (chunk 1) in the same batched step as decodes"}
+
+
+# --------------------------------------------------------------------------- main
 
 def main():
     ap = argparse.ArgumentParser()
@@ -88,6 +365,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", default="matvec,gemm,attention,decode_b1,decode_b128")
+    ap.add_argument("--requests", type=int, default=256, help="requests in the batch-128 decode run")
     ap.add_argument("--rows-per-wave", type=int, default=0)
     ap.add_argument("--kernel", type=int, default=0, help="matvec kernel: 0 auto, 1 one-shot, 2 persistent")
     ap.add_argument("--wgs-per-cu", type=int, default=0)
@@ -96,6 +375,7 @@ def main():
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
               "(the decode path shards by sequence across GPUs, see DESIGN.md)", file=sys.stderr)
         sys.exit(2)
+    only = set(args.only.split(","))
 
     import qraf_amd
     from qraf_amd._lib import call
@@ -103,99 +383,28 @@ def main():
 
     qraf_amd.backend.backend_init(0)
     call("qraf_hip_set_matvec_tuning", args.kernel, args.rows_per_wave, args.wgs_per_cu)
-    stream = Stream()
-    rng = np.random.default_rng(2024)
-    x_host = rng.standard_normal(4096).astype(np.float32)
+    rt = dict(call=call, DeviceBuffer=DeviceBuffer, Event=Event, Graph=Graph, stream=Stream(), lib=qraf_amd.lib)
 
-    cases = []
-    for (name, dt, n, k) in CASES:
-        wbytes = n * row_bytes(dt, k)
-        copies = max(2, math.ceil(POOL_BYTES / wbytes))
-        pool = DeviceBuffer(copies * wbytes)
-        seed_stream = qraf_amd.lib.qraf_hip_name_hash(f"bench.{name}.{n}x{k}".encode())
-        call("qraf_hip_gen_weights_dev", pool.ptr, dt, n * k, 2024, seed_stream, 0.02, stream.h)
-        for c in range(1, copies):
-            call("qraf_hip_memcpy_d2d", pool.ptr + c * wbytes, pool.ptr, wbytes, stream.h)
-        x = DeviceBuffer.from_array(x_host)
-        y = DeviceBuffer(n * 4)
-        cases.append(dict(name=name, dt=dt, n=n, k=k, wbytes=wbytes, copies=copies, pool=pool, x=x, y=y))
-    stream.synchronize()
-
-    def launch(c, i):
-        call("qraf_hip_matvec_q_dev", c["pool"].ptr + (i % c["copies"]) * c["wbytes"], c["dt"], 32, c["n"], c["k"],
-             c["x"].ptr, c["y"].ptr, stream.h)
-
-    # warmup (eager)
-    for i in range(args.warmup):
-        for c in cases:
-            launch(c, i)
-    stream.synchronize()
-
-    # capture K launches per case; timed region = the four graph launches
-    graphs = []
-    for c in cases:
-        g = Graph(stream)
-        with g:
-            for i in range(args.steps):
-                launch(c, args.warmup + i)
-        graphs.append(g)
-    for g in graphs:  # one untimed replay so graph upload is out of the timed region
-        g.launch()
-    stream.synchronize()
-    ev = [Event() for _ in range(len(cases) + 1)]
-    call("qraf_hip_device_synchronize")
-    ev[0].record(stream)
-    for i, g in enumerate(graphs):
-        g.launch()
-        ev[i + 1].record(stream)
-    stream.synchronize()
-    call("qraf_hip_device_synchronize")
-    per_case = []
-    total_ms, total_bytes = 0.0, 0
-    for i, c in enumerate(cases):
-        ms = ev[i].elapsed_ms(ev[i + 1])
-        b = alg_bytes(c["dt"], c["n"], c["k"])
-        us = ms * 1e3 / args.steps
-        per_case.append({"case": f"{c['name']} {c['n']}x{c['k']}", "us_per_launch": round(us, 3),
-                         "alg_bytes": b, "GB_s": round(b / (us * 1e-6) / 1e9, 1),
-                         "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                         "pool_copies": c["copies"]})
-        total_ms += ms
-        total_bytes += b * args.steps
-    value = total_bytes / (total_ms * 1e-3) / 1e9
-
-    # cache-resident reference point (same weight copy every launch), labelled as such
-    cache_res = []
-    for c in cases:
-        g = Graph(stream)
-        with g:
-            for i in range(200):
-                call("qraf_hip_matvec_q_dev", c["pool"].ptr, c["dt"], 32, c["n"], c["k"], c["x"].ptr, c["y"].ptr,
-                     stream.h)
-        g.launch()
-        stream.synchronize()
-        e0, e1 = Event(), Event()
-        e0.record(stream)
-        g.launch()
-        e1.record(stream)
-        us = e0.elapsed_ms(e1) * 1e3 / 200
-        cache_res.append({"case": f"{c['name']} {c['n']}x{c['k']}", "GB_s": round(
-            alg_bytes(c["dt"], c["n"], c["k"]) / (us * 1e-6) / 1e9, 1)})
-        g.destroy()
+    value, total_ms, per_case, cache_res, hosts = bench_matvec(args, rt)
+    print(f"# matvec done: {value:.1f} GB/s", file=sys.stderr, flush=True)
+    extra = {}
+    for part, fn in (("gemm", bench_gemm), ("attention", bench_attention), ("decode_b1", bench_decode_b1),
+                     ("decode_b128", bench_decode_b128)):
+        if part in only:
+            extra[part] = fn(args, rt)
+            print(f"# {part} done", file=sys.stderr, flush=True)
 
     dom = max(per_case, key=lambda p: p["us_per_launch"])  # dominant kernel: longest launch
     roofline = {"bound": "hbm", "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "qmv_q8_kernel" if dom["case"].startswith("q8") else "qmv_q4_kernel",
+                "kernel": "qmv_persist_kernel<8,1>" if dom["case"].startswith("q8") else "qmv_persist_kernel<4,2>",
                 "case": dom["case"], "alg_bytes_per_launch": dom["alg_bytes"]}
-
     cpu = None
     if not args.no_cpu:
-        hosts = []
-        for c in cases:
-            wq = DeviceBuffer.download(c["pool"], np.uint8, c["wbytes"])
-            hosts.append((c["name"], c["dt"], c["n"], c["k"], wq, x_host))
-        cpu = cpu_baseline(hosts, args.cpu_seconds)
+        cpu = cpu_baseline_matvec(hosts, args.cpu_seconds)
+        if "decode_b1" in only:
+            extra["cpu_decode_b1"] = cpu_decode_b1()
+        print("# cpu baseline done", file=sys.stderr, flush=True)
 
     out = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
            "warmup": args.warmup, "ms_per_step": round(total_ms / args.steps, 5), "higher_is_better": True,
@@ -205,6 +414,7 @@ def main():
                                   "step, weights rotating through >320 MB pools per case",
                       "cases": [p["case"] for p in per_case]},
            "per_case": per_case, "cache_resident": cache_res, "roofline": roofline, "cpu_baseline": cpu}
+    out.update(extra)
     print(json.dumps(out), flush=True)
 
 
