@@ -205,8 +205,11 @@ def bench_gemm(args, rt):
                 dx = DeviceBuffer.from_array(rng.standard_normal((b, k)).astype(np.float32))
                 xh, xl, y = DeviceBuffer(b * k * 2), DeviceBuffer(b * k * 2), DeviceBuffer(b * n * 4)
                 call("qraf_hip_split_bf16_dev", dx.ptr, xh.ptr, xl.ptr, b, k, stream.h)
+                wsb = lib.qraf_hip_qgemm_workspace_bytes(dt, n, k, b)
+                ws = DeviceBuffer(wsb) if wsb else None
                 us = graph_time_us(rt, lambda i: call("qraf_hip_qgemm_dev", pool.ptr + (i % copies) * wbytes, dt, 32,
-                                                      n, k, xh.ptr, xl.ptr, b, y.ptr, None, stream.h), 100)
+                                                      n, k, xh.ptr, xl.ptr, b, y.ptr, None,
+                                                      ws.ptr if ws else None, wsb, stream.h), 100)
                 by, fl = mv_bytes(dt, n, k, b), 2.0 * b * n * k
                 out.append({"case": f"{fmt} {n}x{k} B={b}", "us": round(us, 2),
                             "GB_s": round(by / (us * 1e-6) / 1e9, 1), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 2)})

@@ -174,15 +174,41 @@ int qraf_hip_rope_append_dev(const float* qkv, const float* bias, int32_t n_seqs
  * qraf_hip_qgemm_dev.  rows x cols elements, row-major. */
 int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int32_t rows, int32_t cols,
                             void* stream);
+/* Tuning of qraf_hip_qgemm_dev for batches over 32 rows: waves 4 or 8 per
+ * workgroup (128 or 256 weight rows), splits > 0 forces the split count;
+ * 0 restores the automatic choice.  Affects qraf_hip_qgemm_workspace_bytes
+ * too.  No counterpart in the reference (a performance knob). */
+int qraf_hip_set_qgemm_tuning(int waves, int splits);
+/* Workspace (bytes) that lets qraf_hip_qgemm_dev split the in_dim range of an
+ * out_dim x in_dim product at this batch across workgroups; 0 when it does
+ * not split. */
+uint64_t qraf_hip_qgemm_workspace_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim, int32_t batch);
 /* dispatch_matvec_q (backend.cpp:131-199) for `batch` activation rows at
  * once on the matrix cores: y[m][i] = dot(row_i(w), x[m]) (+ add[m][i] when add
- * is not NULL), m < batch <= 128, i < out_dim.  w: Q8_0 (4-byte aligned) or
- * Q4_0 (2-byte aligned), block size 32, in_dim a multiple of 32; x given as the hi/lo planes of
- * qraf_hip_split_bf16_dev (16-byte aligned).  Error bound per output:
- * (2^-17 + (in_dim+2) 2^-24) sum_k |w_k x_k|. */
+ * is not NULL; add may equal y), m < batch, i < out_dim.  w: Q8_0 (4-byte
+ * aligned) or Q4_0 (2-byte aligned), block size 32, in_dim a multiple of 32;
+ * x given as the hi/lo planes of qraf_hip_split_bf16_dev (16-byte aligned).
+ * workspace (16-byte aligned, no initialisation needed) of at least
+ * qraf_hip_qgemm_workspace_bytes enables the split-K path; NULL runs one
+ * split.  The split-K sum is taken in a fixed order: results are
+ * deterministic.  Calls that share a workspace must not overlap.
+ * Error bound per output: (2^-17 + (in_dim+2) 2^-24) sum_k |w_k x_k|. */
 int qraf_hip_qgemm_dev(const void* w, uint32_t dtype, uint32_t block_size, uint32_t out_dim, uint32_t in_dim,
                        const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, float* y, const float* add,
-                       void* stream);
+                       void* workspace, uint64_t workspace_bytes, void* stream);
+/* Tile-major copy of a Q8_0/Q4_0 matrix (block size 32), the weight operand of
+ * qraf_hip_qgemm_tiled_dev: for every 16-row tile and quant block, the 16
+ * block scales then the 16 rows' 32 quants (rows past out_dim are zero), so a
+ * wavefront's weight loads are contiguous.  The same bytes as the reference
+ * layout (quantize.h:11-30), reordered; no counterpart in the reference. */
+uint64_t qraf_hip_tiled_weight_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim);
+int qraf_hip_repack_tiles_dev(const void* w, uint32_t dtype, uint32_t out_dim, uint32_t in_dim, void* dst,
+                              void* stream);
+/* qraf_hip_qgemm_dev on a tile-major weight copy (16-byte aligned); results
+ * are bit-identical to qraf_hip_qgemm_dev on the source matrix. */
+int qraf_hip_qgemm_tiled_dev(const void* w_tiled, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
+                             const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, float* y, const float* add,
+                             void* workspace, uint64_t workspace_bytes, void* stream);
 
 /* ------------------------------------------------------------- engine */
 

@@ -56,8 +56,13 @@ int launch_dot(const float* a, const float* b, int n, float* out, hipStream_t s)
 int launch_ew(int op, float* x, const float* y, float sc, int n, hipStream_t s);
 
 int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s);
+// split-K partial tiles go to ws when it is large enough (qgemm_workspace_bytes), else one split
 int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
-                 float* Y, const float* add, hipStream_t s);
+                 float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled = false);
+size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M);
+// tile-major copy of a Q8_0/Q4_0 matrix for launch_qgemm(..., tiled = true)
+size_t tiled_weight_bytes(uint32_t dtype, int N, int K);
+int launch_repack_tiles(const void* W, uint32_t dtype, int N, int K, void* dst, hipStream_t s);
 size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx);
 int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv_dtype, const int32_t* page_table,
                      int max_pages, const int32_t* ctx, int n, int H, int Hkv, int hd, int page_size, float scale,

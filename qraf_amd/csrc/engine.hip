@@ -161,6 +161,8 @@ struct qraf_engine {
         uint8_t* wo = nullptr;
         uint8_t* wgu = nullptr;
         uint8_t* wd = nullptr;
+        // tile-major copies of the quantized projections for the batched GEMM
+        uint8_t *wqkv_t = nullptr, *wo_t = nullptr, *wgu_t = nullptr, *wd_t = nullptr;
         float* bqkv = nullptr;
         float* an = nullptr;
         float* fn = nullptr;
@@ -173,6 +175,7 @@ struct qraf_engine {
     uint32_t dt_embed = 0xFFFFFFFFu;
     uint8_t* head = nullptr;
     uint32_t dt_head = 0xFFFFFFFFu;
+    uint8_t* head_t = nullptr;  // tile-major copy of the LM head (or the tied embedding)
     float* onorm = nullptr;
     std::vector<void*> allocs;
 
@@ -199,6 +202,8 @@ struct qraf_engine {
     uint32_t* h_amax = nullptr;
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
+    void* gemm_ws = nullptr;  // split-K partial tiles of the batched projections
+    size_t gemm_ws_bytes = 0;
     size_t in_words = 0;
 };
 
@@ -327,6 +332,14 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     e->attn_ws_bytes = attn_workspace_bytes(B, (int)c.num_heads, (int)kvh, hd, e->capacity);
     A(e->attn_ws, e->attn_ws_bytes);
     A(e->rope, (size_t)e->capacity * hd * 4);
+    {
+        const int shapes[5][2] = {{e->qkvd, D}, {D, e->qd}, {2 * F, D}, {D, F}, {V, D}};
+        for (uint32_t dt : {DT_Q8_0, DT_Q4_0})
+            for (auto& sh : shapes)
+                for (int m = 2; m <= B; m++)
+                    e->gemm_ws_bytes = std::max(e->gemm_ws_bytes, qgemm_workspace_bytes(dt, sh[0], sh[1], m));
+    }
+    if (e->gemm_ws_bytes) A(e->gemm_ws, e->gemm_ws_bytes);
 #undef A
     if (hipMemset(e->attn_ws, 0, e->attn_ws_bytes) != hipSuccess ||
         hipHostMalloc((void**)&e->h_in, e->in_words * 4, hipHostMallocDefault) != hipSuccess ||
@@ -563,6 +576,25 @@ int qraf_engine_finalize(qraf_engine* e) {
     for (size_t l = 0; l < e->layers.size(); l++)
         QH_REQUIRE(e->layers[l].have == T_ALL, QRAF_HIP_ERR_STATE, "finalize: layer %zu incomplete (mask %x)", l,
                    e->layers[l].have);
+    // Batched steps run the matrix-core GEMM on tile-major copies of the
+    // quantized weights (same bytes, reordered so wavefront loads are contiguous).
+    if (e->o.max_batch > 1 && !e->finalized) {
+        const qraf_model_config& c = e->c;
+        const int D = (int)c.hidden_size, F = (int)c.intermediate_size;
+        auto tile = [&](const uint8_t* w, uint32_t dt, int N, int K, uint8_t** out) -> int {
+            if ((dt != DT_Q8_0 && dt != DT_Q4_0) || K % 32) return QRAF_HIP_OK;
+            QH_TRY(ealloc(e, (void**)out, tiled_weight_bytes(dt, N, K)));
+            return launch_repack_tiles(w, dt, N, K, *out, e->stream);
+        };
+        for (auto& L : e->layers) {
+            QH_TRY(tile(L.wqkv, L.dt_attn, e->qkvd, D, &L.wqkv_t));
+            QH_TRY(tile(L.wo, L.dt_attn, D, e->qd, &L.wo_t));
+            QH_TRY(tile(L.wgu, L.dt_mlp, 2 * F, D, &L.wgu_t));
+            QH_TRY(tile(L.wd, L.dt_mlp, D, F, &L.wd_t));
+        }
+        QH_TRY(tile(e->head ? e->head : e->embed, e->head ? e->dt_head : e->dt_embed, (int)c.vocab_size, D, &e->head_t));
+        QH_CHECK_HIP(hipStreamSynchronize(e->stream));
+    }
     e->finalized = true;
     return QRAF_HIP_OK;
 }
@@ -676,7 +708,8 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
     const float scale = 1.0f / sqrtf((float)hd);  // attention.cpp:122
 
     // y[n][N] = x[n][K] * W^T (+ add): matvec at batch 1, else the matrix-core GEMM
-    auto proj = [&](const uint8_t* W, uint32_t dt, int N, int K, const float* x, int rows, float* y,
+    // Wt: the tile-major copy (batched steps); K not a multiple of 32: one matvec per row
+    auto proj = [&](const uint8_t* W, const uint8_t* Wt, uint32_t dt, int N, int K, const float* x, int rows, float* y,
                     const float* add) -> int {
         if (dt == DT_F32) {
             for (int r = 0; r < rows; r++)
@@ -684,9 +717,14 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
                                          add ? add + (size_t)r * N : nullptr));
             return QRAF_HIP_OK;
         }
-        if (rows == 1) return launch_matvec_q(W, dt, 32, N, K, x, y, s, add);
+        if (rows == 1 || !Wt) {
+            for (int r = 0; r < rows; r++)
+                QH_TRY(launch_matvec_q(W, dt, 32, N, K, x + (size_t)r * K, y + (size_t)r * N, s,
+                                       add ? add + (size_t)r * N : nullptr));
+            return QRAF_HIP_OK;
+        }
         QH_TRY(launch_split_bf16(x, e->xh, e->xl, rows, K, 0, nullptr, s));
-        return launch_qgemm(W, dt, 32, N, K, e->xh, e->xl, rows, y, add, s);
+        return launch_qgemm(Wt, dt, 32, N, K, e->xh, e->xl, rows, y, add, e->gemm_ws, e->gemm_ws_bytes, s, true);
     };
 
     hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, 32, D, d_tok, e->h);
@@ -697,22 +735,23 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;
         hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.an, D, c.rms_norm_eps, e->xn,
                            nullptr);
-        QH_TRY(proj(L.wqkv, L.dt_attn, e->qkvd, D, e->xn, n, e->qkv, nullptr));
+        QH_TRY(proj(L.wqkv, L.wqkv_t, L.dt_attn, e->qkvd, D, e->xn, n, e->qkv, nullptr));
         QH_TRY(launch_rope_append(e->qkv, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
                                   e->o.kv_dtype, d_ptab, MP, ps, s));
         QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale, e->capacity,
                                 e->att, e->attn_ws, e->attn_ws_bytes, s));
-        QH_TRY(proj(L.wo, L.dt_attn, D, e->qd, e->att, n, e->h, e->h));  // + residual (transformer.cpp:593)
+        QH_TRY(proj(L.wo, L.wo_t, L.dt_attn, D, e->qd, e->att, n, e->h, e->h));  // + residual (transformer.cpp:593)
         hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.fn, D, c.rms_norm_eps, e->xn,
                            nullptr);
-        QH_TRY(proj(L.wgu, L.dt_mlp, 2 * F, D, e->xn, n, e->gu, nullptr));
-        if (n == 1 || L.dt_mlp == DT_F32) {
+        QH_TRY(proj(L.wgu, L.wgu_t, L.dt_mlp, 2 * F, D, e->xn, n, e->gu, nullptr));
+        if (n == 1 || !L.wd_t) {
             hipLaunchKernelGGL(silu_gate_kernel, dim3(std::min((n * F + 255) / 256, 4096)), dim3(256), 0, s, e->gu, F,
                                n, e->act);
-            QH_TRY(proj(L.wd, L.dt_mlp, D, F, e->act, n, e->h, e->h));  // + residual (transformer.cpp:601)
+            QH_TRY(proj(L.wd, L.wd_t, L.dt_mlp, D, F, e->act, n, e->h, e->h));  // + residual (transformer.cpp:601)
         } else {
             QH_TRY(launch_split_bf16(e->gu, e->xh, e->xl, n, F, 1, nullptr, s));  // SiLU-gate fused into the split
-            QH_TRY(launch_qgemm(L.wd, L.dt_mlp, 32, D, F, e->xh, e->xl, n, e->h, e->h, s));
+            QH_TRY(launch_qgemm(L.wd_t, L.dt_mlp, 32, D, F, e->xh, e->xl, n, e->h, e->h, e->gemm_ws, e->gemm_ws_bytes, s,
+                                true));
         }
     }
     QH_CHECK_HIP(hipGetLastError());
@@ -722,7 +761,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
                            c.rms_norm_eps, e->xhead, d_lrows);
         const uint8_t* W = e->head ? e->head : e->embed;  // tied head reads the embedding (transformer.cpp:392-400)
         const uint32_t dt = e->head ? e->dt_head : e->dt_embed;
-        QH_TRY(proj(W, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
+        QH_TRY(proj(W, e->head_t, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
         hipLaunchKernelGGL(argmax_rows_kernel, dim3(n_logit_rows), dim3(256), 0, s, e->logits, V, e->amax);
         QH_CHECK_HIP(hipGetLastError());
         if (logits)

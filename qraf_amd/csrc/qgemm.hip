@@ -1,10 +1,10 @@
 // qgemm.hip -- batched Q8_0 / Q4_0 GEMM on gfx950 matrix cores.
 //
 // Y[m][n] = sum_k X[m][k] * W[n][k]  (+ add[m][n])  for a continuous-batch
-// decode step: the B rows of X are B sequences' activations, W is a weight
+// decode step: the M rows of X are M sequences' activations, W is a weight
 // matrix in the reference's Q8_0/Q4_0 block layout (quantize.h:11-30).  The
 // reference has no batched product: this is dispatch_matvec_q
-// (backend.cpp:131-199) applied to B vectors at once.
+// (backend.cpp:131-199) applied to M vectors at once.
 //
 // Exactness: each quant block is one K=32 step of v_mfma_f32_16x16x32_bf16.
 // Weights enter as bf16 copies of the block integers (exact: |q| <= 127), X
@@ -14,14 +14,23 @@
 // is scaled by its fp32 (Q8) or fp16 (Q4) scale with one FMA per output:
 //     |y - y_exact| <= (2^-17 + (K + 2) 2^-24) sum_k |w_k x_k|.
 //
-// Tiling: a workgroup of 4 waves owns 64 weight rows (16 per wave) and all
-// B <= 128 batch rows (8 row tiles of 16).  Per K step the workgroup stages
-// X[0:B, 32 k] hi/lo in LDS (rows padded to 80 B: conflict-free ds_read_b128)
-// with a double buffer; every wave reads each weight block once, converts it
-// to bf16 in registers and reuses it for all batch row tiles.
+// Tiling.  A workgroup (4 waves) owns a tile of MW batch rows x 128 weight
+// rows over a range of quant blocks.  For MW > 32 the waves form a 2 x 2
+// grid, each wave 64 weight rows (four 16-row MFMA tiles) x MW/2 batch rows;
+// otherwise the four waves split the 128 weight rows.  X is staged in LDS KC
+// quant blocks at a time (both planes; KC = 2, 4 or 8 as the batch tile
+// shrinks, so every stage moves enough bytes; rows padded so ds_read_b128 of
+// an MFMA operand is conflict-free), double-buffered with one barrier per
+// stage; each X fragment read from LDS feeds TN weight tiles.  Weights are
+// read straight into registers through a buffer resource, two stages ahead.
 // MFMA operand layout (16x16x32): lane l supplies row l%16, k = 8*(l/16)..+7
 // of A (= X) and of B^T (= W); it receives D[4*(l/16) + r][l%16], r = 0..3,
 // i.e. four batch rows of one weight row, so one block scale per lane.
+//
+// Split-K.  When the weight matrix has too few 128-row tiles to fill the
+// chip, the block range is split S ways; each split writes an fp32 partial
+// tile to a workspace and qgemm_reduce_kernel adds the S partials in split
+// order (deterministic), plus the residual.
 #include "common.h"
 
 namespace qraf_hip {
@@ -30,11 +39,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
+typedef uint32_t u32a2 __attribute__((aligned(2)));
 
-constexpr int GW = 256;       // threads per workgroup
-constexpr int GN = 64;        // weight rows per workgroup
-constexpr int GMAX = 128;     // max batch rows
-constexpr int XROW = 40;      // LDS row stride in bf16 (80 B)
+constexpr int QG_MCHUNK = 128;         // batch rows per workgroup at most
 
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
     uint32_t b = __builtin_bit_cast(uint32_t, f);
@@ -64,119 +71,389 @@ __global__ void split_bf16_kernel(const float* __restrict__ x, uint16_t* __restr
     }
 }
 
-// 8 weights of row `rp`, block b, k = 8*seg..+7 as bf16x8, and the block scale
+// Raw weight fragment of one lane for one (16-row tile, block): the block
+// scale and the 8 quants k = 8*seg..8*seg+7 of the lane's row.
 template <int FMT>
-__device__ __forceinline__ void load_wblock(const uint8_t* rp, int b, int seg, bf16x8& w, float& scale) {
-    if (FMT == 8) {
-        const uint8_t* p = rp + (size_t)b * 36;
-        scale = __builtin_bit_cast(float, *(const uint32_t*)p);
-        const u32x2a4 q = *(const u32x2a4*)(p + 4 + 8 * seg);
-        uint32_t f[8];
+struct WRaw;
+template <>
+struct WRaw<8> {
+    uint32_t scale;  // fp32 bits
+    uint32_t q0, q1;  // int8 x 8
+};
+template <>
+struct WRaw<4> {
+    uint32_t scale;  // fp16 bits
+    uint32_t q;       // 8 nibbles: byte j = elements 2j (low), 2j+1 (high)
+};
+
+// Raw buffer resource over [p, p + bytes): a load whose VGPR offset is at or
+// past `bytes` returns zeros (gfx9 raw buffer: 32-bit data format, no swizzle).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* p, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, (int)bytes, 0x00020000);
+}
+constexpr uint32_t OOB = 0x80000000u;  // VGPR offset that is always out of range
+
+// sc: byte offset of the lane's row, qo: of its 8 quants within a block,
+// boff: the (uniform) byte offset of the block within a row
+template <int FMT>
+__device__ __forceinline__ void load_raw(rsrc_t w, uint32_t sc, uint32_t qo, uint32_t boff, WRaw<FMT>& r);
+template <>
+__device__ __forceinline__ void load_raw<8>(rsrc_t w, uint32_t sc, uint32_t qo, uint32_t boff, WRaw<8>& r) {
+    r.scale = __builtin_amdgcn_raw_buffer_load_b32(w, sc, boff, 0);
+    const auto q = __builtin_amdgcn_raw_buffer_load_b64(w, qo, boff, 0);  // 36-byte blocks: 4-byte aligned
+    r.q0 = q[0];
+    r.q1 = q[1];
+}
+template <>
+__device__ __forceinline__ void load_raw<4>(rsrc_t w, uint32_t sc, uint32_t qo, uint32_t boff, WRaw<4>& r) {
+    // 18-byte blocks: every field is read with aligned 16-bit loads
+    r.scale = __builtin_amdgcn_raw_buffer_load_b16(w, sc, boff, 0);
+    const uint32_t a = __builtin_amdgcn_raw_buffer_load_b16(w, qo, boff, 0);
+    const uint32_t b = __builtin_amdgcn_raw_buffer_load_b16(w, qo + 2, boff, 0);
+    r.q = a | (b << 16);
+}
+
+// Tile-major weights (repack_tiles_kernel): for every 16-row tile and quant
+// block, the 16 scales then the 16 rows' quants, so one load instruction of a
+// wave reads contiguous memory.  sc / qo: byte offsets of the lane's scale and
+// 8 quants within the first tile-block, boff: the (uniform) offset of the block.
+template <int FMT>
+__device__ __forceinline__ void load_tiled(rsrc_t w, uint32_t sc, uint32_t qo, uint32_t boff, WRaw<FMT>& r);
+template <>
+__device__ __forceinline__ void load_tiled<8>(rsrc_t w, uint32_t sc, uint32_t qo, uint32_t boff, WRaw<8>& r) {
+    r.scale = __builtin_amdgcn_raw_buffer_load_b32(w, sc, boff, 0);
+    const auto q = __builtin_amdgcn_raw_buffer_load_b64(w, qo, boff, 0);
+    r.q0 = q[0];
+    r.q1 = q[1];
+}
+template <>
+__device__ __forceinline__ void load_tiled<4>(rsrc_t w, uint32_t sc, uint32_t qo, uint32_t boff, WRaw<4>& r) {
+    r.scale = __builtin_amdgcn_raw_buffer_load_b16(w, sc, boff, 0);
+    r.q = __builtin_amdgcn_raw_buffer_load_b32(w, qo, boff, 0);
+}
+
+// bytes of one tile-block: 16 scales + 16 rows of 32 quants
+__host__ __device__ constexpr int tile_block_bytes(int fmt) { return fmt == 8 ? 16 * 36 : 16 * 18; }
+
+// Reference row-major blocks -> tile-major: thread per (tile, block, row).
+// Rows past N are zero (scale 0, quants 0).
+template <int FMT>
+__global__ void repack_tiles_kernel(const uint8_t* __restrict__ src, int N, int nb, uint8_t* __restrict__ dst) {
+    constexpr int BB = FMT == 8 ? 36 : 18, SB = FMT == 8 ? 4 : 2, QB = BB - SB, TB = tile_block_bytes(FMT);
+    const size_t rb = (size_t)nb * BB;
+    const size_t total = (size_t)((N + 15) / 16) * nb * 16;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
+        const int r = (int)(i & 15);
+        const size_t tb = i >> 4;  // tile * nb + block
+        const size_t t = tb / nb, b = tb % nb;
+        const size_t row = t * 16 + r;
+        uint8_t* d = dst + tb * TB;
+        uint16_t* ds = (uint16_t*)(d + SB * r);
+        uint16_t* dq = (uint16_t*)(d + 16 * SB + QB * r);
+        if (row < (size_t)N) {
+            const uint16_t* sp = (const uint16_t*)(src + row * rb + b * BB);  // 2-byte aligned fields
 #pragma unroll
-        for (int j = 0; j < 8; j++) {
-            const uint32_t d = j < 4 ? q[0] : q[1];
-            f[j] = __builtin_bit_cast(uint32_t, (float)(int8_t)(d >> (8 * (j & 3))));
+            for (int h = 0; h < SB / 2; h++) ds[h] = sp[h];
+#pragma unroll
+            for (int h = 0; h < QB / 2; h++) dq[h] = sp[SB / 2 + h];
+        } else {
+#pragma unroll
+            for (int h = 0; h < SB / 2; h++) ds[h] = 0;
+#pragma unroll
+            for (int h = 0; h < QB / 2; h++) dq[h] = 0;
         }
-        u32x4 packed;
-#pragma unroll
-        for (int j = 0; j < 4; j++) packed[j] = __builtin_amdgcn_perm(f[2 * j + 1], f[2 * j], 0x07060302u);
-        w = __builtin_bit_cast(bf16x8, packed);
-    } else {
-        // Q4 rows are 4-byte aligned but blocks are 18 B, so block fields are
-        // only 2-byte aligned: read them with 16-bit loads, never past the block.
-        const uint16_t* p = (const uint16_t*)(rp + (size_t)b * 18);
-        scale = (float)__builtin_bit_cast(_Float16, p[0]);
-        const uint32_t d = (uint32_t)p[1 + 2 * seg] | ((uint32_t)p[2 + 2 * seg] << 16);  // nibble bytes 4seg..4seg+3
-        uint32_t f[8];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const uint32_t byte = (d >> (8 * j)) & 0xFFu;
-            f[2 * j] = __builtin_bit_cast(uint32_t, (float)(int)(byte & 15u) - 8.0f);
-            f[2 * j + 1] = __builtin_bit_cast(uint32_t, (float)(int)(byte >> 4) - 8.0f);
-        }
-        u32x4 packed;
-#pragma unroll
-        for (int j = 0; j < 4; j++) packed[j] = __builtin_amdgcn_perm(f[2 * j + 1], f[2 * j], 0x07060302u);
-        w = __builtin_bit_cast(bf16x8, packed);
     }
 }
 
-// MT: number of 16-row batch tiles (1..8)
-template <int FMT, int MT>
-__global__ __launch_bounds__(GW) void qgemm_kernel(const uint8_t* __restrict__ W, size_t row_bytes, int N, int K,
-                                                  const uint16_t* __restrict__ xh, const uint16_t* __restrict__ xl,
-                                                  int M, float* __restrict__ Y, const float* __restrict__ add) {
-    __shared__ __align__(16) uint16_t sx[2][2][GMAX * XROW];  // [buffer][hi/lo][row * XROW + k]
+__device__ __forceinline__ uint32_t bf16_pair(float even, float odd) {
+    // exact small integers: the bf16 value is the high half of the fp32 bits
+    return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, odd), __builtin_bit_cast(uint32_t, even), 0x07060302u);
+}
+
+template <int FMT>
+__device__ __forceinline__ void convert(const WRaw<FMT>& r, bf16x8& w, float& scale);
+template <>
+__device__ __forceinline__ void convert<8>(const WRaw<8>& r, bf16x8& w, float& scale) {
+    scale = __builtin_bit_cast(float, r.scale);
+    u32x4 p;
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const uint32_t d = j ? r.q1 : r.q0;
+        p[2 * j] = bf16_pair((float)(int8_t)(d), (float)(int8_t)(d >> 8));
+        p[2 * j + 1] = bf16_pair((float)(int8_t)(d >> 16), (float)(int8_t)(d >> 24));
+    }
+    w = __builtin_bit_cast(bf16x8, p);
+}
+template <>
+__device__ __forceinline__ void convert<4>(const WRaw<4>& r, bf16x8& w, float& scale) {
+    scale = (float)__builtin_bit_cast(_Float16, (uint16_t)r.scale);
+    // nibble u -> signed byte u - 8: (u + 0x78) ^ 0x80, no carry between bytes
+    const uint32_t lo = ((r.q & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+    const uint32_t hi = (((r.q >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
+    u32x4 p;
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+        p[j] = bf16_pair((float)(int8_t)(lo >> (8 * j)), (float)(int8_t)(hi >> (8 * j)));
+    w = __builtin_bit_cast(bf16x8, p);
+}
+
+// WM x WN waves (batch x weight rows); TM: 16-row batch tiles per wave; TN:
+// 16-row weight tiles per wave; KC: quant blocks per stage.  A workgroup
+// owns WM*TM*16 batch rows x WN*TN*16 weight rows.
+//
+// Pipeline (two stages per loop trip, no register copies): while stage c
+// computes from LDS buffer c&1 and weight registers set c&1, X of stage c+1
+// sits in registers (stored to LDS after the compute, one barrier per
+// stage) and the weights of stage c+1 are in flight into the other set; the
+// weights of stage c+2 are requested as soon as stage c has consumed its set.
+template <int FMT, int WM, int WNW, int TM, int TN, int KC, bool TILED>
+__global__ __launch_bounds__(64 * WM * WNW, 512 / (64 * WM * WNW)) void qgemm_kernel(
+    const uint8_t* __restrict__ W, size_t row_bytes, int N, int nb, const uint16_t* __restrict__ xh,
+    const uint16_t* __restrict__ xl, int K, int M, float* Y, const float* add, int bps, float* __restrict__ part) {
+    constexpr int QG_THREADS = 64 * WM * WNW;
+    constexpr int QG_NW = WNW * TN * 16;
+    static_assert(QG_THREADS % (KC * 4) == 0, "stage shape");
+    constexpr int MW = WM * TM * 16;
+    constexpr int XS = KC * 32 + 8;  // LDS row stride in bf16: (4 KC + 1) 16-byte units, odd -> conflict-free
+    constexpr int PLANE = MW * XS;
+    constexpr int PIECES = 2 * MW * KC * 4;  // 16-byte pieces of X per stage
+    constexpr int PP = PIECES / QG_THREADS;
+    static_assert(PIECES % QG_THREADS == 0, "staging shape");
+    __shared__ __align__(16) uint16_t sx[2 * 2 * PLANE];  // [buffer][plane][MW][XS]
+
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n0 = blockIdx.x * GN + wave * 16;
-    const int wr = min(n0 + (lane & 15), N - 1);  // weight row of this lane (clamped)
-    const int seg = lane >> 4;
-    const uint8_t* rp = W + (size_t)wr * row_bytes;
-    const int nb = K / 32;
-    const int Mp = MT * 16;
+    const int wm = wave / WNW, wn = wave % WNW;
+    const int seg = lane >> 4, l16 = lane & 15;
+    const int m0 = blockIdx.z * MW;
+    const int nbase = blockIdx.x * QG_NW + wn * TN * 16;
+    const int b_begin = blockIdx.y * bps;  // bps: a positive multiple of 2 KC
+    const int b_end = min(nb, b_begin + bps);
+    const int nchunks = bps / KC;  // even; blocks past b_end are read clamped and weighted 0
 
-    // stage X[:, 32b..32b+31] (hi and lo) into buffer `buf`: 2*Mp rows of 64 B
-    auto stage = [&](int buf, int b) {
-        for (int i = tid; i < Mp * 2 * 4; i += GW) {  // 16-byte pieces: row, plane, quarter
-            const int q = i & 3, plane = (i >> 2) & 1, m = i >> 3;
-            u32x4 v = {0, 0, 0, 0};
-            if (m < M) {
-                const uint16_t* src = (plane ? xl : xh) + (size_t)m * K + 32 * b + 8 * q;
-                v = *(const u32x4*)src;
-            }
-            *(u32x4*)&sx[buf][plane][m * XROW + 8 * q] = v;
-        }
-    };
-
-    f32x4 acc[MT];
+    // block stride of the weight stream: a row's next block (reference
+    // layout) or the tile's next tile-block (tile-major layout)
+    constexpr int BB = TILED ? tile_block_bytes(FMT) : (FMT == 8 ? 36 : 18);
+    const int ntile16 = (N + 15) / 16;
+    const size_t wbytes = TILED ? (size_t)ntile16 * nb * BB : (size_t)N * row_bytes;
+    const rsrc_t wrs = make_rsrc(W, (uint32_t)min(wbytes, (size_t)0xFFFFFFFFu));
+    uint32_t wsc[TN], wq[TN];  // per weight tile: scale offset, quant offset
 #pragma unroll
-    for (int t = 0; t < MT; t++) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    bf16x8 wcur;
-    float scur;
-    load_wblock<FMT>(rp, 0, seg, wcur, scur);
-    stage(0, 0);
-    __syncthreads();
-    for (int b = 0; b < nb; b++) {
-        const int buf = b & 1;
-        bf16x8 wnext;
-        float snext;
-        if (b + 1 < nb) {
-            load_wblock<FMT>(rp, b + 1, seg, wnext, snext);
-            stage(buf ^ 1, b + 1);
-        }
-#pragma unroll
-        for (int t = 0; t < MT; t++) {
-            const int row = t * 16 + (lane & 15);
-            const bf16x8 ah = *(const bf16x8*)&sx[buf][0][row * XROW + 8 * seg];
-            const bf16x8 al = *(const bf16x8*)&sx[buf][1][row * XROW + 8 * seg];
-            f32x4 c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wcur, f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wcur, c, 0, 0, 0);
-#pragma unroll
-            for (int r = 0; r < 4; r++) acc[t][r] = __builtin_fmaf(c[r], scur, acc[t][r]);
-        }
-        __syncthreads();
-        if (b + 1 < nb) {
-            wcur = wnext;
-            scur = snext;
+    for (int u = 0; u < TN; u++) {
+        if (TILED) {
+            const uint32_t tb = (uint32_t)((size_t)min((nbase >> 4) + u, ntile16 - 1) * nb * BB);
+            wsc[u] = tb + (FMT == 8 ? 4 * l16 : 2 * l16);
+            wq[u] = tb + (FMT == 8 ? 64 + 32 * l16 + 8 * seg : 32 + 16 * l16 + 4 * seg);
+        } else {
+            wsc[u] = (uint32_t)((size_t)min(nbase + u * 16 + l16, N - 1) * row_bytes);
+            wq[u] = wsc[u] + (FMT == 8 ? 4 + 8 * seg : 2 + 4 * seg);
         }
     }
 
-    const int n = n0 + (lane & 15);
-    if (n < N) {
+    // X staging: piece p of this thread is (row r, plane, 16-byte quarter q of
+    // block j of the stage); q and j are the same for every p.
+    // Rows past M read row M-1 (finite data whose outputs are never stored);
+    // blocks past the end are clamped to the last block (never used).
+    const int xq = tid % (KC * 4), xj = xq >> 2;
+    const uint16_t* xptr[PP];
+    int xlds[PP];
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
+    for (int p = 0; p < PP; p++) {
+        const int rest = (tid + p * QG_THREADS) / (KC * 4);
+        const int plane = rest & 1, r = rest >> 1, m = m0 + r;
+        xptr[p] = (plane ? xl : xh) + (size_t)min(m, M - 1) * K + (xq & 3) * 8;
+        xlds[p] = plane * PLANE + r * XS + xq * 8;
+    }
+    u32x4 xr[PP];
+    auto load_x = [&](int c) {
+        const int boff = min(b_begin + c * KC + xj, nb - 1) * 32;
+#pragma unroll
+        for (int p = 0; p < PP; p++) xr[p] = *(const u32x4*)(xptr[p] + boff);
+    };
+    auto store_x = [&](int buf) {
+#pragma unroll
+        for (int p = 0; p < PP; p++) *(u32x4*)&sx[buf * 2 * PLANE + xlds[p]] = xr[p];
+    };
+    auto load_w = [&](WRaw<FMT>(&dst)[KC][TN], int c) {
+        const int cb = b_begin + c * KC;
+#pragma unroll
+        for (int j = 0; j < KC; j++) {
+            const uint32_t boff = (uint32_t)max(min(cb + j, b_end - 1), 0) * BB;
+#pragma unroll
+            for (int u = 0; u < TN; u++) {
+                if (TILED) load_tiled<FMT>(wrs, wsc[u], wq[u], boff, dst[j][u]);
+                else load_raw<FMT>(wrs, wsc[u], wq[u], boff, dst[j][u]);
+            }
+        }
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int u = 0; u < TN; u++) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](int c, const WRaw<FMT>(&wc)[KC][TN]) {
+        const int buf = c & 1, cb = b_begin + c * KC;
+#pragma unroll
+        for (int j = 0; j < KC; j++) {
+            const bool valid = cb + j < b_end;  // uniform; an invalid block's scale is 0 (its data is finite)
+            bf16x8 wf[TN];
+            float sc[TN];
+#pragma unroll
+            for (int u = 0; u < TN; u++) {
+                WRaw<FMT> r = wc[j][u];
+                r.scale = valid ? r.scale : 0u;
+                convert<FMT>(r, wf[u], sc[u]);
+            }
+#pragma unroll
+            for (int t = 0; t < TM; t++) {
+                const int row = (wm * TM + t) * 16 + l16;
+                const bf16x8 ah = *(const bf16x8*)&sx[(buf * 2 + 0) * PLANE + row * XS + j * 32 + seg * 8];
+                const bf16x8 al = *(const bf16x8*)&sx[(buf * 2 + 1) * PLANE + row * XS + j * 32 + seg * 8];
+#pragma unroll
+                for (int u = 0; u < TN; u++) {
+                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[u], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[u], d, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[t][u][r] = __builtin_fmaf(d[r], sc[u], acc[t][u][r]);
+                }
+            }
+        }
+    };
+    // one stage: compute c, publish X of c+1, request X and weights of c+2
+    // (past the end these are clamped loads that are never read)
+    // (past the end these are clamped loads that are never read).  X loads are
+    // issued before weight loads so that waiting for X never waits for weights.
+    auto step = [&](int c, WRaw<FMT>(&wc)[KC][TN]) {
+        compute(c, wc);
+        __builtin_amdgcn_sched_barrier(0);
+        store_x((c & 1) ^ 1);
+        __builtin_amdgcn_sched_barrier(0);
+        load_x(c + 2);
+        __builtin_amdgcn_sched_barrier(0);
+        load_w(wc, c + 2);
+        __syncthreads();
+    };
+
+    WRaw<FMT> wa[KC][TN], wb[KC][TN];
+    load_w(wa, 0);
+    load_x(0);
+    store_x(0);
+    load_x(1);
+    __builtin_amdgcn_sched_barrier(0);
+    load_w(wb, 1);
+    __syncthreads();
+    for (int c = 0; c < nchunks; c += 2) {
+        step(c, wa);
+        step(c + 1, wb);
+    }
+
+    // epilogue: direct (+ residual) or this split's partial tile
+    float* dst = part ? part + (size_t)blockIdx.y * M * N : Y;
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+#pragma unroll
+        for (int u = 0; u < TN; u++) {
+            const int n = nbase + u * 16 + l16;
 #pragma unroll
             for (int r = 0; r < 4; r++) {
-                const int m = t * 16 + 4 * seg + r;
-                if (m < M) {
-                    float v = acc[t][r];
-                    if (add) v += add[(size_t)m * N + n];
-                    Y[(size_t)m * N + n] = v;
+                const int m = m0 + (wm * TM + t) * 16 + seg * 4 + r;
+                if (m < M && n < N) {
+                    float v = acc[t][u][r];
+                    if (!part && add) v += add[(size_t)m * N + n];
+                    dst[(size_t)m * N + n] = v;
                 }
             }
         }
     }
+}
+
+// Y = sum_{s < S} part[s] (+ add), in split order.
+__global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float* __restrict__ part, int S, size_t MN, float* Y,
+                                                           const float* add) {
+    const size_t n4 = MN / 4;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += (size_t)gridDim.x * blockDim.x) {
+        f32x4 v = ((const f32x4*)part)[i];
+        for (int s = 1; s < S; s++) {
+            const f32x4 p = ((const f32x4*)(part + (size_t)s * MN))[i];
+            v[0] += p[0];
+            v[1] += p[1];
+            v[2] += p[2];
+            v[3] += p[3];
+        }
+        if (add) {
+            const f32x4 a = ((const f32x4*)add)[i];
+            v[0] += a[0];
+            v[1] += a[1];
+            v[2] += a[2];
+            v[3] += a[3];
+        }
+        ((f32x4*)Y)[i] = v;
+    }
+    for (size_t i = n4 * 4 + (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < MN;
+         i += (size_t)gridDim.x * blockDim.x) {
+        float v = part[i];
+        for (int s = 1; s < S; s++) v += part[(size_t)s * MN + i];
+        if (add) v += add[i];
+        Y[i] = v;
+    }
+}
+
+struct QgPlan {
+    int WM, WN, TM, TN, KC, MW, NW, ntiles, mchunks, S, bps;
+    size_t ws_bytes;
+};
+
+// Tuning overrides (qraf_hip_set_qgemm_tuning): 0 = automatic.
+static int g_qg_waves = 0;   // 4 or 8 waves per workgroup for batch tiles > 32 rows
+static int g_qg_splits = 0;  // forced split count
+
+// Tile shape and split count for an N x K matrix times M rows.  Batch tiles
+// of more than 32 rows use 2 x WN waves of 64 weight rows each; smaller ones
+// 4 waves of 32 weight rows.  Splits are added (powers of two, at most 64)
+// while the grid has fewer workgroups than the chip has slots for and every
+// split keeps at least one ping-pong pair of stages.
+static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes) {
+    QgPlan p{};
+    const int Mc = min(M, QG_MCHUNK);
+    p.WM = Mc > 32 ? 2 : 1;
+    p.TM = (Mc + 16 * p.WM - 1) / (16 * p.WM);
+    p.TN = p.WM == 2 ? 4 : 2;
+    p.WN = p.WM == 2 ? (g_qg_waves == 8 ? 4 : 2) : 4;
+    p.MW = p.WM * p.TM * 16;
+    p.NW = p.WN * p.TN * 16;
+    p.KC = p.MW <= 32 ? 8 : p.MW <= 64 ? 4 : 2;  // keep the X stage near 16-32 KB
+    p.ntiles = (N + p.NW - 1) / p.NW;
+    p.mchunks = (M + p.MW - 1) / p.MW;
+    const int nb = K / 32;
+    const size_t tiles = (size_t)p.ntiles * p.mchunks;
+    const size_t slots = p.WM * p.WN == 8 ? 256 : 512;  // workgroups resident at once (LDS / waves)
+    (void)row_bytes;
+    const int pair = 2 * p.KC;  // blocks per ping-pong pair of stages
+    int S = 1;
+    if (g_qg_splits > 0) {
+        S = g_qg_splits;
+    } else {
+        while (S < 64 && tiles * S < slots && nb >= 2 * S * pair) S *= 2;
+    }
+    p.bps = ((nb + S - 1) / S + pair - 1) / pair * pair;
+    p.S = (nb + p.bps - 1) / p.bps;  // no empty splits
+    p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
+    return p;
+}
+
+int set_qgemm_tuning(int waves, int splits) {
+    QH_REQUIRE(waves == 0 || waves == 4 || waves == 8, QRAF_HIP_ERR_INVALID, "qgemm tuning: waves %d", waves);
+    QH_REQUIRE(splits >= 0 && splits <= 256, QRAF_HIP_ERR_INVALID, "qgemm tuning: splits %d", splits);
+    g_qg_waves = waves;
+    g_qg_splits = splits;
+    return QRAF_HIP_OK;
+}
+
+size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M) {
+    if ((dtype != DT_Q8_0 && dtype != DT_Q4_0) || N <= 0 || K <= 0 || K % 32 || M <= 0) return 0;
+    return qgemm_plan(N, K, M, q_row_bytes(dtype, 32, K)).ws_bytes;
 }
 
 int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s) {
@@ -188,33 +465,89 @@ int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, 
     return QRAF_HIP_OK;
 }
 
+size_t tiled_weight_bytes(uint32_t dtype, int N, int K) {
+    if ((dtype != DT_Q8_0 && dtype != DT_Q4_0) || N <= 0 || K <= 0 || K % 32) return 0;
+    return (size_t)((N + 15) / 16) * (K / 32) * tile_block_bytes(dtype == DT_Q8_0 ? 8 : 4);
+}
+
+int launch_repack_tiles(const void* W, uint32_t dtype, int N, int K, void* dst, hipStream_t s) {
+    QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "repack: unsupported dtype %u", dtype);
+    QH_REQUIRE(K % 32 == 0 && K > 0 && N > 0, QRAF_HIP_ERR_INVALID, "repack: K=%d must be a positive multiple of 32", K);
+    QH_REQUIRE(W && dst && (((uintptr_t)W) & 1) == 0 && (((uintptr_t)dst) & 15) == 0, QRAF_HIP_ERR_INVALID,
+               "repack: null or misaligned pointer");
+    const size_t total = (size_t)((N + 15) / 16) * (K / 32) * 16;
+    const int grid = (int)min((total + 255) / 256, (size_t)8192);
+    if (dtype == DT_Q8_0)
+        hipLaunchKernelGGL(repack_tiles_kernel<8>, dim3(grid), dim3(256), 0, s, (const uint8_t*)W, N, K / 32,
+                           (uint8_t*)dst);
+    else
+        hipLaunchKernelGGL(repack_tiles_kernel<4>, dim3(grid), dim3(256), 0, s, (const uint8_t*)W, N, K / 32,
+                           (uint8_t*)dst);
+    QH_CHECK_HIP(hipGetLastError());
+    return QRAF_HIP_OK;
+}
+
 int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
-                 float* Y, const float* add, hipStream_t s) {
+                 float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled) {
     QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "qgemm: unsupported dtype %u", dtype);
     QH_REQUIRE(bs == 32, QRAF_HIP_ERR_DTYPE, "qgemm: block size %d (32 required)", bs);
     QH_REQUIRE(K % 32 == 0 && K > 0 && N > 0, QRAF_HIP_ERR_INVALID, "qgemm: K=%d must be a positive multiple of 32", K);
-    QH_REQUIRE(M > 0 && M <= GMAX, QRAF_HIP_ERR_INVALID, "qgemm: batch %d outside 1..%d", M, GMAX);
+    QH_REQUIRE(M > 0, QRAF_HIP_ERR_INVALID, "qgemm: batch %d", M);
     QH_REQUIRE(W && xh && xl && Y, QRAF_HIP_ERR_INVALID, "qgemm: null pointer");
     // Q8 blocks are read with 4-byte loads (36-byte blocks keep rows 4-aligned),
-    // Q4 blocks with 2-byte loads (18-byte blocks)
-    QH_REQUIRE((((uintptr_t)W) & (dtype == DT_Q8_0 ? 3 : 1)) == 0 && (((uintptr_t)xh) & 15) == 0 &&
+    // Q4 blocks with 2-byte-aligned loads (18-byte blocks); X rows with 16-byte loads
+    QH_REQUIRE((((uintptr_t)W) & (tiled ? 15 : dtype == DT_Q8_0 ? 3 : 1)) == 0 && (((uintptr_t)xh) & 15) == 0 &&
                    (((uintptr_t)xl) & 15) == 0,
                QRAF_HIP_ERR_INVALID, "qgemm: misaligned operands");
     const size_t rb = q_row_bytes(dtype, bs, K);
-    const int MT = (M + 15) / 16;
-    dim3 grid((N + GN - 1) / GN);
-#define QH_G(F, T)                                                                                          \
-    case T:                                                                                                 \
-        hipLaunchKernelGGL((qgemm_kernel<F, T>), grid, dim3(GW), 0, s, (const uint8_t*)W, rb, N, K, xh, xl, M, \
-                           Y, add);                                                                         \
-        break;
-    if (dtype == DT_Q8_0) {
-        switch (MT) { QH_G(8, 1) QH_G(8, 2) QH_G(8, 3) QH_G(8, 4) QH_G(8, 5) QH_G(8, 6) QH_G(8, 7) QH_G(8, 8) }
-    } else {
-        switch (MT) { QH_G(4, 1) QH_G(4, 2) QH_G(4, 3) QH_G(4, 4) QH_G(4, 5) QH_G(4, 6) QH_G(4, 7) QH_G(4, 8) }
+    const int nb = K / 32;
+    QgPlan p = qgemm_plan(N, K, M, rb);
+    float* part = nullptr;
+    if (p.S > 1) {
+        if (ws && ws_bytes >= p.ws_bytes && (((uintptr_t)ws) & 15) == 0) {
+            part = (float*)ws;
+        } else {  // no (or too small a) workspace: one split
+            p.S = 1;
+            p.bps = (nb + 2 * p.KC - 1) / (2 * p.KC) * (2 * p.KC);
+        }
     }
+    QH_REQUIRE(p.mchunks <= 65535, QRAF_HIP_ERR_INVALID, "qgemm: batch %d too large", M);
+    const dim3 grid(p.ntiles, p.S, p.mchunks);
+#define QH_G(F, WM_, WN_, TM_, TN_, KC_)                                                                           \
+    if (tiled)                                                                                                     \
+        hipLaunchKernelGGL((qgemm_kernel<F, WM_, WN_, TM_, TN_, KC_, true>), grid, dim3(64 * WM_ * WN_), 0, s,       \
+                           (const uint8_t*)W, rb, N, nb, xh, xl, K, M, Y, add, p.bps, part);                       \
+    else                                                                                                           \
+        hipLaunchKernelGGL((qgemm_kernel<F, WM_, WN_, TM_, TN_, KC_, false>), grid, dim3(64 * WM_ * WN_), 0, s,      \
+                           (const uint8_t*)W, rb, N, nb, xh, xl, K, M, Y, add, p.bps, part)
+#define QH_GW(F, WN_)                               \
+    if (p.TM == 2) QH_G(F, 2, WN_, 2, 4, 4);        \
+    else if (p.TM == 3) QH_G(F, 2, WN_, 3, 4, 2);   \
+    else QH_G(F, 2, WN_, 4, 4, 2);
+#define QH_GF(F)                                    \
+    if (p.WM == 1) {                                \
+        if (p.TM == 1) QH_G(F, 1, 4, 1, 2, 8);      \
+        else QH_G(F, 1, 4, 2, 2, 8);                \
+    } else if (p.WN == 4) {                         \
+        QH_GW(F, 4)                                 \
+    } else {                                        \
+        QH_GW(F, 2)                                 \
+    }
+    if (dtype == DT_Q8_0) {
+        QH_GF(8)
+    } else {
+        QH_GF(4)
+    }
+#undef QH_GF
+#undef QH_GW
 #undef QH_G
     QH_CHECK_HIP(hipGetLastError());
+    if (part) {
+        const size_t MN = (size_t)M * N;
+        const int rgrid = (int)min((MN / 4 + 255) / 256 + 1, (size_t)2048);
+        hipLaunchKernelGGL(qgemm_reduce_kernel, dim3(rgrid), dim3(256), 0, s, part, p.S, MN, Y, add);
+        QH_CHECK_HIP(hipGetLastError());
+    }
     return QRAF_HIP_OK;
 }
 
@@ -227,12 +560,39 @@ int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int3
     return qraf_hip::launch_split_bf16(x, x_hi, x_lo, rows, cols, 0, nullptr, qraf_hip::as_stream(stream));
 }
 
+int qraf_hip_set_qgemm_tuning(int waves, int splits) {
+    qraf_hip::clear_error();
+    return qraf_hip::set_qgemm_tuning(waves, splits);
+}
+
+uint64_t qraf_hip_qgemm_workspace_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim, int32_t batch) {
+    return qraf_hip::qgemm_workspace_bytes(dtype, (int)out_dim, (int)in_dim, batch);
+}
+
 int qraf_hip_qgemm_dev(const void* w, uint32_t dtype, uint32_t block_size, uint32_t out_dim, uint32_t in_dim,
                        const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, float* y, const float* add,
-                       void* stream) {
+                       void* workspace, uint64_t workspace_bytes, void* stream) {
     qraf_hip::clear_error();
     return qraf_hip::launch_qgemm(w, dtype, block_size ? (int)block_size : 32, (int)out_dim, (int)in_dim, x_hi, x_lo,
-                                  batch, y, add, qraf_hip::as_stream(stream));
+                                  batch, y, add, workspace, workspace_bytes, qraf_hip::as_stream(stream), false);
+}
+
+uint64_t qraf_hip_tiled_weight_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim) {
+    return qraf_hip::tiled_weight_bytes(dtype, (int)out_dim, (int)in_dim);
+}
+
+int qraf_hip_repack_tiles_dev(const void* w, uint32_t dtype, uint32_t out_dim, uint32_t in_dim, void* dst,
+                              void* stream) {
+    qraf_hip::clear_error();
+    return qraf_hip::launch_repack_tiles(w, dtype, (int)out_dim, (int)in_dim, dst, qraf_hip::as_stream(stream));
+}
+
+int qraf_hip_qgemm_tiled_dev(const void* w_tiled, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
+                             const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, float* y, const float* add,
+                             void* workspace, uint64_t workspace_bytes, void* stream) {
+    qraf_hip::clear_error();
+    return qraf_hip::launch_qgemm(w_tiled, dtype, 32, (int)out_dim, (int)in_dim, x_hi, x_lo, batch, y, add, workspace,
+                                  workspace_bytes, qraf_hip::as_stream(stream), true);
 }
 
 }  // extern "C"

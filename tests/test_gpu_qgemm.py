@@ -13,18 +13,40 @@ from oracle import pyoracle as po
 pytestmark = pytest.mark.gpu
 
 
-def run_gemm(hip, wq, dt, N, K, X, add=None):
+def run_gemm(hip, wq, dt, N, K, X, add=None, split=True, in_place=False, repeats=1, tiled=False):
+    """split: pass the split-K workspace (as the engine does); in_place: the
+    residual is added into y itself (add == y); tiled: repack the weights
+    tile-major on the device and use the tiled GEMM."""
     from qraf_amd.backend import DeviceBuffer
-    call = hip._lib.call
+    call, lib = hip._lib.call, hip._lib.lib
     M = X.shape[0]
     dw, dx = DeviceBuffer.from_array(wq), DeviceBuffer.from_array(X)
+    if tiled:
+        dtl = DeviceBuffer(lib.qraf_hip_tiled_weight_bytes(dt, N, K))
+        call("qraf_hip_repack_tiles_dev", dw.ptr, dt, N, K, dtl.ptr, None)
     dh, dl = DeviceBuffer(M * K * 2), DeviceBuffer(M * K * 2)
     dy = DeviceBuffer(M * N * 4)
-    da = DeviceBuffer.from_array(add) if add is not None else None
+    da = DeviceBuffer.from_array(add) if add is not None and not in_place else None
+    wsb = lib.qraf_hip_qgemm_workspace_bytes(dt, N, K, M) if split else 0
+    ws = DeviceBuffer(wsb) if wsb else None
     call("qraf_hip_split_bf16_dev", dx.ptr, dh.ptr, dl.ptr, M, K, None)
-    call("qraf_hip_qgemm_dev", dw.ptr, dt, 32, N, K, dh.ptr, dl.ptr, M, dy.ptr, da.ptr if da else None, None)
-    call("qraf_hip_stream_synchronize", None)
-    return dy.download(np.float32, M * N).reshape(M, N), dh.download(np.uint16, M * K), dl.download(np.uint16, M * K)
+    outs = []
+    for _ in range(repeats):
+        if in_place:
+            dy.upload(np.ascontiguousarray(add, np.float32))
+        a = dy.ptr if in_place else (da.ptr if da else None)
+        if tiled:
+            call("qraf_hip_qgemm_tiled_dev", dtl.ptr, dt, N, K, dh.ptr, dl.ptr, M, dy.ptr, a, ws.ptr if ws else None,
+                 wsb, None)
+        else:
+            call("qraf_hip_qgemm_dev", dw.ptr, dt, 32, N, K, dh.ptr, dl.ptr, M, dy.ptr, a, ws.ptr if ws else None, wsb,
+                 None)
+        call("qraf_hip_stream_synchronize", None)
+        outs.append(dy.download(np.float32, M * N).reshape(M, N))
+    Y = outs[0]
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), Y.view(np.uint32)), "repeated GEMM differs"
+    return Y, dh.download(np.uint16, M * K), dl.download(np.uint16, M * K)
 
 
 def check(Y, wq, dt, N, K, X, add=None):
@@ -43,8 +65,9 @@ def check(Y, wq, dt, N, K, X, add=None):
 
 CASES = [
     # (N, K, batch): Qwen2.5-3B projection shapes at the continuous-batch sizes, ragged cases
-    (2048, 2048, 128), (256, 2048, 64), (11008, 2048, 32), (2048, 11008, 8),
-    (2560, 2048, 17), (100, 64, 1), (65, 96, 3), (1000, 576, 100), (576, 1536, 16),
+    (2048, 2048, 128), (256, 2048, 64), (11008, 2048, 32), (2048, 11008, 8), (2048, 11008, 128),
+    (2560, 2048, 17), (100, 64, 1), (65, 96, 3), (1000, 576, 100), (576, 1536, 16), (300, 2048, 80),
+    (700, 4096, 48), (130, 128, 2), (2048, 2048, 200), (513, 1024, 257),
 ]
 
 
@@ -56,17 +79,61 @@ def test_qgemm_vs_oracle(hip, dt, case):
     rng = np.random.default_rng(N + K + M + dt)
     wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
     X = rng.standard_normal((M, K)).astype(np.float32)
-    Y, _, _ = run_gemm(hip, wq, dt, N, K, X)
+    Y, _, _ = run_gemm(hip, wq, dt, N, K, X, repeats=2)
     check(Y, wq, dt, N, K, X)
+    Y1, _, _ = run_gemm(hip, wq, dt, N, K, X, split=False)  # one split, no workspace
+    check(Y1, wq, dt, N, K, X)
+    # tile-major weights: the same arithmetic in the same order, bit for bit
+    Yt, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True)
+    assert np.array_equal(Yt.view(np.uint32), Y.view(np.uint32))
 
 
-def test_qgemm_residual_epilogue(hip):
+def tile_major_reference(wq, dt, N, K):
+    """The documented tile-major layout, built from the reference bytes with numpy."""
+    bb, sb = (36, 4) if dt == po.Q8_0 else (18, 2)
+    nb, nt = K // 32, (N + 15) // 16
+    rows = np.zeros((nt * 16, nb, bb), np.uint8)
+    rows[:N] = wq.reshape(N, nb, bb)
+    t = rows.reshape(nt, 16, nb, bb).transpose(0, 2, 1, 3)  # tile, block, row, bytes
+    return np.concatenate([t[..., :sb].reshape(nt, nb, 16 * sb), t[..., sb:].reshape(nt, nb, 16 * (bb - sb))],
+                          axis=2).reshape(-1)
+
+
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("shape", [(2048, 2048), (100, 64), (65, 96), (1000, 576)], ids=lambda c: "x".join(map(str, c)))
+def test_repack_tiles_layout(hip, dt, shape):
+    from qraf_amd.backend import DeviceBuffer
+    call, lib = hip._lib.call, hip._lib.lib
+    N, K = shape
+    rng = np.random.default_rng(N * K + dt)
+    wq = po.quantize(dt, rng.standard_normal(N * K).astype(np.float32))
+    nbytes = lib.qraf_hip_tiled_weight_bytes(dt, N, K)
+    ref = tile_major_reference(wq, dt, N, K)
+    assert nbytes == ref.size
+    dw, dt_ = DeviceBuffer.from_array(wq), DeviceBuffer(nbytes)
+    call("qraf_hip_repack_tiles_dev", dw.ptr, dt, N, K, dt_.ptr, None)
+    call("qraf_hip_stream_synchronize", None)
+    assert np.array_equal(dt_.download(np.uint8, nbytes), ref)
+
+
+def test_qgemm_split_k_is_used(hip):
+    lib = hip._lib.lib
+    # few 128-row tiles and a long K: the split-K path must be chosen
+    assert lib.qraf_hip_qgemm_workspace_bytes(po.Q4_0, 2048, 11008, 128) > 0
+    assert lib.qraf_hip_qgemm_workspace_bytes(po.Q8_0, 2048, 2048, 8) > 0
+    # many tiles: no split
+    assert lib.qraf_hip_qgemm_workspace_bytes(po.Q4_0, 151936, 2048, 128) == 0
+
+
+@pytest.mark.parametrize("split", [True, False])
+@pytest.mark.parametrize("in_place", [True, False])
+def test_qgemm_residual_epilogue(hip, split, in_place):
     rng = np.random.default_rng(5)
     N, K, M = 2048, 2048, 40
     wq = po.quantize(po.Q8_0, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
     X = rng.standard_normal((M, K)).astype(np.float32)
     add = rng.standard_normal((M, N)).astype(np.float32)
-    Y, _, _ = run_gemm(hip, wq, po.Q8_0, N, K, X, add)
+    Y, _, _ = run_gemm(hip, wq, po.Q8_0, N, K, X, add, split=split, in_place=in_place)
     check(Y, wq, po.Q8_0, N, K, X, add)
 
 
