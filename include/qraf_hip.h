@@ -129,23 +129,27 @@ uint64_t qraf_hip_name_hash(const char* name);
 
 /* ------------------------------------------- ragged paged decode attention */
 
-/* Workspace bytes for qraf_hip_paged_attention_dev.  The workspace must be
- * zero-filled once after allocation; the kernels leave it ready for the next
- * call (its first bytes are per-sequence merge counters). */
+/* Workspace bytes for qraf_hip_paged_attention_dev (chunk partials of long
+ * contexts); no initialisation needed.  Calls sharing one must not overlap. */
 uint64_t qraf_hip_attention_workspace_bytes(int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads,
                                             int32_t head_dim, int32_t max_ctx);
 /* The score / softmax / weighted-sum loops of attention_forward
  * (attention.cpp:122-150) for a ragged batch of n_seqs sequences that each
  * attend with one query token:
  *   q        [n_seqs][n_heads][head_dim] f32, RoPE already applied
- *   k_cache, v_cache  [num_pages][n_kv_heads][page_size][head_dim], F32 or F16
+ *   k_cache  [num_pages][n_kv_heads][page_size][head_dim], F32 or F16
+ *   v_cache  F32: [num_pages][n_kv_heads][page_size][head_dim]
+ *            F16: [num_pages][n_kv_heads][head_dim][page_size] (dimension-major
+ *            in a page, the layout qraf_hip_rope_append_dev writes)
  *   page_table [n_seqs][max_pages_per_seq] physical page of logical page j
  *   ctx_lens [n_seqs] positions attended (1 <= ctx <= max_ctx), on the device
  *   out      [n_seqs][n_heads][head_dim] f32
  * Query head h reads KV head h / (n_heads / n_kv_heads) (attention.cpp:127);
  * scale is 1/sqrt(head_dim) in the reference (attention.cpp:122).
  * head_dim 64 or 128 with n_heads / n_kv_heads in {1,2,3,4,6,8,12,16}, or
- * head_dim 16 or 32 with n_heads / n_kv_heads in {1,2,4,8}. */
+ * head_dim 16 or 32 with n_heads / n_kv_heads in {1,2,4,8}.  F16 pages with
+ * head_dim 64/128 and page_size % 4 == 0 run on the matrix cores.  Page
+ * contents at positions >= ctx are never used (NaN there is harmless). */
 int qraf_hip_paged_attention_dev(const float* q, const void* k_cache, const void* v_cache, uint32_t kv_dtype,
                                  const int32_t* page_table, int32_t max_pages_per_seq, const int32_t* ctx_lens,
                                  int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,

@@ -3,10 +3,14 @@
 // Replaces the per-head score / softmax / weighted-sum loops of
 // attention_forward (reference attention.cpp:122-150) and the KVCache store
 // (attention.cpp:39-44, :119), for a batch of sequences that each add one
-// token.  KV layout in HBM, per layer:
-//     K, V : [num_pages][Hkv][page_size][head_dim]   (f32 or f16)
+// token.  KV layout in HBM, per layer (a page holds page_size positions):
+//     K     : [num_pages][Hkv][page_size][head_dim]   (f32 or f16)
+//     V f32 : [num_pages][Hkv][page_size][head_dim]
+//     V f16 : [num_pages][Hkv][head_dim][page_size]   (dimension-major in a page)
 // and a page table per sequence maps logical page j (positions
-// j*page_size .. +page_size-1) to a physical page.
+// j*page_size .. +page_size-1) to a physical page.  fp16 V is stored
+// dimension-major so that the matrix-core kernel's V operand (consecutive
+// positions of one dimension) is a contiguous load.
 //
 // Work decomposition: the context of every sequence is cut into chunks of
 // CH = 256 positions; one workgroup handles one (sequence, chunk) item for
@@ -15,12 +19,17 @@
 // batch, which every workgroup recomputes in LDS from the device-resident
 // context lengths, so the packing follows whatever lengths are on the device
 // when the kernel runs (no host round trip).  Sequences with several chunks
-// write (max, sum, unnormalised output) partials; the last chunk to finish
-// (an atomic counter per sequence and KV head) merges them in chunk order.
+// write (max, sum, unnormalised output) partials, which attn_merge_kernel (a
+// second launch, one workgroup per sequence and KV head) combines in chunk
+// order.
 //
-// Scores: thread = position; q is read from LDS (broadcast), K rows with
-// 16-byte loads.  Output: thread = (head subset, dimension), V rows read
-// coalesced, probabilities broadcast from LDS.  fp32 arithmetic throughout.
+// Two kernels share this decomposition.  attn_mfma_kernel (fp16 pages,
+// head_dim 64 or 128, up to 16 query heads per KV head) runs q.K^T and P.V
+// on v_mfma_f32_16x16x32_f16: K and V enter as stored (fp16, exact), q and the
+// probabilities as fp16 hi + lo pairs (q scaled per head by a power of two so
+// hi + lo carries 22 bits of it), products accumulate in fp32.
+// attn_decode_kernel (the rest) is plain fp32 VALU code: scores with
+// thread = position, output with thread = (head, dimension).
 #include <math.h>
 
 #include "common.h"
@@ -55,10 +64,57 @@ struct AttnArgs {
     float* out;                // [n][H][HD]
     float* part_o;             // [items][H][HD]   (multi-chunk partials)
     float* part_ml;            // [items][H][2]
-    uint32_t* counters;        // [n][Hkv]          zero on entry, zero on exit
+    uint32_t* counters;        // [n][Hkv]          (reserved)
     int n, H, Hkv, page_size, max_pages, max_ctx;
     float scale;
 };
+
+// Item -> (sequence, chunk): every workgroup computes the exclusive prefix
+// sum of ceil(ctx_s / ACH) over the batch in LDS (4 entries per thread, wave
+// scan, then across the 4 waves), then finds its sequence by bisection.
+// Returns false for items past the total (the grid is sized for max_ctx).
+__device__ __forceinline__ bool attn_item(const AttnArgs& a, int* s_pref, int& s, int& chunk, int& nchunks) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n = a.n;
+    __shared__ int s_wtot[4];
+    int c[4], run = 0;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int i = tid * 4 + j;
+        c[j] = i < n ? (min(a.ctx[i], a.max_ctx) + ACH - 1) / ACH : 0;
+        run += c[j];
+    }
+    int incl = run;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const int v = __shfl_up(incl, o);
+        if (lane >= o) incl += v;
+    }
+    if (lane == 63) s_wtot[wave] = incl;
+    __syncthreads();
+    int off = incl - run;
+    for (int w = 0; w < wave; w++) off += s_wtot[w];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int i = tid * 4 + j;
+        off += c[j];
+        if (i < n) s_pref[i + 1] = off;
+    }
+    if (tid == 0) s_pref[0] = 0;
+    __syncthreads();
+    const int item = blockIdx.x;
+    if (item >= s_pref[n]) return false;
+    int lo = 0, hi = n - 1;  // largest s with s_pref[s] <= item
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (s_pref[mid] <= item) lo = mid;
+        else hi = mid - 1;
+    }
+    s = lo;
+    chunk = item - s_pref[s];
+    nchunks = s_pref[s + 1] - s_pref[s];
+    return true;
+}
 
 template <typename KT, int HD, int G>
 __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
@@ -69,51 +125,12 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     __shared__ float s_q[G][HD];
     __shared__ float s_p[G][ACH];
     __shared__ float s_red[G][4];
-    __shared__ int s_last;
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kvh = blockIdx.y;
-    const int n = a.n;
-
-    // ---- item -> (sequence, chunk): exclusive prefix sum of chunk counts
-    // (block scan: 4 entries per thread, wave scan, then across the 4 waves)
-    {
-        int c[4], run = 0;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = tid * 4 + j;
-            c[j] = i < n ? (min(a.ctx[i], a.max_ctx) + ACH - 1) / ACH : 0;
-            run += c[j];
-        }
-        int incl = run;
-#pragma unroll
-        for (int o = 1; o < 64; o <<= 1) {
-            const int v = __shfl_up(incl, o);
-            if (lane >= o) incl += v;
-        }
-        __shared__ int s_wtot[4];
-        if (lane == 63) s_wtot[wave] = incl;
-        __syncthreads();
-        int off = incl - run;
-        for (int w = 0; w < wave; w++) off += s_wtot[w];
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int i = tid * 4 + j;
-            off += c[j];
-            if (i < n) s_pref[i + 1] = off;
-        }
-        if (tid == 0) s_pref[0] = 0;
-        __syncthreads();
-    }
     const int item = blockIdx.x;
-    if (item >= s_pref[n]) return;
-    int lo = 0, hi = n - 1;  // largest s with s_pref[s] <= item
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s_pref[mid] <= item) lo = mid;
-        else hi = mid - 1;
-    }
-    const int s = lo, chunk = item - s_pref[s], nchunks = s_pref[s + 1] - s_pref[s];
+    int s, chunk, nchunks;
+    if (!attn_item(a, s_pref, s, chunk, nchunks)) return;
     const int ctx = min(a.ctx[s], a.max_ctx);
     const int t0 = chunk * ACH;
 
@@ -197,11 +214,13 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
             const int page = a.page_table[(size_t)s * a.max_pages + lp];
             vpage = vc + ((size_t)page * a.Hkv + kvh) * a.page_size * HD;
         }
-        const KT* vrow = vpage + (size_t)(tp % a.page_size) * HD;
+        const int tin = tp % a.page_size;
 #pragma unroll
         for (int j = 0; j < HPT; j++) {
             const int oi = tid + ACH * j;
-            if (oi < NOUT) o[j] = __builtin_fmaf(s_p[oi / HD][tt], kv_load(vrow + oi % HD), o[j]);
+            // f32 pages: V row-major per position; f16 pages: dimension-major
+            const KT* vp = sizeof(KT) == 4 ? vpage + (size_t)tin * HD + oi % HD : vpage + (size_t)(oi % HD) * a.page_size + tin;
+            if (oi < NOUT) o[j] = __builtin_fmaf(s_p[oi / HD][tt], kv_load(vp), o[j]);
         }
     }
 
@@ -214,7 +233,7 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
         return;
     }
 
-    // ---- multi-chunk: publish partials, last chunk merges in chunk order
+    // ---- multi-chunk: publish (max, sum, unnormalised output) for attn_merge_kernel
 #pragma unroll
     for (int j = 0; j < HPT; j++) {
         const int oi = tid + ACH * j;
@@ -224,21 +243,242 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
         a.part_ml[((size_t)item * a.H + kvh * G + tid) * 2 + 0] = m[tid];
         a.part_ml[((size_t)item * a.H + kvh * G + tid) * 2 + 1] = l[tid];
     }
-    __threadfence();
-    __syncthreads();
-    if (tid == 0) {
-        const uint32_t prev = atomicAdd(&a.counters[(size_t)s * a.Hkv + kvh], 1u);
-        s_last = (prev == (uint32_t)nchunks - 1);
+}
+
+// ---------------------------------------------------------------------------
+// Matrix-core decode attention for fp16 pages (see the file comment).  One
+// workgroup = one (sequence, ACH-position chunk, KV head); wave w takes the
+// chunk's positions 64w .. 64w+63 as four 16-position tiles.
+//
+// q.K^T, per tile: A = K (lane: position l%16, 8 dimensions), B = q^T (lane:
+// head l%16, the same 8 dimensions), D[position][head]; heads >= G are zero
+// columns.  P.V, per 32 positions: A = P (lane: head l%16, 8 positions),
+// B = V (lane: dimension l%16, the same 8 positions, contiguous in a
+// dimension-major page), D[head][dimension].  Lane (l%16, s = l/16) holds
+// positions 4s..4s+3 of every score tile, so its P operand for tiles 2b, 2b+1
+// is positions {4s..4s+3} and {16+4s..16+4s+3}, and its V operand is the same
+// two 4-position runs.  Positions at or past ctx get score -inf (p = 0) and
+// their V values are zeroed, so page contents past ctx never matter.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4a __attribute__((ext_vector_type(4)));
+
+// zero the fp16 lanes of a 4-position run (2 dwords) at or past ctx
+__device__ __forceinline__ uint2 mask_run(uint2 v, int pos0, int ctx) {
+    const int k = ctx - pos0;  // valid positions in the run
+    if (k >= 4) return v;
+    if (k <= 0) return make_uint2(0u, 0u);
+    if (k == 1) return make_uint2(v.x & 0xFFFFu, 0u);
+    if (k == 2) return make_uint2(v.x, 0u);
+    return make_uint2(v.x, v.y & 0xFFFFu);
+}
+
+template <int HD>
+__global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
+    static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    constexpr int KK = HD / 32;  // MFMA k-steps per score tile
+    constexpr int DPL = HD / 4;  // dimensions per lane in q.K^T: lane s covers DPL*s .. DPL*s+DPL-1
+    constexpr int DT = HD / 16;  // 16-dimension output tiles
+    constexpr int QS = HD + 8;   // q plane row stride (fp16): 16-byte reads of 16 rows hit distinct banks
+    __shared__ int s_pref[1025];
+    __shared__ __align__(16) _Float16 s_q[2][16][QS];
+    __shared__ float s_qs[16];
+    __shared__ float s_m[4][16], s_l[4][16];
+    __shared__ float s_o[4][16][HD];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int l16 = lane & 15, seg = lane >> 4;
+    const int kvh = blockIdx.y;
+    const int item = blockIdx.x;
+    int s, chunk, nchunks;
+    if (!attn_item(a, s_pref, s, chunk, nchunks)) return;
+    const int ctx = min(a.ctx[s], a.max_ctx);
+    const int ps = a.page_size;
+    const int32_t* ptab = a.page_table + (size_t)s * a.max_pages;
+
+    // ---- q of the G heads as fp16 hi + lo, scaled per head by 2^e so that
+    // max|q| lands in [2^14, 2^15): hi + lo then carries 22 bits of every
+    // element that matters at fp32 precision
+    for (int h = wave; h < 16; h += 4) {
+        constexpr int PER = HD / 64;
+        float v[PER];
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            v[i] = h < G ? a.q[((size_t)s * a.H + kvh * G + h) * HD + lane + 64 * i] : 0.f;
+            mx = fmaxf(mx, fabsf(v[i]));
+        }
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        float sigma = 1.f;
+        if (mx > 0.f && mx <= 3.0e38f) {
+            int e;
+            frexpf(mx, &e);
+            sigma = ldexpf(1.f, min(15 - e, 120));
+        }
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const float x = v[i] * sigma;
+            const _Float16 hi = (_Float16)x;
+            s_q[0][h][lane + 64 * i] = hi;
+            s_q[1][h][lane + 64 * i] = (_Float16)(x - (float)hi);
+        }
+        if (lane == 0) s_qs[h] = a.scale / sigma;  // attention.cpp:134: dot * scale
     }
     __syncthreads();
-    if (!s_last) return;
-    __threadfence();
-    const int base = s_pref[s];
+
+    const _Float16* kc = (const _Float16*)a.kc;
+    const _Float16* vc = (const _Float16*)a.vc;
+    const int pw = chunk * ACH + 64 * wave;  // first position of this wave
+    const bool active = pw < ctx;            // wave-uniform
+
+    // ---- scores of 4 tiles: sc[t][r] = position pw + 16t + 4seg + r, head l16
+    f32x4a sc[4];
 #pragma unroll
-    for (int j = 0; j < HPT; j++) {
-        const int oi = tid + ACH * j;
-        if (oi >= NOUT) continue;
-        const size_t hidx = (size_t)kvh * G + oi / HD;
+    for (int t = 0; t < 4; t++) sc[t] = f32x4a{0.f, 0.f, 0.f, 0.f};
+    if (active) {
+        f16x8 qh[KK], ql[KK];
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) {
+            qh[kk] = *(const f16x8*)&s_q[0][l16][DPL * seg + 8 * kk];
+            ql[kk] = *(const f16x8*)&s_q[1][l16][DPL * seg + 8 * kk];
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++) {
+            const int pc = min(pw + 16 * t + l16, ctx - 1);  // clamped: past-ctx scores are masked below
+            const int page = ptab[pc / ps];
+            const _Float16* kr = kc + (((size_t)page * a.Hkv + kvh) * ps + pc % ps) * HD + DPL * seg;
+            f32x4a d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+                const f16x8 kf = *(const f16x8*)(kr + 8 * kk);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[kk], d, 0, 0, 0);
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[kk], d, 0, 0, 0);
+            }
+            sc[t] = d;
+        }
+    }
+
+    // ---- softmax statistics over the workgroup's positions, per head l16
+    const float qs = s_qs[l16];
+    float mloc = -INFINITY;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const bool ok = active && pw + 16 * t + 4 * seg + r < ctx;
+            sc[t][r] = ok ? sc[t][r] * qs : -INFINITY;
+            mloc = fmaxf(mloc, sc[t][r]);
+        }
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+    mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+    if (seg == 0) s_m[wave][l16] = mloc;
+    __syncthreads();
+    const float m = fmaxf(fmaxf(s_m[0][l16], s_m[1][l16]), fmaxf(s_m[2][l16], s_m[3][l16]));
+    float lsum = 0.f;
+#pragma unroll
+    for (int t = 0; t < 4; t++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const float p = sc[t][r] == -INFINITY ? 0.f : __expf(sc[t][r] - m);
+            sc[t][r] = p;
+            lsum += p;
+        }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (seg == 0) s_l[wave][l16] = lsum;
+
+    // ---- P.V over the wave's 64 positions (two 32-position MFMA steps)
+    f32x4a o[DT];
+#pragma unroll
+    for (int d = 0; d < DT; d++) o[d] = f32x4a{0.f, 0.f, 0.f, 0.f};
+    if (active) {
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+            f16x8 ph, pl;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float p = sc[2 * b + (i >> 2)][i & 3];
+                const _Float16 h = (_Float16)p;
+                ph[i] = h;
+                pl[i] = (_Float16)(p - (float)h);
+            }
+            // the lane's two 4-position runs; clamped into the context (their
+            // values are masked), 4-aligned so a run never leaves a page
+            const int pa = pw + 32 * b + 4 * seg, pb = pa + 16;
+            const int last = (ctx - 1) & ~3;
+            const int pac = min(pa, last), pbc = min(pb, last);
+            const _Float16* va = vc + ((size_t)ptab[pac / ps] * a.Hkv + kvh) * HD * ps + pac % ps;
+            const _Float16* vb = vc + ((size_t)ptab[pbc / ps] * a.Hkv + kvh) * HD * ps + pbc % ps;
+            const bool edge = pw + 32 * b + 32 > ctx;  // wave-uniform
+#pragma unroll
+            for (int d = 0; d < DT; d++) {
+                const int dim = 16 * d + l16;
+                uint2 ra = *(const uint2*)(va + (size_t)dim * ps);
+                uint2 rb = *(const uint2*)(vb + (size_t)dim * ps);
+                if (edge) {
+                    ra = mask_run(ra, pa, ctx);
+                    rb = mask_run(rb, pb, ctx);
+                }
+                const uint4 r4 = make_uint4(ra.x, ra.y, rb.x, rb.y);
+                const f16x8 vf = __builtin_bit_cast(f16x8, r4);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vf, o[d], 0, 0, 0);
+                o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, o[d], 0, 0, 0);
+            }
+        }
+    }
+
+    // ---- combine the 4 waves: o[d][r] = O[head 4seg+r][dim 16d+l16]
+#pragma unroll
+    for (int d = 0; d < DT; d++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int h = 4 * seg + r;
+            if (h < G) s_o[wave][h][16 * d + l16] = o[d][r];
+        }
+    __syncthreads();
+    const size_t hbase = (size_t)s * a.H + kvh * G;
+    if (nchunks == 1) {
+        for (int i = tid; i < G * HD; i += ACH) {
+            const int h = i / HD, dd = i % HD;
+            const float O = (s_o[0][h][dd] + s_o[1][h][dd]) + (s_o[2][h][dd] + s_o[3][h][dd]);
+            const float L = (s_l[0][h] + s_l[1][h]) + (s_l[2][h] + s_l[3][h]);
+            a.out[(hbase + h) * HD + dd] = O / L;
+        }
+        return;
+    }
+    // ---- multi-chunk: publish (max, sum, unnormalised output) for attn_merge_kernel
+    const size_t ibase = (size_t)item * a.H + kvh * G;
+    for (int i = tid; i < G * HD; i += ACH) {
+        const int h = i / HD, dd = i % HD;
+        a.part_o[(ibase + h) * HD + dd] = (s_o[0][h][dd] + s_o[1][h][dd]) + (s_o[2][h][dd] + s_o[3][h][dd]);
+    }
+    if (tid < G) {
+        a.part_ml[(ibase + tid) * 2 + 0] = fmaxf(fmaxf(s_m[0][tid], s_m[1][tid]), fmaxf(s_m[2][tid], s_m[3][tid]));
+        a.part_ml[(ibase + tid) * 2 + 1] = (s_l[0][tid] + s_l[1][tid]) + (s_l[2][tid] + s_l[3][tid]);
+    }
+}
+
+// Sequences of several chunks: one workgroup per (sequence, KV head) merges
+// the chunk partials in chunk order (a separate launch: no device-scope
+// fence or atomic, which on a multi-XCD part would write back and invalidate
+// L2 for every workgroup).
+__global__ __launch_bounds__(ACH) void attn_merge_kernel(AttnArgs a, int G, int HD) {
+    const int s = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
+    const int nchunks = (min(a.ctx[s], a.max_ctx) + ACH - 1) / ACH;
+    if (nchunks <= 1) return;
+    // base item: sum of the chunk counts of the sequences before s
+    __shared__ int s_sum[ACH / 64];
+    int part = 0;
+    for (int i = tid; i < s; i += ACH) part += (min(a.ctx[i], a.max_ctx) + ACH - 1) / ACH;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
+    if ((tid & 63) == 0) s_sum[tid >> 6] = part;
+    __syncthreads();
+    const int base = (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]);
+    for (int i = tid; i < G * HD; i += ACH) {
+        const int h = i / HD, dd = i % HD;
+        const size_t hidx = (size_t)kvh * G + h;
         float M = -INFINITY;
         for (int c = 0; c < nchunks; c++) M = fmaxf(M, a.part_ml[((size_t)(base + c) * a.H + hidx) * 2]);
         float L = 0.f, O = 0.f;
@@ -246,11 +486,10 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
             const size_t it = (size_t)(base + c) * a.H + hidx;
             const float w = __expf(a.part_ml[it * 2] - M);
             L = __builtin_fmaf(a.part_ml[it * 2 + 1], w, L);
-            O = __builtin_fmaf(a.part_o[it * HD + oi % HD], w, O);
+            O = __builtin_fmaf(a.part_o[it * HD + dd], w, O);
         }
-        a.out[((size_t)s * a.H + hidx) * HD + oi % HD] = O / L;
+        a.out[((size_t)s * a.H + hidx) * HD + dd] = O / L;
     }
-    if (tid == 0) a.counters[(size_t)s * a.Hkv + kvh] = 0u;  // ready for the next launch
 }
 
 template <typename KT>
@@ -269,6 +508,12 @@ static int launch_attn_t(const AttnArgs& a, int hd, int G, int grid_x, hipStream
 #undef QH_ATTN
     return set_error(QRAF_HIP_ERR_INVALID, "attention: unsupported head_dim %d / group %d", hd, G);
 }
+
+#define QH_TRY_ATTN(expr)                   \
+    do {                                    \
+        int rc_ = (expr);                   \
+        if (rc_ != QRAF_HIP_OK) return rc_; \
+    } while (0)
 
 size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx) {
     const size_t items = (size_t)n * ((max_ctx + ACH - 1) / ACH);
@@ -295,7 +540,7 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     a.ctx = ctx;
     a.out = out;
     uint8_t* w = (uint8_t*)ws;
-    a.counters = (uint32_t*)w;  // zeroed by the caller once; kernels leave them zero
+    a.counters = (uint32_t*)w;  // reserved
     w += ((size_t)n * Hkv * 4 + 255) / 256 * 256;
     a.part_ml = (float*)w;
     w += (size_t)items * H * 2 * 4;
@@ -308,8 +553,23 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     a.max_ctx = max_ctx;
     a.scale = scale;
     const int G = H / Hkv;
-    if (kv_dtype == DT_F32) return launch_attn_t<float>(a, hd, G, items, st);
-    return launch_attn_t<_Float16>(a, hd, G, items, st);
+    if (kv_dtype == DT_F32) {
+        QH_TRY_ATTN(launch_attn_t<float>(a, hd, G, items, st));
+    } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0) {
+        const dim3 grid(items, Hkv);
+        if (hd == 128)
+            hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(ACH), 0, st, a, G);
+        else
+            hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(ACH), 0, st, a, G);
+        QH_CHECK_HIP(hipGetLastError());
+    } else {
+        QH_TRY_ATTN(launch_attn_t<_Float16>(a, hd, G, items, st));
+    }
+    if (max_ctx > ACH) {  // some sequence may span several chunks
+        hipLaunchKernelGGL(attn_merge_kernel, dim3(n, Hkv), dim3(ACH), 0, st, a, G, hd);
+        QH_CHECK_HIP(hipGetLastError());
+    }
+    return QRAF_HIP_OK;
 }
 
 // ----------------------------------------------------------------------------
@@ -357,7 +617,10 @@ __global__ void rope_append_kernel(const float* __restrict__ qkv, const float* _
             float v = src[qd + kvd + j];
             if (bias) v = __fadd_rn(v, bias[qd + kvd + j]);
             const int vh = j / hd;
-            vc[(((size_t)page * Hkv + vh) * page_size + off) * hd + j % hd] = (KT)v;
+            if (sizeof(KT) == 4)
+                vc[(((size_t)page * Hkv + vh) * page_size + off) * hd + j % hd] = (KT)v;
+            else  // fp16 pages keep V dimension-major
+                vc[(((size_t)page * Hkv + vh) * hd + j % hd) * page_size + off] = (KT)v;
         }
     }
 }

@@ -4,6 +4,9 @@ step against the oracle (attention.cpp:100-150 restated in oracle.c).
 K/V live in randomly permuted physical pages; the oracle gathers each
 sequence's rows in position order (fp16 pages converted to f32 first, the
 same values the kernel reads) and runs the reference's per-head math.
+fp16 pages hold V dimension-major ([page][kv head][dim][position]); the
+tests keep the logical [page][kv head][position][dim] arrays and transpose
+V when they upload it.
 
 Tolerance (floating point, different summation order and chunked online
 softmax instead of one sequential pass): |gpu - oracle| <= 1e-5 + 1e-4 |oracle|.
@@ -18,7 +21,10 @@ from oracle import pyoracle as po
 pytestmark = pytest.mark.gpu
 
 
-def build_cache(rng, ctxs, Hkv, hd, page_size, kv_dtype, extra_pages=7):
+def build_cache(rng, ctxs, Hkv, hd, page_size, kv_dtype, extra_pages=7, poison=False):
+    """Logical [page][kv head][position][dim] K and V.  poison: positions at
+    or past each sequence's context in its last page hold NaN, which the
+    kernels must never let reach the output."""
     n = len(ctxs)
     max_ctx = max(ctxs)
     max_pages = (max_ctx + page_size - 1) // page_size
@@ -34,7 +40,17 @@ def build_cache(rng, ctxs, Hkv, hd, page_size, kv_dtype, extra_pages=7):
     np_dt = np.float16 if kv_dtype == po.F16 else np.float32
     K = rng.standard_normal((num_pages, Hkv, page_size, hd)).astype(np_dt)
     V = rng.standard_normal((num_pages, Hkv, page_size, hd)).astype(np_dt)
+    if poison:
+        for s, c in enumerate(ctxs):
+            if c % page_size:
+                last = table[s, (c - 1) // page_size]
+                K[last, :, c % page_size:, :] = np.nan
+                V[last, :, c % page_size:, :] = np.nan
     return table, K, V, max_pages
+
+
+def device_v(V, kv_dtype):
+    return np.ascontiguousarray(V.transpose(0, 1, 3, 2)) if kv_dtype == po.F16 else V
 
 
 def gather(table, cache, s, ctx, page_size):
@@ -50,7 +66,7 @@ def run_attention(hip, q, table, K, V, ctxs, H, Hkv, hd, page_size, kv_dtype, ma
     ws_bytes = hip.lib.qraf_hip_attention_workspace_bytes(n, H, Hkv, hd, max_ctx)
     ws = DeviceBuffer(ws_bytes)
     ws.zero()
-    dq, dK, dV = DeviceBuffer.from_array(q), DeviceBuffer.from_array(K), DeviceBuffer.from_array(V)
+    dq, dK, dV = DeviceBuffer.from_array(q), DeviceBuffer.from_array(K), DeviceBuffer.from_array(device_v(V, kv_dtype))
     dt, dc = DeviceBuffer.from_array(table), DeviceBuffer.from_array(np.array(ctxs, np.int32))
     out = DeviceBuffer(n * H * hd * 4)
     res = []
@@ -92,14 +108,28 @@ def test_attention_ragged_batch_config(hip, kv_dtype):
     check(got[0], oracle_attention(q, table, K, V, ctxs, H, Hkv, hd, ps))
 
 
-@pytest.mark.parametrize("H,Hkv,hd", [(9, 3, 64), (16, 16, 64), (4, 1, 128), (32, 4, 128), (12, 2, 64)])
+@pytest.mark.parametrize("H,Hkv,hd", [(9, 3, 64), (16, 16, 64), (4, 1, 128), (32, 4, 128), (12, 2, 64), (16, 1, 128),
+                                     (4, 1, 16), (8, 2, 32)])
 @pytest.mark.parametrize("kv_dtype", [po.F16, po.F32])
 def test_attention_edge_lengths(hip, H, Hkv, hd, kv_dtype):
+    # head_dim 16 and 32 take the VALU kernel for fp16 pages too
     rng = np.random.default_rng(H * 7 + hd)
     ctxs = [1, 2, 15, 16, 17, 255, 256, 257, 511, 512, 513, 1000, 3]
     ps = 16
-    table, K, V, _ = build_cache(rng, ctxs, Hkv, hd, ps, kv_dtype)
+    table, K, V, _ = build_cache(rng, ctxs, Hkv, hd, ps, kv_dtype, poison=True)
     q = (rng.standard_normal((len(ctxs), H * hd)) * 2).astype(np.float32)
+    got = run_attention(hip, q, table, K, V, ctxs, H, Hkv, hd, ps, kv_dtype, max(ctxs))
+    check(got[0], oracle_attention(q, table, K, V, ctxs, H, Hkv, hd, ps))
+
+
+@pytest.mark.parametrize("ps", [4, 8, 32, 64])
+@pytest.mark.parametrize("kv_dtype", [po.F16, po.F32])
+def test_attention_page_sizes(hip, ps, kv_dtype):
+    rng = np.random.default_rng(ps)
+    ctxs = [1, 5, 33, 64, 100, 257, 700]
+    H, Hkv, hd = 16, 2, 128
+    table, K, V, _ = build_cache(rng, ctxs, Hkv, hd, ps, kv_dtype, poison=True)
+    q = rng.standard_normal((len(ctxs), H * hd)).astype(np.float32)
     got = run_attention(hip, q, table, K, V, ctxs, H, Hkv, hd, ps, kv_dtype, max(ctxs))
     check(got[0], oracle_attention(q, table, K, V, ctxs, H, Hkv, hd, ps))
 
@@ -144,7 +174,9 @@ def test_rope_append_vs_oracle(hip, kv_dtype):
     call("qraf_hip_stream_synchronize", None)
     qo = dq.download(np.float32, n * H * hd).reshape(n, H * hd)
     Kc = dK.download(np_dt, num_pages * Hkv * ps * hd).reshape(num_pages, Hkv, ps, hd)
-    Vc = dV.download(np_dt, num_pages * Hkv * ps * hd).reshape(num_pages, Hkv, ps, hd)
+    Vc = dV.download(np_dt, num_pages * Hkv * ps * hd)
+    Vc = (Vc.reshape(num_pages, Hkv, hd, ps).transpose(0, 1, 3, 2) if kv_dtype == po.F16
+          else Vc.reshape(num_pages, Hkv, ps, hd))
     fp = po._fp
     for s in range(n):
         row = qkv[s] + bias  # attention.cpp:100-102 (dispatch_add)
