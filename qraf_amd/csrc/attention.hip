@@ -32,6 +32,8 @@
 // thread = position, output with thread = (head, dimension).
 #include <math.h>
 
+#include <algorithm>
+
 #include "common.h"
 
 namespace qraf_hip {
@@ -61,13 +63,21 @@ struct AttnArgs {
     const void* vc;            // layer V pages
     const int32_t* page_table; // [n][max_pages]
     const int32_t* ctx;        // [n] positions attended (pos + 1)
-    float* out;                // [n][H][HD]
+    float* out;                // [n][H][HD] f32, or (out_hi != null) the bf16 split planes below
+    uint16_t* out_hi;          // [n][H][HD] hi plane of qraf_hip_split_bf16_dev form
+    uint16_t* out_lo;          // [n][H][HD] lo plane
     float* part_o;             // [items][H][HD]   (multi-chunk partials)
     float* part_ml;            // [items][H][2]
     uint32_t* counters;        // [n][Hkv]          (reserved)
     int n, H, Hkv, page_size, max_pages, max_ctx;
     float scale;
 };
+
+// final output element: f32, or split into the bf16 planes a GEMM consumes
+__device__ __forceinline__ void attn_store(const AttnArgs& a, size_t i, float v) {
+    if (a.out_hi) split_bf16(v, &a.out_hi[i], &a.out_lo[i]);
+    else a.out[i] = v;
+}
 
 // Item -> (sequence, chunk): every workgroup computes the exclusive prefix
 // sum of ceil(ctx_s / ACH) over the batch in LDS (4 entries per thread, wave
@@ -228,7 +238,7 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
         for (int j = 0; j < HPT; j++) {
             const int oi = tid + ACH * j;
-            if (oi < NOUT) a.out[((size_t)s * a.H + kvh * G) * HD + oi] = o[j] / l[oi / HD];
+            if (oi < NOUT) attn_store(a, ((size_t)s * a.H + kvh * G) * HD + oi, o[j] / l[oi / HD]);
         }
         return;
     }
@@ -443,7 +453,7 @@ __global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
             const int h = i / HD, dd = i % HD;
             const float O = (s_o[0][h][dd] + s_o[1][h][dd]) + (s_o[2][h][dd] + s_o[3][h][dd]);
             const float L = (s_l[0][h] + s_l[1][h]) + (s_l[2][h] + s_l[3][h]);
-            a.out[(hbase + h) * HD + dd] = O / L;
+            attn_store(a, (hbase + h) * HD + dd, O / L);
         }
         return;
     }
@@ -488,7 +498,7 @@ __global__ __launch_bounds__(ACH) void attn_merge_kernel(AttnArgs a, int G, int 
             L = __builtin_fmaf(a.part_ml[it * 2 + 1], w, L);
             O = __builtin_fmaf(a.part_o[it * HD + dd], w, O);
         }
-        a.out[((size_t)s * a.H + hidx) * HD + dd] = O / L;
+        attn_store(a, ((size_t)s * a.H + hidx) * HD + dd, O / L);
     }
 }
 
@@ -522,8 +532,10 @@ size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx) {
 
 int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv_dtype, const int32_t* page_table,
                      int max_pages, const int32_t* ctx, int n, int H, int Hkv, int hd, int page_size, float scale,
-                     int max_ctx, float* out, void* ws, size_t ws_bytes, hipStream_t st) {
-    QH_REQUIRE(q && kc && vc && page_table && ctx && out && ws, QRAF_HIP_ERR_INVALID, "attention: null pointer");
+                     int max_ctx, float* out, void* ws, size_t ws_bytes, hipStream_t st, uint16_t* out_hi,
+                     uint16_t* out_lo) {
+    QH_REQUIRE(q && kc && vc && page_table && ctx && (out || (out_hi && out_lo)) && ws, QRAF_HIP_ERR_INVALID,
+               "attention: null pointer");
     QH_REQUIRE(n > 0 && n <= 1024, QRAF_HIP_ERR_INVALID, "attention: batch %d outside 1..1024", n);
     QH_REQUIRE(Hkv > 0 && H % Hkv == 0, QRAF_HIP_ERR_INVALID, "attention: %d heads not a multiple of %d kv heads", H, Hkv);
     QH_REQUIRE(page_size > 0 && max_pages > 0 && max_ctx > 0 && max_ctx <= max_pages * page_size, QRAF_HIP_ERR_INVALID,
@@ -539,6 +551,8 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     a.page_table = page_table;
     a.ctx = ctx;
     a.out = out;
+    a.out_hi = out_hi;
+    a.out_lo = out_lo;
     uint8_t* w = (uint8_t*)ws;
     a.counters = (uint32_t*)w;  // reserved
     w += ((size_t)n * Hkv * 4 + 255) / 256 * 256;
@@ -576,26 +590,33 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
 // Per-token post-processing of the fused QKV projection (attention.cpp:100-119):
 // bias add (F32 biases only, transformer.cpp:45-50), interleaved-pair RoPE on
 // every q and k head (ops.cpp:158-177), and the store of k, v at the token's
-// position into the paged cache.  One workgroup per sequence.
+// position into the paged cache.  Grid-stride over (sequence, work element):
+// a rotated pair of a q or k head, or one v element.  qkv may be S slices
+// (GEMM split-K partials) of `slice` floats, summed in slice order.
 // ----------------------------------------------------------------------------
 template <typename KT>
 __global__ void rope_append_kernel(const float* __restrict__ qkv, const float* __restrict__ bias, int H, int Hkv,
                                    int hd, const int32_t* __restrict__ pos, const float* __restrict__ rope,
                                    float* __restrict__ q_out, KT* __restrict__ kc, KT* __restrict__ vc,
-                                   const int32_t* __restrict__ page_table, int max_pages, int page_size) {
-    const int s = blockIdx.x;
+                                   const int32_t* __restrict__ page_table, int max_pages, int page_size, int n, int S,
+                                   size_t slice) {
     const int qd = H * hd, kvd = Hkv * hd, row = qd + 2 * kvd;
-    const float* src = qkv + (size_t)s * row;
+    const int per = (qd + kvd) / 2 + kvd;  // work elements per sequence
+    for (size_t w = (size_t)blockIdx.x * blockDim.x + threadIdx.x; w < (size_t)n * per;
+         w += (size_t)gridDim.x * blockDim.x) {
+    const int s = (int)(w / per), e = (int)(w % per);
+    const size_t rbase = (size_t)s * row;
+    auto ld = [&](int i) { return sum_slices(qkv, S, slice, rbase + i); };
     const int p = pos[s];
     const int page = page_table[(size_t)s * max_pages + p / page_size], off = p % page_size;
     const float* cs = rope + (size_t)p * hd;  // (cos, sin) of pair i/2 at [i], [i+1]
     // pairs (i, i+1) of q heads, then k heads: rotate; v: copy.  Products are
     // rounded separately (no FMA contraction), as the reference's scalar code.
-    for (int e = threadIdx.x; e < (qd + kvd) / 2 + kvd; e += blockDim.x) {
+    {
         if (e < (qd + kvd) / 2) {
             const int i0 = 2 * e;  // element index in [0, qd + kvd)
             const int i = i0 % hd;   // even index inside the head
-            float a = src[i0], b = src[i0 + 1];
+            float a = ld(i0), b = ld(i0 + 1);
             if (bias) {
                 a = __fadd_rn(a, bias[i0]);
                 b = __fadd_rn(b, bias[i0 + 1]);
@@ -614,7 +635,7 @@ __global__ void rope_append_kernel(const float* __restrict__ qkv, const float* _
             }
         } else {
             const int j = e - (qd + kvd) / 2;  // v element
-            float v = src[qd + kvd + j];
+            float v = ld(qd + kvd + j);
             if (bias) v = __fadd_rn(v, bias[qd + kvd + j]);
             const int vh = j / hd;
             if (sizeof(KT) == 4)
@@ -623,19 +644,22 @@ __global__ void rope_append_kernel(const float* __restrict__ qkv, const float* _
                 vc[(((size_t)page * Hkv + vh) * hd + j % hd) * page_size + off] = (KT)v;
         }
     }
+    }
 }
 
 int launch_rope_append(const float* qkv, const float* bias, int n, int H, int Hkv, int hd, const int32_t* pos,
                        const float* rope, float* q_out, void* kc, void* vc, uint32_t kv_dtype,
-                       const int32_t* page_table, int max_pages, int page_size, hipStream_t st) {
-    QH_REQUIRE(qkv && pos && rope && q_out && kc && vc && page_table && n > 0 && hd % 2 == 0, QRAF_HIP_ERR_INVALID,
-               "rope_append: bad arguments");
+                       const int32_t* page_table, int max_pages, int page_size, hipStream_t st, int S, size_t slice) {
+    QH_REQUIRE(qkv && pos && rope && q_out && kc && vc && page_table && n > 0 && hd % 2 == 0 && S >= 1,
+               QRAF_HIP_ERR_INVALID, "rope_append: bad arguments");
+    const size_t work = (size_t)n * ((H * hd + Hkv * hd) / 2 + Hkv * hd);
+    const int grid = (int)std::min<size_t>((work + 255) / 256, 4096);
     if (kv_dtype == DT_F32)
-        hipLaunchKernelGGL(rope_append_kernel<float>, dim3(n), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos, rope,
-                           q_out, (float*)kc, (float*)vc, page_table, max_pages, page_size);
+        hipLaunchKernelGGL(rope_append_kernel<float>, dim3(grid), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos, rope,
+                           q_out, (float*)kc, (float*)vc, page_table, max_pages, page_size, n, S, slice);
     else if (kv_dtype == DT_F16)
-        hipLaunchKernelGGL(rope_append_kernel<_Float16>, dim3(n), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos, rope,
-                           q_out, (_Float16*)kc, (_Float16*)vc, page_table, max_pages, page_size);
+        hipLaunchKernelGGL(rope_append_kernel<_Float16>, dim3(grid), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos,
+                           rope, q_out, (_Float16*)kc, (_Float16*)vc, page_table, max_pages, page_size, n, S, slice);
     else
         return set_error(QRAF_HIP_ERR_DTYPE, "rope_append: KV dtype %u", kv_dtype);
     QH_CHECK_HIP(hipGetLastError());

@@ -55,21 +55,55 @@ int launch_dot(const float* a, const float* b, int n, float* out, hipStream_t s)
 // op: 0 silu, 1 add, 2 mul, 3 scale
 int launch_ew(int op, float* x, const float* y, float sc, int n, hipStream_t s);
 
-int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s);
+// x = hi + lo + r, |r| <= 2^-17 |x|: round-to-nearest-even bf16 of x, then of the rest
+__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
+    const uint32_t b = __builtin_bit_cast(uint32_t, f);
+    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ void split_bf16(float v, uint16_t* hi, uint16_t* lo) {
+    const uint32_t h = f32_to_bf16_rne(v);
+    *hi = (uint16_t)h;
+    *lo = (uint16_t)f32_to_bf16_rne(v - __builtin_bit_cast(float, h << 16));
+}
+
+// element e of S slices (GEMM split-K partials) of `slice` floats, summed in
+// slice order; loads go out 8 slices at a time
+__device__ __forceinline__ float sum_slices(const float* __restrict__ p, int S, size_t slice, size_t e) {
+    float acc = p[e];
+    int k = 1;
+    for (; k + 8 <= S; k += 8) {
+        float t[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) t[u] = p[(size_t)(k + u) * slice + e];
+#pragma unroll
+        for (int u = 0; u < 8; u++) acc += t[u];
+    }
+    for (; k < S; k++) acc += p[(size_t)k * slice + e];
+    return acc;
+}
+
+// x may be S slices of `slice` floats each (GEMM partials), summed in slice order
+int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s,
+                      int S = 1, size_t slice = 0);
 // split-K partial tiles go to ws when it is large enough (qgemm_workspace_bytes), else one split
 int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
-                 float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled = false);
+                 float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled = false,
+                 int* slices = nullptr);
 size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M);
+// bytes of the [S][M][N] partial slices launch_qgemm(..., slices) writes
+size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M);
 // tile-major copy of a Q8_0/Q4_0 matrix for launch_qgemm(..., tiled = true)
 size_t tiled_weight_bytes(uint32_t dtype, int N, int K);
 int launch_repack_tiles(const void* W, uint32_t dtype, int N, int K, void* dst, hipStream_t s);
 size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx);
 int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv_dtype, const int32_t* page_table,
                      int max_pages, const int32_t* ctx, int n, int H, int Hkv, int hd, int page_size, float scale,
-                     int max_ctx, float* out, void* ws, size_t ws_bytes, hipStream_t st);
+                     int max_ctx, float* out, void* ws, size_t ws_bytes, hipStream_t st, uint16_t* out_hi = nullptr,
+                     uint16_t* out_lo = nullptr);
 int launch_rope_append(const float* qkv, const float* bias, int n, int H, int Hkv, int hd, const int32_t* pos,
                        const float* rope, float* q_out, void* kc, void* vc, uint32_t kv_dtype,
-                       const int32_t* page_table, int max_pages, int page_size, hipStream_t st);
+                       const int32_t* page_table, int max_pages, int page_size, hipStream_t st, int S = 1,
+                       size_t slice = 0);
 int launch_gen_weights(void* dst, uint32_t dtype, uint64_t count, uint64_t seed, uint64_t stream_id, float stddev,
                        hipStream_t s);
 int launch_quantize(const float* src, uint64_t count, uint32_t dtype, void* dst, hipStream_t s);

@@ -81,6 +81,68 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restri
     for (int i = threadIdx.x; i < D; i += 256) out[(size_t)s * D + i] = __fmul_rn(__fmul_rn(xr[i], r), w[i]);
 }
 
+// Residual add of a projection's split-K partials, then the next RMSNorm into
+// the bf16 planes the following GEMM reads (one 1024-thread workgroup per
+// row, J elements per thread):
+//     h += (part[0] + ... + part[S-1])        (transformer.cpp:593 / :601)
+//     xh + xl = rms_norm(h) * w               (ops.cpp:107-118)
+// S = 0: no residual (h as is); w = null: residual only.
+template <int J>
+__global__ __launch_bounds__(1024) void residual_norm_split_kernel(const float* __restrict__ part, int S, size_t slice,
+                                                                  float* __restrict__ h, const float* __restrict__ w,
+                                                                  int D, float eps, uint16_t* __restrict__ xh,
+                                                                  uint16_t* __restrict__ xl) {
+    __shared__ float red[16];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    float* hr = h + (size_t)m * D;
+    float v[J];
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int i = tid + 1024 * j;
+        v[j] = 0.f;
+        if (i < D) {
+            v[j] = hr[i];
+            if (S > 0) {
+                v[j] = sum_slices(part, S, slice, (size_t)m * D + i) + v[j];
+                hr[i] = v[j];
+            }
+        }
+        ss = __builtin_fmaf(v[j], v[j], ss);
+    }
+    if (!w) return;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) ss += red[k];
+    const float r = 1.0f / sqrtf(ss / (float)D + eps);
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+        const int i = tid + 1024 * j;
+        if (i < D) {
+            const size_t e = (size_t)m * D + i;
+            split_bf16(__fmul_rn(__fmul_rn(v[j], r), w[i]), &xh[e], &xl[e]);
+        }
+    }
+}
+
+static int launch_residual_norm_split(const float* part, int S, size_t slice, float* h, const float* w, int D, float eps,
+                                      uint16_t* xh, uint16_t* xl, int rows, hipStream_t s) {
+    QH_REQUIRE(D <= 8192, QRAF_HIP_ERR_INVALID, "residual/norm: hidden size %d > 8192", D);
+#define QH_RNS(Jv) hipLaunchKernelGGL(residual_norm_split_kernel<Jv>, dim3(rows), dim3(1024), 0, s, part, S, slice, h, w, \
+                                      D, eps, xh, xl)
+    if (D <= 1024) QH_RNS(1);
+    else if (D <= 2048) QH_RNS(2);
+    else if (D <= 4096) QH_RNS(4);
+    else QH_RNS(8);
+#undef QH_RNS
+    QH_CHECK_HIP(hipGetLastError());
+    return QRAF_HIP_OK;
+}
+
 // silu_inplace then mul_inplace (attention.cpp:177-178) on interleaved gate/up rows
 __global__ void silu_gate_kernel(const float* __restrict__ gu, int F, int n, float* __restrict__ act) {
     const size_t total = (size_t)n * F;
@@ -204,6 +266,9 @@ struct qraf_engine {
     size_t attn_ws_bytes = 0;
     void* gemm_ws = nullptr;  // split-K partial tiles of the batched projections
     size_t gemm_ws_bytes = 0;
+    void* part_ws = nullptr;  // [S][rows][N] partials the fused batched layer sums downstream
+    size_t part_ws_bytes = 0;
+    bool fused = false;  // every layer has tile-major copies: batched steps run the fused pipeline
     size_t in_words = 0;
 };
 
@@ -340,6 +405,14 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
                     e->gemm_ws_bytes = std::max(e->gemm_ws_bytes, qgemm_workspace_bytes(dt, sh[0], sh[1], m));
     }
     if (e->gemm_ws_bytes) A(e->gemm_ws, e->gemm_ws_bytes);
+    {
+        const int shapes[4][2] = {{e->qkvd, D}, {D, e->qd}, {2 * F, D}, {D, F}};
+        for (uint32_t dt : {DT_Q8_0, DT_Q4_0})
+            for (auto& sh : shapes)
+                for (int m = 2; m <= B; m++)
+                    e->part_ws_bytes = std::max(e->part_ws_bytes, qgemm_partials_bytes(dt, sh[0], sh[1], m));
+    }
+    if (e->part_ws_bytes) A(e->part_ws, e->part_ws_bytes);
 #undef A
     if (hipMemset(e->attn_ws, 0, e->attn_ws_bytes) != hipSuccess ||
         hipHostMalloc((void**)&e->h_in, e->in_words * 4, hipHostMallocDefault) != hipSuccess ||
@@ -594,6 +667,8 @@ int qraf_engine_finalize(qraf_engine* e) {
         }
         QH_TRY(tile(e->head ? e->head : e->embed, e->head ? e->dt_head : e->dt_embed, (int)c.vocab_size, D, &e->head_t));
         QH_CHECK_HIP(hipStreamSynchronize(e->stream));
+        e->fused = e->part_ws != nullptr;
+        for (auto& L : e->layers) e->fused = e->fused && L.wqkv_t && L.wo_t && L.wgu_t && L.wd_t;
     }
     e->finalized = true;
     return QRAF_HIP_OK;
@@ -729,7 +804,37 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
 
     hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, 32, D, d_tok, e->h);
     QH_CHECK_HIP(hipGetLastError());
-    for (uint32_t l = 0; l < c.num_layers; l++) {
+    if (n > 1 && e->fused) {
+        // Batched layer on the matrix cores, 9 launches: each projection writes
+        // split-K partials that the next kernel sums (with the bias, residual,
+        // norm or SiLU-gate it applies anyway), and every kernel that feeds a
+        // projection writes its input as the bf16 hi/lo planes directly.
+        QH_TRY(launch_residual_norm_split(nullptr, 0, 0, e->h, e->layers[0].an, D, c.rms_norm_eps, e->xh, e->xl, n, s));
+        for (uint32_t l = 0; l < c.num_layers; l++) {
+            qraf_engine::Layer& L = e->layers[l];
+            uint8_t* kc = e->kpool + (size_t)l * e->layer_kv_bytes;
+            uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;
+            float* P = (float*)e->part_ws;
+            int S = 0;
+            QH_TRY(launch_qgemm(L.wqkv_t, L.dt_attn, 32, e->qkvd, D, e->xh, e->xl, n, e->qkv, nullptr, P,
+                                e->part_ws_bytes, s, true, &S));
+            QH_TRY(launch_rope_append(P, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
+                                      e->o.kv_dtype, d_ptab, MP, ps, s, S, (size_t)n * e->qkvd));
+            QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale,
+                                    e->capacity, nullptr, e->attn_ws, e->attn_ws_bytes, s, e->xh, e->xl));
+            QH_TRY(launch_qgemm(L.wo_t, L.dt_attn, 32, D, e->qd, e->xh, e->xl, n, e->qkv, nullptr, P, e->part_ws_bytes,
+                                s, true, &S));
+            QH_TRY(launch_residual_norm_split(P, S, (size_t)n * D, e->h, L.fn, D, c.rms_norm_eps, e->xh, e->xl, n, s));
+            QH_TRY(launch_qgemm(L.wgu_t, L.dt_mlp, 32, 2 * F, D, e->xh, e->xl, n, e->qkv, nullptr, P,
+                                e->part_ws_bytes, s, true, &S));
+            QH_TRY(launch_split_bf16(P, e->xh, e->xl, n, F, 1, nullptr, s, S, (size_t)n * 2 * F));
+            QH_TRY(launch_qgemm(L.wd_t, L.dt_mlp, 32, D, F, e->xh, e->xl, n, e->qkv, nullptr, P, e->part_ws_bytes, s,
+                                true, &S));
+            const float* wn = l + 1 < c.num_layers ? e->layers[l + 1].an : nullptr;  // last layer: residual only
+            QH_TRY(launch_residual_norm_split(P, S, (size_t)n * D, e->h, wn, D, c.rms_norm_eps, e->xh, e->xl, n, s));
+        }
+    }
+    for (uint32_t l = 0; l < c.num_layers && !(n > 1 && e->fused); l++) {
         qraf_engine::Layer& L = e->layers[l];
         uint8_t* kc = e->kpool + (size_t)l * e->layer_kv_bytes;
         uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;

@@ -43,31 +43,25 @@ typedef uint32_t u32a2 __attribute__((aligned(2)));
 
 constexpr int QG_MCHUNK = 128;         // batch rows per workgroup at most
 
-__device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
-    uint32_t b = __builtin_bit_cast(uint32_t, f);
-    return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
-}
-
 // X fp32 [M][K] -> hi, lo bf16 planes [M][K] (hi = rne(x), lo = rne(x - hi)).
 // op 0: x as given; op 1: x = silu(g) * u from an interleaved gate/up row
 // [M][2K] (g = even columns, u = odd columns), ops.cpp:218-222 then :275-279.
+// x may be S slices (GEMM split-K partials) of `slice` floats, summed in order.
 __global__ void split_bf16_kernel(const float* __restrict__ x, uint16_t* __restrict__ hi, uint16_t* __restrict__ lo,
-                                  int M, int K, int op, float* __restrict__ xout) {
+                                  int M, int K, int op, float* __restrict__ xout, int S, size_t slice) {
     const size_t n = (size_t)M * K;
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) {
         float v;
         if (op == 1) {
             const size_t m = i / K, k = i % K;
-            const float g = x[m * 2 * K + 2 * k], u = x[m * 2 * K + 2 * k + 1];
+            const size_t e = m * 2 * K + 2 * k;
+            const float g = sum_slices(x, S, slice, e), u = sum_slices(x, S, slice, e + 1);
             v = __fmul_rn(g / (1.0f + expf(-g)), u);
             if (xout) xout[i] = v;
         } else {
-            v = x[i];
+            v = sum_slices(x, S, slice, i);
         }
-        const uint32_t h = f32_to_bf16_rne(v);
-        const float r = v - __builtin_bit_cast(float, h << 16);
-        hi[i] = (uint16_t)h;
-        lo[i] = (uint16_t)f32_to_bf16_rne(r);
+        split_bf16(v, &hi[i], &lo[i]);
     }
 }
 
@@ -456,11 +450,17 @@ size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M) {
     return qgemm_plan(N, K, M, q_row_bytes(dtype, 32, K)).ws_bytes;
 }
 
-int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s) {
-    QH_REQUIRE(x && hi && lo && M > 0 && K > 0, QRAF_HIP_ERR_INVALID, "split: bad arguments");
+size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M) {
+    if ((dtype != DT_Q8_0 && dtype != DT_Q4_0) || N <= 0 || K <= 0 || K % 32 || M <= 0) return 0;
+    return (size_t)qgemm_plan(N, K, M, q_row_bytes(dtype, 32, K)).S * M * N * 4;
+}
+
+int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s,
+                      int S, size_t slice) {
+    QH_REQUIRE(x && hi && lo && M > 0 && K > 0 && S >= 1, QRAF_HIP_ERR_INVALID, "split: bad arguments");
     const size_t n = (size_t)M * K;
     const int grid = (int)min((n + 255) / 256, (size_t)4096);
-    hipLaunchKernelGGL(split_bf16_kernel, dim3(grid), dim3(256), 0, s, x, hi, lo, M, K, op, xout);
+    hipLaunchKernelGGL(split_bf16_kernel, dim3(grid), dim3(256), 0, s, x, hi, lo, M, K, op, xout, S, slice);
     QH_CHECK_HIP(hipGetLastError());
     return QRAF_HIP_OK;
 }
@@ -488,7 +488,7 @@ int launch_repack_tiles(const void* W, uint32_t dtype, int N, int K, void* dst, 
 }
 
 int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
-                 float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled) {
+                 float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled, int* slices) {
     QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "qgemm: unsupported dtype %u", dtype);
     QH_REQUIRE(bs == 32, QRAF_HIP_ERR_DTYPE, "qgemm: block size %d (32 required)", bs);
     QH_REQUIRE(K % 32 == 0 && K > 0 && N > 0, QRAF_HIP_ERR_INVALID, "qgemm: K=%d must be a positive multiple of 32", K);
@@ -503,7 +503,13 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
     const int nb = K / 32;
     QgPlan p = qgemm_plan(N, K, M, rb);
     float* part = nullptr;
-    if (p.S > 1) {
+    if (slices) {  // partials mode: S slices [S][M][N] in ws, summed by the caller's next kernel
+        QH_REQUIRE(ws && ws_bytes >= (size_t)p.S * M * N * 4 && (((uintptr_t)ws) & 15) == 0 && !add,
+                   QRAF_HIP_ERR_INVALID, "qgemm: partials need a workspace of %zu bytes and no residual",
+                   (size_t)p.S * M * N * 4);
+        part = (float*)ws;
+        *slices = p.S;
+    } else if (p.S > 1) {
         if (ws && ws_bytes >= p.ws_bytes && (((uintptr_t)ws) & 15) == 0) {
             part = (float*)ws;
         } else {  // no (or too small a) workspace: one split
@@ -542,7 +548,7 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
 #undef QH_GW
 #undef QH_G
     QH_CHECK_HIP(hipGetLastError());
-    if (part) {
+    if (part && !slices) {
         const size_t MN = (size_t)M * N;
         const int rgrid = (int)min((MN / 4 + 255) / 256 + 1, (size_t)2048);
         hipLaunchKernelGGL(qgemm_reduce_kernel, dim3(rgrid), dim3(256), 0, s, part, p.S, MN, Y, add);
