@@ -178,11 +178,12 @@ int qraf_hip_rope_append_dev(const float* qkv, const float* bias, int32_t n_seqs
  * qraf_hip_qgemm_dev.  rows x cols elements, row-major. */
 int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int32_t rows, int32_t cols,
                             void* stream);
-/* Tuning of qraf_hip_qgemm_dev for batches over 32 rows: waves 4 or 8 per
- * workgroup (128 or 256 weight rows), splits > 0 forces the split count;
- * 0 restores the automatic choice.  Affects qraf_hip_qgemm_workspace_bytes
- * too.  No counterpart in the reference (a performance knob). */
-int qraf_hip_set_qgemm_tuning(int waves, int splits);
+/* Tuning of the batched GEMM for batches over 32 rows: waves 4 or 8 per
+ * workgroup (128 or 256 weight rows), splits > 0 forces the split count,
+ * pipe 1 / -1 forces the pipelined tiled kernel on / off; 0 restores the
+ * automatic choice.  Affects the workspace queries too.  No counterpart in
+ * the reference (a performance knob). */
+int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe);
 /* Workspace (bytes) that lets qraf_hip_qgemm_dev split the in_dim range of an
  * out_dim x in_dim product at this batch across workgroups; 0 when it does
  * not split. */
@@ -208,8 +209,10 @@ int qraf_hip_qgemm_dev(const void* w, uint32_t dtype, uint32_t block_size, uint3
 uint64_t qraf_hip_tiled_weight_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim);
 int qraf_hip_repack_tiles_dev(const void* w, uint32_t dtype, uint32_t out_dim, uint32_t in_dim, void* dst,
                               void* stream);
-/* qraf_hip_qgemm_dev on a tile-major weight copy (16-byte aligned); results
- * are bit-identical to qraf_hip_qgemm_dev on the source matrix. */
+/* qraf_hip_qgemm_dev on a tile-major weight copy (16-byte aligned), with its
+ * own split-K workspace size (batches over 32 rows run a pipelined kernel
+ * with 256-row weight tiles). */
+uint64_t qraf_hip_qgemm_tiled_workspace_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim, int32_t batch);
 int qraf_hip_qgemm_tiled_dev(const void* w_tiled, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
                              const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, float* y, const float* add,
                              void* workspace, uint64_t workspace_bytes, void* stream);

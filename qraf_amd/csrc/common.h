@@ -89,9 +89,9 @@ int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, 
 int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
                  float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled = false,
                  int* slices = nullptr);
-size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M);
+size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M, bool tiled = false);
 // bytes of the [S][M][N] partial slices launch_qgemm(..., slices) writes
-size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M);
+size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M, bool tiled = false);
 // tile-major copy of a Q8_0/Q4_0 matrix for launch_qgemm(..., tiled = true)
 size_t tiled_weight_bytes(uint32_t dtype, int N, int K);
 int launch_repack_tiles(const void* W, uint32_t dtype, int N, int K, void* dst, hipStream_t s);

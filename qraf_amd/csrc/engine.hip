@@ -20,6 +20,7 @@
 // SiLU-gate -> down projection with the residual add; final RMSNorm, LM head
 // for the rows that want logits, argmax on the device.  Batch 1 runs on the
 // streaming matvec, larger batches on the matrix-core GEMM.
+#include <limits.h>
 #include <math.h>
 #include <string.h>
 
@@ -194,6 +195,83 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restric
     }
 }
 
+// Two-pass Sampler::argmax for long rows: 32 chunks per row, each scanned by
+// one workgroup with 8 loads in flight per thread (ascending index per thread,
+// so strict '>' keeps the lowest index), then a per-row pass over the chunk
+// winners in chunk order.  Ties across threads/chunks go to the lower index.
+constexpr int ARGMAX_CHUNKS = 32;
+
+__device__ __forceinline__ void argmax_take(float& best, int& bi, float v, int i) {
+    if (v > best || (v == best && i < bi)) {
+        best = v;
+        bi = i;
+    }
+}
+
+__device__ __forceinline__ void argmax_block(float& best, int& bi) {
+    __shared__ float sv[4];
+    __shared__ int si[4];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) argmax_take(best, bi, __shfl_xor(best, o), __shfl_xor(bi, o));
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = best;
+        si[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0)
+        for (int w = 1; w < 4; w++) argmax_take(best, bi, sv[w], si[w]);
+}
+
+__global__ __launch_bounds__(256) void argmax_chunk_kernel(const float* __restrict__ logits, int V,
+                                                          float* __restrict__ pv, int* __restrict__ pi) {
+    const int row = blockIdx.y, c = blockIdx.x;
+    const int len = (V + ARGMAX_CHUNKS - 1) / ARGMAX_CHUNKS;
+    const int c0 = c * len, c1 = min(V, c0 + len);
+    const float* l = logits + (size_t)row * V;
+    float best = -INFINITY;
+    int bi = INT_MAX;
+    for (int base = c0 + (int)threadIdx.x; base < c1; base += 256 * 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = base + 256 * u;
+            v[u] = i < c1 ? l[i] : -INFINITY;
+        }
+#pragma unroll
+        for (int u = 0; u < 8; u++) {
+            const int i = base + 256 * u;
+            if (i < c1 && (bi == INT_MAX || v[u] > best)) {
+                best = v[u];
+                bi = i;
+            }
+        }
+    }
+    argmax_block(best, bi);
+    if (threadIdx.x == 0) {
+        pv[row * ARGMAX_CHUNKS + c] = best;
+        pi[row * ARGMAX_CHUNKS + c] = bi;
+    }
+}
+
+__global__ void argmax_final_kernel(const float* __restrict__ pv, const int* __restrict__ pi, int V,
+                                    uint32_t* __restrict__ out) {
+    const int row = blockIdx.x;
+    if (threadIdx.x != 0) return;
+    float best = -INFINITY;
+    int bi = INT_MAX;
+    for (int c = 0; c < ARGMAX_CHUNKS; c++) {
+        const int i = pi[row * ARGMAX_CHUNKS + c];
+        if (i == INT_MAX) continue;  // empty chunk
+        if (bi == INT_MAX) {
+            best = pv[row * ARGMAX_CHUNKS + c];
+            bi = i;
+        } else {
+            argmax_take(best, bi, pv[row * ARGMAX_CHUNKS + c], i);
+        }
+    }
+    out[row] = (uint32_t)(bi == INT_MAX || bi >= V ? 0 : bi);
+}
+
 __global__ void fill_kernel(float* p, float v, size_t n) {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x) p[i] = v;
 }
@@ -266,6 +344,8 @@ struct qraf_engine {
     size_t attn_ws_bytes = 0;
     void* gemm_ws = nullptr;  // split-K partial tiles of the batched projections
     size_t gemm_ws_bytes = 0;
+    float* am_val = nullptr;  // argmax chunk winners [max_batch][32]
+    int* am_idx = nullptr;
     void* part_ws = nullptr;  // [S][rows][N] partials the fused batched layer sums downstream
     size_t part_ws_bytes = 0;
     bool fused = false;  // every layer has tile-major copies: batched steps run the fused pipeline
@@ -392,6 +472,8 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     A(e->xh, (size_t)B * kmax * 2 + 64);
     A(e->xl, (size_t)B * kmax * 2 + 64);
     A(e->amax, (size_t)B * 4);
+    A(e->am_val, (size_t)B * ARGMAX_CHUNKS * 4);
+    A(e->am_idx, (size_t)B * ARGMAX_CHUNKS * 4);
     e->in_words = (size_t)B * (4 + e->max_pages);
     A(e->d_in, e->in_words * 4);
     e->attn_ws_bytes = attn_workspace_bytes(B, (int)c.num_heads, (int)kvh, hd, e->capacity);
@@ -402,7 +484,8 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
         for (uint32_t dt : {DT_Q8_0, DT_Q4_0})
             for (auto& sh : shapes)
                 for (int m = 2; m <= B; m++)
-                    e->gemm_ws_bytes = std::max(e->gemm_ws_bytes, qgemm_workspace_bytes(dt, sh[0], sh[1], m));
+                    e->gemm_ws_bytes = std::max({e->gemm_ws_bytes, qgemm_workspace_bytes(dt, sh[0], sh[1], m),
+                                                  qgemm_workspace_bytes(dt, sh[0], sh[1], m, true)});
     }
     if (e->gemm_ws_bytes) A(e->gemm_ws, e->gemm_ws_bytes);
     {
@@ -410,7 +493,7 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
         for (uint32_t dt : {DT_Q8_0, DT_Q4_0})
             for (auto& sh : shapes)
                 for (int m = 2; m <= B; m++)
-                    e->part_ws_bytes = std::max(e->part_ws_bytes, qgemm_partials_bytes(dt, sh[0], sh[1], m));
+                    e->part_ws_bytes = std::max(e->part_ws_bytes, qgemm_partials_bytes(dt, sh[0], sh[1], m, true));
     }
     if (e->part_ws_bytes) A(e->part_ws, e->part_ws_bytes);
 #undef A
@@ -756,6 +839,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
     int32_t* ctx = pos + n;
     int32_t* lrows = ctx + n;
     int32_t* ptab = lrows + n;
+    int step_ctx = 1;  // longest context of this step: sizes the attention grid (and skips the merge)
     for (int i = 0; i < n; i++) {
         qraf_engine::Seq& sq = e->seqs[seq_ids[i]];
         while ((int)sq.pages.size() < positions[i] / ps + 1) {
@@ -766,6 +850,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         tok[i] = (int32_t)tokens[i];
         pos[i] = positions[i];
         ctx[i] = positions[i] + 1;
+        step_ctx = std::max(step_ctx, ctx[i]);
         if (!want_logits || want_logits[i]) lrows[n_logit_rows++] = i;
         for (int j = 0; j < MP; j++) ptab[(size_t)i * MP + j] = j < (int)sq.pages.size() ? sq.pages[j] : 0;
     }
@@ -821,7 +906,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
             QH_TRY(launch_rope_append(P, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
                                       e->o.kv_dtype, d_ptab, MP, ps, s, S, (size_t)n * e->qkvd));
             QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale,
-                                    e->capacity, nullptr, e->attn_ws, e->attn_ws_bytes, s, e->xh, e->xl));
+                                    step_ctx, nullptr, e->attn_ws, e->attn_ws_bytes, s, e->xh, e->xl));
             QH_TRY(launch_qgemm(L.wo_t, L.dt_attn, 32, D, e->qd, e->xh, e->xl, n, e->qkv, nullptr, P, e->part_ws_bytes,
                                 s, true, &S));
             QH_TRY(launch_residual_norm_split(P, S, (size_t)n * D, e->h, L.fn, D, c.rms_norm_eps, e->xh, e->xl, n, s));
@@ -843,7 +928,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         QH_TRY(proj(L.wqkv, L.wqkv_t, L.dt_attn, e->qkvd, D, e->xn, n, e->qkv, nullptr));
         QH_TRY(launch_rope_append(e->qkv, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
                                   e->o.kv_dtype, d_ptab, MP, ps, s));
-        QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale, e->capacity,
+        QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale, step_ctx,
                                 e->att, e->attn_ws, e->attn_ws_bytes, s));
         QH_TRY(proj(L.wo, L.wo_t, L.dt_attn, D, e->qd, e->att, n, e->h, e->h));  // + residual (transformer.cpp:593)
         hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.fn, D, c.rms_norm_eps, e->xn,
@@ -867,7 +952,9 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         const uint8_t* W = e->head ? e->head : e->embed;  // tied head reads the embedding (transformer.cpp:392-400)
         const uint32_t dt = e->head ? e->dt_head : e->dt_embed;
         QH_TRY(proj(W, e->head_t, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
-        hipLaunchKernelGGL(argmax_rows_kernel, dim3(n_logit_rows), dim3(256), 0, s, e->logits, V, e->amax);
+        hipLaunchKernelGGL(argmax_chunk_kernel, dim3(ARGMAX_CHUNKS, n_logit_rows), dim3(256), 0, s, e->logits, V,
+                           e->am_val, e->am_idx);
+        hipLaunchKernelGGL(argmax_final_kernel, dim3(n_logit_rows), dim3(64), 0, s, e->am_val, e->am_idx, V, e->amax);
         QH_CHECK_HIP(hipGetLastError());
         if (logits)
             QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_rows * V * 4, hipMemcpyDeviceToHost, s));

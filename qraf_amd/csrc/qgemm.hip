@@ -31,6 +31,8 @@
 // chip, the block range is split S ways; each split writes an fp32 partial
 // tile to a workspace and qgemm_reduce_kernel adds the S partials in split
 // order (deterministic), plus the residual.
+#include <type_traits>
+
 #include "common.h"
 
 namespace qraf_hip {
@@ -363,6 +365,239 @@ __global__ __launch_bounds__(64 * WM * WNW, 512 / (64 * WM * WNW)) void qgemm_ke
     }
 }
 
+// ---------------------------------------------------------------------------
+// Pipelined GEMM for tile-major weights and batches over 32 rows.
+//
+// Workgroup tile: MW = 32*TM batch rows x NW = 32*TN weight rows, 4 waves in
+// a 2 x 2 grid, each wave TM x TN MFMA tiles of 16 x 16.  Three LDS stage
+// buffers, each holding KC quant blocks of X (both bf16 planes) and of W, are
+// filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds): while
+// stage c computes, stages c+1 and c+2 are in flight.  One raw s_barrier per
+// stage, after the wave's own loads of stage c have landed (explicit vmcnt
+// wait with one stage still outstanding) and its LDS reads are done.
+// X rows in LDS are XOR-swizzled by 16-byte piece (slot = piece ^ (row & 7))
+// so the MFMA operand reads of 16 rows are bank-conflict-free; the swizzle
+// is applied through the per-lane global source addresses of the DMA.
+// Blocks past the split's range (stage padding) are read from wherever the
+// clamped or out-of-range address points (zeros or finite data) and weighted
+// by a zero scale.
+// ---------------------------------------------------------------------------
+// Direct-to-LDS 16-byte load: lane i writes LDS [lds + 16 i, +16) from its
+// own voffset.  Issued as inline asm so that the compiler tracks none of these
+// loads (it would otherwise wait for all of them before every LDS read it
+// cannot prove disjoint): the kernel counts them itself (vmcnt) and every
+// other vector memory access of the kernel happens after the final drain.
+typedef int v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ v4i make_rsrc_words(const void* p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)p;
+    return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
+}
+__device__ __forceinline__ void dma16(v4i rsrc, uint32_t voff, const void* lds) {
+    const uint32_t m0v = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+    __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                     :
+                     : "v"(voff), "s"(rsrc), "s"(m0v)
+                     : "memory", "m0");
+}
+
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_barrier" ::: "memory"); }
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+}
+
+// The three stage buffers are file-scope LDS objects reached through
+// compile-time accessors: the compiler then sees that a DMA into one buffer
+// does not alias reads of another and inserts no waits of its own.
+constexpr int QG_STAGE_MAX = 53248;
+__shared__ __align__(16) uint8_t qg_sb0[QG_STAGE_MAX];
+__shared__ __align__(16) uint8_t qg_sb1[QG_STAGE_MAX];
+__shared__ __align__(16) uint8_t qg_sb2[QG_STAGE_MAX];
+template <int B>
+__device__ __forceinline__ uint8_t* qg_stage() {
+    return B == 0 ? qg_sb0 : B == 1 ? qg_sb1 : qg_sb2;
+}
+
+// WN: waves along the weight rows (2 x WN waves); wave tile 16*TM x 16*TN.
+template <int FMT, int TM, int TN, int KC, int WN>
+struct PipeGeom {
+    static constexpr int NWV = 2 * WN;                // waves per workgroup
+    static constexpr int MW = 32 * TM, NW = 16 * TN * WN;
+    static constexpr int TB = tile_block_bytes(FMT);
+    static constexpr int XROW = KC * 64;              // bytes of one X row (one plane) per stage
+    static constexpr int XPL = MW * XROW;             // bytes of one plane per stage
+    static constexpr int XT = 2 * XPL / 1024;         // X DMA instructions per stage (1 KB each)
+    static constexpr int XI = XT / NWV;               // ... per wave
+    static constexpr int WBYTES = (NW / 16) * KC * TB;
+    static constexpr int WT = (WBYTES + 1023) / 1024;  // W DMA instructions per stage
+    static constexpr int WIL = WT / NWV, WEXTRA = WT % NWV;  // waves < WEXTRA issue WIL + 1
+    static constexpr int WIH = WIL + (WEXTRA ? 1 : 0);
+    static constexpr int STAGE = 2 * XPL + WT * 1024;  // bytes per stage buffer
+    static_assert(XT % NWV == 0, "X stage must split evenly over the waves");
+    static_assert((XPL / 16) % 64 == 0, "an X DMA instruction must stay in one plane");
+    static_assert(KC * 4 >= 8, "swizzle needs 8 pieces per row");
+    static_assert(STAGE <= QG_STAGE_MAX, "stage buffer too small");
+};
+
+template <int FMT, int TM, int TN, int KC, int WN>
+__global__ __launch_bounds__(128 * WN, 1) void qgemm_pipe_kernel(const uint8_t* __restrict__ Wt, int N, int nb,
+                                                                 const uint16_t* __restrict__ xh,
+                                                                 const uint16_t* __restrict__ xl, int K, int M,
+                                                                 float* Y, const float* add, int bps,
+                                                                 float* __restrict__ part) {
+    using G = PipeGeom<FMT, TM, TN, KC, WN>;
+    constexpr int MW = G::MW, NW = G::NW, TB = G::TB, NWV = G::NWV;
+
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: selects descriptors and M0
+    const int wm = wave / WN, wn = wave % WN;
+    const bool wextra = wave < G::WEXTRA;  // this wave issues one more W instruction per stage
+    const int seg = lane >> 4, l16 = lane & 15;
+    const int m0 = blockIdx.z * MW;
+    const int n0 = blockIdx.x * NW;
+    const int b_begin = blockIdx.y * bps;  // bps: a positive multiple of 3 KC
+    const int b_end = min(nb, b_begin + bps);
+    const int nstages = bps / KC;  // a multiple of 3
+
+    // ---- DMA source offsets (bytes), fixed per lane and instruction; the
+    // stage's first block adds cb*64 (X) or cb*TB (W)
+    const uint32_t xbytes = (uint32_t)((size_t)M * K * 2);
+    const v4i xrs[2] = {make_rsrc_words(xh, xbytes), make_rsrc_words(xl, xbytes)};
+    const int ntile16 = (N + 15) / 16;
+    const v4i wrs = make_rsrc_words(Wt, (uint32_t)min((size_t)ntile16 * nb * TB, (size_t)0xFFFFFFFFu));
+    uint32_t xo[G::XI], wo[G::WIH];
+#pragma unroll
+    for (int q = 0; q < G::XI; q++) {
+        const int f = (q * NWV + wave) * 64 + lane;  // 16-byte slot in the stage's X area
+        const int plane = f / (G::XPL / 16);
+        const int rem = f % (G::XPL / 16);
+        const int row = rem / (KC * 4), slot = rem % (KC * 4);
+        const int piece = slot ^ (row & 7);
+        (void)plane;
+        xo[q] = (uint32_t)((size_t)min(m0 + row, M - 1) * K * 2) + 16u * piece;
+    }
+#pragma unroll
+    for (int q = 0; q < G::WIH; q++) {
+        const int f = (q * NWV + wave) * 64 + lane;  // 16-byte slot in the stage's W area
+        const int u = min((16 * f) / (KC * TB), NW / 16 - 1);  // slots past WBYTES re-read the last tile
+        const int off = (16 * f) % (KC * TB);
+        const int T = min(n0 / 16 + u, ntile16 - 1);
+        wo[q] = (uint32_t)((size_t)T * nb * TB) + off;
+    }
+    auto issue = [&](auto bsel, int c) {
+        uint8_t* buf = qg_stage<decltype(bsel)::value>();
+        const int cb = min(b_begin + c * KC, b_end - 1);  // stages past the range re-read valid blocks
+#pragma unroll
+        for (int q = 0; q < G::XI; q++) {
+            const int plane = ((q * NWV + wave) * 64) / (G::XPL / 16);  // wave-uniform
+            dma16(xrs[plane], xo[q] + (uint32_t)cb * 64u, buf + (size_t)(q * NWV + wave) * 1024);
+        }
+#pragma unroll
+        for (int q = 0; q < G::WIL; q++)
+            dma16(wrs, wo[q] + (uint32_t)cb * TB, buf + 2 * G::XPL + (size_t)(q * NWV + wave) * 1024);
+        if (G::WEXTRA && wextra)
+            dma16(wrs, wo[G::WIH - 1] + (uint32_t)cb * TB, buf + 2 * G::XPL + (size_t)(G::WIL * NWV + wave) * 1024);
+    };
+    // this wave's loads of the oldest stage in flight have landed (one stage may
+    // remain outstanding) and its LDS reads are done
+    auto wait_stage = [&]() {
+        if (wextra) wait_vm_lgkm0<G::XI + G::WIH>();
+        else wait_vm_lgkm0<G::XI + G::WIL>();
+    };
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int t = 0; t < TM; t++)
+#pragma unroll
+        for (int u = 0; u < TN; u++) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    auto compute = [&](auto bsel, int c) {
+        const uint8_t* buf = qg_stage<decltype(bsel)::value>();
+        const int cb = b_begin + c * KC;
+        // one block at a time: unrolled over blocks, the scheduler hoists both
+        // blocks' fragment reads and spills
+#pragma unroll 1
+        for (int j = 0; j < KC; j++) {
+            const bool valid = cb + j < b_end;  // uniform; invalid blocks get scale 0
+            bf16x8 wf[TN];
+            float sc[TN];
+#pragma unroll
+            for (int u = 0; u < TN; u++) {
+                const uint8_t* tb = buf + 2 * G::XPL + ((wn * TN + u) * KC + j) * TB;
+                WRaw<FMT> r;
+                if (FMT == 8) {
+                    r.scale = *(const uint32_t*)(tb + 4 * l16);
+                    const uint2 q = *(const uint2*)(tb + 64 + 32 * l16 + 8 * seg);
+                    reinterpret_cast<uint32_t*>(&r)[1] = q.x;
+                    reinterpret_cast<uint32_t*>(&r)[2] = q.y;
+                } else {
+                    r.scale = *(const uint16_t*)(tb + 2 * l16);
+                    reinterpret_cast<uint32_t*>(&r)[1] = *(const uint32_t*)(tb + 32 + 16 * l16 + 4 * seg);
+                }
+                r.scale = valid ? r.scale : 0u;
+                convert<FMT>(r, wf[u], sc[u]);
+            }
+#pragma unroll
+            for (int t = 0; t < TM; t++) {
+                const int row = (wm * TM + t) * 16 + l16;
+                const int slot = (4 * j + seg) ^ (row & 7);
+                const bf16x8 ah = *(const bf16x8*)(buf + row * G::XROW + 16 * slot);
+                const bf16x8 al = *(const bf16x8*)(buf + G::XPL + row * G::XROW + 16 * slot);
+#pragma unroll
+                for (int u = 0; u < TN; u++) {
+                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[u], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[u], d, 0, 0, 0);
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[t][u][r] = __builtin_fmaf(d[r], sc[u], acc[t][u][r]);
+                }
+            }
+        }
+    };
+
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using B2 = std::integral_constant<int, 2>;
+    issue(B0{}, 0);
+    issue(B1{}, 1);
+    for (int c = 0; c < nstages; c += 3) {
+        wait_stage();
+        lds_barrier();
+        issue(B2{}, c + 2);
+        compute(B0{}, c);
+        wait_stage();
+        lds_barrier();
+        issue(B0{}, c + 3);
+        compute(B1{}, c + 1);
+        wait_stage();
+        lds_barrier();
+        issue(B1{}, c + 4);
+        compute(B2{}, c + 2);
+    }
+    wait_vm_lgkm0<0>();  // drain the past-the-end stages before the workgroup exits
+
+    // epilogue: direct (+ residual) or this split's partial tile
+    float* dst = part ? part + (size_t)blockIdx.y * M * N : Y;
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+#pragma unroll
+        for (int u = 0; u < TN; u++) {
+            const int n = n0 + (wn * TN + u) * 16 + l16;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = m0 + (wm * TM + t) * 16 + seg * 4 + r;
+                if (m < M && n < N) {
+                    float v = acc[t][u][r];
+                    if (!part && add) v += add[(size_t)m * N + n];
+                    dst[(size_t)m * N + n] = v;
+                }
+            }
+        }
+    }
+}
+
 // Y = sum_{s < S} part[s] (+ add), in split order.
 __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float* __restrict__ part, int S, size_t MN, float* Y,
                                                            const float* add) {
@@ -396,21 +631,48 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float* __restri
 
 struct QgPlan {
     int WM, WN, TM, TN, KC, MW, NW, ntiles, mchunks, S, bps;
+    bool pipe;  // qgemm_pipe_kernel (tile-major weights, batch tiles over 32 rows)
     size_t ws_bytes;
 };
 
 // Tuning overrides (qraf_hip_set_qgemm_tuning): 0 = automatic.
 static int g_qg_waves = 0;   // 4 or 8 waves per workgroup for batch tiles > 32 rows
 static int g_qg_splits = 0;  // forced split count
+static int g_qg_pipe = 0;    // 1: pipelined kernel for every tiled batch over 32 rows, -1: never
 
 // Tile shape and split count for an N x K matrix times M rows.  Batch tiles
 // of more than 32 rows use 2 x WN waves of 64 weight rows each; smaller ones
 // 4 waves of 32 weight rows.  Splits are added (powers of two, at most 64)
 // while the grid has fewer workgroups than the chip has slots for and every
 // split keeps at least one ping-pong pair of stages.
-static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes) {
+static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
     QgPlan p{};
     const int Mc = min(M, QG_MCHUNK);
+    const bool pipe = g_qg_pipe > 0 || (g_qg_pipe == 0 && N >= 8192);
+    if (tiled && Mc > 32 && pipe) {
+        // pipelined kernel: 2 x 2 waves of 16*TM x 128 rows, 3-stage LDS ring, 1 workgroup per CU
+        p.pipe = true;
+        p.WM = 2;
+        p.WN = 2;
+        p.TM = (Mc + 31) / 32;
+        p.TN = 4;
+        p.KC = 2;
+        p.MW = 32 * p.TM;
+        p.NW = 256;
+        p.ntiles = (N + p.NW - 1) / p.NW;
+        p.mchunks = (M + p.MW - 1) / p.MW;
+        const int nb = K / 32;
+        const size_t tiles = (size_t)p.ntiles * p.mchunks;
+        const int unit = 3 * p.KC;  // blocks per trip of the 3-stage loop
+        int S = 1;
+        if (g_qg_splits > 0) S = g_qg_splits;
+        else  // about one round of workgroups (one per CU): a second, partial round costs a full stage loop
+            while (S < 64 && tiles * S * 2 <= 200 && nb >= 2 * S * unit) S *= 2;
+        p.bps = ((nb + S - 1) / S + unit - 1) / unit * unit;
+        p.S = (nb + p.bps - 1) / p.bps;
+        p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
+        return p;
+    }
     p.WM = Mc > 32 ? 2 : 1;
     p.TM = (Mc + 16 * p.WM - 1) / (16 * p.WM);
     p.TN = p.WM == 2 ? 4 : 2;
@@ -437,22 +699,24 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes) {
     return p;
 }
 
-int set_qgemm_tuning(int waves, int splits) {
+int set_qgemm_tuning(int waves, int splits, int pipe) {
     QH_REQUIRE(waves == 0 || waves == 4 || waves == 8, QRAF_HIP_ERR_INVALID, "qgemm tuning: waves %d", waves);
     QH_REQUIRE(splits >= 0 && splits <= 256, QRAF_HIP_ERR_INVALID, "qgemm tuning: splits %d", splits);
+    QH_REQUIRE(pipe >= -1 && pipe <= 1, QRAF_HIP_ERR_INVALID, "qgemm tuning: pipe %d", pipe);
     g_qg_waves = waves;
     g_qg_splits = splits;
+    g_qg_pipe = pipe;
     return QRAF_HIP_OK;
 }
 
-size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M) {
+size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M, bool tiled) {
     if ((dtype != DT_Q8_0 && dtype != DT_Q4_0) || N <= 0 || K <= 0 || K % 32 || M <= 0) return 0;
-    return qgemm_plan(N, K, M, q_row_bytes(dtype, 32, K)).ws_bytes;
+    return qgemm_plan(N, K, M, q_row_bytes(dtype, 32, K), tiled).ws_bytes;
 }
 
-size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M) {
+size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M, bool tiled) {
     if ((dtype != DT_Q8_0 && dtype != DT_Q4_0) || N <= 0 || K <= 0 || K % 32 || M <= 0) return 0;
-    return (size_t)qgemm_plan(N, K, M, q_row_bytes(dtype, 32, K)).S * M * N * 4;
+    return (size_t)qgemm_plan(N, K, M, q_row_bytes(dtype, 32, K), tiled).S * M * N * 4;
 }
 
 int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s,
@@ -501,7 +765,7 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
                QRAF_HIP_ERR_INVALID, "qgemm: misaligned operands");
     const size_t rb = q_row_bytes(dtype, bs, K);
     const int nb = K / 32;
-    QgPlan p = qgemm_plan(N, K, M, rb);
+    QgPlan p = qgemm_plan(N, K, M, rb, tiled);
     float* part = nullptr;
     if (slices) {  // partials mode: S slices [S][M][N] in ws, summed by the caller's next kernel
         QH_REQUIRE(ws && ws_bytes >= (size_t)p.S * M * N * 4 && (((uintptr_t)ws) & 15) == 0 && !add,
@@ -514,11 +778,27 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
             part = (float*)ws;
         } else {  // no (or too small a) workspace: one split
             p.S = 1;
-            p.bps = (nb + 2 * p.KC - 1) / (2 * p.KC) * (2 * p.KC);
+            const int unit = (p.pipe ? 3 : 2) * p.KC;
+            p.bps = (nb + unit - 1) / unit * unit;
         }
     }
     QH_REQUIRE(p.mchunks <= 65535, QRAF_HIP_ERR_INVALID, "qgemm: batch %d too large", M);
     const dim3 grid(p.ntiles, p.S, p.mchunks);
+    if (p.pipe) {
+#define QH_P(F, TM_)                                                                                        \
+    hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, 4, 2, 4>), grid, dim3(512), 0, s, (const uint8_t*)W, N, nb, xh, xl, \
+                       K, M, Y, add, p.bps, part)
+        if (dtype == DT_Q8_0) {
+            if (p.TM == 2) QH_P(8, 2);
+            else if (p.TM == 3) QH_P(8, 3);
+            else QH_P(8, 4);
+        } else {
+            if (p.TM == 2) QH_P(4, 2);
+            else if (p.TM == 3) QH_P(4, 3);
+            else QH_P(4, 4);
+        }
+#undef QH_P
+    } else {
 #define QH_G(F, WM_, WN_, TM_, TN_, KC_)                                                                           \
     if (tiled)                                                                                                     \
         hipLaunchKernelGGL((qgemm_kernel<F, WM_, WN_, TM_, TN_, KC_, true>), grid, dim3(64 * WM_ * WN_), 0, s,       \
@@ -547,6 +827,7 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
 #undef QH_GF
 #undef QH_GW
 #undef QH_G
+    }
     QH_CHECK_HIP(hipGetLastError());
     if (part && !slices) {
         const size_t MN = (size_t)M * N;
@@ -566,13 +847,17 @@ int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int3
     return qraf_hip::launch_split_bf16(x, x_hi, x_lo, rows, cols, 0, nullptr, qraf_hip::as_stream(stream));
 }
 
-int qraf_hip_set_qgemm_tuning(int waves, int splits) {
+int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe) {
     qraf_hip::clear_error();
-    return qraf_hip::set_qgemm_tuning(waves, splits);
+    return qraf_hip::set_qgemm_tuning(waves, splits, pipe);
 }
 
 uint64_t qraf_hip_qgemm_workspace_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim, int32_t batch) {
-    return qraf_hip::qgemm_workspace_bytes(dtype, (int)out_dim, (int)in_dim, batch);
+    return qraf_hip::qgemm_workspace_bytes(dtype, (int)out_dim, (int)in_dim, batch, false);
+}
+
+uint64_t qraf_hip_qgemm_tiled_workspace_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim, int32_t batch) {
+    return qraf_hip::qgemm_workspace_bytes(dtype, (int)out_dim, (int)in_dim, batch, true);
 }
 
 int qraf_hip_qgemm_dev(const void* w, uint32_t dtype, uint32_t block_size, uint32_t out_dim, uint32_t in_dim,

@@ -27,7 +27,8 @@ def run_gemm(hip, wq, dt, N, K, X, add=None, split=True, in_place=False, repeats
     dh, dl = DeviceBuffer(M * K * 2), DeviceBuffer(M * K * 2)
     dy = DeviceBuffer(M * N * 4)
     da = DeviceBuffer.from_array(add) if add is not None and not in_place else None
-    wsb = lib.qraf_hip_qgemm_workspace_bytes(dt, N, K, M) if split else 0
+    wsq = lib.qraf_hip_qgemm_tiled_workspace_bytes if tiled else lib.qraf_hip_qgemm_workspace_bytes
+    wsb = wsq(dt, N, K, M) if split else 0
     ws = DeviceBuffer(wsb) if wsb else None
     call("qraf_hip_split_bf16_dev", dx.ptr, dh.ptr, dl.ptr, M, K, None)
     outs = []
@@ -83,9 +84,14 @@ def test_qgemm_vs_oracle(hip, dt, case):
     check(Y, wq, dt, N, K, X)
     Y1, _, _ = run_gemm(hip, wq, dt, N, K, X, split=False)  # one split, no workspace
     check(Y1, wq, dt, N, K, X)
-    # tile-major weights: the same arithmetic in the same order, bit for bit
-    Yt, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True)
-    assert np.array_equal(Yt.view(np.uint32), Y.view(np.uint32))
+    # tile-major weights: up to 32 rows the same kernel and split, bit for bit;
+    # larger batches run the pipelined kernel (own tiling and split)
+    Yt, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, repeats=2)
+    check(Yt, wq, dt, N, K, X)
+    if M <= 32:
+        assert np.array_equal(Yt.view(np.uint32), Y.view(np.uint32))
+    Yt1, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
+    check(Yt1, wq, dt, N, K, X)
 
 
 def tile_major_reference(wq, dt, N, K):
@@ -116,6 +122,26 @@ def test_repack_tiles_layout(hip, dt, shape):
     assert np.array_equal(dt_.download(np.uint8, nbytes), ref)
 
 
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("case", [(8192, 1024, 100), (2048, 2048, 128), (300, 512, 64), (1000, 576, 33)],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_qgemm_pipelined_kernel(hip, dt, case):
+    """The pipelined tiled kernel (direct-to-LDS 3-stage ring) forced on for
+    every shape, with and without split-K, against the oracle."""
+    N, K, M = case
+    rng = np.random.default_rng(N + 3 * K + M + dt)
+    wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    hip._lib.call("qraf_hip_set_qgemm_tuning", 0, 0, 1)
+    try:
+        Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, repeats=2)
+        Y1, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
+    finally:
+        hip._lib.call("qraf_hip_set_qgemm_tuning", 0, 0, 0)
+    check(Y, wq, dt, N, K, X)
+    check(Y1, wq, dt, N, K, X)
+
+
 def test_qgemm_split_k_is_used(hip):
     lib = hip._lib.lib
     # few 128-row tiles and a long K: the split-K path must be chosen
@@ -125,15 +151,16 @@ def test_qgemm_split_k_is_used(hip):
     assert lib.qraf_hip_qgemm_workspace_bytes(po.Q4_0, 151936, 2048, 128) == 0
 
 
+@pytest.mark.parametrize("tiled", [False, True])
 @pytest.mark.parametrize("split", [True, False])
 @pytest.mark.parametrize("in_place", [True, False])
-def test_qgemm_residual_epilogue(hip, split, in_place):
+def test_qgemm_residual_epilogue(hip, split, in_place, tiled):
     rng = np.random.default_rng(5)
     N, K, M = 2048, 2048, 40
     wq = po.quantize(po.Q8_0, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
     X = rng.standard_normal((M, K)).astype(np.float32)
     add = rng.standard_normal((M, N)).astype(np.float32)
-    Y, _, _ = run_gemm(hip, wq, po.Q8_0, N, K, X, add, split=split, in_place=in_place)
+    Y, _, _ = run_gemm(hip, wq, po.Q8_0, N, K, X, add, split=split, in_place=in_place, tiled=tiled)
     check(Y, wq, po.Q8_0, N, K, X, add)
 
 
