@@ -43,6 +43,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "Q4/Q8 decode tok/s at batch 1 & 128; qmatvec achieved HBM GB/s vs peak"
 HBM_PEAK_GBS = 8000.0      # MI355X published HBM3E bandwidth
+MFMA_BF16_TFLOPS = 2500.0  # MI355X published dense bf16 matrix peak (the GEMM issues 2 MFMAs per product: hi + lo)
 POOL_BYTES = 320 << 20     # > 256 MB MALL
 Q8, Q4, F32, F16 = 10, 20, 0, 1
 MV_CASES = [("q8_0", Q8, 4096, 4096), ("q8_0", Q8, 11008, 4096), ("q4_0", Q4, 4096, 4096), ("q4_0", Q4, 11008, 4096)]
@@ -201,19 +202,36 @@ def bench_gemm(args, rt):
                  stream.h)
             for c in range(1, copies):
                 call("qraf_hip_memcpy_d2d", pool.ptr + c * wbytes, pool.ptr, wbytes, stream.h)
+            # the engine's form: a tile-major copy (same bytes, reordered at load time)
+            tbytes = lib.qraf_hip_tiled_weight_bytes(dt, n, k)
+            tcopies = max(2, math.ceil(POOL_BYTES / tbytes))
+            tpool = DeviceBuffer(tcopies * tbytes)
+            for c in range(tcopies):
+                call("qraf_hip_repack_tiles_dev", pool.ptr + (c % copies) * wbytes, dt, n, k, tpool.ptr + c * tbytes,
+                     stream.h)
             for b in (8, 32, 64, 128):
                 dx = DeviceBuffer.from_array(rng.standard_normal((b, k)).astype(np.float32))
                 xh, xl, y = DeviceBuffer(b * k * 2), DeviceBuffer(b * k * 2), DeviceBuffer(b * n * 4)
                 call("qraf_hip_split_bf16_dev", dx.ptr, xh.ptr, xl.ptr, b, k, stream.h)
                 wsb = lib.qraf_hip_qgemm_workspace_bytes(dt, n, k, b)
                 ws = DeviceBuffer(wsb) if wsb else None
-                us = graph_time_us(rt, lambda i: call("qraf_hip_qgemm_dev", pool.ptr + (i % copies) * wbytes, dt, 32,
-                                                      n, k, xh.ptr, xl.ptr, b, y.ptr, None,
-                                                      ws.ptr if ws else None, wsb, stream.h), 100)
+                us_ref = graph_time_us(rt, lambda i: call("qraf_hip_qgemm_dev", pool.ptr + (i % copies) * wbytes, dt,
+                                                          32, n, k, xh.ptr, xl.ptr, b, y.ptr, None,
+                                                          ws.ptr if ws else None, wsb, stream.h), 100)
+                wsbt = lib.qraf_hip_qgemm_tiled_workspace_bytes(dt, n, k, b)
+                wst = DeviceBuffer(wsbt) if wsbt else None
+                us = graph_time_us(rt, lambda i: call("qraf_hip_qgemm_tiled_dev", tpool.ptr + (i % tcopies) * tbytes,
+                                                      dt, n, k, xh.ptr, xl.ptr, b, y.ptr, None,
+                                                      wst.ptr if wst else None, wsbt, stream.h), 100)
                 by, fl = mv_bytes(dt, n, k, b), 2.0 * b * n * k
                 out.append({"case": f"{fmt} {n}x{k} B={b}", "us": round(us, 2),
-                            "GB_s": round(by / (us * 1e-6) / 1e9, 1), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 2)})
+                            "GB_s": round(by / (us * 1e-6) / 1e9, 1), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 2),
+                            "mfma_frac": round(2 * fl / (us * 1e-6) / 1e12 / MFMA_BF16_TFLOPS, 4),
+                            "us_reference_layout": round(us_ref, 2)})
+                for d in (dx, xh, xl, y):
+                    d.free()
             pool.free()
+            tpool.free()
     return out
 
 
@@ -351,12 +369,44 @@ def bench_decode_b128(args, rt):
     done = sched.run()
     el = time.perf_counter() - t0
     gen = sum(len(r.generated) for r in done)
+    steady = steady_decode_b128(e, rng, args.decode_steps)
     e.close()
     return {"model": "Qwen2.5-3B architecture, Q4_0 weights, tied head, QKV bias, fp16 KV pages, random init",
             "requests": args.requests, "max_concurrent": 128, "generated_tokens": gen, "steps": sched.steps,
             "rows_processed": sched.rows, "wall_s": round(el, 3), "generated_tok_s": round(gen / el, 1),
             "rows_per_s": round(sched.rows / el, 1), "ms_per_step": round(el / sched.steps * 1e3, 3),
-            "note": "prompt tokens are fed one per step (chunk 1) in the same batched step as decodes"}
+            "note": "continuous batching: prompt tokens are fed one per step (chunk 1) in the same batched step as "
+                    "decodes, requests admitted as others finish",
+            "steady_decode": steady}
+
+
+def steady_decode_b128(e, rng, steps):
+    """128 concurrent sequences at ragged contexts (prompt U[16,512] plus U[0,255] generated, the run above's
+    distribution), prefilled in 128-row steps; then `steps` decode steps of 128 rows, every row generating
+    (greedy, device argmax).  Timed: the decode steps only."""
+    n, V = 128, QWEN["vocab"]
+    seqs = [e.seq_create() for _ in range(n)]
+    ctx = rng.integers(16, 513, n) + rng.integers(0, 256, n)
+    rows = [(s, p) for s, c in zip(seqs, ctx) for p in range(int(c))]
+    for i in range(0, len(rows), 128):
+        ch = rows[i:i + 128]
+        e.step([s for s, _ in ch], rng.integers(0, V, len(ch)).tolist(), [p for _, p in ch],
+               want_logits=np.zeros(len(ch), np.uint8), logits=False, argmax=False)
+    toks = rng.integers(0, V, n).tolist()
+    pos = ctx.astype(np.int64).copy()
+    for _ in range(3):  # warm-up decode steps
+        _, nx = e.step(seqs, toks, pos.tolist())
+        toks, pos = nx.tolist(), pos + 1
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, nx = e.step(seqs, toks, pos.tolist())
+        toks, pos = nx.tolist(), pos + 1
+    el = time.perf_counter() - t0
+    for s in seqs:
+        e.seq_release(s)
+    return {"sequences": n, "context_mean_at_start": round(float(ctx.mean()) + 3, 1),
+            "context_max_at_end": int(pos.max()), "decode_steps": steps, "ms_per_step": round(el / steps * 1e3, 3),
+            "decode_tok_s": round(n * steps / el, 1)}
 
 
 # --------------------------------------------------------------------------- main
@@ -370,6 +420,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--only", default="matvec,gemm,attention,decode_b1,decode_b128")
     ap.add_argument("--requests", type=int, default=256, help="requests in the batch-128 decode run")
+    ap.add_argument("--decode-steps", type=int, default=64, help="timed steps of the steady 128-sequence decode")
     ap.add_argument("--rows-per-wave", type=int, default=0)
     ap.add_argument("--kernel", type=int, default=0, help="matvec kernel: 0 auto, 1 one-shot, 2 persistent")
     ap.add_argument("--wgs-per-cu", type=int, default=0)
