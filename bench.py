@@ -89,6 +89,20 @@ def graph_time_us(rt, body, iters):
 
 # --------------------------------------------------------------------------- matvec (headline)
 
+def ring_kernel_name(case):
+    """Template name of the ring kernel the automatic choice runs for a C2 case
+    ('q8_0 11008x4096'): <format, rows per wave, x loads per thread, depth, waves per workgroup>."""
+    fmt, shape = case.split()
+    n, k = (int(v) for v in shape.split("x"))
+    q8 = fmt == "q8_0"
+    nw = 4 if (not q8 and n >= 8192) else 8
+    r = 2 if (not q8 and n >= 8192 and n % 2 == 0) else 1
+    per = 64 * nw * (4 if q8 else 8)
+    xj = -(-k // per)
+    xj = next(v for v in (1, 2, 4, 8, 12) if v >= xj)
+    return f"qmv_ring_kernel<{8 if q8 else 4}, {r}, {xj}, 2, {nw}>"
+
+
 def bench_matvec(args, rt):
     call, DeviceBuffer, Event, Graph, stream, lib = (rt[k] for k in ("call", "DeviceBuffer", "Event", "Graph", "stream",
                                                                      "lib"))
@@ -422,7 +436,8 @@ def main():
     ap.add_argument("--requests", type=int, default=256, help="requests in the batch-128 decode run")
     ap.add_argument("--decode-steps", type=int, default=64, help="timed steps of the steady 128-sequence decode")
     ap.add_argument("--rows-per-wave", type=int, default=0)
-    ap.add_argument("--kernel", type=int, default=0, help="matvec kernel: 0 auto, 1 one-shot, 2 persistent")
+    ap.add_argument("--kernel", type=int, default=0,
+                    help="matvec kernel: 0 auto, 1 one-shot, 2 persistent, 3 ring (8-wave groups), 4 ring (4-wave groups)")
     ap.add_argument("--wgs-per-cu", type=int, default=0)
     args = ap.parse_args()
     if args.gpus != 1:
@@ -451,7 +466,7 @@ def main():
     dom = max(per_case, key=lambda p: p["us_per_launch"])  # dominant kernel: longest launch
     roofline = {"bound": "hbm", "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
                 "frac": round(dom["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": "qmv_persist_kernel<8,1>" if dom["case"].startswith("q8") else "qmv_persist_kernel<4,2>",
+                "kernel": ring_kernel_name(dom["case"]),
                 "case": dom["case"], "alg_bytes_per_launch": dom["alg_bytes"]}
     cpu = None
     if not args.no_cpu:

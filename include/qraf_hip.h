@@ -109,8 +109,11 @@ int qraf_hip_matvec_q_dev(const void* w, uint32_t dtype, uint32_t block_size, ui
 int qraf_hip_matvec_f32_dev(const float* W, const float* x, float* y, uint32_t out_dim,
                             uint32_t in_dim, void* stream);
 /* Tuning of the batch-1 kernel (process-wide): kernel 0 = automatic,
- * 1 = one-shot, 2 = persistent streaming; rows per wave 0 (automatic), 1, 2,
- * 4 or 8; workgroups per CU for the persistent kernel (0 = automatic). */
+ * 1 = one-shot, 2 = persistent streaming, 3 / 4 = ring with workgroups of
+ * 8 / 4 waves (the automatic choice is 3 when K % 32 == 0, x is 16-byte
+ * aligned and x fits the ring's staging); rows per wave 0 (automatic), 1, 2,
+ * 4 or 8 (the ring kernel takes 1 or 2); workgroups per CU for the
+ * persistent and ring kernels (0 = automatic). */
 int qraf_hip_set_matvec_tuning(int kernel, int rows, int wgs_per_cu);
 
 /* quantize_q8_0 / quantize_q4_0 (quantize.cpp:105-183) on the device, block

@@ -9,7 +9,7 @@
 //                                          elem 2j+1 (high nibble)], value = nibble - 8
 // The fast kernel works on 36-byte "units": one Q8_0 block or a pair of Q4_0
 // blocks.  Lane l of a wave owns units l, l+64, ... of every row it visits
-// and loads each unit with one dword + two dwordx4 loads (4-byte aligned),
+// and loads each unit with two dwordx4 loads + one dword (4-byte aligned),
 // so a wave reads 2304 contiguous bytes per row step.  The activation vector
 // is staged once per workgroup in LDS, padded to 36 floats per 32-element
 // block (16-byte aligned, free of bank conflicts for ds_read_b128), and for
@@ -71,20 +71,28 @@ __device__ __forceinline__ float wave_reduce_rows(float (&acc)[R], int lane, int
 // and every iteration requests the next unit's weights before it computes the
 // current one, so each wave keeps two units x R rows of loads in flight.
 // ----------------------------------------------------------------------------
+// A unit's 36 bytes as the hardware loads them: bytes 0-15, 16-31, 32-35.
+// (Declared in this order on purpose: a layout that does not match the load
+// split makes the compiler copy registers right after the loads, which waits
+// for them.)  dword(w, r, i) is dword i (0..8) of row r's unit.
 template <int R>
 struct Units {
-    uint32_t s[R];
     u32x4a4 a[R], b[R];
+    uint32_t c[R];
 };
+template <int R>
+__device__ __forceinline__ uint32_t dword(const Units<R>& w, int r, int i) {
+    return i < 4 ? w.a[r][i] : i < 8 ? w.b[r][i - 4] : w.c[r];
+}
 
 template <int R>
 __device__ __forceinline__ void load_units(Units<R>& w, const uint8_t* const (&rowp)[R], int u) {
 #pragma unroll
     for (int r = 0; r < R; r++) {
         const uint8_t* p = rowp[r] + (size_t)u * 36;
-        w.s[r] = *(const uint32_t*)p;
-        w.a[r] = *(const u32x4a4*)(p + 4);
-        w.b[r] = *(const u32x4a4*)(p + 20);
+        w.a[r] = *(const u32x4a4*)p;
+        w.b[r] = *(const u32x4a4*)(p + 16);
+        w.c[r] = *(const uint32_t*)(p + 32);
     }
 }
 
@@ -99,11 +107,11 @@ __device__ __forceinline__ void q8_compute(const Units<R>& w, const float* xs, f
         float bs = 0.f;
 #pragma unroll
         for (int j = 0; j < 8; j++) {
-            uint32_t d = j < 4 ? w.a[r][j] : w.b[r][j - 4];
+            const uint32_t d = dword(w, r, 1 + j);
 #pragma unroll
             for (int k = 0; k < 4; k++) bs = __builtin_fmaf((float)(int8_t)(d >> (8 * k)), xr[j][k], bs);
         }
-        acc[r] = __builtin_fmaf(bs, __builtin_bit_cast(float, w.s[r]), acc[r]);
+        acc[r] = __builtin_fmaf(bs, __builtin_bit_cast(float, dword(w, r, 0)), acc[r]);
     }
 }
 
@@ -119,7 +127,9 @@ __device__ __forceinline__ void q4_compute(const Units<R>& w, const float* xu, f
 #pragma unroll
     for (int r = 0; r < R; r++) {
         // unit dwords: s = 0, a = 1..4, b = 5..8
-        uint32_t dw[9] = {w.s[r], w.a[r][0], w.a[r][1], w.a[r][2], w.a[r][3], w.b[r][0], w.b[r][1], w.b[r][2], w.b[r][3]};
+        uint32_t dw[9];
+#pragma unroll
+        for (int i = 0; i < 9; i++) dw[i] = dword(w, r, i);
         float be = 0.f, bo = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
@@ -347,6 +357,198 @@ __global__ __launch_bounds__(WG) void qmv_persist_kernel(const uint8_t* __restri
 }
 
 // ----------------------------------------------------------------------------
+// Ring kernel (the default fast path).  What decides its speed, measured with
+// per-wave timestamps on MI355X:
+//  * x must reach LDS before the weight flood.  Every workgroup reads the same
+//    x; requested behind ~10 MB of first weight loads it arrives ~3 us late and
+//    holds every wave at the staging barrier.  Each thread's x loads are issued
+//    first (XJ float4 per thread, branch-free: addresses are clamped and
+//    out-of-range stores go to a spare LDS slot), and larger workgroups (NW
+//    waves) cut the number of times the same x lines are requested.
+//  * the weight ring must stay full: every step issues the loads of the step
+//    D-1 ahead before touching the current one (a scheduling barrier keeps the
+//    compiler from hoisting the current step's use above them), the loop body
+//    has no branch around loads or their uses (ragged unit columns are masked
+//    with a select, steps past the end recompute a duplicate and skip only the
+//    store), and the residual values are loaded at entry, before x, so no late
+//    load forces a full wait at the end of a row.
+//  * every wave owns the same number of row groups (the launcher sizes the grid
+//    so), otherwise the waves holding one extra group finish alone.
+// Step it of a wave: row group gw + (it / J) * nw, unit column it % J.
+// ----------------------------------------------------------------------------
+constexpr int RING_KA = 4;  // row groups per wave whose residual values are preloaded
+
+// Opaque redefinition of a step's registers: their uses cannot move above this
+// point, so the compiler's wait for them lands here (after the next step's
+// loads are issued), not at the loop latch where it would drain the ring.
+template <int R>
+__device__ __forceinline__ void pin_units(Units<R>& b) {
+#pragma unroll
+    for (int r = 0; r < R; r++) __asm__ volatile("" : "+v"(b.a[r]), "+v"(b.b[r]), "+v"(b.c[r])::"memory");
+}
+
+template <int R>
+__device__ __forceinline__ void q8_compute_masked(const Units<R>& w, const float* xs, float (&acc)[R], bool valid) {
+    const f32x4* xv = (const f32x4*)xs;
+    f32x4 xr[8];
+#pragma unroll
+    for (int j = 0; j < 8; j++) xr[j] = xv[j];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        float bs = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const uint32_t d = dword(w, r, 1 + j);
+#pragma unroll
+            for (int k = 0; k < 4; k++) bs = __builtin_fmaf((float)(int8_t)(d >> (8 * k)), xr[j][k], bs);
+        }
+        const float t = __builtin_fmaf(bs, __builtin_bit_cast(float, dword(w, r, 0)), acc[r]);
+        acc[r] = valid ? t : acc[r];
+    }
+}
+
+template <int R>
+__device__ __forceinline__ void q4_compute_masked(const Units<R>& w, const float* xu, float (&acc)[R], bool valid) {
+    float t[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) t[r] = acc[r];
+    q4_compute<R>(w, xu, t);
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = valid ? t[r] : acc[r];
+}
+
+template <int FMT, int R, int XJ, int D, int NW>
+__global__ __launch_bounds__(64 * NW) void qmv_ring_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
+                                                          int K, int nb, const float* __restrict__ x, float* y,
+                                                          const float* add) {
+    extern __shared__ __align__(16) float sx[];
+    constexpr int NT = 64 * NW;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int U = FMT == 8 ? nb : nb >> 1;
+    const int J = (U + 63) >> 6;
+    const int ngroups = (N + R - 1) / R;
+    const int gw = blockIdx.x * NW + wave, nw = gridDim.x * NW;
+    const int my_groups = gw < ngroups ? (ngroups - 1 - gw) / nw + 1 : 0;
+    const int n_it = my_groups * J;
+    const int t = threadIdx.x;
+    const int rr = lane / (64 / R);  // the row of its group this lane stores after the reduction
+
+    // 0. residual values of this lane's rows (the launcher guarantees my_groups <= RING_KA when add is set)
+    float addv[RING_KA];
+#pragma unroll
+    for (int i = 0; i < RING_KA; i++)
+        addv[i] = add ? add[min((gw + i * nw) * R + rr, N - 1)] : 0.f;
+
+    // 1. x loads.  Q8: float4 f = t + NT i holds elements 4f..4f+3;
+    //    Q4: 8-element group g = t + NT i.  (K % 32 == 0, x 16-byte aligned.)
+    constexpr int XL = FMT == 8 ? XJ : 2 * XJ;
+    f32x4 xr[XL];
+    const int n4 = K >> 2;
+#pragma unroll
+    for (int i = 0; i < XJ; i++) {
+        if (FMT == 8) {
+            xr[i] = *(const f32x4*)(x + 4 * min(t + NT * i, n4 - 1));
+        } else {
+            const int g = min(t + NT * i, (n4 >> 1) - 1);
+            xr[2 * i] = *(const f32x4*)(x + 8 * g);
+            xr[2 * i + 1] = *(const f32x4*)(x + 8 * g + 4);
+        }
+    }
+    // 2. x into LDS (Q8: 36-float blocks; Q4: block pairs, even/odd elements
+    //    permuted, plus block sums), the layout stage_x builds.
+    if (FMT == 8) {
+        const int spare = nb * XS8;
+#pragma unroll
+        for (int i = 0; i < XJ; i++) {
+            const int f = t + NT * i;
+            const int off = f < n4 ? (f >> 3) * XS8 + ((f & 7) << 2) : spare;
+            *(f32x4*)(sx + off) = xr[i];
+        }
+    } else {
+        const int spare = (nb >> 1) * XS4;
+#pragma unroll
+        for (int i = 0; i < XJ; i++) {
+            const int g = t + NT * i;
+            const f32x4 a = xr[2 * i], b = xr[2 * i + 1];
+            float part = ((a[0] + a[2]) + (b[0] + b[2])) + ((a[1] + a[3]) + (b[1] + b[3]));
+            part += __shfl_xor(part, 1);
+            part += __shfl_xor(part, 2);
+            const int blk = g >> 2, gg = g & 3;
+            const bool ok = g < (n4 >> 1);
+            const int base = ok ? (blk >> 1) * XS4 + (blk & 1) * 36 : spare;
+            *(f32x4*)(sx + base + (ok ? gg * 8 : 0)) = f32x4{a[0], a[2], b[0], b[2]};
+            *(f32x4*)(sx + base + (ok ? gg * 8 + 4 : 4)) = f32x4{a[1], a[3], b[1], b[3]};
+            if (gg == 0) sx[base + (ok ? 32 : 8)] = part;
+        }
+    }
+
+    // 3. the weight ring
+    const int last = max(n_it - 1, 0);
+    auto issue = [&](int it, Units<R>& b) {
+        const int i = min(it, last);
+        const int g = gw + (i / J) * nw, j = i % J;
+        const uint8_t* rp[R];
+#pragma unroll
+        for (int r = 0; r < R; r++) rp[r] = W + (size_t)min(g * R + r, N - 1) * row_bytes;
+        load_units<R>(b, rp, min(lane + 64 * j, U - 1));
+    };
+    Units<R> buf[D];
+#pragma unroll
+    for (int d = 0; d < D - 1; d++) issue(d, buf[d]);
+    __syncthreads();
+    if (add) {
+        // the residual values were requested before x: take them now, while
+        // only the ring prologue is in flight behind them
+#pragma unroll
+        for (int i = 0; i < RING_KA; i++) __asm__ volatile("" : "+v"(addv[i]));
+    }
+
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) acc[r] = 0.f;
+    float add_cur = addv[0];
+    float v_done = 0.f;  // the last finished row group's value (re-stored by steps past the end)
+    // The loop body is branch-free: a branch inside it splits the live ranges of
+    // the ring registers and the copies that follow wait for their loads.  So
+    // every step reduces and stores: a row group's partial sums are stored
+    // before its final sum (the same wave, the same address, in order), and a
+    // step past the end stores the last finished value again.  (R divides N on
+    // this path, so every stored row exists.)
+    for (int it0 = 0; it0 < n_it; it0 += D) {
+#pragma unroll
+        for (int d = 0; d < D; d++) {
+            const int it = it0 + d;
+            issue(it + D - 1, buf[(d + D - 1) % D]);
+            __builtin_amdgcn_sched_barrier(0);
+            pin_units<R>(buf[d]);
+            const int i = min(it, last);
+            const int j = i % J;
+            const int u = lane + 64 * j;
+            const bool valid = u < U && it < n_it;
+            const int uc = min(u, U - 1);
+            if (FMT == 8) q8_compute_masked<R>(buf[d], sx + uc * XS8, acc, valid);
+            else q4_compute_masked<R>(buf[d], sx + uc * XS4, acc, valid);
+            float red[R];
+#pragma unroll
+            for (int r = 0; r < R; r++) red[r] = acc[r];
+            int rrr;
+            const float v = wave_reduce_rows<R>(red, lane, &rrr) + add_cur;
+            const bool fin = j == J - 1;
+            const float vs = it < n_it ? v : v_done;
+            const int g = gw + (i / J) * nw;
+            y[g * R + rr] = vs;
+            v_done = fin ? vs : v_done;
+#pragma unroll
+            for (int r = 0; r < R; r++) acc[r] = fin ? 0.f : acc[r];
+#pragma unroll
+            for (int k = 0; k + 1 < RING_KA; k++) addv[k] = fin ? addv[k + 1] : addv[k];
+            add_cur = fin ? addv[0] : add_cur;
+        }
+    }
+}
+
+// ----------------------------------------------------------------------------
 // General path: any block size, any alignment (byte loads).  One wave per row;
 // lane l takes blocks l, l+64, ...  Follows the reference's block geometry
 // exactly, including the Q4 odd-tail rule (this_block/2 pairs).
@@ -415,13 +617,13 @@ __global__ __launch_bounds__(WG) void mv_f32_kernel(const float* __restrict__ W,
 // Launchers
 // ----------------------------------------------------------------------------
 static int g_rows_per_wave = 0;  // 0: automatic; else 1, 2, 4 or 8
-static int g_kernel = 0;         // 0: automatic, 1: one-shot, 2: persistent streaming
-static int g_wgs_per_cu = 0;     // persistent grid size per CU (0: automatic)
+static int g_kernel = 0;         // 0: automatic, 1: one-shot, 2: persistent streaming, 3 / 4: ring, 8 / 4 waves per workgroup
+static int g_wgs_per_cu = 0;     // persistent / ring grid size per CU (0: automatic)
 
 int set_matvec_tuning(int kernel, int r, int wgs_per_cu) {
     QH_REQUIRE(r == 0 || r == 1 || r == 2 || r == 4 || r == 8, QRAF_HIP_ERR_INVALID,
                "rows per wave must be 0 (auto), 1, 2, 4 or 8");
-    QH_REQUIRE(kernel >= 0 && kernel <= 2, QRAF_HIP_ERR_INVALID, "kernel must be 0, 1 or 2");
+    QH_REQUIRE(kernel >= 0 && kernel <= 4, QRAF_HIP_ERR_INVALID, "kernel must be 0..4");
     QH_REQUIRE(wgs_per_cu >= 0 && wgs_per_cu <= 16, QRAF_HIP_ERR_INVALID, "workgroups per CU must be 0..16");
     g_rows_per_wave = r;
     g_kernel = kernel;
@@ -441,6 +643,22 @@ static int cu_count() {
 }
 
 typedef void (*qmv_fn)(const uint8_t*, uint32_t, int, int, int, const float*, float*, const float*);
+
+// workgroups of `threads` threads and `lds` bytes of LDS that fit on one CU at
+// once (cached per kernel and LDS size: the launch path calls this per matvec)
+static hipError_t resident_wgs(const void* kf, int threads, size_t lds, int* out) {
+    struct Entry { const void* k; size_t lds; int n; };
+    thread_local Entry cache[64];
+    thread_local int used = 0;
+    for (int i = 0; i < used; i++)
+        if (cache[i].k == kf && cache[i].lds == lds) { *out = cache[i].n; return hipSuccess; }
+    int n = 0;
+    hipError_t e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kf, threads, lds);
+    if (e != hipSuccess) return e;
+    if (used < 64) cache[used++] = {kf, lds, n};
+    *out = n;
+    return hipSuccess;
+}
 
 template <int FMT, int R, int J>
 static qmv_fn oneshot_if_valid() {
@@ -480,6 +698,23 @@ static qmv_fn pick_kernel(int R, int J) {
     }
 }
 
+// ring kernel instances: XJ in {1, 2, 4, 8, 12} (x loads per thread, rounded
+// up; the extra loads are clamped duplicates), R in {1, 2}, D = 2, NW in {4, 8}
+template <int FMT, int R, int NW>
+static qmv_fn pick_ring_xj(int xj) {
+    if (xj <= 1) return qmv_ring_kernel<FMT, R, 1, 2, NW>;
+    if (xj <= 2) return qmv_ring_kernel<FMT, R, 2, 2, NW>;
+    if (xj <= 4) return qmv_ring_kernel<FMT, R, 4, 2, NW>;
+    if (xj <= 8) return qmv_ring_kernel<FMT, R, 8, 2, NW>;
+    if (xj <= 12) return qmv_ring_kernel<FMT, R, 12, 2, NW>;
+    return nullptr;
+}
+template <int FMT>
+static qmv_fn pick_ring(int R, int NW, int xj) {
+    if (R == 1) return NW == 4 ? pick_ring_xj<FMT, 1, 4>(xj) : pick_ring_xj<FMT, 1, 8>(xj);
+    return NW == 4 ? pick_ring_xj<FMT, 2, 4>(xj) : pick_ring_xj<FMT, 2, 8>(xj);
+}
+
 int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x, float* y,
                     hipStream_t s, const float* add) {
     QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "unsupported weight dtype %u", dtype);
@@ -495,12 +730,49 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
     if (fast) {
         const int U = dtype == DT_Q8_0 ? nb : nb / 2;
         const int J = (U + 63) / 64;
-        // Automatic choice (measured on MI355X with weights streamed from HBM):
-        // the persistent kernel for large matrices (R=1 / 4 WGs per CU for Q8,
-        // R=2 / 2 WGs per CU for Q4), the one-shot kernel when there are fewer
-        // than 4 row groups per wave slot.
-        int kern = g_kernel;
+        // Automatic choice (measured on MI355X, weights streamed from HBM): the
+        // one-shot kernel below ~6 MB of weights (it has the whole matrix in
+        // flight at once), else the ring kernel: Q8 one row per wave, 8-wave
+        // workgroups, 2 per CU; Q4 one row per wave, 1 such workgroup per CU,
+        // or for N >= 8192 two rows per wave in 4-wave workgroups, 4 per CU.
+        const bool big = (size_t)N * rb >= ((size_t)6 << 20);
+        const bool q4_wide = dtype == DT_Q4_0 && N >= 8192;
+        int kern_req = g_kernel;
+        if (kern_req == 0 && big) kern_req = q4_wide ? 4 : 3;
+        const int NWr = kern_req == 4 ? 4 : 8;  // waves per workgroup (kernel 3: 8, kernel 4: 4)
+        const int xj = dtype == DT_Q8_0 ? (int)((K + 64 * NWr * 4 - 1) / (64 * NWr * 4))
+                                        : (int)((K + 64 * NWr * 8 - 1) / (64 * NWr * 8));
+        // the ring kernel needs whole blocks, a 16-byte aligned x and x within its staging
+        const bool ring_ok = (K % 32) == 0 && (((uintptr_t)x) & 15) == 0 && xj <= 12 && lds + 64 <= 160 * 1024;
+        int kern = kern_req;
         if (kern == 0) kern = (N >= 8192 && J <= 8) ? 2 : 1;
+        if ((kern == 3 || kern == 4) && ring_ok) {
+            int R = g_rows_per_wave ? min(g_rows_per_wave, 2) : (g_kernel == 0 && q4_wide ? 2 : 1);
+            if (N % R) R = 1;  // every stored row must exist
+            qmv_fn kf = dtype == DT_Q8_0 ? pick_ring<8>(R, NWr, xj) : pick_ring<4>(R, NWr, xj);
+            QH_REQUIRE(kf, QRAF_HIP_ERR_INVALID, "no ring matvec kernel for K=%u", K);
+            const size_t lds_r = lds + 16 * sizeof(float);  // + the spare slot for out-of-range x stores
+            if (lds_r > 65536)
+                QH_CHECK_HIP(hipFuncSetAttribute((const void*)kf, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_r));
+            // never more workgroups per CU than fit at once (the rest would run as a second round)
+            int fit = 0;
+            QH_CHECK_HIP(resident_wgs((const void*)kf, 64 * NWr, lds_r, &fit));
+            const int dflt = dtype == DT_Q8_0 ? 16 / NWr : (q4_wide && NWr == 4 ? 4 : 1);
+            const int wgs_per_cu = max(1, min(g_wgs_per_cu ? g_wgs_per_cu : dflt, fit));
+            // equal row groups per wave: k = ceil(groups / max waves), then as few waves as hold k
+            // each; with a residual every wave must hold at most RING_KA groups
+            const int ngroups = (int)((N + R - 1) / R);
+            int wmax = wgs_per_cu * NWr * cu_count();
+            if (add) wmax = max(wmax, (ngroups + RING_KA - 1) / RING_KA);
+            const int k = (ngroups + wmax - 1) / wmax;
+            const int waves = (ngroups + k - 1) / k;
+            const int grid = (waves + NWr - 1) / NWr;
+            hipLaunchKernelGGL(kf, dim3(grid), dim3(64 * NWr), lds_r, s, W, (uint32_t)rb, (int)N, (int)K, nb, x, y, add);
+            QH_CHECK_HIP(hipGetLastError());
+            return QRAF_HIP_OK;
+        }
+        // persistent kernel when the ring does not apply and there are many rows, else one-shot
+        if (kern >= 3) kern = (N >= 8192 && J <= 8) ? 2 : 1;
         if (kern == 2 || J > 8) {
             const int R = g_rows_per_wave ? min(g_rows_per_wave, 4) : (dtype == DT_Q8_0 ? 1 : 2);
             const int ngroups = (int)((N + R - 1) / R);

@@ -73,6 +73,30 @@ def test_forward_logits_vs_oracle(hip, name):
     tf.engine.close()
 
 
+@pytest.mark.parametrize("tuning", [(3, 1, 0), (3, 2, 0), (4, 1, 2), (4, 2, 4), (1, 0, 0), (2, 0, 0)],
+                         ids=lambda t: "k%d_r%d_w%d" % t)
+@pytest.mark.parametrize("name", ["q8_hd64_gqa3", "q4_gqa8_hd128"])
+def test_forward_logits_matvec_kernels(hip, name, tuning):
+    """Every batch-1 matvec of the decode forced onto one kernel variant: the
+    ring kernels (3, 4) also take the in-place residual of the O and down
+    projections through their preloaded residual values."""
+    kw, seed = SMALL[name]
+    print(f"engine forward {name} matvec tuning {tuning}", flush=True)
+    m = oracle_model(kw, seed)
+    tf = upload(m, kw)
+    L = po.lib()
+    prompt = [L.or_gen_token(seed, i, kw["vocab"]) for i in range(6)]
+    hip.lib.qraf_hip_set_matvec_tuning(*tuning)
+    try:
+        m.reset()
+        tf.reset()
+        for pos, t in enumerate(prompt):
+            check_logits(tf.forward(t, pos), m.forward(t, pos), f"{name} {tuning} pos {pos}")
+    finally:
+        hip.lib.qraf_hip_set_matvec_tuning(0, 0, 0)
+        tf.engine.close()
+
+
 @pytest.mark.parametrize("name", ["q8_llama", "q4_qwen2_tied_bias", "f32_llama"])
 def test_golden_logits_and_streams(hip, name):
     # the fixtures were written by the compiled reference itself

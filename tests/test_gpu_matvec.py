@@ -69,11 +69,12 @@ def test_matvec_q_vs_oracle(hip, dt, shape):
 
 
 @pytest.mark.parametrize("kernel,rows,wgs", [(1, 1, 0), (1, 2, 0), (1, 4, 0), (1, 8, 0), (2, 1, 4), (2, 2, 2),
-                                             (2, 4, 1), (2, 2, 8)])
+                                             (2, 4, 1), (2, 2, 8), (3, 1, 0), (3, 2, 1), (3, 1, 3), (4, 1, 2),
+                                             (4, 2, 4), (4, 2, 16)])
 @pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
 @pytest.mark.parametrize("k", [2048, 11008])
-def test_matvec_kernel_variants(hip, kernel, rows, wgs, dt, k):
-    n = 1000
+@pytest.mark.parametrize("n", [1000, 999])
+def test_matvec_kernel_variants(hip, kernel, rows, wgs, dt, k, n):
     rng = np.random.default_rng(rows + k)
     wq = po.quantize(dt, (rng.standard_normal(n * k) * 0.02).astype(np.float32))
     x = rng.standard_normal(k).astype(np.float32)
