@@ -89,6 +89,12 @@ def graph_time_us(rt, body, iters):
 
 # --------------------------------------------------------------------------- matvec (headline)
 
+# HBM bytes per launch from rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of this
+# bench (scaled by the counters' reading for a copy kernel of known size);
+# reported only for the kernel they were measured on.
+MEASURED_TRAFFIC = {("qmv_ring_kernel<8, 1, 2, 2, 8>", "q8_0 11008x4096"): 50937856}
+
+
 def ring_kernel_name(case):
     """Template name of the ring kernel the automatic choice runs for a C2 case
     ('q8_0 11008x4096'): <format, rows per wave, x loads per thread, depth, waves per workgroup>."""
@@ -109,7 +115,10 @@ def bench_matvec(args, rt):
     rng = np.random.default_rng(2024)
     x_host = rng.standard_normal(4096).astype(np.float32)
     cases = []
+    wanted = [c.strip() for c in args.cases.split(",") if c.strip()] if args.cases else None
     for (name, dt, n, k) in MV_CASES:
+        if wanted is not None and f"{name} {n}x{k}" not in wanted:
+            continue
         wbytes = n * row_bytes(dt, k)
         copies = max(2, math.ceil(POOL_BYTES / wbytes))
         pool = DeviceBuffer(copies * wbytes)
@@ -435,6 +444,9 @@ def main():
     ap.add_argument("--only", default="matvec,gemm,attention,decode_b1,decode_b128")
     ap.add_argument("--requests", type=int, default=256, help="requests in the batch-128 decode run")
     ap.add_argument("--decode-steps", type=int, default=64, help="timed steps of the steady 128-sequence decode")
+    ap.add_argument("--cases", default="",
+                    help="restrict the matvec leg to these cases, e.g. 'q8_0 11008x4096' (comma-separated; "
+                         "a profile of one case then has one shape per kernel)")
     ap.add_argument("--rows-per-wave", type=int, default=0)
     ap.add_argument("--kernel", type=int, default=0,
                     help="matvec kernel: 0 auto, 1 one-shot, 2 persistent, 3 ring (8-wave groups), 4 ring (4-wave groups)")
@@ -464,9 +476,13 @@ def main():
             print(f"# {part} done", file=sys.stderr, flush=True)
 
     dom = max(per_case, key=lambda p: p["us_per_launch"])  # dominant kernel: longest launch
+    kname = ring_kernel_name(dom["case"])
+    traffic = MEASURED_TRAFFIC.get((kname, dom["case"]))
     roofline = {"bound": "hbm", "achieved": dom["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                "frac": round(dom["GB_s"] / HBM_PEAK_GBS, 4), "traffic": None,
-                "kernel": ring_kernel_name(dom["case"]),
+                "frac": round(dom["GB_s"] / HBM_PEAK_GBS, 4), "traffic": traffic,
+                "traffic_source": "profiles/qmv_matvec_isolated.md (FETCH_SIZE, WRITE_SIZE scaled by a copy kernel)"
+                if traffic else None,
+                "kernel": kname,
                 "case": dom["case"], "alg_bytes_per_launch": dom["alg_bytes"]}
     cpu = None
     if not args.no_cpu:
