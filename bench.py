@@ -313,6 +313,7 @@ def bench_decode_b1(args, rt):
     e = Engine(cfg, kv_dtype=F32, max_batch=1)
     e.generate_weights(Q8, Q8, Q8, False, False, 1)
     e.finalize()
+    e.set_graphs(not args.no_graphs)
     prompt = np.random.default_rng(1).integers(0, SMOL["vocab"], 32).tolist()
     n_gen = 128
 
@@ -379,6 +380,7 @@ def bench_decode_b128(args, rt):
     e = Engine(cfg, kv_dtype=F16, max_batch=128)
     e.generate_weights(Q4, Q4, Q4, True, True, 3)
     e.finalize()
+    e.set_graphs(not args.no_graphs)
     rng = np.random.default_rng(3)
     warm = BatchScheduler(e, max_batch=128)
     for _ in range(4):
@@ -447,6 +449,8 @@ def main():
     ap.add_argument("--cases", default="",
                     help="restrict the matvec leg to these cases, e.g. 'q8_0 11008x4096' (comma-separated; "
                          "a profile of one case then has one shape per kernel)")
+    ap.add_argument("--no-graphs", action="store_true",
+                    help="decode legs launch every step's kernels eagerly instead of replaying step graphs")
     ap.add_argument("--rows-per-wave", type=int, default=0)
     ap.add_argument("--kernel", type=int, default=0,
                     help="matvec kernel: 0 auto, 1 one-shot, 2 persistent, 3 ring (8-wave groups), 4 ring (4-wave groups)")

@@ -279,6 +279,11 @@ int qraf_engine_free_pages(qraf_engine* engine, int32_t* free_pages);
  * Transformer::forward (transformer.cpp:573-639) for many sequences at once. */
 int qraf_engine_step(qraf_engine* engine, int32_t n_rows, const int32_t* seq_ids, const uint32_t* tokens,
                      const int32_t* positions, const uint8_t* want_logits, float* logits, uint32_t* next_tokens);
+/* Steps are captured once per shape (rows, logit rows, head, context bound
+ * rounded up to a power of two, kernel tuning) into a HIP graph and replayed
+ * (on = 1, the default); on = 0 launches every step's kernels eagerly.  No
+ * reference counterpart: an execution detail of qraf_engine_step. */
+int qraf_engine_set_graphs(qraf_engine* engine, int32_t on);
 /* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)
  * on the engine's default sequence, and Transformer::reset() (:641-643). */
 int qraf_engine_forward(qraf_engine* engine, uint32_t token, int32_t pos, float* logits);

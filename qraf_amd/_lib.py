@@ -105,6 +105,7 @@ SIGNATURES.update({
     "qraf_engine_seq_length": (C.c_int, [vp, C.c_int32, i32p]),
     "qraf_engine_free_pages": (C.c_int, [vp, i32p]),
     "qraf_engine_step": (C.c_int, [vp, C.c_int32, i32p, u32p, i32p, C.POINTER(C.c_uint8), fp, u32p]),
+    "qraf_engine_set_graphs": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_forward": (C.c_int, [vp, C.c_uint32, C.c_int32, fp]),
     "qraf_engine_reset": (C.c_int, [vp]),
 })

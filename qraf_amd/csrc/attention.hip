@@ -130,10 +130,13 @@ template <typename KT, int HD, int G>
 __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     static_assert(HD % 8 == 0, "head_dim must be a multiple of 8");
     constexpr int NOUT = G * HD;                 // outputs of this workgroup
-    constexpr int HPT = (NOUT + ACH - 1) / ACH;  // outputs per thread in the PV phase
+    constexpr int HPT = (NOUT + ACH - 1) / ACH;  // outputs per thread at the end
+    constexpr int NG = ACH / HD;                 // position groups of the PV phase
+    constexpr int PADP = 8 * NG;                 // past-the-end slots its unrolled loop may touch
     __shared__ int s_pref[1025];
     __shared__ float s_q[G][HD];
-    __shared__ float s_p[G][ACH];
+    __shared__ float s_p[G][ACH + PADP];         // probabilities (zero past the end); then PV partials
+    __shared__ uint32_t s_voff[ACH + PADP];      // element offset of each position's V row in the layer pages
     __shared__ float s_red[G][4];
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -152,6 +155,16 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     const KT* kc = (const KT*)a.kc;
     const KT* vc = (const KT*)a.vc;
     const int t = t0 + tid;
+    {
+        // V row of position t (positions past the end read position t0's row,
+        // which exists, with probability 0)
+        const int tv = t < ctx ? t : t0;
+        const uint32_t page = (uint32_t)a.page_table[(size_t)s * a.max_pages + tv / a.page_size];
+        const uint32_t row = (page * a.Hkv + kvh) * a.page_size;
+        const uint32_t off = sizeof(KT) == 4 ? (row + tv % a.page_size) * HD : row * HD + tv % a.page_size;
+        s_voff[tid] = off;
+        if (tid < PADP) s_voff[ACH + tid] = off;  // any existing row: its probability is 0
+    }
     float sc[G];
 #pragma unroll
     for (int h = 0; h < G; h++) sc[h] = 0.f;
@@ -198,6 +211,7 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     for (int h = 0; h < G; h++) {
         const float p = (t < ctx) ? __expf(sc[h] - m[h]) : 0.f;
         s_p[h][tid] = p;
+        if (tid < PADP) s_p[h][ACH + tid] = 0.f;
         float v = p;
 #pragma unroll
         for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
@@ -207,31 +221,42 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
     for (int h = 0; h < G; h++) l[h] = (s_red[h][0] + s_red[h][1]) + (s_red[h][2] + s_red[h][3]);
 
-    // ---- weighted sum of V: thread handles outputs o = tid + 256*j (head
-    // o / HD, dimension o % HD); for head_dim >= 64 a wave's 64 outputs share
-    // one head, so the probabilities are LDS broadcasts and V reads coalesce.
+    // ---- weighted sum of V.  Thread (dimension d = tid % HD, group g = tid /
+    // HD) sums positions g, g + NG, ... of the chunk for all G heads at once
+    // (each V element is loaded once for the heads that share it), with 8
+    // independent loads in flight; the NG group sums are then added in group
+    // order.  For f32 pages and head_dim >= 64 a wave reads one V row.
+    const int dd = tid % HD, grp = tid / HD;
+    const int tend = min(ACH, ctx - t0);
+    const KT* vd = vc + (sizeof(KT) == 4 ? (size_t)dd : (size_t)dd * a.page_size);
+    float acc[G];
+#pragma unroll
+    for (int h = 0; h < G; h++) acc[h] = 0.f;
+    for (int tt = grp; tt < tend; tt += NG * 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; u++) v[u] = kv_load(vd + s_voff[tt + NG * u]);
+#pragma unroll
+        for (int u = 0; u < 8; u++)
+#pragma unroll
+            for (int h = 0; h < G; h++) acc[h] = __builtin_fmaf(s_p[h][tt + NG * u], v[u], acc[h]);
+    }
+    __syncthreads();  // every probability read: s_p now holds the group partials [NG][G][HD]
+    float* s_acc = &s_p[0][0];
+#pragma unroll
+    for (int h = 0; h < G; h++) s_acc[(grp * G + h) * HD + dd] = acc[h];
+    __syncthreads();
     float o[HPT];
 #pragma unroll
-    for (int j = 0; j < HPT; j++) o[j] = 0.f;
-    const int tend = min(ACH, ctx - t0);
-    int cur_lp = -1;
-    const KT* vpage = nullptr;
-    for (int tt = 0; tt < tend; tt++) {
-        const int tp = t0 + tt;
-        const int lp = tp / a.page_size;
-        if (lp != cur_lp) {
-            cur_lp = lp;
-            const int page = a.page_table[(size_t)s * a.max_pages + lp];
-            vpage = vc + ((size_t)page * a.Hkv + kvh) * a.page_size * HD;
-        }
-        const int tin = tp % a.page_size;
+    for (int j = 0; j < HPT; j++) {
+        const int oi = tid + ACH * j;
+        float sum = 0.f;
+        if (oi < NOUT) {
+            const int h = oi / HD, d = oi % HD;
 #pragma unroll
-        for (int j = 0; j < HPT; j++) {
-            const int oi = tid + ACH * j;
-            // f32 pages: V row-major per position; f16 pages: dimension-major
-            const KT* vp = sizeof(KT) == 4 ? vpage + (size_t)tin * HD + oi % HD : vpage + (size_t)(oi % HD) * a.page_size + tin;
-            if (oi < NOUT) o[j] = __builtin_fmaf(s_p[oi / HD][tt], kv_load(vp), o[j]);
+            for (int g = 0; g < NG; g++) sum += s_acc[(g * G + h) * HD + d];
         }
+        o[j] = sum;
     }
 
     if (nchunks == 1) {

@@ -49,6 +49,10 @@ int launch_matvec_q(const void* W, uint32_t dtype, int bs, uint32_t N, uint32_t 
 int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s,
                       const float* add = nullptr);
 int set_matvec_tuning(int kernel, int rows, int wgs_per_cu);
+// Bumped by every tuning call: captured launch sequences (the engine's step
+// graphs) record it and are rebuilt when it changes.
+uint32_t tuning_generation();
+void bump_tuning_generation();
 int launch_rms_norm(float* x, const float* w, int n, float eps, hipStream_t s);
 int launch_softmax(float* x, int n, hipStream_t s);
 int launch_dot(const float* a, const float* b, int n, float* out, hipStream_t s);

@@ -350,7 +350,30 @@ struct qraf_engine {
     size_t part_ws_bytes = 0;
     bool fused = false;  // every layer has tile-major copies: batched steps run the fused pipeline
     size_t in_words = 0;
+
+    // Captured steps.  A step's launch sequence depends only on its row count,
+    // its logit-row count, whether the head runs, the attention grid's context
+    // bound and the kernel tuning; everything else (tokens, positions, page
+    // tables) reaches the device through the pinned staging copy the graph
+    // itself performs.  Replaying it saves the host ~300 kernel launches per
+    // decode step.
+    struct StepGraph {
+        int n = 0, n_logit_rows = 0, ctx = 0;
+        bool head = false;
+        uint32_t gen = 0;
+        hipGraphExec_t exec = nullptr;
+        uint64_t used = 0;
+    };
+    std::vector<StepGraph> graphs;
+    bool use_graphs = true;
+    uint64_t graph_clock = 0;
+    void drop_graphs() {
+        for (auto& g : graphs) hipGraphExecDestroy(g.exec);
+        graphs.clear();
+    }
 };
+
+constexpr size_t MAX_STEP_GRAPHS = 48;
 
 static int ealloc(qraf_engine* e, void** p, size_t bytes) {
     hipError_t r = hipMalloc(p, bytes ? bytes : 16);
@@ -517,6 +540,7 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
 int qraf_engine_destroy(qraf_engine* e) {
     if (!e) return QRAF_HIP_OK;
     hipStreamSynchronize(e->stream);
+    e->drop_graphs();
     for (void* p : e->allocs) hipFree(p);
     if (e->h_in) hipHostFree(e->h_in);
     if (e->h_amax) hipHostFree(e->h_amax);
@@ -856,7 +880,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
     }
     hipStream_t s = e->stream;
     const size_t words = (size_t)n * (4 + MP);
-    QH_CHECK_HIP(hipMemcpyAsync(e->d_in, e->h_in, words * 4, hipMemcpyHostToDevice, s));
+    const bool head = n_logit_rows > 0 && (logits || next_tokens);
     const int32_t* d_tok = e->d_in;
     const int32_t* d_pos = d_tok + n;
     const int32_t* d_ctx = d_pos + n;
@@ -887,81 +911,146 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         return launch_qgemm(Wt, dt, 32, N, K, e->xh, e->xl, rows, y, add, e->gemm_ws, e->gemm_ws_bytes, s, true);
     };
 
-    hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, 32, D, d_tok, e->h);
-    QH_CHECK_HIP(hipGetLastError());
-    if (n > 1 && e->fused) {
-        // Batched layer on the matrix cores, 9 launches: each projection writes
-        // split-K partials that the next kernel sums (with the bias, residual,
-        // norm or SiLU-gate it applies anyway), and every kernel that feeds a
-        // projection writes its input as the bf16 hi/lo planes directly.
-        QH_TRY(launch_residual_norm_split(nullptr, 0, 0, e->h, e->layers[0].an, D, c.rms_norm_eps, e->xh, e->xl, n, s));
-        for (uint32_t l = 0; l < c.num_layers; l++) {
+    // The whole step, stream-ordered: staging copy, embedding, layers, head and
+    // argmax.  ctx_grid >= every row's context sizes the attention grid.
+    auto enqueue = [&](int ctx_grid) -> int {
+        QH_CHECK_HIP(hipMemcpyAsync(e->d_in, e->h_in, words * 4, hipMemcpyHostToDevice, s));
+        hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, 32, D, d_tok, e->h);
+        QH_CHECK_HIP(hipGetLastError());
+        if (n > 1 && e->fused) {
+            // Batched layer on the matrix cores, 9 launches: each projection writes
+            // split-K partials that the next kernel sums (with the bias, residual,
+            // norm or SiLU-gate it applies anyway), and every kernel that feeds a
+            // projection writes its input as the bf16 hi/lo planes directly.
+            QH_TRY(launch_residual_norm_split(nullptr, 0, 0, e->h, e->layers[0].an, D, c.rms_norm_eps, e->xh, e->xl, n, s));
+            for (uint32_t l = 0; l < c.num_layers; l++) {
+                qraf_engine::Layer& L = e->layers[l];
+                uint8_t* kc = e->kpool + (size_t)l * e->layer_kv_bytes;
+                uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;
+                float* P = (float*)e->part_ws;
+                int S = 0;
+                QH_TRY(launch_qgemm(L.wqkv_t, L.dt_attn, 32, e->qkvd, D, e->xh, e->xl, n, e->qkv, nullptr, P,
+                                    e->part_ws_bytes, s, true, &S));
+                QH_TRY(launch_rope_append(P, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
+                                          e->o.kv_dtype, d_ptab, MP, ps, s, S, (size_t)n * e->qkvd));
+                QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale,
+                                        ctx_grid, nullptr, e->attn_ws, e->attn_ws_bytes, s, e->xh, e->xl));
+                QH_TRY(launch_qgemm(L.wo_t, L.dt_attn, 32, D, e->qd, e->xh, e->xl, n, e->qkv, nullptr, P, e->part_ws_bytes,
+                                    s, true, &S));
+                QH_TRY(launch_residual_norm_split(P, S, (size_t)n * D, e->h, L.fn, D, c.rms_norm_eps, e->xh, e->xl, n, s));
+                QH_TRY(launch_qgemm(L.wgu_t, L.dt_mlp, 32, 2 * F, D, e->xh, e->xl, n, e->qkv, nullptr, P,
+                                    e->part_ws_bytes, s, true, &S));
+                QH_TRY(launch_split_bf16(P, e->xh, e->xl, n, F, 1, nullptr, s, S, (size_t)n * 2 * F));
+                QH_TRY(launch_qgemm(L.wd_t, L.dt_mlp, 32, D, F, e->xh, e->xl, n, e->qkv, nullptr, P, e->part_ws_bytes, s,
+                                    true, &S));
+                const float* wn = l + 1 < c.num_layers ? e->layers[l + 1].an : nullptr;  // last layer: residual only
+                QH_TRY(launch_residual_norm_split(P, S, (size_t)n * D, e->h, wn, D, c.rms_norm_eps, e->xh, e->xl, n, s));
+            }
+        }
+        for (uint32_t l = 0; l < c.num_layers && !(n > 1 && e->fused); l++) {
             qraf_engine::Layer& L = e->layers[l];
             uint8_t* kc = e->kpool + (size_t)l * e->layer_kv_bytes;
             uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;
-            float* P = (float*)e->part_ws;
-            int S = 0;
-            QH_TRY(launch_qgemm(L.wqkv_t, L.dt_attn, 32, e->qkvd, D, e->xh, e->xl, n, e->qkv, nullptr, P,
-                                e->part_ws_bytes, s, true, &S));
-            QH_TRY(launch_rope_append(P, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
-                                      e->o.kv_dtype, d_ptab, MP, ps, s, S, (size_t)n * e->qkvd));
-            QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale,
-                                    step_ctx, nullptr, e->attn_ws, e->attn_ws_bytes, s, e->xh, e->xl));
-            QH_TRY(launch_qgemm(L.wo_t, L.dt_attn, 32, D, e->qd, e->xh, e->xl, n, e->qkv, nullptr, P, e->part_ws_bytes,
-                                s, true, &S));
-            QH_TRY(launch_residual_norm_split(P, S, (size_t)n * D, e->h, L.fn, D, c.rms_norm_eps, e->xh, e->xl, n, s));
-            QH_TRY(launch_qgemm(L.wgu_t, L.dt_mlp, 32, 2 * F, D, e->xh, e->xl, n, e->qkv, nullptr, P,
-                                e->part_ws_bytes, s, true, &S));
-            QH_TRY(launch_split_bf16(P, e->xh, e->xl, n, F, 1, nullptr, s, S, (size_t)n * 2 * F));
-            QH_TRY(launch_qgemm(L.wd_t, L.dt_mlp, 32, D, F, e->xh, e->xl, n, e->qkv, nullptr, P, e->part_ws_bytes, s,
-                                true, &S));
-            const float* wn = l + 1 < c.num_layers ? e->layers[l + 1].an : nullptr;  // last layer: residual only
-            QH_TRY(launch_residual_norm_split(P, S, (size_t)n * D, e->h, wn, D, c.rms_norm_eps, e->xh, e->xl, n, s));
+            hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.an, D, c.rms_norm_eps, e->xn,
+                               nullptr);
+            QH_TRY(proj(L.wqkv, L.wqkv_t, L.dt_attn, e->qkvd, D, e->xn, n, e->qkv, nullptr));
+            QH_TRY(launch_rope_append(e->qkv, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
+                                      e->o.kv_dtype, d_ptab, MP, ps, s));
+            QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale, ctx_grid,
+                                    e->att, e->attn_ws, e->attn_ws_bytes, s));
+            QH_TRY(proj(L.wo, L.wo_t, L.dt_attn, D, e->qd, e->att, n, e->h, e->h));  // + residual (transformer.cpp:593)
+            hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.fn, D, c.rms_norm_eps, e->xn,
+                               nullptr);
+            QH_TRY(proj(L.wgu, L.wgu_t, L.dt_mlp, 2 * F, D, e->xn, n, e->gu, nullptr));
+            if (n == 1 || !L.wd_t) {
+                hipLaunchKernelGGL(silu_gate_kernel, dim3(std::min((n * F + 255) / 256, 4096)), dim3(256), 0, s, e->gu, F,
+                                   n, e->act);
+                QH_TRY(proj(L.wd, L.wd_t, L.dt_mlp, D, F, e->act, n, e->h, e->h));  // + residual (transformer.cpp:601)
+            } else {
+                QH_TRY(launch_split_bf16(e->gu, e->xh, e->xl, n, F, 1, nullptr, s));  // SiLU-gate fused into the split
+                QH_TRY(launch_qgemm(L.wd_t, L.dt_mlp, 32, D, F, e->xh, e->xl, n, e->h, e->h, e->gemm_ws, e->gemm_ws_bytes, s,
+                                    true));
+            }
         }
-    }
-    for (uint32_t l = 0; l < c.num_layers && !(n > 1 && e->fused); l++) {
-        qraf_engine::Layer& L = e->layers[l];
-        uint8_t* kc = e->kpool + (size_t)l * e->layer_kv_bytes;
-        uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;
-        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.an, D, c.rms_norm_eps, e->xn,
-                           nullptr);
-        QH_TRY(proj(L.wqkv, L.wqkv_t, L.dt_attn, e->qkvd, D, e->xn, n, e->qkv, nullptr));
-        QH_TRY(launch_rope_append(e->qkv, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
-                                  e->o.kv_dtype, d_ptab, MP, ps, s));
-        QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale, step_ctx,
-                                e->att, e->attn_ws, e->attn_ws_bytes, s));
-        QH_TRY(proj(L.wo, L.wo_t, L.dt_attn, D, e->qd, e->att, n, e->h, e->h));  // + residual (transformer.cpp:593)
-        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.fn, D, c.rms_norm_eps, e->xn,
-                           nullptr);
-        QH_TRY(proj(L.wgu, L.wgu_t, L.dt_mlp, 2 * F, D, e->xn, n, e->gu, nullptr));
-        if (n == 1 || !L.wd_t) {
-            hipLaunchKernelGGL(silu_gate_kernel, dim3(std::min((n * F + 255) / 256, 4096)), dim3(256), 0, s, e->gu, F,
-                               n, e->act);
-            QH_TRY(proj(L.wd, L.wd_t, L.dt_mlp, D, F, e->act, n, e->h, e->h));  // + residual (transformer.cpp:601)
-        } else {
-            QH_TRY(launch_split_bf16(e->gu, e->xh, e->xl, n, F, 1, nullptr, s));  // SiLU-gate fused into the split
-            QH_TRY(launch_qgemm(L.wd_t, L.dt_mlp, 32, D, F, e->xh, e->xl, n, e->h, e->h, e->gemm_ws, e->gemm_ws_bytes, s,
-                                true));
-        }
-    }
-    QH_CHECK_HIP(hipGetLastError());
-    if (n_logit_rows > 0 && (logits || next_tokens)) {
-        // final norm of the rows that want logits (transformer.cpp:605), then the head
-        hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n_logit_rows), dim3(256), 0, s, e->h, e->onorm, D,
-                           c.rms_norm_eps, e->xhead, d_lrows);
-        const uint8_t* W = e->head ? e->head : e->embed;  // tied head reads the embedding (transformer.cpp:392-400)
-        const uint32_t dt = e->head ? e->dt_head : e->dt_embed;
-        QH_TRY(proj(W, e->head_t, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
-        hipLaunchKernelGGL(argmax_chunk_kernel, dim3(ARGMAX_CHUNKS, n_logit_rows), dim3(256), 0, s, e->logits, V,
-                           e->am_val, e->am_idx);
-        hipLaunchKernelGGL(argmax_final_kernel, dim3(n_logit_rows), dim3(64), 0, s, e->am_val, e->am_idx, V, e->amax);
         QH_CHECK_HIP(hipGetLastError());
-        if (logits)
-            QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_rows * V * 4, hipMemcpyDeviceToHost, s));
-        if (next_tokens)
-            QH_CHECK_HIP(hipMemcpyAsync(next_tokens, e->amax, (size_t)n_logit_rows * 4, hipMemcpyDeviceToHost, s));
+        if (head) {
+            // final norm of the rows that want logits (transformer.cpp:605), then the head
+            hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n_logit_rows), dim3(256), 0, s, e->h, e->onorm, D,
+                               c.rms_norm_eps, e->xhead, d_lrows);
+            const uint8_t* W = e->head ? e->head : e->embed;  // tied head reads the embedding (transformer.cpp:392-400)
+            const uint32_t dt = e->head ? e->dt_head : e->dt_embed;
+            QH_TRY(proj(W, e->head_t, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
+            hipLaunchKernelGGL(argmax_chunk_kernel, dim3(ARGMAX_CHUNKS, n_logit_rows), dim3(256), 0, s, e->logits, V,
+                               e->am_val, e->am_idx);
+            hipLaunchKernelGGL(argmax_final_kernel, dim3(n_logit_rows), dim3(64), 0, s, e->am_val, e->am_idx, V, e->amax);
+            QH_CHECK_HIP(hipGetLastError());
+        }
+        return QRAF_HIP_OK;
+    };
+
+    if (e->use_graphs) {
+        // context bound rounded up to a power of two (>= one attention chunk) so
+        // that a decode reuses one graph for many steps
+        int ctx_grid = 256;
+        while (ctx_grid < step_ctx) ctx_grid *= 2;
+        ctx_grid = std::min(ctx_grid, e->capacity);
+        const uint32_t gen = tuning_generation();
+        qraf_engine::StepGraph* g = nullptr;
+        for (auto& sg : e->graphs)
+            if (sg.n == n && sg.n_logit_rows == n_logit_rows && sg.ctx == ctx_grid && sg.head == head && sg.gen == gen)
+                g = &sg;
+        if (!g) {
+            hipGraph_t graph = nullptr;
+            QH_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+            const int rc = enqueue(ctx_grid);
+            const hipError_t ec = hipStreamEndCapture(s, &graph);
+            if (rc != QRAF_HIP_OK) {
+                if (graph) hipGraphDestroy(graph);
+                return rc;
+            }
+            QH_CHECK_HIP(ec);
+            hipGraphExec_t exec = nullptr;
+            const hipError_t ei = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+            hipGraphDestroy(graph);
+            QH_CHECK_HIP(ei);
+            if (e->graphs.size() >= MAX_STEP_GRAPHS) {  // evict the least recently used
+                auto lru = std::min_element(e->graphs.begin(), e->graphs.end(),
+                                            [](const qraf_engine::StepGraph& a, const qraf_engine::StepGraph& b) {
+                                                return a.used < b.used;
+                                            });
+                hipGraphExecDestroy(lru->exec);
+                e->graphs.erase(lru);
+            }
+            qraf_engine::StepGraph sg;
+            sg.n = n;
+            sg.n_logit_rows = n_logit_rows;
+            sg.ctx = ctx_grid;
+            sg.head = head;
+            sg.gen = gen;
+            sg.exec = exec;
+            e->graphs.push_back(sg);
+            g = &e->graphs.back();
+        }
+        g->used = ++e->graph_clock;
+        QH_CHECK_HIP(hipGraphLaunch(g->exec, s));
+    } else {
+        QH_TRY(enqueue(step_ctx));
     }
+    if (head && logits)
+        QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_rows * V * 4, hipMemcpyDeviceToHost, s));
+    if (head && next_tokens)
+        QH_CHECK_HIP(hipMemcpyAsync(next_tokens, e->amax, (size_t)n_logit_rows * 4, hipMemcpyDeviceToHost, s));
     QH_CHECK_HIP(hipStreamSynchronize(s));
+    return QRAF_HIP_OK;
+}
+
+// Graph capture and replay of steps (on by default); off: every step launches eagerly.
+int qraf_engine_set_graphs(qraf_engine* e, int32_t on) {
+    clear_error();
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "set_graphs: null engine");
+    QH_CHECK_HIP(hipStreamSynchronize(e->stream));
+    e->use_graphs = on != 0;
+    if (!e->use_graphs) e->drop_graphs();
     return QRAF_HIP_OK;
 }
 

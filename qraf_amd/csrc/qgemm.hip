@@ -706,6 +706,7 @@ int set_qgemm_tuning(int waves, int splits, int pipe) {
     g_qg_waves = waves;
     g_qg_splits = splits;
     g_qg_pipe = pipe;
+    bump_tuning_generation();
     return QRAF_HIP_OK;
 }
 

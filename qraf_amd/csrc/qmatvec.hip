@@ -20,6 +20,8 @@
 // fp32; each wave reduces its R rows with a transposing butterfly.
 #include "common.h"
 
+#include <atomic>
+
 namespace qraf_hip {
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4), aligned(4)));
@@ -620,6 +622,10 @@ static int g_rows_per_wave = 0;  // 0: automatic; else 1, 2, 4 or 8
 static int g_kernel = 0;         // 0: automatic, 1: one-shot, 2: persistent streaming, 3 / 4: ring, 8 / 4 waves per workgroup
 static int g_wgs_per_cu = 0;     // persistent / ring grid size per CU (0: automatic)
 
+static std::atomic<uint32_t> g_tuning_gen{0};
+uint32_t tuning_generation() { return g_tuning_gen.load(std::memory_order_relaxed); }
+void bump_tuning_generation() { g_tuning_gen.fetch_add(1, std::memory_order_relaxed); }
+
 int set_matvec_tuning(int kernel, int r, int wgs_per_cu) {
     QH_REQUIRE(r == 0 || r == 1 || r == 2 || r == 4 || r == 8, QRAF_HIP_ERR_INVALID,
                "rows per wave must be 0 (auto), 1, 2, 4 or 8");
@@ -628,6 +634,7 @@ int set_matvec_tuning(int kernel, int r, int wgs_per_cu) {
     g_rows_per_wave = r;
     g_kernel = kernel;
     g_wgs_per_cu = wgs_per_cu;
+    bump_tuning_generation();
     return QRAF_HIP_OK;
 }
 

@@ -67,6 +67,10 @@ class Engine:
     def finalize(self):
         call("qraf_engine_finalize", self.h)
 
+    def set_graphs(self, on: bool):
+        """Replay captured step graphs (default) or launch every step eagerly."""
+        call("qraf_engine_set_graphs", self.h, int(bool(on)))
+
     def seq_create(self) -> int:
         i = C.c_int32()
         call("qraf_engine_seq_create", self.h, C.byref(i))

@@ -194,6 +194,44 @@ def test_batched_logits_and_chunked_prefill(hip):
     e.close()
 
 
+@pytest.mark.parametrize("name", ["q8_hd64_gqa3", "q4_gqa8_hd128"])
+def test_step_graph_replay_equals_eager(hip, name):
+    """Captured step graphs (the default) against eager launches of the same
+    steps: bit-identical logits, for batch-1 decode across context buckets
+    (positions up to 300 cross the 256-position bound) and for batched
+    chunked-prefill steps; every graph is replayed several times with eager
+    steps and host synchronisation in between."""
+    from qraf_amd.engine import Engine
+    kw, seed = SMALL[name]
+    m = oracle_model(kw, seed)
+    L = po.lib()
+    toks = [L.or_gen_token(seed + 5, i, kw["vocab"]) for i in range(300)]
+    runs = []
+    for graphs in (True, False):
+        e = Engine(engine_config(dict(kw, max_seq=512)), kv_dtype=po.F16, max_batch=8)
+        for tname, dt, shape, data in m.tensors():
+            e.set_tensor(tname, dt, shape, data)
+        e.finalize()
+        e.set_graphs(graphs)
+        a, b = e.seq_create(), e.seq_create()
+        out = []
+        # b: prefill in 4-row chunks alongside a's single rows (mixed shapes)
+        for i in range(0, 40, 4):
+            lg, _ = e.step([a] + [b] * 4, [toks[i // 4]] + toks[i:i + 4], [i // 4] + list(range(i, i + 4)),
+                           logits=True, argmax=False)
+            out.append(lg.copy())
+        # a: batch-1 decode to position 300 (graph replays within each bucket)
+        for p in range(10, 300):
+            lg, _ = e.step([a], [toks[p]], [p], logits=True, argmax=False)
+            if p % 7 == 0 or p in (255, 256, 257):
+                out.append(lg.copy())
+        runs.append(out)
+        e.close()
+    assert len(runs[0]) == len(runs[1])
+    for k, (g, x) in enumerate(zip(*runs)):
+        assert np.array_equal(g.view(np.uint32), x.view(np.uint32)), f"{name}: step {k} differs"
+
+
 def test_page_exhaustion_is_clean(hip):
     from qraf_amd.engine import Engine
     kw, seed = SMALL["q8_llama"]
