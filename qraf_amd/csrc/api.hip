@@ -85,12 +85,6 @@ static int staging(int i, size_t bytes, void** out) {
 
 using namespace qraf_hip;
 
-#define QH_TRY(expr)                        \
-    do {                                    \
-        int rc_ = (expr);                   \
-        if (rc_ != QRAF_HIP_OK) return rc_; \
-    } while (0)
-
 extern "C" {
 
 const char* qraf_hip_last_error(void) { return g_err; }

@@ -544,12 +544,6 @@ static int launch_attn_t(const AttnArgs& a, int hd, int G, int grid_x, hipStream
     return set_error(QRAF_HIP_ERR_INVALID, "attention: unsupported head_dim %d / group %d", hd, G);
 }
 
-#define QH_TRY_ATTN(expr)                   \
-    do {                                    \
-        int rc_ = (expr);                   \
-        if (rc_ != QRAF_HIP_OK) return rc_; \
-    } while (0)
-
 size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx) {
     const size_t items = (size_t)n * ((max_ctx + ACH - 1) / ACH);
     return items * H * hd * 4 + items * H * 2 * 4 + (size_t)n * Hkv * 4 + 256;
@@ -593,7 +587,7 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     a.scale = scale;
     const int G = H / Hkv;
     if (kv_dtype == DT_F32) {
-        QH_TRY_ATTN(launch_attn_t<float>(a, hd, G, items, st));
+        QH_TRY(launch_attn_t<float>(a, hd, G, items, st));
     } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0) {
         const dim3 grid(items, Hkv);
         if (hd == 128)
@@ -602,7 +596,7 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
             hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(ACH), 0, st, a, G);
         QH_CHECK_HIP(hipGetLastError());
     } else {
-        QH_TRY_ATTN(launch_attn_t<_Float16>(a, hd, G, items, st));
+        QH_TRY(launch_attn_t<_Float16>(a, hd, G, items, st));
     }
     if (max_ctx > ACH) {  // some sequence may span several chunks
         hipLaunchKernelGGL(attn_merge_kernel, dim3(n, Hkv), dim3(ACH), 0, st, a, G, hd);

@@ -31,6 +31,13 @@ void clear_error();
         if (!(cond)) return ::qraf_hip::set_error(code, __VA_ARGS__); \
     } while (0)
 
+// Propagates a failed status (the error text is already set).
+#define QH_TRY(expr)                        \
+    do {                                    \
+        int rc_ = (expr);                   \
+        if (rc_ != QRAF_HIP_OK) return rc_; \
+    } while (0)
+
 // Bytes of one quantized block (reference quantize.cpp:107, :146).
 __host__ __device__ inline size_t q_block_bytes(uint32_t dtype, int bs) {
     if (dtype == DT_Q8_0) return 4 + (size_t)bs;
@@ -44,8 +51,22 @@ __host__ __device__ inline size_t q_row_bytes(uint32_t dtype, int bs, uint32_t i
 
 // Kernel launchers (device pointers; stream-ordered; no synchronisation).
 // add (optional, may alias y): y[i] = dot(row_i, x) + add[i]
+// How a batch-1 matvec forms its x while staging it, instead of a separate
+// kernel writing x first (x then names the source):
+//   XP_NONE       x as is
+//   XP_NORM       rms_norm(x) * w  (ops.cpp:107-118), x of K elements
+//   XP_SILU_GATE  silu(x[2i]) * x[2i+1]  (x: interleaved gate/up rows, 2K elements)
+// Kernels that cannot form x themselves get it from a prep kernel writing
+// `xbuf` (K floats) first.
+enum { XP_NONE = 0, XP_NORM = 1, XP_SILU_GATE = 2 };
+struct MvPrep {
+    int op = XP_NONE;
+    const float* w = nullptr;  // XP_NORM weights
+    float eps = 0.f;           // XP_NORM epsilon
+    float* xbuf = nullptr;     // scratch for the prep-kernel fallback
+};
 int launch_matvec_q(const void* W, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x,
-                    float* y, hipStream_t s, const float* add = nullptr);
+                    float* y, hipStream_t s, const float* add = nullptr, const MvPrep* prep = nullptr);
 int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s,
                       const float* add = nullptr);
 int set_matvec_tuning(int kernel, int rows, int wgs_per_cu);
@@ -69,6 +90,9 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t* hi, uint16_t* lo) 
     *hi = (uint16_t)h;
     *lo = (uint16_t)f32_to_bf16_rne(v - __builtin_bit_cast(float, h << 16));
 }
+
+// SiLU-gate of one gate/up pair (ops.cpp:218-222 then :275-279): silu(g) * u
+__device__ __forceinline__ float silu_gate(float g, float u) { return __fmul_rn(g / (1.0f + expf(-g)), u); }
 
 // element e of S slices (GEMM split-K partials) of `slice` floats, summed in
 // slice order; loads go out 8 slices at a time

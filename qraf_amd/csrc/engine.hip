@@ -150,7 +150,7 @@ __global__ void silu_gate_kernel(const float* __restrict__ gu, int F, int n, flo
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += (size_t)gridDim.x * blockDim.x) {
         const size_t s = i / F, j = i % F;
         const float g = gu[s * 2 * F + 2 * j], u = gu[s * 2 * F + 2 * j + 1];
-        act[i] = __fmul_rn(g / (1.0f + expf(-g)), u);
+        act[i] = silu_gate(g, u);
     }
 }
 
@@ -383,12 +383,6 @@ static int ealloc(qraf_engine* e, void** p, size_t bytes) {
     e->allocs.push_back(*p);
     return QRAF_HIP_OK;
 }
-
-#define QH_TRY(expr)                        \
-    do {                                    \
-        int rc_ = (expr);                   \
-        if (rc_ != QRAF_HIP_OK) return rc_; \
-    } while (0)
 
 static size_t dt_row_bytes(uint32_t dt, uint32_t cols) {
     if (dt == DT_F32) return (size_t)cols * 4;
@@ -893,8 +887,21 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
 
     // y[n][N] = x[n][K] * W^T (+ add): matvec at batch 1, else the matrix-core GEMM
     // Wt: the tile-major copy (batched steps); K not a multiple of 32: one matvec per row
+    // prep (optional): x is formed from its source first (norm or SiLU-gate):
+    // inside the matvec at batch 1, else by a kernel writing prep->xbuf
     auto proj = [&](const uint8_t* W, const uint8_t* Wt, uint32_t dt, int N, int K, const float* x, int rows, float* y,
-                    const float* add) -> int {
+                    const float* add, const MvPrep* prep = nullptr) -> int {
+        if (prep && (dt == DT_F32 || rows != 1)) {
+            if (prep->op == XP_NORM)
+                hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, s, x, prep->w, K, prep->eps,
+                                   prep->xbuf, nullptr);
+            else
+                hipLaunchKernelGGL(silu_gate_kernel, dim3(std::min((rows * K + 255) / 256, 4096)), dim3(256), 0, s, x,
+                                   K, rows, prep->xbuf);
+            QH_CHECK_HIP(hipGetLastError());
+            x = prep->xbuf;
+            prep = nullptr;
+        }
         if (dt == DT_F32) {
             for (int r = 0; r < rows; r++)
                 QH_TRY(launch_matvec_f32((const float*)W, x + (size_t)r * K, y + (size_t)r * N, N, K, s,
@@ -904,7 +911,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         if (rows == 1 || !Wt) {
             for (int r = 0; r < rows; r++)
                 QH_TRY(launch_matvec_q(W, dt, 32, N, K, x + (size_t)r * K, y + (size_t)r * N, s,
-                                       add ? add + (size_t)r * N : nullptr));
+                                       add ? add + (size_t)r * N : nullptr, prep));
             return QRAF_HIP_OK;
         }
         QH_TRY(launch_split_bf16(x, e->xh, e->xl, rows, K, 0, nullptr, s));
@@ -951,21 +958,18 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
             qraf_engine::Layer& L = e->layers[l];
             uint8_t* kc = e->kpool + (size_t)l * e->layer_kv_bytes;
             uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;
-            hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.an, D, c.rms_norm_eps, e->xn,
-                               nullptr);
-            QH_TRY(proj(L.wqkv, L.wqkv_t, L.dt_attn, e->qkvd, D, e->xn, n, e->qkv, nullptr));
+            const MvPrep attn_norm{XP_NORM, L.an, c.rms_norm_eps, e->xn};  // transformer.cpp:586
+            QH_TRY(proj(L.wqkv, L.wqkv_t, L.dt_attn, e->qkvd, D, e->h, n, e->qkv, nullptr, &attn_norm));
             QH_TRY(launch_rope_append(e->qkv, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
                                       e->o.kv_dtype, d_ptab, MP, ps, s));
             QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale, ctx_grid,
                                     e->att, e->attn_ws, e->attn_ws_bytes, s));
             QH_TRY(proj(L.wo, L.wo_t, L.dt_attn, D, e->qd, e->att, n, e->h, e->h));  // + residual (transformer.cpp:593)
-            hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n), dim3(256), 0, s, e->h, L.fn, D, c.rms_norm_eps, e->xn,
-                               nullptr);
-            QH_TRY(proj(L.wgu, L.wgu_t, L.dt_mlp, 2 * F, D, e->xn, n, e->gu, nullptr));
+            const MvPrep ffn_norm{XP_NORM, L.fn, c.rms_norm_eps, e->xn};  // transformer.cpp:595
+            QH_TRY(proj(L.wgu, L.wgu_t, L.dt_mlp, 2 * F, D, e->h, n, e->gu, nullptr, &ffn_norm));
             if (n == 1 || !L.wd_t) {
-                hipLaunchKernelGGL(silu_gate_kernel, dim3(std::min((n * F + 255) / 256, 4096)), dim3(256), 0, s, e->gu, F,
-                                   n, e->act);
-                QH_TRY(proj(L.wd, L.wd_t, L.dt_mlp, D, F, e->act, n, e->h, e->h));  // + residual (transformer.cpp:601)
+                const MvPrep gate{XP_SILU_GATE, nullptr, 0.f, e->act};  // attention.cpp:172-183
+                QH_TRY(proj(L.wd, L.wd_t, L.dt_mlp, D, F, e->gu, n, e->h, e->h, &gate));  // + residual (transformer.cpp:601)
             } else {
                 QH_TRY(launch_split_bf16(e->gu, e->xh, e->xl, n, F, 1, nullptr, s));  // SiLU-gate fused into the split
                 QH_TRY(launch_qgemm(L.wd_t, L.dt_mlp, 32, D, F, e->xh, e->xl, n, e->h, e->h, e->gemm_ws, e->gemm_ws_bytes, s,
@@ -975,11 +979,16 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         QH_CHECK_HIP(hipGetLastError());
         if (head) {
             // final norm of the rows that want logits (transformer.cpp:605), then the head
-            hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n_logit_rows), dim3(256), 0, s, e->h, e->onorm, D,
-                               c.rms_norm_eps, e->xhead, d_lrows);
             const uint8_t* W = e->head ? e->head : e->embed;  // tied head reads the embedding (transformer.cpp:392-400)
             const uint32_t dt = e->head ? e->dt_head : e->dt_embed;
-            QH_TRY(proj(W, e->head_t, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
+            if (n == 1 && dt != DT_F32) {
+                const MvPrep out_norm{XP_NORM, e->onorm, c.rms_norm_eps, e->xhead};
+                QH_TRY(proj(W, e->head_t, dt, V, D, e->h, 1, e->logits, nullptr, &out_norm));
+            } else {
+                hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n_logit_rows), dim3(256), 0, s, e->h, e->onorm, D,
+                                   c.rms_norm_eps, e->xhead, d_lrows);
+                QH_TRY(proj(W, e->head_t, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
+            }
             hipLaunchKernelGGL(argmax_chunk_kernel, dim3(ARGMAX_CHUNKS, n_logit_rows), dim3(256), 0, s, e->logits, V,
                                e->am_val, e->am_idx);
             hipLaunchKernelGGL(argmax_final_kernel, dim3(n_logit_rows), dim3(64), 0, s, e->am_val, e->am_idx, V, e->amax);

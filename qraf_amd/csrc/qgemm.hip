@@ -58,7 +58,7 @@ __global__ void split_bf16_kernel(const float* __restrict__ x, uint16_t* __restr
             const size_t m = i / K, k = i % K;
             const size_t e = m * 2 * K + 2 * k;
             const float g = sum_slices(x, S, slice, e), u = sum_slices(x, S, slice, e + 1);
-            v = __fmul_rn(g / (1.0f + expf(-g)), u);
+            v = silu_gate(g, u);
             if (xout) xout[i] = v;
         } else {
             v = sum_slices(x, S, slice, i);

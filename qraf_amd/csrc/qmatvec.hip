@@ -154,17 +154,57 @@ __device__ __forceinline__ void q4_compute(const Units<R>& w, const float* xu, f
     }
 }
 
-template <int FMT>
-__device__ __forceinline__ void stage_x(float* sx, const float* __restrict__ x, int K, int nb) {
+// ---- forming x while staging it (MvPrep): element i of x from its source
+template <int XP>
+__device__ __forceinline__ float x_elem(const float* __restrict__ x, int i, float r, const float* __restrict__ w) {
+    if (XP == XP_NORM) return __fmul_rn(__fmul_rn(x[i], r), w[i]);
+    if (XP == XP_SILU_GATE) return silu_gate(x[2 * i], x[2 * i + 1]);
+    return x[i];
+}
+// elements i..i+3 (i % 4 == 0, i + 3 < K, x and w 16-byte aligned)
+template <int XP>
+__device__ __forceinline__ f32x4 x_vec4(const float* __restrict__ x, int i, float r, const float* __restrict__ w) {
+    if (XP == XP_SILU_GATE) {
+        const f32x4 a = *(const f32x4*)(x + 2 * i), b = *(const f32x4*)(x + 2 * i + 4);
+        return f32x4{silu_gate(a[0], a[1]), silu_gate(a[2], a[3]), silu_gate(b[0], b[1]), silu_gate(b[2], b[3])};
+    }
+    f32x4 v = *(const f32x4*)(x + i);
+    if (XP == XP_NORM) {
+        const f32x4 ww = *(const f32x4*)(w + i);
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = __fmul_rn(__fmul_rn(v[e], r), ww[e]);
+    }
+    return v;
+}
+// 1 / sqrt(mean(x^2) + eps) for a 256-thread workgroup: the reduction of the
+// engine's rmsnorm_rows_kernel (strided fma per thread, wave butterfly, the
+// four waves in pairs), so a fused norm equals the separate one bit for bit
+__device__ __forceinline__ float norm_r_256(const float* __restrict__ x, int K, float eps) {
+    __shared__ float red[4];
+    float ss = 0.f;
+    for (int i = threadIdx.x; i < K; i += 256) ss = __builtin_fmaf(x[i], x[i], ss);
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    return 1.0f / sqrtf(ss / (float)K + eps);
+}
+
+template <int FMT, int XP = XP_NONE>
+__device__ __forceinline__ void stage_x(float* sx, const float* __restrict__ x, int K, int nb,
+                                        const float* __restrict__ xw = nullptr, float eps = 0.f) {
+    const float r = XP == XP_NORM ? norm_r_256(x, K, eps) : 1.f;
+    const bool vec = (((uintptr_t)x) & 15) == 0 && (XP != XP_NORM || (((uintptr_t)xw) & 15) == 0);
     if (FMT == 8) {
         // thread t stages elements 4t..4t+3 (one float4, inside one block)
         for (int i = threadIdx.x * 4; i < nb * 32; i += WG * 4) {
             f32x4 v;
-            if (i + 3 < K && ((((uintptr_t)x) & 15) == 0)) {
-                v = *(const f32x4*)(x + i);
+            if (i + 3 < K && vec) {
+                v = x_vec4<XP>(x, i, r, xw);
             } else {
 #pragma unroll
-                for (int e = 0; e < 4; e++) v[e] = (i + e < K) ? x[i + e] : 0.f;
+                for (int e = 0; e < 4; e++) v[e] = (i + e < K) ? x_elem<XP>(x, i + e, r, xw) : 0.f;
             }
             *(f32x4*)(sx + (i >> 5) * XS8 + (i & 31)) = v;
         }
@@ -178,13 +218,13 @@ __device__ __forceinline__ void stage_x(float* sx, const float* __restrict__ x, 
             const int t = base + threadIdx.x;
             const int i = t * 8;
             float v[8];
-            if (t < nthr && i + 7 < Keff && ((((uintptr_t)x) & 15) == 0)) {
-                f32x4 a = *(const f32x4*)(x + i), b = *(const f32x4*)(x + i + 4);
+            if (t < nthr && i + 7 < Keff && vec) {
+                f32x4 a = x_vec4<XP>(x, i, r, xw), b = x_vec4<XP>(x, i + 4, r, xw);
                 v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3];
                 v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; e++) v[e] = (t < nthr && i + e < Keff) ? x[i + e] : 0.f;
+                for (int e = 0; e < 8; e++) v[e] = (t < nthr && i + e < Keff) ? x_elem<XP>(x, i + e, r, xw) : 0.f;
             }
             float part = ((v[0] + v[2]) + (v[4] + v[6])) + ((v[1] + v[3]) + (v[5] + v[7]));
             part += __shfl_xor(part, 1);
@@ -204,7 +244,8 @@ __device__ __forceinline__ void stage_x(float* sx, const float* __restrict__ x, 
 template <int FMT, int R>
 __global__ __launch_bounds__(WG) void qmv_stream_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
                                                      int K, int nb, const float* __restrict__ x,
-                                                     float* __restrict__ y, const float* __restrict__ add) {
+                                                     float* __restrict__ y, const float* __restrict__ add,
+                                                     const float*, float) {
     extern __shared__ __align__(16) float sx[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * R;
@@ -250,10 +291,11 @@ __global__ __launch_bounds__(WG) void qmv_stream_kernel(const uint8_t* __restric
 // few microseconds long, and a load -> use -> load chain per wave would pay
 // the HBM latency several times.
 // ----------------------------------------------------------------------------
-template <int FMT, int R, int J>
+template <int FMT, int R, int J, int XP = XP_NONE>
 __global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
                                                         int K, int nb, const float* __restrict__ x,
-                                                        float* __restrict__ y, const float* __restrict__ add) {
+                                                        float* __restrict__ y, const float* __restrict__ add,
+                                                        const float* __restrict__ xw, float eps) {
     extern __shared__ __align__(16) float sx[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * R;
@@ -267,7 +309,7 @@ __global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restri
 #pragma unroll
     for (int j = 0; j < J; j++) load_units<R>(w[j], rowp, min(lane + 64 * j, U - 1));
 
-    stage_x<FMT>(sx, x, K, nb);
+    stage_x<FMT, XP>(sx, x, K, nb, xw, eps);
     __syncthreads();
 
     float acc[R];
@@ -295,7 +337,8 @@ __global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restri
 template <int FMT, int R>
 __global__ __launch_bounds__(WG) void qmv_persist_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
                                                         int K, int nb, const float* __restrict__ x,
-                                                        float* __restrict__ y, const float* __restrict__ add) {
+                                                        float* __restrict__ y, const float* __restrict__ add,
+                                                        const float*, float) {
     extern __shared__ __align__(16) float sx[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int U = FMT == 8 ? nb : nb >> 1;
@@ -419,10 +462,10 @@ __device__ __forceinline__ void q4_compute_masked(const Units<R>& w, const float
     for (int r = 0; r < R; r++) acc[r] = valid ? t[r] : acc[r];
 }
 
-template <int FMT, int R, int XJ, int D, int NW>
+template <int FMT, int R, int XJ, int D, int NW, int XP = XP_NONE>
 __global__ __launch_bounds__(64 * NW) void qmv_ring_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
                                                           int K, int nb, const float* __restrict__ x, float* y,
-                                                          const float* add) {
+                                                          const float* add, const float* __restrict__ xw, float eps) {
     extern __shared__ __align__(16) float sx[];
     constexpr int NT = 64 * NW;
     const int lane = threadIdx.x & 63;
@@ -443,19 +486,67 @@ __global__ __launch_bounds__(64 * NW) void qmv_ring_kernel(const uint8_t* __rest
         addv[i] = add ? add[min((gw + i * nw) * R + rr, N - 1)] : 0.f;
 
     // 1. x loads.  Q8: float4 f = t + NT i holds elements 4f..4f+3;
-    //    Q4: 8-element group g = t + NT i.  (K % 32 == 0, x 16-byte aligned.)
+    //    Q4: 8-element group g = t + NT i = float4s 2g, 2g+1.  (K % 32 == 0,
+    //    x 16-byte aligned.)  Slot k of xr holds x float4 xf[k]; the source
+    //    is read raw first (twice the floats for the SiLU-gate), then x formed.
     constexpr int XL = FMT == 8 ? XJ : 2 * XJ;
-    f32x4 xr[XL];
+    constexpr int SL = XP == XP_SILU_GATE ? 2 * XL : XL;
     const int n4 = K >> 2;
+    int xf[XL];
+    bool xok[XL];
 #pragma unroll
     for (int i = 0; i < XJ; i++) {
         if (FMT == 8) {
-            xr[i] = *(const f32x4*)(x + 4 * min(t + NT * i, n4 - 1));
+            xok[i] = t + NT * i < n4;
+            xf[i] = min(t + NT * i, n4 - 1);
         } else {
-            const int g = min(t + NT * i, (n4 >> 1) - 1);
-            xr[2 * i] = *(const f32x4*)(x + 8 * g);
-            xr[2 * i + 1] = *(const f32x4*)(x + 8 * g + 4);
+            const int g = t + NT * i;
+            xok[2 * i] = xok[2 * i + 1] = g < (n4 >> 1);
+            xf[2 * i] = 2 * min(g, (n4 >> 1) - 1);
+            xf[2 * i + 1] = xf[2 * i] + 1;
         }
+    }
+    f32x4 raw[SL];
+    f32x4 wr[XP == XP_NORM ? XL : 1];
+#pragma unroll
+    for (int k = 0; k < XL; k++) {
+        if (XP == XP_SILU_GATE) {
+            raw[2 * k] = *(const f32x4*)(x + 8 * xf[k]);
+            raw[2 * k + 1] = *(const f32x4*)(x + 8 * xf[k] + 4);
+        } else {
+            raw[k] = *(const f32x4*)(x + 4 * xf[k]);
+            if (XP == XP_NORM) wr[k] = *(const f32x4*)(xw + 4 * xf[k]);
+        }
+    }
+    f32x4 xr[XL];
+    if (XP == XP_NORM) {
+        // 1 / sqrt(mean(x^2) + eps): this thread's elements, then the waves in order
+        __shared__ float red[NW];
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < XL; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) ss = xok[k] ? __builtin_fmaf(raw[k][e], raw[k][e], ss) : ss;
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        ss = red[0];
+#pragma unroll
+        for (int w = 1; w < NW; w++) ss += red[w];
+        const float r = 1.0f / sqrtf(ss / (float)K + eps);
+#pragma unroll
+        for (int k = 0; k < XL; k++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) xr[k][e] = __fmul_rn(__fmul_rn(raw[k][e], r), wr[k][e]);
+    } else if (XP == XP_SILU_GATE) {
+#pragma unroll
+        for (int k = 0; k < XL; k++)
+            xr[k] = f32x4{silu_gate(raw[2 * k][0], raw[2 * k][1]), silu_gate(raw[2 * k][2], raw[2 * k][3]),
+                          silu_gate(raw[2 * k + 1][0], raw[2 * k + 1][1]), silu_gate(raw[2 * k + 1][2], raw[2 * k + 1][3])};
+    } else {
+#pragma unroll
+        for (int k = 0; k < XL; k++) xr[k] = raw[k];
     }
     // 2. x into LDS (Q8: 36-float blocks; Q4: block pairs, even/odd elements
     //    permuted, plus block sums), the layout stage_x builds.
@@ -649,7 +740,8 @@ static int cu_count() {
     return n;
 }
 
-typedef void (*qmv_fn)(const uint8_t*, uint32_t, int, int, int, const float*, float*, const float*);
+typedef void (*qmv_fn)(const uint8_t*, uint32_t, int, int, int, const float*, float*, const float*, const float*,
+                       float);
 
 // workgroups of `threads` threads and `lds` bytes of LDS that fit on one CU at
 // once (cached per kernel and LDS size: the launch path calls this per matvec)
@@ -667,37 +759,43 @@ static hipError_t resident_wgs(const void* kf, int threads, size_t lds, int* out
     return hipSuccess;
 }
 
-template <int FMT, int R, int J>
+// one-shot instances: R * J <= 8; with x formed in the kernel (XP) for J <= 4
+template <int FMT, int R, int J, int XP>
 static qmv_fn oneshot_if_valid() {
-    if constexpr (R * J <= 8) return qmv_oneshot_kernel<FMT, R, J>;
+    if constexpr (R * J <= 8 && (XP == XP_NONE || J <= 4)) return qmv_oneshot_kernel<FMT, R, J, XP>;
     else return nullptr;
 }
-
-template <int FMT, int R>
+template <int FMT, int R, int XP>
 static qmv_fn pick_oneshot(int J) {
     switch (J) {
-        case 1: return oneshot_if_valid<FMT, R, 1>();
-        case 2: return oneshot_if_valid<FMT, R, 2>();
-        case 3: return oneshot_if_valid<FMT, R, 3>();
-        case 4: return oneshot_if_valid<FMT, R, 4>();
-        case 5: return oneshot_if_valid<FMT, R, 5>();
-        case 6: return oneshot_if_valid<FMT, R, 6>();
-        case 7: return oneshot_if_valid<FMT, R, 7>();
-        case 8: return oneshot_if_valid<FMT, R, 8>();
+        case 1: return oneshot_if_valid<FMT, R, 1, XP>();
+        case 2: return oneshot_if_valid<FMT, R, 2, XP>();
+        case 3: return oneshot_if_valid<FMT, R, 3, XP>();
+        case 4: return oneshot_if_valid<FMT, R, 4, XP>();
+        case 5: return oneshot_if_valid<FMT, R, 5, XP>();
+        case 6: return oneshot_if_valid<FMT, R, 6, XP>();
+        case 7: return oneshot_if_valid<FMT, R, 7, XP>();
+        case 8: return oneshot_if_valid<FMT, R, 8, XP>();
         default: return nullptr;
     }
 }
-
-template <int FMT>
-static qmv_fn pick_kernel(int R, int J) {
-    if (J <= 8) {
-        switch (R) {
-            case 1: return pick_oneshot<FMT, 1>(J);
-            case 2: return pick_oneshot<FMT, 2>(J);
-            case 4: return pick_oneshot<FMT, 4>(J);
-            default: return pick_oneshot<FMT, 8>(J);
-        }
+template <int FMT, int XP>
+static qmv_fn pick_oneshot_r(int R, int J) {
+    switch (R) {
+        case 1: return pick_oneshot<FMT, 1, XP>(J);
+        case 2: return pick_oneshot<FMT, 2, XP>(J);
+        case 4: return pick_oneshot<FMT, 4, XP>(J);
+        default: return pick_oneshot<FMT, 8, XP>(J);
     }
+}
+template <int FMT>
+static qmv_fn pick_oneshot_xp(int R, int J, int xp) {
+    if (xp == XP_NORM) return pick_oneshot_r<FMT, XP_NORM>(R, J);
+    if (xp == XP_SILU_GATE) return pick_oneshot_r<FMT, XP_SILU_GATE>(R, J);
+    return pick_oneshot_r<FMT, XP_NONE>(R, J);
+}
+template <int FMT>
+static qmv_fn pick_stream(int R) {
     switch (R) {
         case 1: return qmv_stream_kernel<FMT, 1>;
         case 2: return qmv_stream_kernel<FMT, 2>;
@@ -706,28 +804,75 @@ static qmv_fn pick_kernel(int R, int J) {
 }
 
 // ring kernel instances: XJ in {1, 2, 4, 8, 12} (x loads per thread, rounded
-// up; the extra loads are clamped duplicates), R in {1, 2}, D = 2, NW in {4, 8}
-template <int FMT, int R, int NW>
+// up; the extra loads are clamped duplicates), R in {1, 2}, D = 2, NW in
+// {4, 8}; x formed in the kernel (XP) with NW = 8 only
+template <int FMT, int R, int NW, int XP>
 static qmv_fn pick_ring_xj(int xj) {
-    if (xj <= 1) return qmv_ring_kernel<FMT, R, 1, 2, NW>;
-    if (xj <= 2) return qmv_ring_kernel<FMT, R, 2, 2, NW>;
-    if (xj <= 4) return qmv_ring_kernel<FMT, R, 4, 2, NW>;
-    if (xj <= 8) return qmv_ring_kernel<FMT, R, 8, 2, NW>;
-    if (xj <= 12) return qmv_ring_kernel<FMT, R, 12, 2, NW>;
-    return nullptr;
+    if constexpr (NW == 4 && XP != XP_NONE) {
+        return nullptr;
+    } else {
+        if (xj <= 1) return qmv_ring_kernel<FMT, R, 1, 2, NW, XP>;
+        if (xj <= 2) return qmv_ring_kernel<FMT, R, 2, 2, NW, XP>;
+        if (xj <= 4) return qmv_ring_kernel<FMT, R, 4, 2, NW, XP>;
+        if (xj <= 8) return qmv_ring_kernel<FMT, R, 8, 2, NW, XP>;
+        if (xj <= 12) return qmv_ring_kernel<FMT, R, 12, 2, NW, XP>;
+        return nullptr;
+    }
+}
+template <int FMT, int XP>
+static qmv_fn pick_ring_r(int R, int NW, int xj) {
+    if (R == 1) return NW == 4 ? pick_ring_xj<FMT, 1, 4, XP>(xj) : pick_ring_xj<FMT, 1, 8, XP>(xj);
+    return NW == 4 ? pick_ring_xj<FMT, 2, 4, XP>(xj) : pick_ring_xj<FMT, 2, 8, XP>(xj);
 }
 template <int FMT>
-static qmv_fn pick_ring(int R, int NW, int xj) {
-    if (R == 1) return NW == 4 ? pick_ring_xj<FMT, 1, 4>(xj) : pick_ring_xj<FMT, 1, 8>(xj);
-    return NW == 4 ? pick_ring_xj<FMT, 2, 4>(xj) : pick_ring_xj<FMT, 2, 8>(xj);
+static qmv_fn pick_ring(int R, int NW, int xj, int xp) {
+    if (xp == XP_NORM) return pick_ring_r<FMT, XP_NORM>(R, NW, xj);
+    if (xp == XP_SILU_GATE) return pick_ring_r<FMT, XP_SILU_GATE>(R, NW, xj);
+    return pick_ring_r<FMT, XP_NONE>(R, NW, xj);
+}
+
+// x formed by a kernel of its own (for the matvec kernels that cannot form it)
+__global__ __launch_bounds__(256) void xprep_norm_kernel(const float* __restrict__ x, const float* __restrict__ w, int K,
+                                                         float eps, float* __restrict__ out) {
+    const float r = norm_r_256(x, K, eps);
+    for (int i = threadIdx.x; i < K; i += 256) out[i] = __fmul_rn(__fmul_rn(x[i], r), w[i]);
+}
+__global__ void xprep_silu_gate_kernel(const float* __restrict__ x, int K, float* __restrict__ out) {
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < K; i += gridDim.x * blockDim.x)
+        out[i] = silu_gate(x[2 * i], x[2 * i + 1]);
+}
+static int launch_xprep(const float* x, const MvPrep& p, int K, hipStream_t s) {
+    QH_REQUIRE(p.xbuf, QRAF_HIP_ERR_INVALID, "matvec: this kernel needs a scratch buffer to form x");
+    if (p.op == XP_NORM) {
+        QH_REQUIRE(p.w, QRAF_HIP_ERR_INVALID, "matvec: norm weights missing");
+        hipLaunchKernelGGL(xprep_norm_kernel, dim3(1), dim3(256), 0, s, x, p.w, K, p.eps, p.xbuf);
+    } else {
+        hipLaunchKernelGGL(xprep_silu_gate_kernel, dim3(std::min((K + 255) / 256, 1024)), dim3(256), 0, s, x, K, p.xbuf);
+    }
+    QH_CHECK_HIP(hipGetLastError());
+    return QRAF_HIP_OK;
 }
 
 int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x, float* y,
-                    hipStream_t s, const float* add) {
+                    hipStream_t s, const float* add, const MvPrep* prep) {
     QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "unsupported weight dtype %u", dtype);
     QH_REQUIRE(bs > 0 && bs <= 4096, QRAF_HIP_ERR_INVALID, "bad block size %d", bs);
     QH_REQUIRE(K > 0 && N > 0, QRAF_HIP_ERR_INVALID, "empty matvec (%u x %u)", N, K);
     QH_REQUIRE(Wv && x && y, QRAF_HIP_ERR_INVALID, "null pointer");
+    int xp = prep ? prep->op : XP_NONE;
+    QH_REQUIRE(xp == XP_NONE || xp == XP_NORM || xp == XP_SILU_GATE, QRAF_HIP_ERR_INVALID, "matvec: bad x op %d", xp);
+    QH_REQUIRE(xp != XP_NORM || prep->w, QRAF_HIP_ERR_INVALID, "matvec: norm weights missing");
+    const float* xw = xp == XP_NORM ? prep->w : nullptr;
+    const float eps = xp == XP_NORM ? prep->eps : 0.f;
+    // kernels that cannot form x: a prep kernel writes it to the scratch buffer first
+    auto plain_x = [&]() -> int {
+        if (xp == XP_NONE) return QRAF_HIP_OK;
+        QH_TRY(launch_xprep(x, *prep, (int)K, s));
+        x = prep->xbuf;
+        xp = XP_NONE;
+        xw = nullptr;
+        return QRAF_HIP_OK;
+    };
     const uint8_t* W = (const uint8_t*)Wv;
     const size_t rb = q_row_bytes(dtype, bs, K);
     const int nb = (int)((K + bs - 1) / bs);
@@ -741,22 +886,24 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
         // one-shot kernel below ~6 MB of weights (it has the whole matrix in
         // flight at once), else the ring kernel: Q8 one row per wave, 8-wave
         // workgroups, 2 per CU; Q4 one row per wave, 1 such workgroup per CU,
-        // or for N >= 8192 two rows per wave in 4-wave workgroups, 4 per CU.
+        // or for N >= 8192 two rows per wave in 4-wave workgroups, 4 per CU
+        // (8-wave workgroups when the kernel forms x itself).
         const bool big = (size_t)N * rb >= ((size_t)6 << 20);
         const bool q4_wide = dtype == DT_Q4_0 && N >= 8192;
         int kern_req = g_kernel;
-        if (kern_req == 0 && big) kern_req = q4_wide ? 4 : 3;
-        const int NWr = kern_req == 4 ? 4 : 8;  // waves per workgroup (kernel 3: 8, kernel 4: 4)
+        if (kern_req == 0 && big) kern_req = q4_wide && xp == XP_NONE ? 4 : 3;
+        const int NWr = kern_req == 4 && xp == XP_NONE ? 4 : 8;  // waves per workgroup
         const int xj = dtype == DT_Q8_0 ? (int)((K + 64 * NWr * 4 - 1) / (64 * NWr * 4))
                                         : (int)((K + 64 * NWr * 8 - 1) / (64 * NWr * 8));
         // the ring kernel needs whole blocks, a 16-byte aligned x and x within its staging
-        const bool ring_ok = (K % 32) == 0 && (((uintptr_t)x) & 15) == 0 && xj <= 12 && lds + 64 <= 160 * 1024;
+        const bool ring_ok = (K % 32) == 0 && (((uintptr_t)x) & 15) == 0 && (((uintptr_t)xw) & 15) == 0 &&
+                             xj <= 12 && lds + 64 <= 160 * 1024;
         int kern = kern_req;
         if (kern == 0) kern = (N >= 8192 && J <= 8) ? 2 : 1;
         if ((kern == 3 || kern == 4) && ring_ok) {
-            int R = g_rows_per_wave ? min(g_rows_per_wave, 2) : (g_kernel == 0 && q4_wide ? 2 : 1);
+            int R = g_rows_per_wave ? min(g_rows_per_wave, 2) : (g_kernel == 0 && q4_wide && NWr == 4 ? 2 : 1);
             if (N % R) R = 1;  // every stored row must exist
-            qmv_fn kf = dtype == DT_Q8_0 ? pick_ring<8>(R, NWr, xj) : pick_ring<4>(R, NWr, xj);
+            qmv_fn kf = dtype == DT_Q8_0 ? pick_ring<8>(R, NWr, xj, xp) : pick_ring<4>(R, NWr, xj, xp);
             QH_REQUIRE(kf, QRAF_HIP_ERR_INVALID, "no ring matvec kernel for K=%u", K);
             const size_t lds_r = lds + 16 * sizeof(float);  // + the spare slot for out-of-range x stores
             if (lds_r > 65536)
@@ -774,13 +921,15 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
             const int k = (ngroups + wmax - 1) / wmax;
             const int waves = (ngroups + k - 1) / k;
             const int grid = (waves + NWr - 1) / NWr;
-            hipLaunchKernelGGL(kf, dim3(grid), dim3(64 * NWr), lds_r, s, W, (uint32_t)rb, (int)N, (int)K, nb, x, y, add);
+            hipLaunchKernelGGL(kf, dim3(grid), dim3(64 * NWr), lds_r, s, W, (uint32_t)rb, (int)N, (int)K, nb, x, y, add,
+                               xw, eps);
             QH_CHECK_HIP(hipGetLastError());
             return QRAF_HIP_OK;
         }
         // persistent kernel when the ring does not apply and there are many rows, else one-shot
         if (kern >= 3) kern = (N >= 8192 && J <= 8) ? 2 : 1;
         if (kern == 2 || J > 8) {
+            QH_TRY(plain_x());
             const int R = g_rows_per_wave ? min(g_rows_per_wave, 4) : (dtype == DT_Q8_0 ? 1 : 2);
             const int ngroups = (int)((N + R - 1) / R);
             const int per_cu = g_wgs_per_cu ? g_wgs_per_cu : (dtype == DT_Q8_0 ? 4 : 2);
@@ -790,7 +939,7 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
             else k = R == 1 ? qmv_persist_kernel<4, 1> : R == 2 ? qmv_persist_kernel<4, 2> : qmv_persist_kernel<4, 4>;
             if (lds > 65536)
                 QH_CHECK_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
-            hipLaunchKernelGGL(k, dim3(grid), dim3(WG), lds, s, W, (uint32_t)rb, (int)N, (int)K, nb, x, y, add);
+            hipLaunchKernelGGL(k, dim3(grid), dim3(WG), lds, s, W, (uint32_t)rb, (int)N, (int)K, nb, x, y, add, xw, eps);
             QH_CHECK_HIP(hipGetLastError());
             return QRAF_HIP_OK;
         }
@@ -800,18 +949,23 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
             // but keep at least ~256 workgroups so every CU streams
             R = 8;
             while (R > 1 && (R * J > 8 || (N + 4 * R - 1) / (4 * R) < 256)) R >>= 1;
-        } else if (J <= 8) {
+        } else {
             while (R > 1 && R * J > 8) R >>= 1;
         }
-        qmv_fn k = dtype == DT_Q8_0 ? pick_kernel<8>(R, J) : pick_kernel<4>(R, J);
+        qmv_fn k = dtype == DT_Q8_0 ? pick_oneshot_xp<8>(R, J, xp) : pick_oneshot_xp<4>(R, J, xp);
+        if (!k) {  // no one-shot instance forms this x (J > 4): prepare it separately
+            QH_TRY(plain_x());
+            k = dtype == DT_Q8_0 ? pick_oneshot_xp<8>(R, J, XP_NONE) : pick_oneshot_xp<4>(R, J, XP_NONE);
+        }
         QH_REQUIRE(k, QRAF_HIP_ERR_INVALID, "no matvec kernel for R=%d J=%d", R, J);
         if (lds > 65536)
             QH_CHECK_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
         hipLaunchKernelGGL(k, dim3((N + 4 * R - 1) / (4 * R)), dim3(WG), lds, s, W, (uint32_t)rb, (int)N, (int)K, nb,
-                           x, y, add);
+                           x, y, add, xw, eps);
         QH_CHECK_HIP(hipGetLastError());
         return QRAF_HIP_OK;
     }
+    QH_TRY(plain_x());
     hipLaunchKernelGGL(qmv_generic_kernel, dim3((N + 3) / 4), dim3(WG), 0, s, W, dtype, bs, rb, (int)N, (int)K, x, y,
                        add);
     QH_CHECK_HIP(hipGetLastError());
