@@ -183,10 +183,11 @@ int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int3
                             void* stream);
 /* Tuning of the batched GEMM for batches over 32 rows: waves 4 or 8 per
  * workgroup (128 or 256 weight rows), splits > 0 forces the split count,
- * pipe 1 / -1 forces the pipelined tiled kernel on / off; 0 restores the
+ * pipe 1 / -1 forces the pipelined tiled kernel on / off, batch_chunk 16,
+ * 32, 64 or 128 caps the batch rows one workgroup covers; 0 restores the
  * automatic choice.  Affects the workspace queries too.  No counterpart in
  * the reference (a performance knob). */
-int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe);
+int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe, int batch_chunk);
 /* Workspace (bytes) that lets qraf_hip_qgemm_dev split the in_dim range of an
  * out_dim x in_dim product at this batch across workgroups; 0 when it does
  * not split. */

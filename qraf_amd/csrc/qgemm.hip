@@ -422,10 +422,10 @@ __device__ __forceinline__ uint8_t* qg_stage() {
 }
 
 // WN: waves along the weight rows (2 x WN waves); wave tile 16*TM x 16*TN.
-template <int FMT, int TM, int TN, int KC, int WN>
+template <int FMT, int TM, int TN, int KC, int WN, int WMN>
 struct PipeGeom {
-    static constexpr int NWV = 2 * WN;                // waves per workgroup
-    static constexpr int MW = 32 * TM, NW = 16 * TN * WN;
+    static constexpr int NWV = WMN * WN;              // waves per workgroup
+    static constexpr int MW = 16 * TM * WMN, NW = 16 * TN * WN;
     static constexpr int TB = tile_block_bytes(FMT);
     static constexpr int XROW = KC * 64;              // bytes of one X row (one plane) per stage
     static constexpr int XPL = MW * XROW;             // bytes of one plane per stage
@@ -442,13 +442,13 @@ struct PipeGeom {
     static_assert(STAGE <= QG_STAGE_MAX, "stage buffer too small");
 };
 
-template <int FMT, int TM, int TN, int KC, int WN>
-__global__ __launch_bounds__(128 * WN, 1) void qgemm_pipe_kernel(const uint8_t* __restrict__ Wt, int N, int nb,
+template <int FMT, int TM, int TN, int KC, int WN, int WMN>
+__global__ __launch_bounds__(64 * WMN * WN, 1) void qgemm_pipe_kernel(const uint8_t* __restrict__ Wt, int N, int nb,
                                                                  const uint16_t* __restrict__ xh,
                                                                  const uint16_t* __restrict__ xl, int K, int M,
                                                                  float* Y, const float* add, int bps,
                                                                  float* __restrict__ part) {
-    using G = PipeGeom<FMT, TM, TN, KC, WN>;
+    using G = PipeGeom<FMT, TM, TN, KC, WN, WMN>;
     constexpr int MW = G::MW, NW = G::NW, TB = G::TB, NWV = G::NWV;
 
     const int tid = threadIdx.x, lane = tid & 63;
@@ -639,6 +639,7 @@ struct QgPlan {
 static int g_qg_waves = 0;   // 4 or 8 waves per workgroup for batch tiles > 32 rows
 static int g_qg_splits = 0;  // forced split count
 static int g_qg_pipe = 0;    // 1: pipelined kernel for every tiled batch over 32 rows, -1: never
+static int g_qg_mchunk = 0;  // batch rows per workgroup at most (0: QG_MCHUNK)
 
 // Tile shape and split count for an N x K matrix times M rows.  Batch tiles
 // of more than 32 rows use 2 x WN waves of 64 weight rows each; smaller ones
@@ -647,18 +648,29 @@ static int g_qg_pipe = 0;    // 1: pipelined kernel for every tiled batch over 3
 // split keeps at least one ping-pong pair of stages.
 static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
     QgPlan p{};
-    const int Mc = min(M, QG_MCHUNK);
+    int Mc = min(M, g_qg_mchunk ? g_qg_mchunk : QG_MCHUNK);
     const bool pipe = g_qg_pipe > 0 || (g_qg_pipe == 0 && N >= 8192);
     if (tiled && Mc > 32 && pipe) {
-        // pipelined kernel: 2 x 2 waves of 16*TM x 128 rows, 3-stage LDS ring, 1 workgroup per CU
+        // pipelined kernel, 3-stage LDS ring, 1 workgroup per CU, 256 weight rows:
+        // up to 64 batch rows 2 x 4 waves of 16*TM x 64 rows; beyond, 8 waves
+        // side by side of all 128 batch rows x 32 weight rows (each converted
+        // weight fragment then feeds 8 batch tiles instead of 4)
         p.pipe = true;
-        p.WM = 2;
-        p.WN = 2;
-        p.TM = (Mc + 31) / 32;
-        p.TN = 4;
         p.KC = 2;
-        p.MW = 32 * p.TM;
         p.NW = 256;
+        if (Mc > 64) {
+            p.WM = 1;
+            p.WN = 8;
+            p.TM = 8;
+            p.TN = 2;
+            p.MW = 128;
+        } else {
+            p.WM = 2;
+            p.WN = 4;
+            p.TM = (Mc + 31) / 32;
+            p.TN = 4;
+            p.MW = 32 * p.TM;
+        }
         p.ntiles = (N + p.NW - 1) / p.NW;
         p.mchunks = (M + p.MW - 1) / p.MW;
         const int nb = K / 32;
@@ -673,6 +685,12 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
         p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
         return p;
     }
+    // Narrow products (the non-pipelined path) at batches over 32 rows run in
+    // 32-row chunks: four times the workgroups of one 128-row chunk and a
+    // quarter of the split-K partials (measured on MI355X at the continuous-
+    // batch shapes: QKV 2560x2048 25 -> 19 us, O 2048x2048 22 -> 14 us,
+    // down 2048x11008 37 -> 34 us, partial reduction included).
+    if (!g_qg_mchunk && tiled) Mc = min(Mc, 32);
     p.WM = Mc > 32 ? 2 : 1;
     p.TM = (Mc + 16 * p.WM - 1) / (16 * p.WM);
     p.TN = p.WM == 2 ? 4 : 2;
@@ -699,13 +717,16 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
     return p;
 }
 
-int set_qgemm_tuning(int waves, int splits, int pipe) {
+int set_qgemm_tuning(int waves, int splits, int pipe, int mchunk) {
     QH_REQUIRE(waves == 0 || waves == 4 || waves == 8, QRAF_HIP_ERR_INVALID, "qgemm tuning: waves %d", waves);
+    QH_REQUIRE(mchunk == 0 || mchunk == 16 || mchunk == 32 || mchunk == 64 || mchunk == 128, QRAF_HIP_ERR_INVALID,
+               "qgemm tuning: batch chunk %d", mchunk);
     QH_REQUIRE(splits >= 0 && splits <= 256, QRAF_HIP_ERR_INVALID, "qgemm tuning: splits %d", splits);
     QH_REQUIRE(pipe >= -1 && pipe <= 1, QRAF_HIP_ERR_INVALID, "qgemm tuning: pipe %d", pipe);
     g_qg_waves = waves;
     g_qg_splits = splits;
     g_qg_pipe = pipe;
+    g_qg_mchunk = mchunk;
     bump_tuning_generation();
     return QRAF_HIP_OK;
 }
@@ -786,17 +807,19 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
     QH_REQUIRE(p.mchunks <= 65535, QRAF_HIP_ERR_INVALID, "qgemm: batch %d too large", M);
     const dim3 grid(p.ntiles, p.S, p.mchunks);
     if (p.pipe) {
-#define QH_P(F, TM_)                                                                                        \
-    hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, 4, 2, 4>), grid, dim3(512), 0, s, (const uint8_t*)W, N, nb, xh, xl, \
-                       K, M, Y, add, p.bps, part)
+#define QH_P(F, TM_, TN_, WN_, WM_)                                                                        \
+    hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_>), grid, dim3(512), 0, s, (const uint8_t*)W, N, nb, \
+                       xh, xl, K, M, Y, add, p.bps, part)
         if (dtype == DT_Q8_0) {
-            if (p.TM == 2) QH_P(8, 2);
-            else if (p.TM == 3) QH_P(8, 3);
-            else QH_P(8, 4);
+            if (p.WM == 1) QH_P(8, 8, 2, 8, 1);
+            else if (p.TM == 2) QH_P(8, 2, 4, 4, 2);
+            else if (p.TM == 3) QH_P(8, 3, 4, 4, 2);
+            else QH_P(8, 4, 4, 4, 2);
         } else {
-            if (p.TM == 2) QH_P(4, 2);
-            else if (p.TM == 3) QH_P(4, 3);
-            else QH_P(4, 4);
+            if (p.WM == 1) QH_P(4, 8, 2, 8, 1);
+            else if (p.TM == 2) QH_P(4, 2, 4, 4, 2);
+            else if (p.TM == 3) QH_P(4, 3, 4, 4, 2);
+            else QH_P(4, 4, 4, 4, 2);
         }
 #undef QH_P
     } else {
@@ -848,9 +871,9 @@ int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int3
     return qraf_hip::launch_split_bf16(x, x_hi, x_lo, rows, cols, 0, nullptr, qraf_hip::as_stream(stream));
 }
 
-int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe) {
+int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe, int batch_chunk) {
     qraf_hip::clear_error();
-    return qraf_hip::set_qgemm_tuning(waves, splits, pipe);
+    return qraf_hip::set_qgemm_tuning(waves, splits, pipe, batch_chunk);
 }
 
 uint64_t qraf_hip_qgemm_workspace_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim, int32_t batch) {

@@ -132,12 +132,12 @@ def test_qgemm_pipelined_kernel(hip, dt, case):
     rng = np.random.default_rng(N + 3 * K + M + dt)
     wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
     X = rng.standard_normal((M, K)).astype(np.float32)
-    hip._lib.call("qraf_hip_set_qgemm_tuning", 0, 0, 1)
+    hip._lib.call("qraf_hip_set_qgemm_tuning", 0, 0, 1, 0)
     try:
         Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, repeats=2)
         Y1, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
     finally:
-        hip._lib.call("qraf_hip_set_qgemm_tuning", 0, 0, 0)
+        hip._lib.call("qraf_hip_set_qgemm_tuning", 0, 0, 0, 0)
     check(Y, wq, dt, N, K, X)
     check(Y1, wq, dt, N, K, X)
 
