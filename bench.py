@@ -374,35 +374,65 @@ QWEN = dict(vocab=151936, hidden=2048, layers=36, heads=16, kv_heads=2, inter=11
 
 
 def bench_decode_b128(args, rt):
+    """C5: 128 concurrent requests, continuous batching.  The headline run
+    feeds prompts in chunks (up to --prefill-chunk tokens of one request per
+    step, within a --rows row budget, decode rows first); the token-by-token
+    run (every active request one row per step) is reported beside it."""
     from qraf_amd.engine import BatchScheduler, Engine, model_config
     cfg = model_config(*(QWEN[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq",
                                            "rope_theta", "eps")))
-    e = Engine(cfg, kv_dtype=F16, max_batch=128)
+    rows = max(128, args.rows)
+    pages = 128 * (-(-QWEN["max_seq"] // 16)) + 64
+    e = Engine(cfg, kv_dtype=F16, max_batch=rows, num_pages=pages)
     e.generate_weights(Q4, Q4, Q4, True, True, 3)
     e.finalize()
     e.set_graphs(not args.no_graphs)
     rng = np.random.default_rng(3)
-    warm = BatchScheduler(e, max_batch=128)
-    for _ in range(4):
-        warm.submit(rng.integers(0, QWEN["vocab"], 16).tolist(), 4)
+    warm = BatchScheduler(e, max_batch=128, max_rows=rows, prefill_chunk=args.prefill_chunk)
+    for _ in range(8):
+        warm.submit(rng.integers(0, QWEN["vocab"], 300).tolist(), 4)
     warm.run()
-    sched = BatchScheduler(e, max_batch=128)
+    work = []
     for _ in range(args.requests):
         plen, olen = int(rng.integers(16, 513)), int(rng.integers(64, 257))
-        sched.submit(rng.integers(0, QWEN["vocab"], plen).tolist(), olen)
-    t0 = time.perf_counter()
-    done = sched.run()
-    el = time.perf_counter() - t0
-    gen = sum(len(r.generated) for r in done)
+        work.append((rng.integers(0, QWEN["vocab"], plen).tolist(), olen))
+
+    def run(max_rows, chunk):
+        sched = BatchScheduler(e, max_batch=128, max_rows=max_rows, prefill_chunk=chunk)
+        for p, o in work:
+            sched.submit(p, o)
+        t0 = time.perf_counter()
+        done = sched.run()
+        el = time.perf_counter() - t0
+        gen = sum(len(r.generated) for r in done)
+        return {"generated_tokens": gen, "steps": sched.steps, "rows_processed": sched.rows, "wall_s": round(el, 3),
+                "generated_tok_s": round(gen / el, 1), "rows_per_s": round(sched.rows / el, 1),
+                "ms_per_step": round(el / sched.steps * 1e3, 3)}, [r.generated for r in sorted(done, key=lambda r: r.id)]
+
+    chunked, streams_c = run(rows, args.prefill_chunk)
+    tbt, streams_t = run(128, 1)
     steady = steady_decode_b128(e, rng, args.decode_steps)
     e.close()
-    return {"model": "Qwen2.5-3B architecture, Q4_0 weights, tied head, QKV bias, fp16 KV pages, random init",
-            "requests": args.requests, "max_concurrent": 128, "generated_tokens": gen, "steps": sched.steps,
-            "rows_processed": sched.rows, "wall_s": round(el, 3), "generated_tok_s": round(gen / el, 1),
-            "rows_per_s": round(sched.rows / el, 1), "ms_per_step": round(el / sched.steps * 1e3, 3),
-            "note": "continuous batching: prompt tokens are fed one per step (chunk 1) in the same batched step as "
-                    "decodes, requests admitted as others finish",
-            "steady_decode": steady}
+    out = {"model": "Qwen2.5-3B architecture, Q4_0 weights, tied head, QKV bias, fp16 KV pages, random init",
+           "requests": args.requests, "max_concurrent": 128}
+    out.update(chunked)
+    out.update({"row_budget": rows, "prefill_chunk": args.prefill_chunk,
+                "note": "continuous batching, requests admitted as others finish; each step feeds every decoding "
+                        "request's last token, then prompt chunks within the row budget",
+                "token_by_token": tbt, "stream_agreement": stream_agreement(streams_c, streams_t),
+                "steady_decode": steady})
+    return out
+
+
+def stream_agreement(a, b):
+    """How far two runs' greedy streams of the same requests agree.  Batch
+    composition changes the GEMM's tiling and split, so fp32 rounding differs
+    within the parity tolerance; random-init logits have near-ties, where a
+    different rounding may pick the other token, after which a stream differs."""
+    first = [next((i for i, (x, y) in enumerate(zip(s, t)) if x != y), min(len(s), len(t))) for s, t in zip(a, b)]
+    return {"requests": len(first), "identical": sum(1 for s, t in zip(a, b) if s == t),
+            "first_32_identical": sum(1 for f, s in zip(first, a) if f >= min(32, len(s))),
+            "median_first_difference": int(np.median(first))}
 
 
 def steady_decode_b128(e, rng, steps):
@@ -446,6 +476,8 @@ def main():
     ap.add_argument("--only", default="matvec,gemm,attention,decode_b1,decode_b128")
     ap.add_argument("--requests", type=int, default=256, help="requests in the batch-128 decode run")
     ap.add_argument("--decode-steps", type=int, default=64, help="timed steps of the steady 128-sequence decode")
+    ap.add_argument("--rows", type=int, default=512, help="row budget per step of the continuous-batch run")
+    ap.add_argument("--prefill-chunk", type=int, default=512, help="prompt tokens of one request per step at most")
     ap.add_argument("--cases", default="",
                     help="restrict the matvec leg to these cases, e.g. 'q8_0 11008x4096' (comma-separated; "
                          "a profile of one case then has one shape per kernel)")

@@ -233,7 +233,7 @@ typedef struct qraf_model_config {
 
 /* Engine resources.  kv_dtype F32 (0, the reference's KVCache) or F16;
  * page_size tokens per KV page (0 -> 16, must divide 256); max_batch rows
- * per step (0 -> 1, at most 128); num_pages KV pages per layer (0 -> enough
+ * per step (0 -> 1, at most 1024); num_pages KV pages per layer (0 -> enough
  * for max_batch sequences of min(max_seq_len, 8192) positions). */
 typedef struct qraf_engine_options {
     uint32_t kv_dtype, page_size, max_batch, num_pages;

@@ -365,11 +365,16 @@ struct qraf_engine {
         uint64_t used = 0;
     };
     std::vector<StepGraph> graphs;
+    // shapes seen once: a shape is captured the second time it comes (a
+    // chunked-prefill schedule produces many one-off row counts, whose
+    // capture would cost more than their eager launch)
+    std::vector<StepGraph> seen;
     bool use_graphs = true;
     uint64_t graph_clock = 0;
     void drop_graphs() {
         for (auto& g : graphs) hipGraphExecDestroy(g.exec);
         graphs.clear();
+        seen.clear();
     }
 };
 
@@ -441,7 +446,7 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     if (o.kv_dtype != DT_F32 && o.kv_dtype != DT_F16) return set_error(QRAF_HIP_ERR_DTYPE, "engine: KV dtype %u", o.kv_dtype);
     if (!o.page_size) o.page_size = 16;
     if (!o.max_batch) o.max_batch = 1;
-    QH_REQUIRE(o.max_batch <= 128, QRAF_HIP_ERR_INVALID, "engine: max_batch %u > 128", o.max_batch);
+    QH_REQUIRE(o.max_batch <= 1024, QRAF_HIP_ERR_INVALID, "engine: max_batch %u > 1024", o.max_batch);
     QH_REQUIRE(o.page_size <= 256 && (256 % o.page_size) == 0, QRAF_HIP_ERR_INVALID,
                "engine: page_size must divide 256");
 
@@ -1008,7 +1013,29 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         for (auto& sg : e->graphs)
             if (sg.n == n && sg.n_logit_rows == n_logit_rows && sg.ctx == ctx_grid && sg.head == head && sg.gen == gen)
                 g = &sg;
+        bool second = false;
         if (!g) {
+            for (auto it = e->seen.begin(); it != e->seen.end(); ++it)
+                if (it->n == n && it->n_logit_rows == n_logit_rows && it->ctx == ctx_grid && it->head == head &&
+                    it->gen == gen) {
+                    second = true;
+                    e->seen.erase(it);
+                    break;
+                }
+            if (!second) {
+                qraf_engine::StepGraph sg;
+                sg.n = n;
+                sg.n_logit_rows = n_logit_rows;
+                sg.ctx = ctx_grid;
+                sg.head = head;
+                sg.gen = gen;
+                if (e->seen.size() >= 4 * MAX_STEP_GRAPHS) e->seen.erase(e->seen.begin());
+                e->seen.push_back(sg);
+            }
+        }
+        if (!g && !second) {
+            QH_TRY(enqueue(ctx_grid));  // first sighting: eager
+        } else if (!g) {
             hipGraph_t graph = nullptr;
             QH_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
             const int rc = enqueue(ctx_grid);
@@ -1040,8 +1067,10 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
             e->graphs.push_back(sg);
             g = &e->graphs.back();
         }
-        g->used = ++e->graph_clock;
-        QH_CHECK_HIP(hipGraphLaunch(g->exec, s));
+        if (g) {
+            g->used = ++e->graph_clock;
+            QH_CHECK_HIP(hipGraphLaunch(g->exec, s));
+        }
     } else {
         QH_TRY(enqueue(step_ctx));
     }

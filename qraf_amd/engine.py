@@ -210,19 +210,33 @@ class Request:
 class BatchScheduler:
     """Continuous batching over one Engine (batch_scheduler.h:54-283 contract).
 
-    Each step admits queued requests into free slots (max_batch), then feeds
-    every active request one token: the next prompt token while PREFILLING,
-    the last generated token while DECODING.  A request whose last prompt
-    token was just fed, or that is decoding, gets its next token from this
-    step's logits; it retires on EOS or after max_tokens generated tokens and
-    frees its KV pages for the next admission.  Every request's token stream
-    equals an independent greedy decode of its prompt (the reference's
-    scheduler runs requests one at a time over one shared cache, F3 in the
-    survey, so it offers no batched numerics to mirror)."""
+    Each step admits queued requests into free slots (max_batch concurrent
+    requests), then builds the step's rows within a budget of max_rows (at
+    most the engine's rows per step): every DECODING request feeds its last
+    generated token, then PREFILLING requests, in admission order, feed their
+    next prompt tokens, up to prefill_chunk consecutive positions each, while
+    the budget lasts (chunked prefill: a prompt enters the cache as a
+    batched projection instead of token by token).  A request whose last
+    prompt token was just fed, or that is decoding, gets its next token from
+    this step's logits; it retires on EOS or after max_tokens generated
+    tokens and frees its KV pages for the next admission.  Every request's
+    token stream equals an independent greedy decode of its prompt (the
+    reference's scheduler runs requests one at a time over one shared cache,
+    F3 in the survey, so it offers no batched numerics to mirror).  With the
+    defaults (prefill_chunk 1, max_rows = max_batch) every active request
+    feeds exactly one token per step."""
 
-    def __init__(self, engine: Engine, max_batch: int | None = None):
+    def __init__(self, engine: Engine, max_batch: int | None = None, max_rows: int | None = None,
+                 prefill_chunk: int = 1):
         self.engine = engine
         self.max_batch = max_batch or engine.max_batch
+        self.max_rows = min(max_rows or self.max_batch, engine.max_batch)
+        if self.max_rows < self.max_batch:
+            raise ValueError(f"max_rows {self.max_rows} below max_batch {self.max_batch}: "
+                             "every decoding request needs its row")
+        if prefill_chunk < 1:
+            raise ValueError("prefill_chunk must be >= 1")
+        self.prefill_chunk = prefill_chunk
         self.pending = deque()
         self.active = []
         self.done = []
@@ -257,12 +271,17 @@ class BatchScheduler:
             return False
         rows = []  # (request, token, position, wants logits)
         for r in self.active:
-            if r.state == "PREFILLING":
-                i = r.next_prompt
-                rows.append((r, r.prompt[i], i, i == len(r.prompt) - 1))
-            else:
+            if r.state == "DECODING":
                 pos = len(r.prompt) + len(r.generated) - 1
                 rows.append((r, r.generated[-1], pos, True))
+        budget = self.max_rows - len(rows)
+        for r in self.active:
+            if r.state != "PREFILLING" or budget <= 0:
+                continue
+            c = min(self.prefill_chunk, len(r.prompt) - r.next_prompt, budget)
+            for i in range(r.next_prompt, r.next_prompt + c):
+                rows.append((r, r.prompt[i], i, i == len(r.prompt) - 1))
+            budget -= c
         want = np.array([w for (_, _, _, w) in rows], np.uint8)
         need_host = any(r.penalty != 1.0 for (r, _, _, w) in rows if w)
         lg, nx = self.engine.step([r.seq for (r, _, _, _) in rows], [t for (_, t, _, _) in rows],

@@ -168,6 +168,36 @@ def test_batched_step_equals_single_sequence_decode(hip):
     e.close()
 
 
+@pytest.mark.parametrize("chunk,max_rows,plen", [(7, 32, 9), (64, 40, 9), (3, 4, 9), (512, 512, 31), (300, 300, 33)])
+def test_scheduler_chunked_prefill_streams(hip, chunk, max_rows, plen):
+    """Continuous batching with prompts entering in chunks of up to `chunk`
+    tokens per step within a `max_rows` row budget (decode rows first; the
+    last two cases run steps of several hundred rows, over the GEMM's
+    128-row batch chunk): every request's stream equals its independent
+    greedy decode, and every page comes back."""
+    from qraf_amd.engine import BatchScheduler, Engine
+    kw, seed = SMALL["q4_gqa8_hd128"]
+    m = oracle_model(kw, seed)
+    L = po.lib()
+    e = Engine(engine_config(kw), kv_dtype=po.F16, max_batch=max_rows)
+    for name, dt, shape, data in m.tensors():
+        e.set_tensor(name, dt, shape, data)
+    e.finalize()
+    pool = e.free_pages()
+    prompts = [[L.or_gen_token(300 + r, i, kw["vocab"]) for i in range(2 + plen * r)] for r in range(7)]
+    sched = BatchScheduler(e, max_batch=4, max_rows=max_rows, prefill_chunk=chunk)
+    ids = [sched.submit(p, 6 + 2 * r) for r, p in enumerate(prompts)]
+    done = {r.id: r for r in sched.run()}
+    for r, (i, p) in enumerate(zip(ids, prompts)):
+        assert done[i].generated == m.generate(p, 6 + 2 * r, 1.0, eos=-1), f"request {r}"
+    rows_token_by_token = sum(len(p) + 6 + 2 * r - 1 for r, p in enumerate(prompts))
+    assert sched.rows == rows_token_by_token  # every prompt token and fed-back token exactly once
+    if chunk > 1 and max_rows > 4:
+        assert sched.steps < 25 + 6 * plen  # prompts entered in chunks
+    assert e.free_pages() == pool
+    e.close()
+
+
 def test_batched_logits_and_chunked_prefill(hip):
     from qraf_amd.engine import Engine
     kw, seed = SMALL["q8_hd64_gqa3"]
