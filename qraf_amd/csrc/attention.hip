@@ -14,11 +14,11 @@
 //
 // Work decomposition: the context of every sequence is cut into chunks of
 // CH = 256 positions; one workgroup handles one (sequence, chunk) item for
-// one KV head and all H/Hkv query heads that share it (GQA).  Items are
-// numbered by an exclusive prefix sum of ceil(ctx_s / CH) over the ragged
-// batch, which every workgroup recomputes in LDS from the device-resident
-// context lengths, so the packing follows whatever lengths are on the device
-// when the kernel runs (no host round trip).  Sequences with several chunks
+// one KV head and all H/Hkv query heads that share it (GQA).  The grid has
+// ceil(max_ctx / CH) items per sequence (item = s * that + chunk); a
+// workgroup whose chunk starts at or past its sequence's device-resident
+// context length exits at once, so the lengths can change on the device
+// between launches with no host round trip.  Sequences with several chunks
 // write (max, sum, unnormalised output) partials, which attn_merge_kernel (a
 // second launch, one workgroup per sequence and KV head) combines in chunk
 // order.
@@ -79,51 +79,15 @@ __device__ __forceinline__ void attn_store(const AttnArgs& a, size_t i, float v)
     else a.out[i] = v;
 }
 
-// Item -> (sequence, chunk): every workgroup computes the exclusive prefix
-// sum of ceil(ctx_s / ACH) over the batch in LDS (4 entries per thread, wave
-// scan, then across the 4 waves), then finds its sequence by bisection.
-// Returns false for items past the total (the grid is sized for max_ctx).
-__device__ __forceinline__ bool attn_item(const AttnArgs& a, int* s_pref, int& s, int& chunk, int& nchunks) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int n = a.n;
-    __shared__ int s_wtot[4];
-    int c[4], run = 0;
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int i = tid * 4 + j;
-        c[j] = i < n ? (min(a.ctx[i], a.max_ctx) + ACH - 1) / ACH : 0;
-        run += c[j];
-    }
-    int incl = run;
-#pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const int v = __shfl_up(incl, o);
-        if (lane >= o) incl += v;
-    }
-    if (lane == 63) s_wtot[wave] = incl;
-    __syncthreads();
-    int off = incl - run;
-    for (int w = 0; w < wave; w++) off += s_wtot[w];
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int i = tid * 4 + j;
-        off += c[j];
-        if (i < n) s_pref[i + 1] = off;
-    }
-    if (tid == 0) s_pref[0] = 0;
-    __syncthreads();
-    const int item = blockIdx.x;
-    if (item >= s_pref[n]) return false;
-    int lo = 0, hi = n - 1;  // largest s with s_pref[s] <= item
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (s_pref[mid] <= item) lo = mid;
-        else hi = mid - 1;
-    }
-    s = lo;
-    chunk = item - s_pref[s];
-    nchunks = s_pref[s + 1] - s_pref[s];
-    return true;
+// Item -> (sequence, chunk): item = s * chunks_per_seq + chunk.  Returns
+// false when the chunk starts at or past the sequence's context.
+__device__ __forceinline__ bool attn_item(const AttnArgs& a, int& s, int& chunk, int& nchunks, int& ctx) {
+    const int per = (a.max_ctx + ACH - 1) / ACH;
+    s = blockIdx.x / per;
+    chunk = blockIdx.x - s * per;
+    ctx = min(a.ctx[s], a.max_ctx);
+    nchunks = (ctx + ACH - 1) / ACH;
+    return chunk < nchunks;
 }
 
 template <typename KT, int HD, int G>
@@ -133,7 +97,6 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     constexpr int HPT = (NOUT + ACH - 1) / ACH;  // outputs per thread at the end
     constexpr int NG = ACH / HD;                 // position groups of the PV phase
     constexpr int PADP = 8 * NG;                 // past-the-end slots its unrolled loop may touch
-    __shared__ int s_pref[1025];
     __shared__ float s_q[G][HD];
     __shared__ float s_p[G][ACH + PADP];         // probabilities (zero past the end); then PV partials
     __shared__ uint32_t s_voff[ACH + PADP];      // element offset of each position's V row in the layer pages
@@ -143,8 +106,8 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     const int kvh = blockIdx.y;
     const int item = blockIdx.x;
     int s, chunk, nchunks;
-    if (!attn_item(a, s_pref, s, chunk, nchunks)) return;
-    const int ctx = min(a.ctx[s], a.max_ctx);
+    int ctx;
+    if (!attn_item(a, s, chunk, nchunks, ctx)) return;
     const int t0 = chunk * ACH;
 
     // ---- q of the G heads sharing this KV head
@@ -300,36 +263,46 @@ typedef float f32x4a __attribute__((ext_vector_type(4)));
 
 // zero the fp16 lanes of a 4-position run (2 dwords) at or past ctx
 __device__ __forceinline__ uint2 mask_run(uint2 v, int pos0, int ctx) {
-    const int k = ctx - pos0;  // valid positions in the run
-    if (k >= 4) return v;
-    if (k <= 0) return make_uint2(0u, 0u);
-    if (k == 1) return make_uint2(v.x & 0xFFFFu, 0u);
-    if (k == 2) return make_uint2(v.x, 0u);
-    return make_uint2(v.x, v.y & 0xFFFFu);
+    const int k = ctx - pos0;  // valid positions in the run (selects, no branches)
+    const uint32_t mx = k >= 2 ? 0xFFFFFFFFu : (k == 1 ? 0xFFFFu : 0u);
+    const uint32_t my = k >= 4 ? 0xFFFFFFFFu : (k == 3 ? 0xFFFFu : 0u);
+    return make_uint2(v.x & mx, v.y & my);
 }
 
 template <int HD>
 __global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
     constexpr int KK = HD / 32;  // MFMA k-steps per score tile
-    constexpr int DPL = HD / 4;  // dimensions per lane in q.K^T: lane s covers DPL*s .. DPL*s+DPL-1
+    // q.K^T k-step kk, lane group s = l/16 covers dimensions 8*(4kk+s) .. +7:
+    // the 4 groups of one step read 64 consecutive bytes of a K row
     constexpr int DT = HD / 16;  // 16-dimension output tiles
     constexpr int QS = HD + 8;   // q plane row stride (fp16): 16-byte reads of 16 rows hit distinct banks
-    __shared__ int s_pref[1025];
     __shared__ __align__(16) _Float16 s_q[2][16][QS];
     __shared__ float s_qs[16];
     __shared__ float s_m[4][16], s_l[4][16];
-    __shared__ float s_o[4][16][HD];
+    extern __shared__ float s_odyn[];  // [4][G][HD]: the waves' partial outputs
+    float(*s_o)[HD] = (float(*)[HD])s_odyn;  // s_o[wave * G + head][dim]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int l16 = lane & 15, seg = lane >> 4;
     const int kvh = blockIdx.y;
     const int item = blockIdx.x;
     int s, chunk, nchunks;
-    if (!attn_item(a, s_pref, s, chunk, nchunks)) return;
-    const int ctx = min(a.ctx[s], a.max_ctx);
+    int ctx;
+    if (!attn_item(a, s, chunk, nchunks, ctx)) return;
     const int ps = a.page_size;
     const int32_t* ptab = a.page_table + (size_t)s * a.max_pages;
+    const int pw = chunk * ACH + 64 * wave;  // first position of this wave
+    const bool active = pw < ctx;            // wave-uniform
+
+    // ---- page ids of every K row and V run this lane reads, requested first
+    // (clamped into the context, so every read is inside the page table)
+    int kpg[4], vpg[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) kpg[t] = ptab[min(pw + 16 * t + l16, ctx - 1) / ps];
+    const int vlast = (ctx - 1) & ~3;
+#pragma unroll
+    for (int j = 0; j < 4; j++) vpg[j] = ptab[min(pw + 16 * j + 4 * seg, vlast) / ps];
 
     // ---- q of the G heads as fp16 hi + lo, scaled per head by 2^e so that
     // max|q| lands in [2^14, 2^15): hi + lo then carries 22 bits of every
@@ -364,9 +337,6 @@ __global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
 
     const _Float16* kc = (const _Float16*)a.kc;
     const _Float16* vc = (const _Float16*)a.vc;
-    const int pw = chunk * ACH + 64 * wave;  // first position of this wave
-    const bool active = pw < ctx;            // wave-uniform
-
     // ---- scores of 4 tiles: sc[t][r] = position pw + 16t + 4seg + r, head l16
     f32x4a sc[4];
 #pragma unroll
@@ -375,23 +345,44 @@ __global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
         f16x8 qh[KK], ql[KK];
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) {
-            qh[kk] = *(const f16x8*)&s_q[0][l16][DPL * seg + 8 * kk];
-            ql[kk] = *(const f16x8*)&s_q[1][l16][DPL * seg + 8 * kk];
+            qh[kk] = *(const f16x8*)&s_q[0][l16][8 * (4 * kk + seg)];
+            ql[kk] = *(const f16x8*)&s_q[1][l16][8 * (4 * kk + seg)];
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const int pc = min(pw + 16 * t + l16, ctx - 1);  // clamped: past-ctx scores are masked below
-            const int page = ptab[pc / ps];
-            const _Float16* kr = kc + (((size_t)page * a.Hkv + kvh) * ps + pc % ps) * HD + DPL * seg;
+            const _Float16* kr = kc + (((size_t)kpg[t] * a.Hkv + kvh) * ps + pc % ps) * HD + 8 * seg;
             f32x4a d = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int kk = 0; kk < KK; kk++) {
-                const f16x8 kf = *(const f16x8*)(kr + 8 * kk);
+                const f16x8 kf = *(const f16x8*)(kr + 32 * kk);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[kk], d, 0, 0, 0);
                 d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[kk], d, 0, 0, 0);
             }
             sc[t] = d;
         }
+    }
+
+    // ---- V of the wave's 64 positions, requested before the softmax so its
+    // latency overlaps the score phase.  Per lane and 32-position step b: two
+    // 4-position runs (b*32 + 4seg and +16) per 16-dimension tile, clamped
+    // into the context (values past it are masked), 4-aligned so a run never
+    // leaves a page.
+    uint2 va0[DT], vb0[DT], va1[DT], vb1[DT];
+    auto vload = [&](int b, uint2 (&ra)[DT], uint2 (&rb)[DT]) {
+        const int pac = min(pw + 32 * b + 4 * seg, vlast), pbc = min(pw + 32 * b + 16 + 4 * seg, vlast);
+        const _Float16* va = vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * HD * ps + pac % ps;
+        const _Float16* vb = vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * HD * ps + pbc % ps;
+#pragma unroll
+        for (int d = 0; d < DT; d++) {
+            const int dim = 16 * d + l16;
+            ra[d] = *(const uint2*)(va + (size_t)dim * ps);
+            rb[d] = *(const uint2*)(vb + (size_t)dim * ps);
+        }
+    };
+    if (active) {
+        vload(0, va0, vb0);
+        vload(1, va1, vb1);
     }
 
     // ---- softmax statistics over the workgroup's positions, per head l16
@@ -428,8 +419,7 @@ __global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
 #pragma unroll
     for (int d = 0; d < DT; d++) o[d] = f32x4a{0.f, 0.f, 0.f, 0.f};
     if (active) {
-#pragma unroll
-        for (int b = 0; b < 2; b++) {
+        auto pv = [&](int b, const uint2 (&ra)[DT], const uint2 (&rb)[DT]) {
             f16x8 ph, pl;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
@@ -438,29 +428,17 @@ __global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
                 ph[i] = h;
                 pl[i] = (_Float16)(p - (float)h);
             }
-            // the lane's two 4-position runs; clamped into the context (their
-            // values are masked), 4-aligned so a run never leaves a page
             const int pa = pw + 32 * b + 4 * seg, pb = pa + 16;
-            const int last = (ctx - 1) & ~3;
-            const int pac = min(pa, last), pbc = min(pb, last);
-            const _Float16* va = vc + ((size_t)ptab[pac / ps] * a.Hkv + kvh) * HD * ps + pac % ps;
-            const _Float16* vb = vc + ((size_t)ptab[pbc / ps] * a.Hkv + kvh) * HD * ps + pbc % ps;
-            const bool edge = pw + 32 * b + 32 > ctx;  // wave-uniform
 #pragma unroll
             for (int d = 0; d < DT; d++) {
-                const int dim = 16 * d + l16;
-                uint2 ra = *(const uint2*)(va + (size_t)dim * ps);
-                uint2 rb = *(const uint2*)(vb + (size_t)dim * ps);
-                if (edge) {
-                    ra = mask_run(ra, pa, ctx);
-                    rb = mask_run(rb, pb, ctx);
-                }
-                const uint4 r4 = make_uint4(ra.x, ra.y, rb.x, rb.y);
-                const f16x8 vf = __builtin_bit_cast(f16x8, r4);
+                const uint2 xa = mask_run(ra[d], pa, ctx), xb = mask_run(rb[d], pb, ctx);
+                const f16x8 vf = __builtin_bit_cast(f16x8, make_uint4(xa.x, xa.y, xb.x, xb.y));
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vf, o[d], 0, 0, 0);
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, o[d], 0, 0, 0);
             }
-        }
+        };
+        pv(0, va0, vb0);
+        pv(1, va1, vb1);
     }
 
     // ---- combine the 4 waves: o[d][r] = O[head 4seg+r][dim 16d+l16]
@@ -469,14 +447,14 @@ __global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int h = 4 * seg + r;
-            if (h < G) s_o[wave][h][16 * d + l16] = o[d][r];
+            if (h < G) s_o[wave * G + h][16 * d + l16] = o[d][r];
         }
     __syncthreads();
     const size_t hbase = (size_t)s * a.H + kvh * G;
     if (nchunks == 1) {
         for (int i = tid; i < G * HD; i += ACH) {
             const int h = i / HD, dd = i % HD;
-            const float O = (s_o[0][h][dd] + s_o[1][h][dd]) + (s_o[2][h][dd] + s_o[3][h][dd]);
+            const float O = (s_o[h][dd] + s_o[G + h][dd]) + (s_o[2 * G + h][dd] + s_o[3 * G + h][dd]);
             const float L = (s_l[0][h] + s_l[1][h]) + (s_l[2][h] + s_l[3][h]);
             attn_store(a, (hbase + h) * HD + dd, O / L);
         }
@@ -486,7 +464,7 @@ __global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
     const size_t ibase = (size_t)item * a.H + kvh * G;
     for (int i = tid; i < G * HD; i += ACH) {
         const int h = i / HD, dd = i % HD;
-        a.part_o[(ibase + h) * HD + dd] = (s_o[0][h][dd] + s_o[1][h][dd]) + (s_o[2][h][dd] + s_o[3][h][dd]);
+        a.part_o[(ibase + h) * HD + dd] = (s_o[h][dd] + s_o[G + h][dd]) + (s_o[2 * G + h][dd] + s_o[3 * G + h][dd]);
     }
     if (tid < G) {
         a.part_ml[(ibase + tid) * 2 + 0] = fmaxf(fmaxf(s_m[0][tid], s_m[1][tid]), fmaxf(s_m[2][tid], s_m[3][tid]));
@@ -494,36 +472,50 @@ __global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
     }
 }
 
-// Sequences of several chunks: one workgroup per (sequence, KV head) merges
-// the chunk partials in chunk order (a separate launch: no device-scope
-// fence or atomic, which on a multi-XCD part would write back and invalidate
-// L2 for every workgroup).
-__global__ __launch_bounds__(ACH) void attn_merge_kernel(AttnArgs a, int G, int HD) {
-    const int s = blockIdx.x, kvh = blockIdx.y, tid = threadIdx.x;
-    const int nchunks = (min(a.ctx[s], a.max_ctx) + ACH - 1) / ACH;
-    if (nchunks <= 1) return;
-    // base item: sum of the chunk counts of the sequences before s
-    __shared__ int s_sum[ACH / 64];
-    int part = 0;
-    for (int i = tid; i < s; i += ACH) part += (min(a.ctx[i], a.max_ctx) + ACH - 1) / ACH;
+// Sequences of several chunks: one wave per (sequence, query head) merges
+// the chunk partials (a separate launch: no device-scope fence or atomic,
+// which on a multi-XCD part would write back and invalidate L2 for every
+// workgroup).  Lane c holds chunk c's (m, l) (64 chunks per round), the
+// weights exp(m_c - M) reach every lane by shuffle, and lane d accumulates
+// output dimensions d, d+64, ... over the chunks in chunk order.
+template <int HD>
+__global__ __launch_bounds__(64) void attn_merge_kernel(AttnArgs a) {
+    constexpr int HPL = HD >= 64 ? HD / 64 : 1;  // dimensions per lane
+    const int s = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
+    const int dl = min(lane, HD - 1);            // lanes past a head_dim < 64 redo the last dimension, unstored
+    const int nch = (min(a.ctx[s], a.max_ctx) + ACH - 1) / ACH;
+    if (nch <= 1) return;
+    const size_t base = (size_t)s * ((a.max_ctx + ACH - 1) / ACH) * a.H + h;  // partial row of chunk 0
+    float M = -INFINITY;
+    for (int c = lane; c < nch; c += 64) M = fmaxf(M, a.part_ml[(base + (size_t)c * a.H) * 2]);
 #pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) part += __shfl_xor(part, o);
-    if ((tid & 63) == 0) s_sum[tid >> 6] = part;
-    __syncthreads();
-    const int base = (s_sum[0] + s_sum[1]) + (s_sum[2] + s_sum[3]);
-    for (int i = tid; i < G * HD; i += ACH) {
-        const int h = i / HD, dd = i % HD;
-        const size_t hidx = (size_t)kvh * G + h;
-        float M = -INFINITY;
-        for (int c = 0; c < nchunks; c++) M = fmaxf(M, a.part_ml[((size_t)(base + c) * a.H + hidx) * 2]);
-        float L = 0.f, O = 0.f;
-        for (int c = 0; c < nchunks; c++) {
-            const size_t it = (size_t)(base + c) * a.H + hidx;
-            const float w = __expf(a.part_ml[it * 2] - M);
-            L = __builtin_fmaf(a.part_ml[it * 2 + 1], w, L);
-            O = __builtin_fmaf(a.part_o[it * HD + dd], w, O);
+    for (int o = 32; o >= 1; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
+    float L = 0.f, O[HPL];
+#pragma unroll
+    for (int k = 0; k < HPL; k++) O[k] = 0.f;
+    for (int c0 = 0; c0 < nch; c0 += 64) {
+        const int c = c0 + lane;
+        float w = 0.f, lw = 0.f;
+        if (c < nch) {
+            const size_t it = base + (size_t)c * a.H;
+            w = __expf(a.part_ml[it * 2] - M);
+            lw = a.part_ml[it * 2 + 1] * w;
         }
-        attn_store(a, ((size_t)s * a.H + hidx) * HD + dd, O / L);
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) lw += __shfl_xor(lw, o);
+        L += lw;
+        const int cn = min(64, nch - c0);
+        const float* po = a.part_o + (base + (size_t)c0 * a.H) * HD + dl;
+#pragma unroll 8
+        for (int j = 0; j < cn; j++) {
+            const float wj = __shfl(w, j);
+#pragma unroll
+            for (int k = 0; k < HPL; k++) O[k] = __builtin_fmaf(po[(size_t)j * a.H * HD + 64 * k], wj, O[k]);
+        }
+    }
+    if (lane < HD) {
+#pragma unroll
+        for (int k = 0; k < HPL; k++) attn_store(a, ((size_t)s * a.H + h) * HD + lane + 64 * k, O[k] / L);
     }
 }
 
@@ -591,15 +583,19 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0) {
         const dim3 grid(items, Hkv);
         if (hd == 128)
-            hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(ACH), 0, st, a, G);
+            hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(ACH), 4 * G * 128 * sizeof(float), st, a, G);
         else
-            hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(ACH), 0, st, a, G);
+            hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(ACH), 4 * G * 64 * sizeof(float), st, a, G);
         QH_CHECK_HIP(hipGetLastError());
     } else {
         QH_TRY(launch_attn_t<_Float16>(a, hd, G, items, st));
     }
     if (max_ctx > ACH) {  // some sequence may span several chunks
-        hipLaunchKernelGGL(attn_merge_kernel, dim3(n, Hkv), dim3(ACH), 0, st, a, G, hd);
+        const dim3 mg(n, H);
+        if (hd == 128) hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(64), 0, st, a);
+        else if (hd == 64) hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, st, a);
+        else if (hd == 32) hipLaunchKernelGGL(attn_merge_kernel<32>, mg, dim3(64), 0, st, a);
+        else hipLaunchKernelGGL(attn_merge_kernel<16>, mg, dim3(64), 0, st, a);
         QH_CHECK_HIP(hipGetLastError());
     }
     return QRAF_HIP_OK;
