@@ -269,8 +269,11 @@ __device__ __forceinline__ uint2 mask_run(uint2 v, int pos0, int ctx) {
     return make_uint2(v.x & mx, v.y & my);
 }
 
+// 4 workgroups per CU (at most 128 VGPRs): the K and V loads of one wave
+// already cover its own latency, more resident workgroups cover the
+// prologue and epilogue of the others
 template <int HD>
-__global__ __launch_bounds__(ACH) void attn_mfma_kernel(AttnArgs a, int G) {
+__global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
     constexpr int KK = HD / 32;  // MFMA k-steps per score tile
     // q.K^T k-step kk, lane group s = l/16 covers dimensions 8*(4kk+s) .. +7:
@@ -506,11 +509,18 @@ __global__ __launch_bounds__(64) void attn_merge_kernel(AttnArgs a) {
         L += lw;
         const int cn = min(64, nch - c0);
         const float* po = a.part_o + (base + (size_t)c0 * a.H) * HD + dl;
-#pragma unroll 8
-        for (int j = 0; j < cn; j++) {
-            const float wj = __shfl(w, j);
+        for (int j0 = 0; j0 < cn; j0 += 8) {  // 8 chunks' loads in flight (clamped into the valid ones)
+            float v[8][HPL];
 #pragma unroll
-            for (int k = 0; k < HPL; k++) O[k] = __builtin_fmaf(po[(size_t)j * a.H * HD + 64 * k], wj, O[k]);
+            for (int u = 0; u < 8; u++)
+#pragma unroll
+                for (int k = 0; k < HPL; k++) v[u][k] = po[(size_t)min(j0 + u, cn - 1) * a.H * HD + 64 * k];
+#pragma unroll
+            for (int u = 0; u < 8; u++) {
+                const float wj = __shfl(w, j0 + u);
+#pragma unroll
+                for (int k = 0; k < HPL; k++) O[k] = j0 + u < cn ? __builtin_fmaf(v[u][k], wj, O[k]) : O[k];
+            }
         }
     }
     if (lane < HD) {

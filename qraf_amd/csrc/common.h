@@ -95,8 +95,30 @@ __device__ __forceinline__ void split_bf16(float v, uint16_t* hi, uint16_t* lo) 
 __device__ __forceinline__ float silu_gate(float g, float u) { return __fmul_rn(g / (1.0f + expf(-g)), u); }
 
 // element e of S slices (GEMM split-K partials) of `slice` floats, summed in
-// slice order; loads go out 8 slices at a time
+// slice order.  Up to 8 slices: every load issued before the first add (one
+// round trip); beyond, 8 slices per round trip.
+template <int S>
+__device__ __forceinline__ float sum_slices_n(const float* __restrict__ p, size_t slice, size_t e) {
+    float t[S];
+#pragma unroll
+    for (int u = 0; u < S; u++) t[u] = p[(size_t)u * slice + e];
+    float acc = t[0];
+#pragma unroll
+    for (int u = 1; u < S; u++) acc += t[u];
+    return acc;
+}
 __device__ __forceinline__ float sum_slices(const float* __restrict__ p, int S, size_t slice, size_t e) {
+    switch (S) {
+        case 1: return p[e];
+        case 2: return sum_slices_n<2>(p, slice, e);
+        case 3: return sum_slices_n<3>(p, slice, e);
+        case 4: return sum_slices_n<4>(p, slice, e);
+        case 5: return sum_slices_n<5>(p, slice, e);
+        case 6: return sum_slices_n<6>(p, slice, e);
+        case 7: return sum_slices_n<7>(p, slice, e);
+        case 8: return sum_slices_n<8>(p, slice, e);
+        default: break;
+    }
     float acc = p[e];
     int k = 1;
     for (; k + 8 <= S; k += 8) {

@@ -379,8 +379,7 @@ __global__ __launch_bounds__(64 * WM * WNW, 512 / (64 * WM * WNW)) void qgemm_ke
 // so the MFMA operand reads of 16 rows are bank-conflict-free; the swizzle
 // is applied through the per-lane global source addresses of the DMA.
 // Blocks past the split's range (stage padding) are read from wherever the
-// clamped or out-of-range address points (zeros or finite data) and weighted
-// by a zero scale.
+// clamped or out-of-range address points and not computed.
 // ---------------------------------------------------------------------------
 // Direct-to-LDS 16-byte load: lane i writes LDS [lds + 16 i, +16) from its
 // own voffset.  Issued as inline asm so that the compiler tracks none of these
@@ -458,9 +457,9 @@ __global__ __launch_bounds__(64 * WMN * WN, 1) void qgemm_pipe_kernel(const uint
     const int seg = lane >> 4, l16 = lane & 15;
     const int m0 = blockIdx.z * MW;
     const int n0 = blockIdx.x * NW;
-    const int b_begin = blockIdx.y * bps;  // bps: a positive multiple of 3 KC
+    const int b_begin = blockIdx.y * bps;  // bps: a positive multiple of KC
     const int b_end = min(nb, b_begin + bps);
-    const int nstages = bps / KC;  // a multiple of 3
+    const int nstages = (bps / KC + 2) / 3 * 3;  // whole trips of the 3-stage loop
 
     // ---- DMA source offsets (bytes), fixed per lane and instruction; the
     // stage's first block adds cb*64 (X) or cb*TB (W)
@@ -514,14 +513,44 @@ __global__ __launch_bounds__(64 * WMN * WN, 1) void qgemm_pipe_kernel(const uint
 #pragma unroll
         for (int u = 0; u < TN; u++) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+    // Software pipeline over 16-row batch tiles: the scale FMAs of a tile's
+    // MFMA results are issued two tiles later (between the MFMAs of that
+    // tile), when those results are complete, so the VALU work of a wave runs
+    // while its own MFMAs execute.  Steps s = (block in stage) * TM + t use
+    // result slot s % 4 (TM * KC is a multiple of 4, so the slots repeat per
+    // stage); sP: the scales of the previous block, whose last two tiles are
+    // pending when a block starts.
+    static_assert(TM % 2 == 0 && (TM * KC) % 4 == 0, "result ring");
+    f32x4 dR[4][TN];
+    float sP[TN];
+#pragma unroll
+    for (int u = 0; u < TN; u++) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) dR[q][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        sP[u] = 0.f;
+    }
     auto compute = [&](auto bsel, int c) {
         const uint8_t* buf = qg_stage<decltype(bsel)::value>();
         const int cb = b_begin + c * KC;
-        // one block at a time: unrolled over blocks, the scheduler hoists both
-        // blocks' fragment reads and spills
-#pragma unroll 1
+        // one block at a time where the slots do not depend on the block
+        // (unrolled over blocks, the scheduler hoists both blocks' fragment
+        // reads and spills)
+        constexpr int UJ = TM % 4 == 0 ? 1 : KC;
+#pragma unroll UJ
         for (int j = 0; j < KC; j++) {
-            const bool valid = cb + j < b_end;  // uniform; invalid blocks get scale 0
+            if (cb + j >= b_end) {  // uniform: past the split's range (stage padding)
+#pragma unroll
+                for (int t = 0; t < 2; t++)  // only the previous block's pending tiles
+#pragma unroll
+                    for (int u = 0; u < TN; u++)
+#pragma unroll
+                        for (int r = 0; r < 4; r++)
+                            acc[TM - 2 + t][u][r] =
+                                __builtin_fmaf(dR[(j * TM + t + 2) & 3][u][r], sP[u], acc[TM - 2 + t][u][r]);
+#pragma unroll
+                for (int u = 0; u < TN; u++) sP[u] = 0.f;  // later pending reads add nothing
+                continue;
+            }
             bf16x8 wf[TN];
             float sc[TN];
 #pragma unroll
@@ -537,7 +566,6 @@ __global__ __launch_bounds__(64 * WMN * WN, 1) void qgemm_pipe_kernel(const uint
                     r.scale = *(const uint16_t*)(tb + 2 * l16);
                     reinterpret_cast<uint32_t*>(&r)[1] = *(const uint32_t*)(tb + 32 + 16 * l16 + 4 * seg);
                 }
-                r.scale = valid ? r.scale : 0u;
                 convert<FMT>(r, wf[u], sc[u]);
             }
 #pragma unroll
@@ -546,14 +574,19 @@ __global__ __launch_bounds__(64 * WMN * WN, 1) void qgemm_pipe_kernel(const uint
                 const int slot = (4 * j + seg) ^ (row & 7);
                 const bf16x8 ah = *(const bf16x8*)(buf + row * G::XROW + 16 * slot);
                 const bf16x8 al = *(const bf16x8*)(buf + G::XPL + row * G::XROW + 16 * slot);
+                const int q = (j * TM + t) & 3, pq = (q + 2) & 3;  // this step's slot, the pending one's
+                const int pt = t >= 2 ? t - 2 : TM - 2 + t;         // pending tile
 #pragma unroll
                 for (int u = 0; u < TN; u++) {
-                    f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[u], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[u], d, 0, 0, 0);
+                    const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[u], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    dR[q][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[u], d, 0, 0, 0);
+                    const float ps = t >= 2 ? sc[u] : sP[u];
 #pragma unroll
-                    for (int r = 0; r < 4; r++) acc[t][u][r] = __builtin_fmaf(d[r], sc[u], acc[t][u][r]);
+                    for (int r = 0; r < 4; r++) acc[pt][u][r] = __builtin_fmaf(dR[pq][u][r], ps, acc[pt][u][r]);
                 }
             }
+#pragma unroll
+            for (int u = 0; u < TN; u++) sP[u] = sc[u];
         }
     };
 
@@ -577,6 +610,13 @@ __global__ __launch_bounds__(64 * WMN * WN, 1) void qgemm_pipe_kernel(const uint
         compute(B2{}, c + 2);
     }
     wait_vm_lgkm0<0>();  // drain the past-the-end stages before the workgroup exits
+#pragma unroll
+    for (int u = 0; u < TN; u++)  // the last block's last two tiles (slots 2, 3)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            acc[TM - 2][u][r] = __builtin_fmaf(dR[2][u][r], sP[u], acc[TM - 2][u][r]);
+            acc[TM - 1][u][r] = __builtin_fmaf(dR[3][u][r], sP[u], acc[TM - 1][u][r]);
+        }
 
     // epilogue: direct (+ residual) or this split's partial tile
     float* dst = part ? part + (size_t)blockIdx.y * M * N : Y;
@@ -667,7 +707,7 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
         } else {
             p.WM = 2;
             p.WN = 4;
-            p.TM = (Mc + 31) / 32;
+            p.TM = 2;  // 33..64 rows
             p.TN = 4;
             p.MW = 32 * p.TM;
         }
@@ -680,7 +720,9 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
         if (g_qg_splits > 0) S = g_qg_splits;
         else  // about one round of workgroups (one per CU): a second, partial round costs a full stage loop
             while (S < 64 && tiles * S * 2 <= 200 && nb >= 2 * S * unit) S *= 2;
-        p.bps = ((nb + S - 1) / S + unit - 1) / unit * unit;
+        // whole stages per split; the kernel rounds its stage loop up to whole
+        // trips and skips the blocks past the split
+        p.bps = ((nb + S - 1) / S + p.KC - 1) / p.KC * p.KC;
         p.S = (nb + p.bps - 1) / p.bps;
         p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
         return p;
@@ -800,7 +842,7 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
             part = (float*)ws;
         } else {  // no (or too small a) workspace: one split
             p.S = 1;
-            const int unit = (p.pipe ? 3 : 2) * p.KC;
+            const int unit = (p.pipe ? 1 : 2) * p.KC;
             p.bps = (nb + unit - 1) / unit * unit;
         }
     }
@@ -812,14 +854,10 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
                        xh, xl, K, M, Y, add, p.bps, part)
         if (dtype == DT_Q8_0) {
             if (p.WM == 1) QH_P(8, 8, 2, 8, 1);
-            else if (p.TM == 2) QH_P(8, 2, 4, 4, 2);
-            else if (p.TM == 3) QH_P(8, 3, 4, 4, 2);
-            else QH_P(8, 4, 4, 4, 2);
+            else QH_P(8, 2, 4, 4, 2);
         } else {
             if (p.WM == 1) QH_P(4, 8, 2, 8, 1);
-            else if (p.TM == 2) QH_P(4, 2, 4, 4, 2);
-            else if (p.TM == 3) QH_P(4, 3, 4, 4, 2);
-            else QH_P(4, 4, 4, 4, 2);
+            else QH_P(4, 2, 4, 4, 2);
         }
 #undef QH_P
     } else {
