@@ -22,6 +22,9 @@ The same JSON line also reports the other configurations of the metric:
   gemm         batched Q-GEMM, B in {8,32,64,128}, Qwen2.5-3B projection shapes
   attention    ragged paged decode attention: 128 sequences, context U[128,4096],
                16 q / 2 kv heads, head_dim 128, fp16 K/V
+  steady_b128  (not in the default run) the steady 128-sequence decode of
+               decode_b128 alone, in its own engine, for a profile whose every
+               GEMM runs at 128 rows
 All weights are synthetic (N(0,0.02), generated and quantized on the GPU).
 
     python bench.py [--gpus 1] [--steps 1000] [--warmup 50] [--cpu-seconds 12] [--only matvec,gemm,...]
@@ -216,8 +219,12 @@ def bench_gemm(args, rt):
     call, DeviceBuffer, stream, lib = rt["call"], rt["DeviceBuffer"], rt["stream"], rt["lib"]
     rng = np.random.default_rng(7)
     out = []
+    want = [c.strip() for c in args.gemm_cases.split(",") if c.strip()]
     for dt, fmt in ((Q8, "q8_0"), (Q4, "q4_0")):
         for (n, k) in GEMM_SHAPES:
+            batches = [b for b in (8, 32, 64, 128) if not want or f"{fmt} {n}x{k} B={b}" in want]
+            if not batches:
+                continue
             wbytes = n * row_bytes(dt, k)
             copies = max(2, math.ceil(POOL_BYTES / wbytes))
             pool = DeviceBuffer(copies * wbytes)
@@ -232,7 +239,7 @@ def bench_gemm(args, rt):
             for c in range(tcopies):
                 call("qraf_hip_repack_tiles_dev", pool.ptr + (c % copies) * wbytes, dt, n, k, tpool.ptr + c * tbytes,
                      stream.h)
-            for b in (8, 32, 64, 128):
+            for b in batches:
                 dx = DeviceBuffer.from_array(rng.standard_normal((b, k)).astype(np.float32))
                 xh, xl, y = DeviceBuffer(b * k * 2), DeviceBuffer(b * k * 2), DeviceBuffer(b * n * 4)
                 call("qraf_hip_split_bf16_dev", dx.ptr, xh.ptr, xl.ptr, b, k, stream.h)
@@ -373,20 +380,27 @@ QWEN = dict(vocab=151936, hidden=2048, layers=36, heads=16, kv_heads=2, inter=11
             eps=1e-6)
 
 
-def bench_decode_b128(args, rt):
-    """C5: 128 concurrent requests, continuous batching.  The headline run
-    feeds prompts in chunks (up to --prefill-chunk tokens of one request per
-    step, within a --rows row budget, decode rows first); the token-by-token
-    run (every active request one row per step) is reported beside it."""
-    from qraf_amd.engine import BatchScheduler, Engine, model_config
+def qwen_engine(args, rows):
+    """The Qwen2.5-3B-architecture engine of the batch-128 legs (random Q4_0 weights, fp16 KV pages)."""
+    from qraf_amd.engine import Engine, model_config
     cfg = model_config(*(QWEN[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq",
                                            "rope_theta", "eps")))
-    rows = max(128, args.rows)
     pages = 128 * (-(-QWEN["max_seq"] // 16)) + 64
     e = Engine(cfg, kv_dtype=F16, max_batch=rows, num_pages=pages)
     e.generate_weights(Q4, Q4, Q4, True, True, 3)
     e.finalize()
     e.set_graphs(not args.no_graphs)
+    return e
+
+
+def bench_decode_b128(args, rt):
+    """C5: 128 concurrent requests, continuous batching.  The headline run
+    feeds prompts in chunks (up to --prefill-chunk tokens of one request per
+    step, within a --rows row budget, decode rows first); the token-by-token
+    run (every active request one row per step) is reported beside it."""
+    from qraf_amd.engine import BatchScheduler
+    rows = max(128, args.rows)
+    e = qwen_engine(args, rows)
     rng = np.random.default_rng(3)
     warm = BatchScheduler(e, max_batch=128, max_rows=rows, prefill_chunk=args.prefill_chunk)
     for _ in range(8):
@@ -421,6 +435,14 @@ def bench_decode_b128(args, rt):
                         "request's last token, then prompt chunks within the row budget",
                 "token_by_token": tbt, "stream_agreement": stream_agreement(streams_c, streams_t),
                 "steady_decode": steady})
+    return out
+
+
+def bench_steady_b128(args, rt):
+    """The steady 128-sequence decode alone (every GEMM at 128 rows), for profiling."""
+    e = qwen_engine(args, 128)
+    out = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps)
+    e.close()
     return out
 
 
@@ -481,6 +503,8 @@ def main():
     ap.add_argument("--cases", default="",
                     help="restrict the matvec leg to these cases, e.g. 'q8_0 11008x4096' (comma-separated; "
                          "a profile of one case then has one shape per kernel)")
+    ap.add_argument("--gemm-cases", default="",
+                    help="restrict the GEMM leg to these cases, e.g. 'q4_0 11008x2048 B=128' (comma-separated)")
     ap.add_argument("--no-graphs", action="store_true",
                     help="decode legs launch every step's kernels eagerly instead of replaying step graphs")
     ap.add_argument("--rows-per-wave", type=int, default=0)
@@ -506,7 +530,7 @@ def main():
     print(f"# matvec done: {value:.1f} GB/s", file=sys.stderr, flush=True)
     extra = {}
     for part, fn in (("gemm", bench_gemm), ("attention", bench_attention), ("decode_b1", bench_decode_b1),
-                     ("decode_b128", bench_decode_b128)):
+                     ("decode_b128", bench_decode_b128), ("steady_b128", bench_steady_b128)):
         if part in only:
             extra[part] = fn(args, rt)
             print(f"# {part} done", file=sys.stderr, flush=True)
