@@ -411,12 +411,19 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // The three stage buffers are file-scope LDS objects reached through
 // compile-time accessors: the compiler then sees that a DMA into one buffer
 // does not alias reads of another and inserts no waits of its own.
+// Kernels whose stages fit QG_STAGE_SMALL use the small set (72 KB in all),
+// so two workgroups fit in a CU's LDS.
 constexpr int QG_STAGE_MAX = 53248;
+constexpr int QG_STAGE_SMALL = 24576;
 __shared__ __align__(16) uint8_t qg_sb0[QG_STAGE_MAX];
 __shared__ __align__(16) uint8_t qg_sb1[QG_STAGE_MAX];
 __shared__ __align__(16) uint8_t qg_sb2[QG_STAGE_MAX];
-template <int B>
+__shared__ __align__(16) uint8_t qg_ss0[QG_STAGE_SMALL];
+__shared__ __align__(16) uint8_t qg_ss1[QG_STAGE_SMALL];
+__shared__ __align__(16) uint8_t qg_ss2[QG_STAGE_SMALL];
+template <int B, bool SMALL>
 __device__ __forceinline__ uint8_t* qg_stage() {
+    if (SMALL) return B == 0 ? qg_ss0 : B == 1 ? qg_ss1 : qg_ss2;
     return B == 0 ? qg_sb0 : B == 1 ? qg_sb1 : qg_sb2;
 }
 
@@ -439,10 +446,12 @@ struct PipeGeom {
     static_assert((XPL / 16) % 64 == 0, "an X DMA instruction must stay in one plane");
     static_assert(KC * 4 >= 8, "swizzle needs 8 pieces per row");
     static_assert(STAGE <= QG_STAGE_MAX, "stage buffer too small");
+    static constexpr bool SMALL = STAGE <= QG_STAGE_SMALL;  // two workgroups per CU
+    static constexpr int MINB = SMALL ? 2 : 1;
 };
 
 template <int FMT, int TM, int TN, int KC, int WN, int WMN>
-__global__ __launch_bounds__(64 * WMN * WN, 1) void qgemm_pipe_kernel(const uint8_t* __restrict__ Wt, int N, int nb,
+__global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>::MINB)) void qgemm_pipe_kernel(const uint8_t* __restrict__ Wt, int N, int nb,
                                                                  const uint16_t* __restrict__ xh,
                                                                  const uint16_t* __restrict__ xl, int K, int M,
                                                                  float* Y, const float* add, int bps,
@@ -487,7 +496,7 @@ __global__ __launch_bounds__(64 * WMN * WN, 1) void qgemm_pipe_kernel(const uint
         wo[q] = (uint32_t)((size_t)T * nb * TB) + off;
     }
     auto issue = [&](auto bsel, int c) {
-        uint8_t* buf = qg_stage<decltype(bsel)::value>();
+        uint8_t* buf = qg_stage<decltype(bsel)::value, G::SMALL>();
         const int cb = min(b_begin + c * KC, b_end - 1);  // stages past the range re-read valid blocks
 #pragma unroll
         for (int q = 0; q < G::XI; q++) {
@@ -530,7 +539,7 @@ __global__ __launch_bounds__(64 * WMN * WN, 1) void qgemm_pipe_kernel(const uint
         sP[u] = 0.f;
     }
     auto compute = [&](auto bsel, int c) {
-        const uint8_t* buf = qg_stage<decltype(bsel)::value>();
+        const uint8_t* buf = qg_stage<decltype(bsel)::value, G::SMALL>();
         const int cb = b_begin + c * KC;
         // one block at a time where the slots do not depend on the block
         // (unrolled over blocks, the scheduler hoists both blocks' fragment
@@ -678,7 +687,8 @@ struct QgPlan {
 // Tuning overrides (qraf_hip_set_qgemm_tuning): 0 = automatic.
 static int g_qg_waves = 0;   // 4 or 8 waves per workgroup for batch tiles > 32 rows
 static int g_qg_splits = 0;  // forced split count
-static int g_qg_pipe = 0;    // 1: pipelined kernel for every tiled batch over 32 rows, -1: never
+static int g_qg_pipe = 0;    // 1: pipelined kernel for every tiled batch over 32 rows, 2: its narrow
+                             // 4-wave form, -1: never
 static int g_qg_mchunk = 0;  // batch rows per workgroup at most (0: QG_MCHUNK)
 
 // Tile shape and split count for an N x K matrix times M rows.  Batch tiles
@@ -689,7 +699,37 @@ static int g_qg_mchunk = 0;  // batch rows per workgroup at most (0: QG_MCHUNK)
 static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
     QgPlan p{};
     int Mc = min(M, g_qg_mchunk ? g_qg_mchunk : QG_MCHUNK);
-    const bool pipe = g_qg_pipe > 0 || (g_qg_pipe == 0 && N >= 8192);
+    const bool pipe = g_qg_pipe == 1 || (g_qg_pipe == 0 && N >= 8192);
+    // the narrow form also by default for long, narrow products at > 64 rows
+    // (the down projection: 2048 x 11008 at 128 rows 36 -> 29 us on MI355X,
+    // partial reduction included)
+    const bool narrow = g_qg_pipe == 2 || (g_qg_pipe == 0 && N < 8192 && K >= 8192 && Mc > 64 && !g_qg_mchunk);
+    if (tiled && Mc > 32 && narrow) {
+        // narrow pipelined kernel: 4 waves side by side, 128 weight rows, all
+        // 16*TM batch rows per wave (64 or 128); two workgroups per CU when
+        // the 64-row stages fit the small LDS set
+        p.pipe = true;
+        p.KC = 2;
+        p.WM = 1;
+        p.WN = 4;
+        p.TN = 2;
+        p.TM = g_qg_mchunk == 128 ? 8 : 4;  // 64-row chunks, two workgroups per CU (measured best)
+        p.MW = 16 * p.TM;
+        p.NW = 128;
+        p.ntiles = (N + p.NW - 1) / p.NW;
+        p.mchunks = (M + p.MW - 1) / p.MW;
+        const int nb = K / 32;
+        const size_t tiles = (size_t)p.ntiles * p.mchunks;
+        const size_t slots = p.TM == 4 ? 512 : 256;
+        int S = 1;
+        if (g_qg_splits > 0) S = g_qg_splits;
+        else
+            while (S < 64 && tiles * S * 2 <= slots && nb >= 2 * S * p.KC) S *= 2;
+        p.bps = ((nb + S - 1) / S + p.KC - 1) / p.KC * p.KC;
+        p.S = (nb + p.bps - 1) / p.bps;
+        p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
+        return p;
+    }
     if (tiled && Mc > 32 && pipe) {
         // pipelined kernel, 3-stage LDS ring, 1 workgroup per CU, 256 weight rows:
         // up to 64 batch rows 2 x 4 waves of 16*TM x 64 rows; beyond, 8 waves
@@ -764,7 +804,7 @@ int set_qgemm_tuning(int waves, int splits, int pipe, int mchunk) {
     QH_REQUIRE(mchunk == 0 || mchunk == 16 || mchunk == 32 || mchunk == 64 || mchunk == 128, QRAF_HIP_ERR_INVALID,
                "qgemm tuning: batch chunk %d", mchunk);
     QH_REQUIRE(splits >= 0 && splits <= 256, QRAF_HIP_ERR_INVALID, "qgemm tuning: splits %d", splits);
-    QH_REQUIRE(pipe >= -1 && pipe <= 1, QRAF_HIP_ERR_INVALID, "qgemm tuning: pipe %d", pipe);
+    QH_REQUIRE(pipe >= -1 && pipe <= 2, QRAF_HIP_ERR_INVALID, "qgemm tuning: pipe %d", pipe);
     g_qg_waves = waves;
     g_qg_splits = splits;
     g_qg_pipe = pipe;
@@ -850,13 +890,20 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
     const dim3 grid(p.ntiles, p.S, p.mchunks);
     if (p.pipe) {
 #define QH_P(F, TM_, TN_, WN_, WM_)                                                                        \
-    hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_>), grid, dim3(512), 0, s, (const uint8_t*)W, N, nb, \
+    hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_>), grid, dim3(64 * WN_ * WM_), 0, s,           \
+                       (const uint8_t*)W, N, nb, \
                        xh, xl, K, M, Y, add, p.bps, part)
         if (dtype == DT_Q8_0) {
-            if (p.WM == 1) QH_P(8, 8, 2, 8, 1);
+            if (p.WN == 4 && p.WM == 1) {
+                if (p.TM == 8) QH_P(8, 8, 2, 4, 1);
+                else QH_P(8, 4, 2, 4, 1);
+            } else if (p.WM == 1) QH_P(8, 8, 2, 8, 1);
             else QH_P(8, 2, 4, 4, 2);
         } else {
-            if (p.WM == 1) QH_P(4, 8, 2, 8, 1);
+            if (p.WN == 4 && p.WM == 1) {
+                if (p.TM == 8) QH_P(4, 8, 2, 4, 1);
+                else QH_P(4, 4, 2, 4, 1);
+            } else if (p.WM == 1) QH_P(4, 8, 2, 8, 1);
             else QH_P(4, 2, 4, 4, 2);
         }
 #undef QH_P

@@ -125,14 +125,17 @@ def test_repack_tiles_layout(hip, dt, shape):
 @pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
 @pytest.mark.parametrize("case", [(8192, 1024, 100), (2048, 2048, 128), (300, 512, 64), (1000, 576, 33)],
                          ids=lambda c: "x".join(map(str, c)))
-def test_qgemm_pipelined_kernel(hip, dt, case):
-    """The pipelined tiled kernel (direct-to-LDS 3-stage ring) forced on for
-    every shape, with and without split-K, against the oracle."""
+@pytest.mark.parametrize("form", [(1, 0), (2, 0), (2, 128)], ids=["wide", "narrow64", "narrow128"])
+def test_qgemm_pipelined_kernel(hip, dt, case, form):
+    """The pipelined tiled kernel (direct-to-LDS 3-stage ring), in its wide
+    (8 waves, 256 weight rows) and narrow (4 waves, 128 weight rows; 64- or
+    128-row batch chunks) forms, forced on for every shape, with and without
+    split-K, against the oracle."""
     N, K, M = case
     rng = np.random.default_rng(N + 3 * K + M + dt)
     wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
     X = rng.standard_normal((M, K)).astype(np.float32)
-    hip._lib.call("qraf_hip_set_qgemm_tuning", 0, 0, 1, 0)
+    hip._lib.call("qraf_hip_set_qgemm_tuning", 0, 0, form[0], form[1])
     try:
         Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, repeats=2)
         Y1, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
