@@ -700,10 +700,13 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
     QgPlan p{};
     int Mc = min(M, g_qg_mchunk ? g_qg_mchunk : QG_MCHUNK);
     const bool pipe = g_qg_pipe == 1 || (g_qg_pipe == 0 && N >= 8192);
-    // the narrow form also by default for long, narrow products at > 64 rows
-    // (the down projection: 2048 x 11008 at 128 rows 36 -> 29 us on MI355X,
-    // partial reduction included)
-    const bool narrow = g_qg_pipe == 2 || (g_qg_pipe == 0 && N < 8192 && K >= 8192 && Mc > 64 && !g_qg_mchunk);
+    // the narrow form is the default for narrow products at > 64 rows except
+    // the smallest at <= 128 rows (MI355X, Q4, partial reduction included:
+    // down 2048 x 11008 at 128/256/512 rows 36/61/105 -> 29/43/76 us, QKV
+    // 2560 x 2048 19/28/39 -> 18/23/31 us, O 2048 x 2048 at 256/512 rows
+    // 22/28 -> 20/23 us; O at 128 rows stays at 14 us on qgemm_kernel)
+    const bool narrow = g_qg_pipe == 2 || (g_qg_pipe == 0 && !g_qg_mchunk && N < 8192 && Mc > 64 &&
+                                           (M > 128 || (size_t)N * K > (size_t)4608 * 1024));
     if (tiled && Mc > 32 && narrow) {
         // narrow pipelined kernel: 4 waves side by side, 128 weight rows, all
         // 16*TM batch rows per wave (64 or 128); two workgroups per CU when
@@ -723,8 +726,8 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
         const size_t slots = p.TM == 4 ? 512 : 256;
         int S = 1;
         if (g_qg_splits > 0) S = g_qg_splits;
-        else
-            while (S < 64 && tiles * S * 2 <= slots && nb >= 2 * S * p.KC) S *= 2;
+        else  // at most one round of workgroups, at least 16 blocks per split
+            while (S < 64 && tiles * S * 2 <= slots && nb >= 32 * S) S *= 2;
         p.bps = ((nb + S - 1) / S + p.KC - 1) / p.KC * p.KC;
         p.S = (nb + p.bps - 1) / p.bps;
         p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
