@@ -22,6 +22,8 @@ The same JSON line also reports the other configurations of the metric:
   gemm         batched Q-GEMM, B in {8,32,64,128}, Qwen2.5-3B projection shapes
   attention    ragged paged decode attention: 128 sequences, context U[128,4096],
                16 q / 2 kv heads, head_dim 128, fp16 K/V
+  load         QRAF file -> HBM (qraf_engine_create_from_file) of the
+               Qwen2.5-3B-architecture Q4 model, from a file this leg writes
   steady_b128  (not in the default run) the steady 128-sequence decode of
                decode_b128 alone, in its own engine, for a profile whose every
                GEMM runs at 128 rows
@@ -438,6 +440,132 @@ def bench_decode_b128(args, rt):
     return out
 
 
+def fnv1a(name: str) -> int:
+    h = 14695981039346656037
+    for ch in name.encode():
+        h = ((h ^ ch) * 1099511628211) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def write_qraf_synthetic(path, q, wdt, seed, rt):
+    """A .qraf file (include/qraf/format.h:26-132 layout) holding exactly the
+    weights Engine.generate_weights(wdt, wdt, wdt, tied=True, qkv_bias=True,
+    seed) makes on the device: each tensor from qraf_hip_gen_weights_dev with
+    stream = FNV-1a(name), norms 1, f32 q/k/v biases, no lm_head (tied).
+    Returns the file size."""
+    import struct
+    call, DeviceBuffer, stream = rt["call"], rt["DeviceBuffer"], rt["stream"]
+    D, F, V, nl, H, Hkv = q["hidden"], q["inter"], q["vocab"], q["layers"], q["heads"], q["kv_heads"]
+    hd = D // H
+    qd, kvd = H * hd, Hkv * hd
+    ts = [("model.embed_tokens.weight", wdt, (V, D))]
+    for layer in range(nl):
+        p = f"model.layers.{layer}."
+        ts += [(p + "self_attn.q_proj.weight", wdt, (qd, D)), (p + "self_attn.k_proj.weight", wdt, (kvd, D)),
+               (p + "self_attn.v_proj.weight", wdt, (kvd, D)), (p + "self_attn.o_proj.weight", wdt, (D, qd)),
+               (p + "self_attn.q_proj.bias", F32, (qd,)), (p + "self_attn.k_proj.bias", F32, (kvd,)),
+               (p + "self_attn.v_proj.bias", F32, (kvd,)), (p + "mlp.gate_proj.weight", wdt, (F, D)),
+               (p + "mlp.up_proj.weight", wdt, (F, D)), (p + "mlp.down_proj.weight", wdt, (D, F)),
+               (p + "input_layernorm.weight", F32, (D,)), (p + "post_attention_layernorm.weight", F32, (D,))]
+    ts.append(("model.norm.weight", F32, (D,)))
+    nbytes = lambda dt, sh: sh[0] * row_bytes(dt, sh[1]) if len(sh) == 2 else 4 * sh[0]
+    cfg = [("architecture", 2, "qwen2")] + [(k, 0, q[n]) for k, n in (
+        ("vocab_size", "vocab"), ("hidden_size", "hidden"), ("num_layers", "layers"), ("num_heads", "heads"),
+        ("num_kv_heads", "kv_heads"), ("intermediate_size", "inter"), ("max_seq_len", "max_seq"))] + [
+        ("rope_theta", 1, q["rope_theta"]), ("rms_norm_eps", 1, q["eps"])]
+    strtab, soff = bytearray(), {}
+
+    def sref(x):
+        if x not in soff:
+            soff[x] = len(strtab)
+            strtab.extend(x.encode() + b"\0")
+        return soff[x]
+    for k, ty, v in cfg:
+        sref(k)
+        if ty == 2:
+            sref(v)
+    for n, _, _ in ts:
+        sref(n)
+    cfg_off = 128
+    cfg_blk = struct.pack("<I", len(cfg)) + b"".join(
+        struct.pack("<III", sref(k), ty, sref(v) if ty == 2 else
+                    (struct.unpack("<I", struct.pack("<f", v))[0] if ty == 1 else v)) for k, ty, v in cfg)
+    dir_off = cfg_off + len(cfg_blk)
+    qdir_off = dir_off + 80 * len(ts)
+    str_off = qdir_off + 32
+    off = (str_off + len(strtab) + 63) // 64 * 64
+    data_off, offs = off, []
+    for n, dt, sh in ts:
+        offs.append(off)
+        off = (off + nbytes(dt, sh) + 63) // 64 * 64
+    size = off
+    tdir = b"".join(struct.pack("<QII8IIIQQII", fnv1a(n), sref(n), len(sh), *(list(sh) + [0] * (8 - len(sh))), dt,
+                                0 if dt in (Q8, Q4) else 0xFFFFFFFF, o, nbytes(dt, sh), 0, 0)
+                    for (n, dt, sh), o in zip(ts, offs))
+    qdir = struct.pack("<IIIIffII", 0, wdt, 32, 1, 0.0, 0.0, 1, 0)
+    hdr = struct.pack("<IIQ" + "Q" * 11 + "IIII8s", 0x46415251, 1, size, cfg_off, len(cfg_blk), 0, 0, dir_off,
+                      len(tdir), qdir_off, len(qdir), str_off, len(strtab), data_off, len(ts), 1, 0, 0, b"\0" * 8)
+    big = max(nbytes(dt, sh) for _, dt, sh in ts)
+    buf = DeviceBuffer(big)
+    with open(path, "wb") as f:
+        f.write(hdr + cfg_blk + tdir + qdir + bytes(strtab))
+        for (n, dt, sh), o in zip(ts, offs):
+            cnt = sh[0] * (sh[1] if len(sh) == 2 else 1)
+            if n.endswith("layernorm.weight") or n == "model.norm.weight":
+                data = np.ones(cnt, np.float32).tobytes()
+            else:
+                call("qraf_hip_gen_weights_dev", buf.ptr, dt, cnt, seed, fnv1a(n), 0.02, stream.h)
+                stream.synchronize()  # the download is not ordered after work on this stream
+                data = buf.download(np.uint8, nbytes(dt, sh)).tobytes()
+            f.write(b"\0" * (o - f.tell()))
+            f.write(data)
+        f.write(b"\0" * (size - f.tell()))
+    buf.free()
+    return size
+
+
+def bench_load(args, rt):
+    """QRAF file -> HBM for the Qwen2.5-3B architecture in Q4_0 (tied head,
+    QKV bias): qraf_engine_create_from_file on a file this leg writes (warm
+    page cache), then one forward checked bit for bit against an engine whose
+    weights were generated on the device with the same seed."""
+    import tempfile
+    from qraf_amd.engine import Engine, Transformer, model_config
+    tmp = tempfile.mkdtemp()
+    path = os.path.join(tmp, "qwen3b_q4.qraf")
+    try:
+        t0 = time.perf_counter()
+        size = write_qraf_synthetic(path, QWEN, Q4, 3, rt)
+        t_write = time.perf_counter() - t0
+        loads = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            e = Engine.from_file(path, kv_dtype=F16, max_batch=1)
+            rt["call"]("qraf_hip_device_synchronize")
+            loads.append(time.perf_counter() - t0)
+            if len(loads) < 2:
+                e.close()
+        tf = Transformer(e)
+        cfg = model_config(*(QWEN[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq",
+                                               "rope_theta", "eps")))
+        g = Engine(cfg, kv_dtype=F16, max_batch=1)
+        g.generate_weights(Q4, Q4, Q4, True, True, 3)
+        g.finalize()
+        same = bool(np.array_equal(tf.forward(17, 0), Transformer(g).forward(17, 0)))
+        e.close()
+        g.close()
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+        os.rmdir(tmp)
+    best = min(loads)
+    return {"model": "Qwen2.5-3B architecture, Q4_0, tied head, QKV bias", "file_bytes": size,
+            "load_s": round(best, 3), "load_GB_s": round(size / best / 1e9, 2), "write_s": round(t_write, 2),
+            "logits_equal_device_generated": same,
+            "note": "qraf_engine_create_from_file: validate + map + copy every tensor to HBM + finalize (tile-major "
+                    "repack on the device), file in the page cache; best of 2"}
+
+
 def bench_steady_b128(args, rt):
     """The steady 128-sequence decode alone (every GEMM at 128 rows), for profiling."""
     e = qwen_engine(args, 128)
@@ -495,7 +623,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="matvec,gemm,attention,decode_b1,decode_b128")
+    ap.add_argument("--only", default="matvec,gemm,attention,decode_b1,decode_b128,load")
     ap.add_argument("--requests", type=int, default=256, help="requests in the batch-128 decode run")
     ap.add_argument("--decode-steps", type=int, default=64, help="timed steps of the steady 128-sequence decode")
     ap.add_argument("--rows", type=int, default=512, help="row budget per step of the continuous-batch run")
@@ -530,7 +658,7 @@ def main():
     print(f"# matvec done: {value:.1f} GB/s", file=sys.stderr, flush=True)
     extra = {}
     for part, fn in (("gemm", bench_gemm), ("attention", bench_attention), ("decode_b1", bench_decode_b1),
-                     ("decode_b128", bench_decode_b128), ("steady_b128", bench_steady_b128)):
+                     ("decode_b128", bench_decode_b128), ("steady_b128", bench_steady_b128), ("load", bench_load)):
         if part in only:
             extra[part] = fn(args, rt)
             print(f"# {part} done", file=sys.stderr, flush=True)

@@ -35,6 +35,7 @@ extern "C" {
 #define QRAF_HIP_ERR_HIP (-3)     /* HIP runtime failure               */
 #define QRAF_HIP_ERR_NOMEM (-4)   /* device or page-pool exhaustion    */
 #define QRAF_HIP_ERR_STATE (-5)   /* call not valid in the current state */
+#define QRAF_HIP_ERR_FORMAT (-6)  /* malformed QRAF file                */
 
 #define QRAF_DTYPE_F32 0u
 #define QRAF_DTYPE_F16 1u
@@ -127,7 +128,7 @@ int qraf_hip_quantize_dev(const float* src, uint64_t count, uint32_t dtype, void
  * conventionally qraf_hip_name_hash(tensor name). */
 int qraf_hip_gen_weights_dev(void* dst, uint32_t dtype, uint64_t count, uint64_t seed, uint64_t stream_id,
                              float stddev, void* stream);
-/* FNV-1a of a tensor name (format.h:296-303); returns the hash itself. */
+/* FNV-1a of a tensor name (format.h:136-147); returns the hash itself. */
 uint64_t qraf_hip_name_hash(const char* name);
 
 /* ------------------------------------------- ragged paged decode attention */
@@ -262,6 +263,26 @@ int qraf_engine_generate_weights(qraf_engine* engine, uint32_t weight_dtype, uin
                                  uint32_t head_dtype, int32_t tied, int32_t qkv_bias, uint64_t seed);
 /* Checks that every tensor the forward pass reads is present. */
 int qraf_engine_finalize(qraf_engine* engine);
+
+/* QRAF file -> HBM.  The file layout of include/qraf/format.h:26-132 is
+ * checked as validate_header (src/qraf/header.cpp:8-45) and get_string
+ * (src/qraf/loader.cpp:273-277) do, and strings must end inside the string
+ * table; a malformed file returns QRAF_HIP_ERR_FORMAT, an unreadable path
+ * QRAF_HIP_ERR_INVALID.
+ *
+ * qraf_file_read_config: the model config stored in the file
+ * (QrafModel::parse_config, loader.cpp:133-177), with ModelConfig's defaults
+ * (include/core/types.h:97-124) for absent keys.  Host only: no GPU use.
+ * num_tensors may be NULL.
+ *
+ * qraf_engine_create_from_file: QrafModel::load + Transformer::init
+ * (loader.cpp:51-117, src/nn/transformer.cpp:310-439) in one call: maps the
+ * file, creates an engine with the file's config and `options`, copies every
+ * tensor from the mapping into HBM (qraf_engine_set_tensor) and finalizes.
+ * Runs the LLaMA-family architectures (llama, qwen2, mistral, or none named);
+ * others return QRAF_HIP_ERR_INVALID.  *engine is NULL on failure. */
+int qraf_file_read_config(const char* path, qraf_model_config* config, uint32_t* num_tensors);
+int qraf_engine_create_from_file(const char* path, const qraf_engine_options* options, qraf_engine** engine);
 
 /* Sequences own KV pages; positions are added in order (pos <= length). */
 int qraf_engine_seq_create(qraf_engine* engine, int32_t* seq_id);

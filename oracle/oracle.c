@@ -356,7 +356,7 @@ uint64_t or_mix64(uint64_t z) { /* splitmix64 finaliser */
     return z ^ (z >> 31);
 }
 
-/* format.h:296-303 */
+/* format.h:136-147 */
 uint64_t or_fnv1a(const char* s) {
     uint64_t h = 14695981039346656037ULL;
     for (; *s; s++) {

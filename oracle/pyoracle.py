@@ -269,14 +269,17 @@ class Model:
         n = lib().or_generate(self.h, _u32(p), p.size, max_tokens, penalty, eos, _u32(out))
         return out[:n].tolist()
 
-    def write_qraf(self, path):
-        """Write this model as a .qraf file with the reference's QrafWriter."""
+    def write_qraf(self, path, arch=None):
+        """Write this model as a .qraf file with the reference's QrafWriter
+        (architecture "qwen2" with q/k/v biases, else "llama", unless given)."""
         R = ref()
         if R is None:
             raise RuntimeError("oracle/_ref not built")
         c = self.cfg
         w = R.ref_writer_new()
-        R.ref_writer_config_str(w, b"architecture", b"qwen2" if c.qkv_bias else b"llama")
+        if arch is None:
+            arch = "qwen2" if c.qkv_bias else "llama"
+        R.ref_writer_config_str(w, b"architecture", arch.encode())
         for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq"):
             key = {"vocab": "vocab_size", "hidden": "hidden_size", "layers": "num_layers", "heads": "num_heads",
                    "kv_heads": "num_kv_heads", "inter": "intermediate_size", "max_seq": "max_seq_len"}[k]

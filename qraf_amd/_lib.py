@@ -13,7 +13,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(PKG, "libqraf_hip.so")
 
 OK = 0
-ERR_INVALID, ERR_DTYPE, ERR_HIP, ERR_NOMEM, ERR_STATE = -1, -2, -3, -4, -5
+ERR_INVALID, ERR_DTYPE, ERR_HIP, ERR_NOMEM, ERR_STATE, ERR_FORMAT = -1, -2, -3, -4, -5, -6
 F32, F16, Q8_0, Q4_0 = 0, 1, 10, 20
 
 vp = C.c_void_p
@@ -108,6 +108,8 @@ SIGNATURES.update({
     "qraf_engine_set_graphs": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_forward": (C.c_int, [vp, C.c_uint32, C.c_int32, fp]),
     "qraf_engine_reset": (C.c_int, [vp]),
+    "qraf_file_read_config": (C.c_int, [C.c_char_p, C.POINTER(ModelConfig), u32p]),
+    "qraf_engine_create_from_file": (C.c_int, [C.c_char_p, C.POINTER(EngineOptions), C.POINTER(vp)]),
 })
 
 

@@ -170,7 +170,7 @@ int qraf_hip_quantize_dev(const float* src, uint64_t count, uint32_t dtype, void
     return qraf_hip::launch_quantize(src, count, dtype, dst, qraf_hip::as_stream(stream));
 }
 
-uint64_t qraf_hip_name_hash(const char* name) {  // include/qraf/format.h:296-303
+uint64_t qraf_hip_name_hash(const char* name) {  // include/qraf/format.h:136-147
     uint64_t h = 14695981039346656037ULL;
     for (; name && *name; name++) {
         h ^= (uint64_t)(unsigned char)*name;

@@ -17,6 +17,7 @@ reference does.
 from __future__ import annotations
 
 import ctypes as C
+import os
 from collections import deque
 from dataclasses import dataclass, field
 
@@ -24,11 +25,20 @@ import numpy as np
 
 from ._lib import F16, F32, Q4_0, Q8_0, EngineOptions, ModelConfig, call, fp, i32p, lib, u32p
 
-__all__ = ["Engine", "Transformer", "InferenceEngine", "BatchScheduler", "Request", "model_config"]
+__all__ = ["Engine", "Transformer", "InferenceEngine", "BatchScheduler", "Request", "model_config",
+           "read_file_config"]
 
 
 def model_config(vocab, hidden, layers, heads, kv_heads, inter, max_seq=2048, rope_theta=1e4, eps=1e-5):
     return ModelConfig(vocab, hidden, layers, heads, kv_heads, inter, max_seq, rope_theta, eps)
+
+
+def read_file_config(path: str) -> ModelConfig:
+    """The model config stored in a .qraf file (QrafModel::parse_config,
+    loader.cpp:133-177); host only."""
+    cfg = ModelConfig()
+    call("qraf_file_read_config", os.fsencode(path), C.byref(cfg), None)
+    return cfg
 
 
 class Engine:
@@ -42,6 +52,21 @@ class Engine:
         call("qraf_engine_create", C.byref(config), C.byref(opt), C.byref(h))
         self.h = h.value
         self.vocab = config.vocab_size
+
+    @classmethod
+    def from_file(cls, path: str, kv_dtype=F32, page_size=16, max_batch=1, num_pages=0) -> "Engine":
+        """QrafModel::load + Transformer::init in one call: a .qraf file's
+        config and tensors straight into HBM (qraf_engine_create_from_file)."""
+        cfg = read_file_config(path)
+        self = cls.__new__(cls)
+        self.config = cfg
+        self.max_batch = max_batch
+        opt = EngineOptions(kv_dtype, page_size, max_batch, num_pages)
+        h = C.c_void_p()
+        call("qraf_engine_create_from_file", os.fsencode(path), C.byref(opt), C.byref(h))
+        self.h = h.value
+        self.vocab = cfg.vocab_size
+        return self
 
     def close(self):
         if getattr(self, "h", None):
@@ -125,6 +150,12 @@ class Transformer:
             e.set_tensor(name, dt, shape, data)
         e.finalize()
         return cls(e)
+
+    @classmethod
+    def from_file(cls, path: str, kv_dtype=F32, max_batch=1, num_pages=0, page_size=16):
+        """A .qraf file (QrafModel::load + Transformer::init) straight into HBM."""
+        return cls(Engine.from_file(path, kv_dtype=kv_dtype, page_size=page_size, max_batch=max_batch,
+                                    num_pages=num_pages))
 
     @classmethod
     def synthetic(cls, config: ModelConfig, weight_dtype, seed, embed_dtype=None, head_dtype=None, tied=False,
