@@ -22,6 +22,9 @@ The same JSON line also reports the other configurations of the metric:
   gemm         batched Q-GEMM, B in {8,32,64,128}, Qwen2.5-3B projection shapes
   attention    ragged paged decode attention: 128 sequences, context U[128,4096],
                16 q / 2 kv heads, head_dim 128, fp16 K/V
+  sampler      the device sampler on 128 rows x 151936 logits (penalty,
+               temperature, top-k, top-p); the reference's Sampler per row on
+               the host beside it
   load         QRAF file -> HBM (qraf_engine_create_from_file) of the
                Qwen2.5-3B-architecture Q4 model, from a file this leg writes
   steady_b128  (not in the default run) the steady 128-sequence decode of
@@ -566,6 +569,53 @@ def bench_load(args, rt):
                     "repack on the device), file in the page cache; best of 2"}
 
 
+def bench_sampler(args, rt):
+    """The device sampler (qraf_hip_sample_dev) on 128 rows of Qwen2.5-3B-
+    vocabulary logits with SamplingConfig's defaults (temperature 0.8, top-k
+    40, top-p 0.9, repetition penalty 1.1 over 512 recent tokens per row),
+    captured 20 calls to a graph."""
+    import ctypes as C
+    from qraf_amd._lib import SamplingParams
+    call, DeviceBuffer = rt["call"], rt["DeviceBuffer"]
+    rows, V, nrec = 128, QWEN["vocab"], 512
+    rng = np.random.default_rng(5)
+    dl = DeviceBuffer.from_array((rng.standard_normal((rows, V)) * 3).astype(np.float32))
+    rec = DeviceBuffer.from_array(rng.integers(0, V, (rows, nrec)).astype(np.uint32))
+    cnt = DeviceBuffer.from_array(np.full(rows, nrec, np.int32))
+    uni = DeviceBuffer.from_array(rng.random(rows).astype(np.float32))
+    out = DeviceBuffer(rows * 4)
+    sp = SamplingParams(0.8, 40, 0.9, 1.1)
+    us = graph_time_us(rt, lambda i: call("qraf_hip_sample_dev", dl.ptr, rows, V, C.byref(sp), rec.ptr, cnt.ptr, nrec,
+                                          uni.ptr, out.ptr, rt["stream"].h), 20)
+    sp1 = SamplingParams(0.8, 40, 0.9, 1.0)
+    us_nopen = graph_time_us(rt, lambda i: call("qraf_hip_sample_dev", dl.ptr, rows, V, C.byref(sp1), None, None, 0,
+                                                uni.ptr, out.ptr, rt["stream"].h), 20)
+    for d in (dl, rec, cnt, uni, out):
+        d.free()
+    return {"rows": rows, "vocab": V, "recent_tokens": nrec, "config": "T 0.8, top_k 40, top_p 0.9, penalty 1.1",
+            "us_per_call": round(us, 1), "us_per_call_without_penalty": round(us_nopen, 1),
+            "logits_kept_in_hbm_MB": round(rows * V * 4 / 1e6, 1)}
+
+
+def cpu_sampler():
+    """The reference's Sampler::sample (std::sort over the vocabulary) on one
+    row of the same shape, on the host: ms per draw."""
+    import ctypes as C
+    from oracle import pyoracle as po
+    R = po.ref()
+    if R is None:
+        return None
+    V = QWEN["vocab"]
+    l = (np.random.default_rng(5).standard_normal(V) * 3).astype(np.float32)
+    out = np.zeros(8, np.uint32)
+    t0 = time.perf_counter()
+    R.ref_sample(l.ctypes.data_as(C.POINTER(C.c_float)), V, 0.8, 40, 0.9, 7, 8,
+                 out.ctypes.data_as(C.POINTER(C.c_uint32)))
+    ms = (time.perf_counter() - t0) * 1e3 / 8
+    return {"value": round(ms, 2), "unit": "ms per sampled token (one row)", "cores": 1, "kind": "reference",
+            "sample": f"Sampler::sample on one {V}-logit row, 8 draws, host CPU {host_cpu()}"}
+
+
 def bench_steady_b128(args, rt):
     """The steady 128-sequence decode alone (every GEMM at 128 rows), for profiling."""
     e = qwen_engine(args, 128)
@@ -623,7 +673,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=50)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", default="matvec,gemm,attention,decode_b1,decode_b128,load")
+    ap.add_argument("--only", default="matvec,gemm,attention,decode_b1,decode_b128,load,sampler")
     ap.add_argument("--requests", type=int, default=256, help="requests in the batch-128 decode run")
     ap.add_argument("--decode-steps", type=int, default=64, help="timed steps of the steady 128-sequence decode")
     ap.add_argument("--rows", type=int, default=512, help="row budget per step of the continuous-batch run")
@@ -658,7 +708,8 @@ def main():
     print(f"# matvec done: {value:.1f} GB/s", file=sys.stderr, flush=True)
     extra = {}
     for part, fn in (("gemm", bench_gemm), ("attention", bench_attention), ("decode_b1", bench_decode_b1),
-                     ("decode_b128", bench_decode_b128), ("steady_b128", bench_steady_b128), ("load", bench_load)):
+                     ("decode_b128", bench_decode_b128), ("steady_b128", bench_steady_b128), ("load", bench_load),
+                     ("sampler", bench_sampler)):
         if part in only:
             extra[part] = fn(args, rt)
             print(f"# {part} done", file=sys.stderr, flush=True)
@@ -677,6 +728,8 @@ def main():
         cpu = cpu_baseline_matvec(hosts, args.cpu_seconds)
         if "decode_b1" in only:
             extra["cpu_decode_b1"] = cpu_decode_b1()
+        if "sampler" in only:
+            extra["cpu_sampler"] = cpu_sampler()
         print("# cpu baseline done", file=sys.stderr, flush=True)
 
     out = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,

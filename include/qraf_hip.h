@@ -264,6 +264,33 @@ int qraf_engine_generate_weights(qraf_engine* engine, uint32_t weight_dtype, uin
 /* Checks that every tensor the forward pass reads is present. */
 int qraf_engine_finalize(qraf_engine* engine);
 
+/* Sampler on the device (src/sampling/sampler.cpp).  Parameters as in
+ * SamplingConfig (include/sampling/sampler.h:10-17): temperature <= 0 is
+ * greedy (Sampler::argmax, :25-35); otherwise p = logit / temperature, the
+ * top_k largest (all when top_k <= 0 or >= vocab; at most 1024 candidates
+ * on the device), softmax over them, the top_p nucleus when 0 < top_p < 1,
+ * and the first candidate whose cumulative probability reaches the row's
+ * uniform (Sampler::sample, :57-128).  repetition_penalty != 1 first applies
+ * Sampler::apply_repetition_penalty (:37-49) in place to each row with that
+ * row's recent tokens.  The uniform of a row is the draw the reference's
+ * std::mt19937 would make (std::uniform_real_distribution<float>(0, 1)); the
+ * host supplies it, so that the stream of draws follows the reference's. */
+typedef struct qraf_sampling_params {
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float repetition_penalty;
+} qraf_sampling_params;
+
+/* Device pointers, stream-ordered: logits [rows][vocab] (penalised in
+ * place), recent [rows][recent_stride] with recent_count [rows] valid
+ * entries (may be NULL when repetition_penalty is 1), uniforms [rows] (may
+ * be NULL when greedy), tokens [rows] out.  No device scope synchronisation
+ * and no allocation. */
+int qraf_hip_sample_dev(float* logits, int32_t rows, int32_t vocab, const qraf_sampling_params* params,
+                        const uint32_t* recent, const int32_t* recent_count, int32_t recent_stride,
+                        const float* uniforms, uint32_t* tokens, void* stream);
+
 /* QRAF file -> HBM.  The file layout of include/qraf/format.h:26-132 is
  * checked as validate_header (src/qraf/header.cpp:8-45) and get_string
  * (src/qraf/loader.cpp:273-277) do, and strings must end inside the string
@@ -306,6 +333,16 @@ int qraf_engine_step(qraf_engine* engine, int32_t n_rows, const int32_t* seq_ids
  * (on = 1, the default); on = 0 launches every step's kernels eagerly.  No
  * reference counterpart: an execution detail of qraf_engine_step. */
 int qraf_engine_set_graphs(qraf_engine* engine, int32_t on);
+/* Sampling of the last step's logit rows where they lie in HBM (the rows
+ * that step returned logits or argmax for, in order; row0 .. row0+rows-1 of
+ * them): repetition penalty with each row's recent tokens (host arrays
+ * [rows][recent_stride], recent_count [rows]; may be NULL when the penalty is
+ * 1), then greedy or top-k/top-p sampling with the host uniforms [rows] (may
+ * be NULL when greedy), as qraf_hip_sample_dev.  Only token ids and the
+ * small host arrays cross PCIe. */
+int qraf_engine_sample(qraf_engine* engine, int32_t row0, int32_t rows, const qraf_sampling_params* params,
+                       const uint32_t* recent, const int32_t* recent_count, int32_t recent_stride,
+                       const float* uniforms, uint32_t* tokens);
 /* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)
  * on the engine's default sequence, and Transformer::reset() (:641-643). */
 int qraf_engine_forward(qraf_engine* engine, uint32_t token, int32_t pos, float* logits);

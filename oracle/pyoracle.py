@@ -127,6 +127,10 @@ def ref():
         R.ref_argmax.restype = C.c_uint32
         R.ref_argmax.argtypes = [_fp, C.c_int]
         R.ref_penalty.argtypes = [_fp, C.c_int, _u32p, C.c_int, C.c_float]
+        R.ref_sample.argtypes = [_fp, C.c_int, C.c_float, C.c_int, C.c_float, C.c_uint64, C.c_int, _u32p]
+        R.ref_uniforms.argtypes = [C.c_uint64, C.c_int, _fp]
+        R.ref_engine_generate_sampled.argtypes = [C.c_void_p, _u32p, C.c_int, C.c_int, C.c_float, C.c_int,
+                                                  C.c_float, C.c_float, C.c_uint64, _u32p]
         R.ref_writer_new.restype = C.c_void_p
         R.ref_writer_free.argtypes = [C.c_void_p]
         R.ref_writer_config_u32.argtypes = [C.c_void_p, C.c_char_p, C.c_uint32]
@@ -344,3 +348,10 @@ class RefEngine:
         ms = C.c_double()
         n = self.R.ref_engine_generate(self.h, _u32(p), p.size, max_tokens, penalty, _u32(out), C.byref(ms))
         return out[:n].tolist(), ms.value
+
+    def generate_sampled(self, prompt, max_tokens, temperature, top_k, top_p, penalty, seed):
+        p = np.ascontiguousarray(prompt, dtype=np.uint32)
+        out = np.zeros(max_tokens, dtype=np.uint32)
+        n = self.R.ref_engine_generate_sampled(self.h, _u32(p), p.size, max_tokens, temperature, top_k, top_p,
+                                               penalty, seed, _u32(out))
+        return out[:n].tolist()

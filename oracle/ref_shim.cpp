@@ -19,6 +19,7 @@
 
 #include <cstring>
 #include <memory>
+#include <random>
 #include <string>
 #include <vector>
 
@@ -87,6 +88,29 @@ void ref_penalty(float* l, int n, const uint32_t* toks, int nt, float p) {
     s.apply_repetition_penalty(l, n, std::vector<u32>(toks, toks + nt));
 }
 
+// Sampler::sample (sampler.cpp:57-128) with a seeded config, n_draws times on
+// the same logits; every non-greedy draw takes one uniform from the Sampler's
+// std::mt19937.  Penalty 1: apply_repetition_penalty is a separate call.
+void ref_sample(const float* logits, int V, float temperature, int top_k, float top_p, uint64_t seed, int n_draws,
+                uint32_t* out) {
+    SamplingConfig sc;
+    sc.temperature = temperature;
+    sc.top_k = top_k;
+    sc.top_p = top_p;
+    sc.repetition_penalty = 1.0f;
+    sc.seed = seed;
+    Sampler s(sc);
+    for (int i = 0; i < n_draws; i++) out[i] = s.sample(logits, V);
+}
+// the uniforms a Sampler with this seed draws: std::mt19937 seeded as
+// Sampler::Sampler does (sampler.cpp:9-16), std::uniform_real_distribution<f32>(0, 1)
+void ref_uniforms(uint64_t seed, int n, float* out) {
+    std::mt19937 rng;
+    rng.seed(static_cast<unsigned>(seed));
+    std::uniform_real_distribution<f32> d(0.0f, 1.0f);
+    for (int i = 0; i < n; i++) out[i] = d(rng);
+}
+
 // ---- QRAF file writing through the reference's QrafWriter (writer.cpp) ----
 void* ref_writer_new() { quiet(); return new QrafWriter(); }
 void ref_writer_free(void* w) { delete static_cast<QrafWriter*>(w); }
@@ -152,6 +176,21 @@ int ref_engine_generate(void* e, const uint32_t* prompt, int n, int max_tokens, 
     GenerateResult r = static_cast<InferenceEngine*>(e)->generate_tokens(std::vector<u32>(prompt, prompt + n), gc);
     for (size_t i = 0; i < r.tokens.size(); i++) out[i] = r.tokens[i];
     if (ms) *ms = r.generation_time_ms;
+    return static_cast<int>(r.tokens.size());
+}
+
+// InferenceEngine::generate_tokens with a sampling configuration
+int ref_engine_generate_sampled(void* e, const uint32_t* prompt, int n, int max_tokens, float temperature, int top_k,
+                                float top_p, float penalty, uint64_t seed, uint32_t* out) {
+    GenerateConfig gc;
+    gc.max_tokens = static_cast<u32>(max_tokens);
+    gc.sampling.temperature = temperature;
+    gc.sampling.top_k = top_k;
+    gc.sampling.top_p = top_p;
+    gc.sampling.repetition_penalty = penalty;
+    gc.sampling.seed = seed;
+    GenerateResult r = static_cast<InferenceEngine*>(e)->generate_tokens(std::vector<u32>(prompt, prompt + n), gc);
+    for (size_t i = 0; i < r.tokens.size(); i++) out[i] = r.tokens[i];
     return static_cast<int>(r.tokens.size());
 }
 

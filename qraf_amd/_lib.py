@@ -93,7 +93,17 @@ class EngineOptions(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("kv_dtype", "page_size", "max_batch", "num_pages")]
 
 
+class SamplingParams(C.Structure):
+    """qraf_sampling_params (include/qraf_hip.h)."""
+    _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float),
+                ("repetition_penalty", C.c_float)]
+
+
 SIGNATURES.update({
+    "qraf_hip_sample_dev": (C.c_int, [vp, C.c_int32, C.c_int32, C.POINTER(SamplingParams), vp, vp, C.c_int32, vp, vp,
+                                      vp]),
+    "qraf_engine_sample": (C.c_int, [vp, C.c_int32, C.c_int32, C.POINTER(SamplingParams), u32p, i32p, C.c_int32, fp,
+                                     u32p]),
     "qraf_engine_create": (C.c_int, [C.POINTER(ModelConfig), C.POINTER(EngineOptions), C.POINTER(vp)]),
     "qraf_engine_destroy": (C.c_int, [vp]),
     "qraf_engine_set_tensor": (C.c_int, [vp, C.c_char_p, C.c_uint32, C.c_uint32, u32p, C.c_uint32, vp, C.c_uint64]),

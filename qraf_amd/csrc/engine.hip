@@ -331,6 +331,9 @@ struct qraf_engine {
     };
     std::vector<Seq> seqs;
     int32_t default_seq = -1;
+    int last_logit_rows = 0;          // logit rows the last step left in `logits`
+    uint8_t* samp = nullptr;          // sampling staging: recent tokens, counts, uniforms, tokens
+    size_t samp_cap = 0;
 
     // activations (max_batch rows)
     float *h = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *gu = nullptr, *act = nullptr,
@@ -1074,10 +1077,49 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
     } else {
         QH_TRY(enqueue(step_ctx));
     }
+    e->last_logit_rows = head ? n_logit_rows : 0;
     if (head && logits)
         QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_rows * V * 4, hipMemcpyDeviceToHost, s));
     if (head && next_tokens)
         QH_CHECK_HIP(hipMemcpyAsync(next_tokens, e->amax, (size_t)n_logit_rows * 4, hipMemcpyDeviceToHost, s));
+    QH_CHECK_HIP(hipStreamSynchronize(s));
+    return QRAF_HIP_OK;
+}
+
+// Sampler::apply_repetition_penalty + Sampler::sample on the last step's
+// logit rows (sampler.cpp:37-128), where they lie in HBM.
+int qraf_engine_sample(qraf_engine* e, int32_t row0, int32_t rows, const qraf_sampling_params* p,
+                       const uint32_t* recent, const int32_t* counts, int32_t stride, const float* uniforms,
+                       uint32_t* tokens) {
+    clear_error();
+    QH_REQUIRE(e && p && tokens && rows > 0 && row0 >= 0, QRAF_HIP_ERR_INVALID, "sample: bad arguments");
+    QH_REQUIRE(row0 + rows <= e->last_logit_rows, QRAF_HIP_ERR_STATE,
+               "sample: rows %d..%d, the last step left %d logit rows", row0, row0 + rows - 1, e->last_logit_rows);
+    const bool greedy = !(p->temperature > 0.f);
+    const bool pen = p->repetition_penalty != 1.0f && recent;
+    QH_REQUIRE(!pen || (counts && stride > 0), QRAF_HIP_ERR_INVALID, "sample: recent tokens need counts");
+    QH_REQUIRE(greedy || uniforms, QRAF_HIP_ERR_INVALID, "sample: temperature %g needs uniforms", p->temperature);
+    const size_t rb = ((size_t)rows * 4 + 255) / 256 * 256;
+    const size_t rec = pen ? ((size_t)rows * stride * 4 + 255) / 256 * 256 : 0;
+    const size_t need = 3 * rb + rec;  // tokens, uniforms, counts, recent
+    if (need > e->samp_cap) {
+        const size_t cap = std::max(need, (size_t)1 << 20);
+        QH_TRY(ealloc(e, (void**)&e->samp, cap));  // held until the engine is destroyed
+        e->samp_cap = cap;
+    }
+    hipStream_t s = e->stream;
+    uint32_t* d_tok = (uint32_t*)e->samp;
+    float* d_uni = (float*)(e->samp + rb);
+    int32_t* d_cnt = (int32_t*)(e->samp + 2 * rb);
+    uint32_t* d_rec = (uint32_t*)(e->samp + 3 * rb);
+    if (!greedy) QH_CHECK_HIP(hipMemcpyAsync(d_uni, uniforms, (size_t)rows * 4, hipMemcpyHostToDevice, s));
+    if (pen) {
+        QH_CHECK_HIP(hipMemcpyAsync(d_cnt, counts, (size_t)rows * 4, hipMemcpyHostToDevice, s));
+        QH_CHECK_HIP(hipMemcpyAsync(d_rec, recent, (size_t)rows * stride * 4, hipMemcpyHostToDevice, s));
+    }
+    QH_TRY(launch_sample(e->logits + (size_t)row0 * e->c.vocab_size, rows, (int)e->c.vocab_size, *p,
+                         pen ? d_rec : nullptr, pen ? d_cnt : nullptr, stride, greedy ? nullptr : d_uni, d_tok, s));
+    QH_CHECK_HIP(hipMemcpyAsync(tokens, d_tok, (size_t)rows * 4, hipMemcpyDeviceToHost, s));
     QH_CHECK_HIP(hipStreamSynchronize(s));
     return QRAF_HIP_OK;
 }

@@ -1,0 +1,455 @@
+// sampler.hip -- Sampler on the device: repetition penalty, greedy argmax,
+// temperature + top-k + top-p sampling, for many rows of logits at once.
+//
+// Replaces Sampler::apply_repetition_penalty (reference
+// src/sampling/sampler.cpp:37-49) and Sampler::sample (:57-128) so that a
+// decode step's logits never leave HBM.  The uniform draw of each sampled row
+// comes from the caller (the reference draws it from its std::mt19937 member;
+// the host layer reproduces that stream), so the device work is a pure
+// function of (logits, recent tokens, parameters, uniform).
+//
+// Sampling a row (one workgroup of 1024 threads):
+//   1. probs p_i = logit_i / T, computed where used (the reference's vector).
+//   2. The cutoff-th largest p by radix select over order-preserving 32-bit
+//      keys, 8 bits per pass (4 passes, LDS histograms).
+//   3. The cutoff candidates (keys above the selected one, then the lowest
+//      indices of equal keys) gathered in index order, then bitonic-sorted in
+//      LDS by (p descending, index ascending).  The reference's std::sort
+//      leaves the order of equal p unspecified; this order is one of its
+//      possible results.
+//   4. One thread runs the reference's arithmetic on the sorted candidates
+//      in the reference's order: exp(p - max), sequential sum, divide, top-p
+//      prefix, renormalise, cumulative sum against the uniform.
+// cutoff = top_k when 0 < top_k < vocab, else vocab (sampler.cpp:73-77); it
+// must be at most SAMPLE_MAX_CUTOFF.
+#include <math.h>
+
+#include "common.h"
+
+namespace qraf_hip {
+
+constexpr int SAMPLE_MAX_CUTOFF = 1024;
+constexpr int CAND_CAP = 4096;  // candidates the fast path gathers at most
+
+constexpr int SNT = 1024;  // threads per row (16 waves)
+
+// Row loops: each thread reads 4 float4 (16 logits) before using any, so a
+// workgroup has 16K logits in flight per round trip; f(i, value) is called
+// for every i < V, in increasing i within a thread.
+template <typename F>
+__device__ __forceinline__ void for_row(const float* __restrict__ l, int V, int tid, F&& f) {
+    if ((V & 3) == 0) {
+        const int V4 = V >> 2;
+        const float4* l4 = (const float4*)l;
+        for (int base = tid; base < V4; base += SNT * 4) {
+            float4 v[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) v[u] = l4[min(base + SNT * u, V4 - 1)];
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+                if (base + SNT * u < V4) {
+                    const int i = 4 * (base + SNT * u);
+                    f(i, v[u].x);
+                    f(i + 1, v[u].y);
+                    f(i + 2, v[u].z);
+                    f(i + 3, v[u].w);
+                }
+        }
+    } else {
+        for (int base = tid; base < V; base += SNT * 8) {
+            float v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = l[min(base + SNT * u, V - 1)];
+#pragma unroll
+            for (int u = 0; u < 8; u++)
+                if (base + SNT * u < V) f(base + SNT * u, v[u]);
+        }
+    }
+}
+
+// order-preserving key: a < b  <=>  key(a) < key(b) for non-NaN floats
+__device__ __forceinline__ uint32_t order_key(float f) {
+    const uint32_t b = __float_as_uint(f);
+    return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+// Sampler::apply_repetition_penalty: one thread per row, the row's recent
+// tokens in order (a token listed twice is penalised twice, as in the loop);
+// for histories longer than PEN_LDS
+__global__ void penalty_rows_kernel(float* __restrict__ logits, int V, int rows, const uint32_t* __restrict__ recent,
+                                    const int32_t* __restrict__ counts, int stride, float penalty) {
+    const int row = blockIdx.x * blockDim.x + threadIdx.x;
+    if (row >= rows) return;
+    float* l = logits + (size_t)row * V;
+    const uint32_t* r = recent + (size_t)row * stride;
+    const int n = min(counts[row], stride);
+    for (int i = 0; i < n; i++) {
+        const uint32_t tok = r[i];
+        if (tok >= (uint32_t)V) continue;
+        const float v = l[tok];
+        l[tok] = v > 0.f ? v / penalty : v * penalty;
+    }
+}
+
+// The same, one workgroup per row for histories of at most PEN_LDS tokens:
+// the history is sorted in LDS, and the first thread of each run of one
+// token applies the penalty run-length times to that token.  Distinct
+// tokens are independent and a token's value keeps its sign, so this equals
+// the sequential loop.
+constexpr int PEN_LDS = 4096;
+__global__ __launch_bounds__(256) void penalty_rows_lds_kernel(float* __restrict__ logits, int V,
+                                                               const uint32_t* __restrict__ recent,
+                                                               const int32_t* __restrict__ counts, int stride,
+                                                               float penalty) {
+    __shared__ uint32_t s[PEN_LDS];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    float* l = logits + (size_t)row * V;
+    const uint32_t* r = recent + (size_t)row * stride;
+    const int n = min(counts[row], stride);
+    int P = 1;
+    while (P < n) P <<= 1;
+    for (int i = tid; i < P; i += 256) s[i] = i < n ? r[i] : 0xFFFFFFFFu;  // padding sorts last, is >= V
+    __syncthreads();
+    for (int k = 2; k <= P; k <<= 1)
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < P; i += 256) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const uint32_t a = s[i], b = s[ixj];
+                    if ((a > b) == ((i & k) == 0)) {
+                        s[i] = b;
+                        s[ixj] = a;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    for (int i = tid; i < n; i += 256) {
+        const uint32_t tok = s[i];
+        if (tok >= (uint32_t)V || (i > 0 && s[i - 1] == tok)) continue;
+        int c = 1;
+        while (i + c < n && s[i + c] == tok) c++;
+        float v = l[tok];
+        for (int k = 0; k < c; k++) v = v > 0.f ? v / penalty : v * penalty;
+        l[tok] = v;
+    }
+}
+
+__global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restrict__ logits, int V, float T, int cutoff,
+                                                          float top_p, const float* __restrict__ uniforms,
+                                                          uint32_t* __restrict__ out) {
+    const int tid = threadIdx.x, row = blockIdx.x;
+    const float* l = logits + (size_t)row * V;
+    __shared__ uint32_t hist[256];
+    __shared__ uint32_t s_prefix, s_need;
+    __shared__ int s_cgt[SNT], s_ceq[SNT];
+    __shared__ float cval[CAND_CAP];
+    __shared__ int cidx[CAND_CAP];
+    constexpr int NW = SNT / 64;
+    __shared__ float s_red[2][NW];
+    __shared__ int s_cnt[NW][8];
+    __shared__ int s_n;
+
+    if (!(T > 0.f)) {  // Sampler::argmax (sampler.cpp:25-35): first index of the maximum
+        float best = -INFINITY;
+        int bi = V;
+        for_row(l, V, tid, [&](int i, float v) {  // increasing i per thread
+            if (bi == V || v > best) {
+                best = v;
+                bi = i;
+            }
+        });
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            const float ov = __shfl_xor(best, o);
+            const int oi = __shfl_xor(bi, o);
+            if (ov > best || (ov == best && oi < bi)) {
+                best = ov;
+                bi = oi;
+            }
+        }
+        __shared__ float wv[NW];
+        __shared__ int wi[NW];
+        if ((tid & 63) == 0) {
+            wv[tid >> 6] = best;
+            wi[tid >> 6] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < NW; w++)
+                if (wv[w] > best || (wv[w] == best && wi[w] < bi)) {
+                    best = wv[w];
+                    bi = wi[w];
+                }
+            out[row] = (uint32_t)(bi < V ? bi : 0);
+        }
+        return;
+    }
+
+    // ---- fast path: a threshold t with cutoff <= #{p >= t} <= CAND_CAP, by an
+    // 8-way search between the row's smallest and largest p; then every
+    // p >= t is gathered and sorted.  The sort makes the result independent
+    // of the gather order, and equal to the radix path's.
+    int nsort = cutoff;
+    bool fast = cutoff == V;  // every token a candidate
+    float t = -INFINITY;
+    if (!fast) {
+        float mx = -INFINITY, mn = INFINITY;
+        for_row(l, V, tid, [&](int, float v) {
+            const float p = v / T;
+            mx = fmaxf(mx, p);
+            mn = fminf(mn, p);
+        });
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            mx = fmaxf(mx, __shfl_xor(mx, o));
+            mn = fminf(mn, __shfl_xor(mn, o));
+        }
+        if ((tid & 63) == 0) {
+            s_red[0][tid >> 6] = mx;
+            s_red[1][tid >> 6] = mn;
+        }
+        __syncthreads();
+        for (int w = 0; w < NW; w++) {
+            mx = fmaxf(mx, s_red[0][w]);
+            mn = fminf(mn, s_red[1][w]);
+        }
+        const int target = max(2 * cutoff, 512);
+        if (mx > mn && mx < INFINITY && mn > -INFINITY) {
+            float lo = mn, hi = mx;  // #{p >= lo} = V >= cutoff
+            int clo = V;
+            for (int pass = 0; pass < 16 && clo > target; pass++) {
+                float th[8];
+#pragma unroll
+                for (int j = 0; j < 8; j++) th[j] = lo + (hi - lo) * ((float)(j + 1) / 9.0f);
+                int c[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+                for_row(l, V, tid, [&](int, float v) {
+                    const float p = v / T;
+#pragma unroll
+                    for (int j = 0; j < 8; j++) c[j] += p >= th[j];
+                });
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+#pragma unroll
+                    for (int o = 32; o >= 1; o >>= 1) c[j] += __shfl_xor(c[j], o);
+                }
+                __syncthreads();  // the previous pass's reads of s_cnt are done
+                if ((tid & 63) == 0) {
+#pragma unroll
+                    for (int j = 0; j < 8; j++) s_cnt[tid >> 6][j] = c[j];
+                }
+                __syncthreads();
+                int jb = -1, cb = clo;
+#pragma unroll
+                for (int j = 0; j < 8; j++) {
+                    int cj = 0;
+                    for (int w = 0; w < NW; w++) cj += s_cnt[w][j];
+                    if (cj >= cutoff) {
+                        jb = j;
+                        cb = cj;
+                    }
+                }
+                const float nlo = jb >= 0 ? th[jb] : lo, nhi = jb < 7 ? th[jb + 1] : hi;
+                if (!(nlo > lo || nhi < hi)) break;  // no progress: values too close together
+                lo = nlo;
+                hi = nhi;
+                clo = cb;
+            }
+            if (clo <= CAND_CAP) {
+                fast = true;
+                t = lo;
+                nsort = clo;
+            }
+        }
+    }
+    if (fast) {
+        if (tid == 0) s_n = 0;
+        __syncthreads();
+        for_row(l, V, tid, [&](int i, float v) {
+            const float p = v / T;
+            if (p >= t) {
+                const int k = atomicAdd(&s_n, 1);
+                cval[k] = p;
+                cidx[k] = i;
+            }
+        });
+        __syncthreads();
+        nsort = s_n;
+    } else {
+    // ---- radix select of the cutoff-th largest key
+    uint32_t prefix = 0, mask = 0, need = (uint32_t)cutoff;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        for_row(l, V, tid, [&](int, float v) {
+            const uint32_t k = order_key(v / T);
+            if ((k & mask) == prefix) atomicAdd(&hist[(k >> shift) & 255u], 1u);
+        });
+        __syncthreads();
+        if (tid == 0) {
+            uint32_t acc = 0;
+            int d = 255;
+            for (; d > 0; d--) {
+                if (acc + hist[d] >= need) break;
+                acc += hist[d];
+            }
+            s_prefix = prefix | ((uint32_t)d << shift);
+            s_need = need - acc;
+        }
+        __syncthreads();
+        prefix = s_prefix;
+        need = s_need;
+        mask |= 255u << shift;
+        __syncthreads();
+    }
+    const uint32_t tau = prefix;          // key of the cutoff-th largest p
+    const int n_gt = cutoff - (int)need;  // candidates strictly above it
+
+    // ---- gather in index order: thread t owns [t*ch, (t+1)*ch)
+    const int ch = (V + SNT - 1) / SNT;
+    const int lo = min(V, tid * ch), hi = min(V, lo + ch);
+    int gt = 0, eq = 0;
+    for (int i = lo; i < hi; i++) {
+        const uint32_t k = order_key(l[i] / T);
+        gt += k > tau;
+        eq += k == tau;
+    }
+    s_cgt[tid] = gt;
+    s_ceq[tid] = eq;
+    __syncthreads();
+    if (tid == 0) {  // exclusive prefix sums, in thread (index) order
+        int a = 0, b = 0;
+        for (int t = 0; t < SNT; t++) {
+            const int x = s_cgt[t], y = s_ceq[t];
+            s_cgt[t] = a;
+            s_ceq[t] = b;
+            a += x;
+            b += y;
+        }
+    }
+    __syncthreads();
+    int pg = s_cgt[tid], pe = s_ceq[tid];
+    for (int i = lo; i < hi; i++) {
+        const float p = l[i] / T;
+        const uint32_t k = order_key(p);
+        if (k > tau) {
+            cval[pg] = p;
+            cidx[pg] = i;
+            pg++;
+        } else if (k == tau) {
+            if (pe < (int)need) {
+                cval[n_gt + pe] = p;
+                cidx[n_gt + pe] = i;
+            }
+            pe++;
+        }
+    }
+    }  // radix path
+    int P = 1;
+    while (P < nsort) P <<= 1;
+    for (int i = nsort + tid; i < P; i += SNT) {
+        cval[i] = -INFINITY;
+        cidx[i] = 0x7FFFFFFF;
+    }
+    __syncthreads();
+
+    // ---- bitonic sort: p descending, index ascending
+    for (int k = 2; k <= P; k <<= 1) {
+        for (int j = k >> 1; j > 0; j >>= 1) {
+            for (int i = tid; i < P; i += SNT) {
+                const int ixj = i ^ j;
+                if (ixj > i) {
+                    const float a = cval[i], b = cval[ixj];
+                    const int ia = cidx[i], ib = cidx[ixj];
+                    const bool a_first = a > b || (a == b && ia < ib);
+                    const bool up = (i & k) == 0;  // this half ends in "first" order
+                    if (a_first != up) {
+                        cval[i] = b;
+                        cval[ixj] = a;
+                        cidx[i] = ib;
+                        cidx[ixj] = ia;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+
+    // ---- the reference's arithmetic, in its order (sampler.cpp:79-127)
+    if (tid == 0) {
+        const float max_val = cval[0];
+        float sum = 0.f;
+        for (int i = 0; i < cutoff; i++) {
+            cval[i] = expf(cval[i] - max_val);
+            sum += cval[i];
+        }
+        for (int i = 0; i < cutoff; i++) cval[i] /= sum;
+        int n = cutoff;
+        if (top_p > 0.f && top_p < 1.f) {
+            float cs = 0.f;
+            int nucleus = cutoff;
+            for (int i = 0; i < cutoff; i++) {
+                cs += cval[i];
+                if (cs >= top_p) {
+                    nucleus = i + 1;
+                    break;
+                }
+            }
+            float ns = 0.f;
+            for (int i = 0; i < nucleus; i++) ns += cval[i];
+            for (int i = 0; i < nucleus; i++) cval[i] /= ns;
+            n = nucleus;
+        }
+        const float r = uniforms[row];
+        float cs = 0.f;
+        uint32_t pick = (uint32_t)cidx[n - 1];  // fallback: the last candidate
+        for (int i = 0; i < n; i++) {
+            cs += cval[i];
+            if (r <= cs) {
+                pick = (uint32_t)cidx[i];
+                break;
+            }
+        }
+        out[row] = pick;
+    }
+}
+
+int launch_sample(float* logits, int rows, int V, const qraf_sampling_params& sp, const uint32_t* recent,
+                  const int32_t* counts, int stride, const float* uniforms, uint32_t* out, hipStream_t s) {
+    QH_REQUIRE(logits && out && rows > 0 && V > 0, QRAF_HIP_ERR_INVALID, "sample: bad arguments");
+    const bool greedy = !(sp.temperature > 0.f);
+    const int cutoff = (sp.top_k > 0 && sp.top_k < V) ? sp.top_k : V;
+    QH_REQUIRE(greedy || cutoff <= SAMPLE_MAX_CUTOFF, QRAF_HIP_ERR_INVALID,
+               "sample: %d candidates (top_k %d, vocab %d); the device sampler takes at most %d", cutoff, sp.top_k,
+               V, SAMPLE_MAX_CUTOFF);
+    QH_REQUIRE(greedy || uniforms, QRAF_HIP_ERR_INVALID, "sample: temperature %g needs uniforms", sp.temperature);
+    if (sp.repetition_penalty != 1.0f) {  // sampler.cpp:39
+        QH_REQUIRE(!recent || (counts && stride > 0), QRAF_HIP_ERR_INVALID, "sample: recent tokens need counts");
+        if (recent) {
+            if (stride <= PEN_LDS)
+                hipLaunchKernelGGL(penalty_rows_lds_kernel, dim3(rows), dim3(256), 0, s, logits, V, recent, counts,
+                                   stride, sp.repetition_penalty);
+            else
+                hipLaunchKernelGGL(penalty_rows_kernel, dim3((rows + 63) / 64), dim3(64), 0, s, logits, V, rows,
+                                   recent, counts, stride, sp.repetition_penalty);
+            QH_CHECK_HIP(hipGetLastError());
+        }
+    }
+    hipLaunchKernelGGL(sample_rows_kernel, dim3(rows), dim3(SNT), 0, s, logits, V, sp.temperature, cutoff, sp.top_p,
+                       uniforms, out);
+    QH_CHECK_HIP(hipGetLastError());
+    return QRAF_HIP_OK;
+}
+
+}  // namespace qraf_hip
+
+using namespace qraf_hip;
+
+extern "C" int qraf_hip_sample_dev(float* logits, int32_t rows, int32_t vocab, const qraf_sampling_params* params,
+                                   const uint32_t* recent, const int32_t* recent_count, int32_t recent_stride,
+                                   const float* uniforms, uint32_t* tokens, void* stream) {
+    clear_error();
+    QH_REQUIRE(params, QRAF_HIP_ERR_INVALID, "sample: null params");
+    return launch_sample(logits, rows, vocab, *params, recent, recent_count, recent_stride, uniforms, tokens,
+                         as_stream(stream));
+}

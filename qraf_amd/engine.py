@@ -8,25 +8,30 @@
                      request advances one token per step, all in one batched
                      device step
 
-Sampling is greedy (temperature 0, Sampler::argmax, sampler.cpp:25-35) with
-the reference's repetition penalty (sampler.cpp:37-49).  With penalty 1 the
-argmax runs on the device and only token ids cross PCIe; otherwise the logits
-are copied back and penalised on the host before the argmax, as the
-reference does.
+    SamplingConfig   SamplingConfig (sampler.h:10-17)
+    Sampler          a Sampler's draw stream: std::mt19937 seeded as
+                     Sampler::Sampler (sampler.cpp:9-16) and libstdc++'s
+                     uniform_real_distribution<float>(0, 1)
+
+Sampling runs on the device (qraf_engine_sample): the repetition penalty
+(sampler.cpp:37-49), then greedy argmax (:25-35) or temperature / top-k /
+top-p sampling (:57-128) on the step's logits where they lie in HBM; only
+token ids (and the uniform of each sampled row) cross PCIe.
 """
 from __future__ import annotations
 
 import ctypes as C
 import os
+import random
 from collections import deque
 from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._lib import F16, F32, Q4_0, Q8_0, EngineOptions, ModelConfig, call, fp, i32p, lib, u32p
+from ._lib import F16, F32, Q4_0, Q8_0, EngineOptions, ModelConfig, SamplingParams, call, fp, i32p, lib, u32p
 
 __all__ = ["Engine", "Transformer", "InferenceEngine", "BatchScheduler", "Request", "model_config",
-           "read_file_config"]
+           "read_file_config", "SamplingConfig", "Sampler"]
 
 
 def model_config(vocab, hidden, layers, heads, kv_heads, inter, max_seq=2048, rope_theta=1e4, eps=1e-5):
@@ -39,6 +44,58 @@ def read_file_config(path: str) -> ModelConfig:
     cfg = ModelConfig()
     call("qraf_file_read_config", os.fsencode(path), C.byref(cfg), None)
     return cfg
+
+
+@dataclass
+class SamplingConfig:
+    """SamplingConfig (sampler.h:10-17), with the reference's defaults."""
+    temperature: float = 0.8
+    top_k: int = 40
+    top_p: float = 0.9
+    repetition_penalty: float = 1.1
+    seed: int = 0  # 0: a random seed
+    deterministic: bool = False
+
+    @property
+    def greedy(self) -> bool:
+        return self.deterministic or self.temperature <= 0.0  # sampler.cpp:59-61
+
+    def params(self) -> SamplingParams:
+        return SamplingParams(0.0 if self.greedy else self.temperature, self.top_k, self.top_p,
+                              self.repetition_penalty)
+
+
+def _mt19937_state(seed: int):
+    """std::mt19937::seed(seed): the 624-word state before the first twist."""
+    mt = [seed & 0xFFFFFFFF]
+    for i in range(1, 624):
+        mt.append((1812433253 * (mt[-1] ^ (mt[-1] >> 30)) + i) & 0xFFFFFFFF)
+    return mt
+
+
+class Sampler:
+    """The draw stream of the reference's Sampler (sampler.cpp:9-16): a
+    std::mt19937 seeded with the config's seed (truncated to unsigned; 0 ->
+    random_device), read through uniform_real_distribution<float>(0, 1) as
+    libstdc++ computes it: float(x) / 2^32, 1.0 replaced by the largest float
+    below it.  Python's Mersenne Twister core is the same generator, so the
+    state is installed directly.  One draw per sampled (non-greedy) token, as
+    Sampler::sample makes."""
+
+    def __init__(self, config: SamplingConfig):
+        self.config = config
+        seed = config.seed if config.seed != 0 else int.from_bytes(os.urandom(4), "little")
+        self._rng = random.Random()
+        self._rng.setstate((3, tuple(_mt19937_state(seed & 0xFFFFFFFF)) + (624,), None))
+
+    def uniform(self) -> float:
+        r = np.float32(self._rng.getrandbits(32)) / np.float32(4294967296.0)
+        if r >= np.float32(1.0):
+            r = np.nextafter(np.float32(1.0), np.float32(0.0))
+        return float(r)
+
+    def uniforms(self, n: int) -> np.ndarray:
+        return np.array([self.uniform() for _ in range(n)], np.float32)
 
 
 class Engine:
@@ -134,6 +191,29 @@ class Engine:
         return lg, nx
 
 
+    def sample(self, params: SamplingParams, recent=None, uniforms=None, row0=0, rows=None) -> np.ndarray:
+        """Sampler::apply_repetition_penalty + Sampler::sample on rows row0.. of
+        the last step's logit rows, on the device.  recent: one token list per
+        row (the penalty's history); uniforms: one draw per row when sampling."""
+        n = rows if rows is not None else (len(recent) if recent is not None else len(uniforms))
+        rec = cnt = None
+        stride = 0
+        if recent is not None and params.repetition_penalty != 1.0:
+            stride = max(1, max(len(r) for r in recent))
+            rec = np.zeros((n, stride), np.uint32)
+            cnt = np.zeros(n, np.int32)
+            for i, r in enumerate(recent):
+                rec[i, :len(r)] = r
+                cnt[i] = len(r)
+        uni = None if uniforms is None else np.ascontiguousarray(uniforms, dtype=np.float32)
+        out = np.empty(n, np.uint32)
+        call("qraf_engine_sample", self.h, row0, n, C.byref(params),
+             rec.ctypes.data_as(u32p) if rec is not None else None,
+             cnt.ctypes.data_as(i32p) if cnt is not None else None, stride,
+             uni.ctypes.data_as(fp) if uni is not None else None, out.ctypes.data_as(u32p))
+        return out
+
+
 class Transformer:
     """Transformer::init / forward / reset (transformer.h:55-90) on the GPU."""
 
@@ -194,33 +274,48 @@ def argmax(logits: np.ndarray) -> int:
 
 
 class InferenceEngine:
-    """InferenceEngine::generate_tokens (inference.cpp:68-159), greedy."""
+    """InferenceEngine::generate_tokens (inference.cpp:68-159)."""
 
     def __init__(self, transformer: Transformer, eos_token: int | None = 2):
         self.transformer = transformer
         self.eos = eos_token  # tokenizer.h:62 default when the file has no tokenizer
 
-    def generate_tokens(self, prompt_tokens, max_tokens=256, repetition_penalty=1.1, stop_tokens=()):
+    def generate_tokens(self, prompt_tokens, max_tokens=256, repetition_penalty=1.1, stop_tokens=(),
+                        sampling: SamplingConfig | None = None):
+        """Greedy with `repetition_penalty` unless a SamplingConfig is given.
+        The prompt is fed token by token (inference.cpp:90-99); then every
+        token is the device sampler's pick from the last logits, penalised
+        with the prompt and every generated token so far (inference.cpp:104-
+        116), and is fed back until a stop token or max_tokens."""
         if len(prompt_tokens) == 0:
             raise ValueError("empty prompt")
-        tf = self.transformer
+        if sampling is None:
+            sampling = SamplingConfig(temperature=0.0, top_k=0, top_p=1.0, repetition_penalty=repetition_penalty,
+                                      deterministic=True)
+        sampler = Sampler(sampling) if not sampling.greedy else None
+        params = sampling.params()
+        e = self.transformer.engine
         stops = set(stop_tokens) | ({self.eos} if self.eos is not None else set())
-        tf.reset()
-        logits = None
-        for i, t in enumerate(prompt_tokens):
-            logits = tf.forward(t, i)
-        pos = len(prompt_tokens)
-        recent = list(prompt_tokens)
-        out = []
-        for _ in range(max_tokens):
-            apply_repetition_penalty(logits, recent, repetition_penalty)
-            nxt = argmax(logits)
-            if nxt in stops:
-                break
-            out.append(nxt)
-            recent.append(nxt)
-            logits = tf.forward(nxt, pos)
-            pos += 1
+        self.transformer.reset()  # frees the default sequence's pages
+        seq = e.seq_create()
+        try:
+            last = len(prompt_tokens) - 1
+            for i, t in enumerate(prompt_tokens):
+                e.step([seq], [t], [i], want_logits=[i == last], logits=False, argmax=i == last)
+            pos = len(prompt_tokens)
+            recent = list(prompt_tokens)
+            out = []
+            for _ in range(max_tokens):
+                uni = None if sampler is None else [sampler.uniform()]
+                nxt = int(e.sample(params, [recent], uni, rows=1)[0])
+                if nxt in stops:
+                    break
+                out.append(nxt)
+                recent.append(nxt)
+                e.step([seq], [nxt], [pos], logits=False, argmax=True)
+                pos += 1
+        finally:
+            e.seq_release(seq)
         return out
 
 
@@ -314,10 +409,20 @@ class BatchScheduler:
                 rows.append((r, r.prompt[i], i, i == len(r.prompt) - 1))
             budget -= c
         want = np.array([w for (_, _, _, w) in rows], np.uint8)
-        need_host = any(r.penalty != 1.0 for (r, _, _, w) in rows if w)
         lg, nx = self.engine.step([r.seq for (r, _, _, _) in rows], [t for (_, t, _, _) in rows],
-                                  [p for (_, _, p, _) in rows], want_logits=want, logits=need_host,
-                                  argmax=not need_host)
+                                  [p for (_, _, p, _) in rows], want_logits=want, logits=False, argmax=True)
+        # rows with a repetition penalty: penalty + argmax again on the device,
+        # per run of consecutive logit rows that share a penalty value
+        lrows = [r for (r, _, _, w) in rows if w]
+        i = 0
+        while i < len(lrows):
+            j = i + 1
+            while j < len(lrows) and lrows[j].penalty == lrows[i].penalty:
+                j += 1
+            if lrows[i].penalty != 1.0:
+                gp = SamplingParams(0.0, 0, 1.0, lrows[i].penalty)
+                nx[i:j] = self.engine.sample(gp, [r.prompt + r.generated for r in lrows[i:j]], row0=i)
+            i = j
         self.steps += 1
         self.rows += len(rows)
         k = 0
@@ -329,12 +434,7 @@ class BatchScheduler:
                     r.state = "DECODING"
             if not w:
                 continue
-            if need_host:
-                l = lg[k]
-                apply_repetition_penalty(l, r.prompt + r.generated, r.penalty)
-                t = argmax(l)
-            else:
-                t = int(nx[k])
+            t = int(nx[k])
             k += 1
             if (r.eos is not None and t == r.eos) or len(r.generated) >= r.max_tokens:
                 retire.append(r)

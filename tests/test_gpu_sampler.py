@@ -1,0 +1,133 @@
+"""Device sampler against the compiled reference's Sampler on identical
+logits: the repetition penalty bit for bit (logits penalised in place), the
+greedy argmax, and temperature / top-k / top-p sampling token for token
+(the uniforms are the reference's own draw stream, reproduced on the host).
+Then InferenceEngine with sampling, end to end, against the reference's
+InferenceEngine on the same .qraf file.
+
+Sampling parity is exact on the same logits unless a uniform lands within a
+rounding of a cumulative-probability boundary (device expf against glibc's
+expf); with continuous random logits that has probability of order 1e-6 per
+draw.  Ties between equal probabilities are not ordered by the reference
+(std::sort), so the inputs here have none.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from oracle import pyoracle as po
+
+pytestmark = [pytest.mark.gpu,
+              pytest.mark.skipif(po.ref() is None, reason="oracle/_ref (the compiled reference) is not built")]
+
+u32p = C.POINTER(C.c_uint32)
+fp = C.POINTER(C.c_float)
+
+
+def device_sample(hip, logits_rows, params, recent=None, uniforms=None):
+    from qraf_amd._lib import SamplingParams
+    from qraf_amd.backend import DeviceBuffer
+    rows, V = logits_rows.shape
+    dl = DeviceBuffer.from_array(np.ascontiguousarray(logits_rows, np.float32))
+    out = DeviceBuffer(rows * 4)
+    rec = cnt = uni = None
+    stride = 0
+    if recent is not None:
+        stride = max(1, max(len(r) for r in recent))
+        a = np.zeros((rows, stride), np.uint32)
+        c = np.zeros(rows, np.int32)
+        for i, r in enumerate(recent):
+            a[i, :len(r)] = r
+            c[i] = len(r)
+        rec, cnt = DeviceBuffer.from_array(a), DeviceBuffer.from_array(c)
+    if uniforms is not None:
+        uni = DeviceBuffer.from_array(np.ascontiguousarray(uniforms, np.float32))
+    sp = SamplingParams(*params)
+    hip._lib.call("qraf_hip_sample_dev", dl.ptr, rows, V, C.byref(sp), rec.ptr if rec else None,
+                  cnt.ptr if cnt else None, stride, uni.ptr if uni else None, out.ptr, None)
+    hip._lib.call("qraf_hip_stream_synchronize", None)
+    return out.download(np.uint32, rows), dl.download(np.float32, rows * V).reshape(rows, V)
+
+
+def ref_sample(logits, T, k, p, seed, n):
+    out = np.zeros(n, np.uint32)
+    l = np.ascontiguousarray(logits, np.float32)
+    po.ref().ref_sample(l.ctypes.data_as(fp), l.size, T, k, p, seed, n, out.ctypes.data_as(u32p))
+    return out
+
+
+@pytest.mark.parametrize("V", [1000, 151936])
+@pytest.mark.parametrize("cfg", [(0.8, 40, 0.9), (1.0, 1, 1.0), (0.7, 1024, 0.95), (1.3, 50, 0.0), (0.9, 200, 0.5),
+                                 (2.0, 0, 0.8)], ids=lambda c: "T%g_k%d_p%g" % c)
+def test_sampling_equals_reference_sampler(hip, V, cfg):
+    from qraf_amd.engine import Sampler, SamplingConfig
+    T, k, p = cfg
+    if k == 0 and V > 1024:
+        pytest.skip("every token a candidate: over the device sampler's 1024")
+    rng = np.random.default_rng(V + int(T * 10) + k)
+    n = 96
+    logits = (rng.standard_normal(V) * 3.0).astype(np.float32)
+    seed = 1000 + k
+    print(f"sampler V={V} T={T} top_k={k} top_p={p}", flush=True)
+    want = ref_sample(logits, T, k, p, seed, n)
+    uni = Sampler(SamplingConfig(seed=seed)).uniforms(n)
+    got, _ = device_sample(hip, np.tile(logits, (n, 1)), (T, k, p, 1.0), uniforms=uni)
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {n} draws differ"
+    assert len(set(want.tolist())) > (1 if k != 1 else 0)  # the draws do explore the candidates
+
+
+@pytest.mark.parametrize("V,hist", [(1000, 40), (151936, 40), (1000, 3000), (151936, 5000)])
+def test_penalty_and_greedy_equal_reference(hip, V, hist):
+    """Histories up to 4096 tokens take the LDS-sorted kernel, longer ones
+    the sequential one."""
+    rng = np.random.default_rng(V + hist)
+    rows = 6
+    L = (rng.standard_normal((rows, V)) * 2.0).astype(np.float32)
+    recent = [rng.integers(0, V, hist).tolist() + [5, 5, 5] for _ in range(rows)]  # repeats: applied per occurrence
+    recent[1] = recent[1] + [V + 3]  # out of range: skipped
+    got, pen = device_sample(hip, L, (0.0, 40, 0.9, 1.1), recent=recent)
+    R = po.ref()
+    for i in range(rows):
+        w = L[i].copy()
+        r = np.array(recent[i], np.uint32)
+        R.ref_penalty(w.ctypes.data_as(fp), V, r.ctypes.data_as(u32p), r.size, 1.1)
+        assert np.array_equal(pen[i], w), f"row {i}: penalised logits differ"
+        assert got[i] == R.ref_argmax(w.ctypes.data_as(fp), V), f"row {i}"
+
+
+def test_first_index_of_equal_maxima(hip):
+    L = np.zeros((2, 4096), np.float32)
+    L[0, [7, 100, 4000]] = 3.0
+    L[1, [4095, 4094]] = 1.0
+    got, _ = device_sample(hip, L, (0.0, 0, 1.0, 1.0))
+    assert got.tolist() == [7, 4094]
+
+
+def test_too_many_candidates_is_refused(hip):
+    from qraf_amd._lib import ERR_INVALID, HipError
+    L = np.zeros((1, 4096), np.float32)
+    with pytest.raises(HipError) as e:
+        device_sample(hip, L, (0.8, 0, 0.9, 1.0), uniforms=[0.5])
+    assert e.value.code == ERR_INVALID
+
+
+@pytest.mark.parametrize("cfg", [(0.8, 40, 0.9, 1.1, 7), (1.0, 10, 1.0, 1.0, 3), (0.0, 40, 0.9, 1.3, 1)],
+                         ids=["default", "topk10", "greedy_penalty"])
+def test_generate_with_sampling_equals_reference(hip, tmp_path, cfg):
+    from qraf_amd.engine import InferenceEngine, SamplingConfig, Transformer
+    from tests.test_gpu_engine import SMALL
+    T, k, p, pen, seed = cfg
+    kw, mseed = SMALL["q8_llama"]
+    m = po.Model(po.make_config(**kw), mseed)
+    path = str(tmp_path / "m.qraf")
+    m.write_qraf(path)
+    prompt = [po.lib().or_gen_token(mseed, i, kw["vocab"]) for i in range(8)]
+    ref = po.RefEngine(path)
+    want = ref.generate_sampled(prompt, 24, T, k, p, pen, seed)
+    ref.close()
+    tf = Transformer.from_file(path)
+    got = InferenceEngine(tf).generate_tokens(prompt, 24, sampling=SamplingConfig(T, k, p, pen, seed))
+    tf.engine.close()
+    m.close()
+    assert got == want
