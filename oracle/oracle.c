@@ -326,6 +326,61 @@ void or_attention_decode(const float* q, const float* K, const float* V, int ctx
     free(sc);
 }
 
+/* ---------------- int8 KV (kv_cache_quant.h) ---------------- */
+
+/* QuantizedKVCache::store for one head (kv_cache_quant.h:61-95): amax over
+ * the head, scale = amax / 127, inv = scale > 0 ? 1 / scale : 0,
+ * q = (int8) clamp(round(x * inv), -127, 127), round half away from zero. */
+void or_kv_quant_head(const float* x, int hd, int8_t* q, float* scale) {
+    float amax = 0.0f;
+    for (int d = 0; d < hd; d++) amax = fmaxf(amax, fabsf(x[d]));
+    float s = amax / 127.0f;
+    float inv = (s > 0) ? 1.0f / s : 0.0f;
+    *scale = s;
+    for (int d = 0; d < hd; d++) {
+        float r = roundf(x[d] * inv);
+        q[d] = (int8_t)fmaxf(-127.0f, fminf(127.0f, r));
+    }
+}
+
+/* QuantizedKVCache::dot_with_key (kv_cache_quant.h:118-128) */
+float or_kv_dot_key(const int8_t* kq, float scale, const float* query, int hd) {
+    float sum = 0.0f;
+    for (int d = 0; d < hd; d++) sum += (float)kq[d] * query[d];
+    return sum * scale;
+}
+
+/* attention_forward's scores and weighted sum (attention.cpp:122-150) over
+ * int8 K/V as kv_cache_quant.h reads them: score = dot_with_key (:118-128,
+ * sum of (float)q8 * query, then * scale) * (1/sqrt(hd)); V rows through
+ * dequant_value (:108-116, (float)q8 * scale), accumulated in t order.
+ * K8, V8: [ctx][Hkv][hd]; Ks, Vs: [ctx][Hkv]. */
+void or_attention_decode_i8(const float* q, const int8_t* K8, const float* Ks, const int8_t* V8, const float* Vs,
+                            int ctx, int H, int Hkv, int hd, float* out) {
+    int rep = H / Hkv, kvd = Hkv * hd;
+    float scale = 1.0f / sqrtf((float)hd);
+    float* sc = (float*)malloc(sizeof(float) * (size_t)(ctx > 0 ? ctx : 1));
+    float* vrow = (float*)malloc(sizeof(float) * (size_t)hd);
+    for (int h = 0; h < H; h++) {
+        int kh = h / rep;
+        const float* qh = q + (size_t)h * hd;
+        float* oh = out + (size_t)h * hd;
+        for (int t = 0; t < ctx; t++)
+            sc[t] = or_kv_dot_key(K8 + (size_t)t * kvd + kh * hd, Ks[(size_t)t * Hkv + kh], qh, hd) * scale;
+        or_softmax(sc, ctx);
+        memset(oh, 0, sizeof(float) * hd);
+        for (int t = 0; t < ctx; t++) {
+            const int8_t* vq = V8 + (size_t)t * kvd + kh * hd;
+            float vsc = Vs[(size_t)t * Hkv + kh];
+            for (int d = 0; d < hd; d++) vrow[d] = (float)vq[d] * vsc;
+            float s = sc[t];
+            for (int d = 0; d < hd; d++) oh[d] += s * vrow[d];
+        }
+    }
+    free(vrow);
+    free(sc);
+}
+
 /* ---------------- sampling (sampler.cpp) ---------------- */
 
 /* sampler.cpp:25-35: strict '>', lowest index wins ties */

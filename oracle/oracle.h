@@ -72,6 +72,10 @@ void or_scale(float* x, float s, int n);
 
 /* attention.cpp:122-150 for one sequence: q [H*hd]; K,V [ctx][Hkv*hd] f32;
  * out [H*hd].  scores buffer is internal. */
+void or_kv_quant_head(const float* x, int hd, int8_t* q, float* scale);
+float or_kv_dot_key(const int8_t* kq, float scale, const float* query, int hd);
+void or_attention_decode_i8(const float* q, const int8_t* K8, const float* Ks, const int8_t* V8, const float* Vs,
+                            int ctx, int H, int Hkv, int hd, float* out);
 void or_attention_decode(const float* q, const float* K, const float* V, int ctx,
                          int H, int Hkv, int hd, float* out);
 

@@ -77,6 +77,11 @@ def lib():
         for n in ("or_silu", "or_softmax"):
             getattr(L, n).argtypes = [_fp, C.c_int]
         L.or_attention_decode.argtypes = [_fp, _fp, _fp, C.c_int, C.c_int, C.c_int, C.c_int, _fp]
+        L.or_kv_quant_head.argtypes = [_fp, C.c_int, C.c_void_p, _fp]
+        L.or_kv_dot_key.restype = C.c_float
+        L.or_kv_dot_key.argtypes = [C.c_void_p, C.c_float, _fp, C.c_int]
+        L.or_attention_decode_i8.argtypes = [_fp, C.c_void_p, _fp, C.c_void_p, _fp, C.c_int, C.c_int, C.c_int,
+                                             C.c_int, _fp]
         L.or_argmax.restype = C.c_uint32
         L.or_argmax.argtypes = [_fp, C.c_int]
         L.or_repetition_penalty.argtypes = [_fp, C.c_int, _u32p, C.c_int, C.c_float]
@@ -129,6 +134,7 @@ def ref():
         R.ref_penalty.argtypes = [_fp, C.c_int, _u32p, C.c_int, C.c_float]
         R.ref_sample.argtypes = [_fp, C.c_int, C.c_float, C.c_int, C.c_float, C.c_uint64, C.c_int, _u32p]
         R.ref_uniforms.argtypes = [C.c_uint64, C.c_int, _fp]
+        R.ref_kv_quant.argtypes = [_fp, _fp, C.c_int, C.c_int, _fp, C.c_void_p, _fp, C.c_void_p, _fp, _fp, _fp]
         R.ref_engine_generate_sampled.argtypes = [C.c_void_p, _u32p, C.c_int, C.c_int, C.c_float, C.c_int,
                                                   C.c_float, C.c_float, C.c_uint64, _u32p]
         R.ref_writer_new.restype = C.c_void_p
@@ -210,6 +216,27 @@ def attention_decode(q, K, V, H, Hkv, hd):
     V = np.ascontiguousarray(V, dtype=np.float32)
     out = np.zeros(H * hd, dtype=np.float32)
     lib().or_attention_decode(_f(q), _f(K), _f(V), K.shape[0], H, Hkv, hd, _f(out))
+    return out
+
+
+def kv_quant_heads(x, Hkv, hd):
+    """QuantizedKVCache::store of one position's [Hkv][hd] values: (int8 [Hkv][hd], f32 scales [Hkv])."""
+    x = np.ascontiguousarray(x, dtype=np.float32).reshape(Hkv, hd)
+    q = np.zeros((Hkv, hd), np.int8)
+    s = np.zeros(Hkv, np.float32)
+    for h in range(Hkv):
+        lib().or_kv_quant_head(_f(x[h]), hd, q[h].ctypes.data, _f(s[h:h + 1]))
+    return q, s
+
+
+def attention_decode_i8(q, K8, Ks, V8, Vs, H, Hkv, hd):
+    """K8, V8: int8 [ctx][Hkv][hd]; Ks, Vs: f32 [ctx][Hkv]."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    K8, V8 = np.ascontiguousarray(K8, dtype=np.int8), np.ascontiguousarray(V8, dtype=np.int8)
+    Ks, Vs = np.ascontiguousarray(Ks, dtype=np.float32), np.ascontiguousarray(Vs, dtype=np.float32)
+    out = np.zeros(H * hd, dtype=np.float32)
+    lib().or_attention_decode_i8(_f(q), K8.ctypes.data, _f(Ks), V8.ctypes.data, _f(Vs), K8.shape[0], H, Hkv, hd,
+                                 _f(out))
     return out
 
 

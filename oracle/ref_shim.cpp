@@ -9,6 +9,7 @@
 // (backend.cpp:28-31).
 #include "core/logging.h"
 #include "nn/backend.h"
+#include "nn/kv_cache_quant.h"
 #include "nn/ops.h"
 #include "nn/transformer.h"
 #include "qraf/loader.h"
@@ -109,6 +110,24 @@ void ref_uniforms(uint64_t seed, int n, float* out) {
     rng.seed(static_cast<unsigned>(seed));
     std::uniform_real_distribution<f32> d(0.0f, 1.0f);
     for (int i = 0; i < n; i++) out[i] = d(rng);
+}
+
+// QuantizedKVCache (kv_cache_quant.h, header-only, unused by the reference's
+// own attention): store one position of k and v ([Hkv][hd]) and read back the
+// int8 values, scales, dot_with_key against `query` per head, dequant_value.
+void ref_kv_quant(const float* k, const float* v, int Hkv, int hd, const float* query, int8_t* kq, float* ks,
+                  int8_t* vq, float* vs, float* dots, float* vdeq) {
+    QuantizedKVCache c;
+    c.init(1, Hkv, hd, 1);
+    c.store(0, 0, k, v);
+    memcpy(kq, c.keys_q[0].data(), (size_t)Hkv * hd);
+    memcpy(vq, c.values_q[0].data(), (size_t)Hkv * hd);
+    memcpy(ks, c.key_scales[0].data(), (size_t)Hkv * 4);
+    memcpy(vs, c.value_scales[0].data(), (size_t)Hkv * 4);
+    for (int h = 0; h < Hkv; h++) {
+        dots[h] = c.dot_with_key(0, 0, h, query + (size_t)h * hd);
+        c.dequant_value(0, 0, h, vdeq + (size_t)h * hd);
+    }
 }
 
 // ---- QRAF file writing through the reference's QrafWriter (writer.cpp) ----
