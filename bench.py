@@ -53,7 +53,7 @@ METRIC = "Q4/Q8 decode tok/s at batch 1 & 128; qmatvec achieved HBM GB/s vs peak
 HBM_PEAK_GBS = 8000.0      # MI355X published HBM3E bandwidth
 MFMA_BF16_TFLOPS = 2500.0  # MI355X published dense bf16 matrix peak (the GEMM issues 2 MFMAs per product: hi + lo)
 POOL_BYTES = 320 << 20     # > 256 MB MALL
-Q8, Q4, F32, F16 = 10, 20, 0, 1
+Q8, Q4, F32, F16, I8 = 10, 20, 0, 1, 102
 MV_CASES = [("q8_0", Q8, 4096, 4096), ("q8_0", Q8, 11008, 4096), ("q4_0", Q4, 4096, 4096), ("q4_0", Q4, 11008, 4096)]
 GEMM_SHAPES = [(2048, 2048), (256, 2048), (11008, 2048), (2048, 11008)]
 
@@ -286,23 +286,38 @@ def bench_attention(args, rt):
         m = (c + ps - 1) // ps
         table[s, :m] = perm[k:k + m]
         k += m
-    kv_words = num_pages * Hkv * ps * hd // 2  # fp16 pages, filled with N(0,1) bit patterns of f32 pairs
-    K, V = DeviceBuffer(kv_words * 4), DeviceBuffer(kv_words * 4)
-    Kh = rng.standard_normal(kv_words * 2).astype(np.float16)
-    K.upload(Kh)
-    V.upload(rng.standard_normal(kv_words * 2).astype(np.float16))
     q = DeviceBuffer.from_array(rng.standard_normal((n, H * hd)).astype(np.float32))
     dt_, dc = DeviceBuffer.from_array(table), DeviceBuffer.from_array(ctxs)
     out = DeviceBuffer(n * H * hd * 4)
     wsb = lib.qraf_hip_attention_workspace_bytes(n, H, Hkv, hd, max_ctx)
     ws = DeviceBuffer(wsb)
     ws.zero()
-    us = graph_time_us(rt, lambda i: call("qraf_hip_paged_attention_dev", q.ptr, K.ptr, V.ptr, F16, dt_.ptr, max_pages,
-                                          dc.ptr, n, H, Hkv, hd, ps, np.float32(1 / math.sqrt(hd)), max_ctx, out.ptr,
-                                          ws.ptr, wsb, stream.h), 50)
-    by = int(ctxs.sum()) * Hkv * hd * 2 * 2 + 2 * n * H * hd * 4
-    return {"us": round(us, 2), "sum_ctx": int(ctxs.sum()), "alg_bytes": by, "GB_s": round(by / (us * 1e-6) / 1e9, 1),
-            "frac_hbm_peak": round(by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    def leg(kv, K, V, pos_bytes):
+        us = graph_time_us(rt, lambda i: call("qraf_hip_paged_attention_dev", q.ptr, K.ptr, V.ptr, kv, dt_.ptr,
+                                              max_pages, dc.ptr, n, H, Hkv, hd, ps, np.float32(1 / math.sqrt(hd)),
+                                              max_ctx, out.ptr, ws.ptr, wsb, stream.h), 50)
+        by = int(ctxs.sum()) * Hkv * pos_bytes * 2 + 2 * n * H * hd * 4
+        return {"us": round(us, 2), "sum_ctx": int(ctxs.sum()), "alg_bytes": by,
+                "GB_s": round(by / (us * 1e-6) / 1e9, 1), "frac_hbm_peak": round(by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+
+    # fp16 pages, N(0,1)
+    kv_half = num_pages * Hkv * ps * hd
+    K, V = DeviceBuffer(kv_half * 2), DeviceBuffer(kv_half * 2)
+    K.upload(rng.standard_normal(kv_half).astype(np.float16))
+    V.upload(rng.standard_normal(kv_half).astype(np.float16))
+    res = leg(F16, K, V, hd * 2)
+    del K, V
+    # int8 pages (a position of one KV head: hd bytes + a f32 scale), bytes ~ N(0, 40), scales 0.02
+    blocks = np.empty((num_pages * Hkv, ps * (hd + 4)), np.uint8)
+    K8, V8 = DeviceBuffer(blocks.size), DeviceBuffer(blocks.size)
+    for buf in (K8, V8):
+        blocks[:, :ps * hd] = np.clip(np.rint(rng.standard_normal((num_pages * Hkv, ps * hd)) * 40), -127,
+                                      127).astype(np.int8).view(np.uint8)
+        blocks[:, ps * hd:] = np.full((num_pages * Hkv, ps), 0.02, np.float32).view(np.uint8)
+        buf.upload(blocks)
+    res["int8_pages"] = leg(I8, K8, V8, hd + 4)
+    return res
 
 
 # --------------------------------------------------------------------------- decode, batch 1
@@ -385,13 +400,13 @@ QWEN = dict(vocab=151936, hidden=2048, layers=36, heads=16, kv_heads=2, inter=11
             eps=1e-6)
 
 
-def qwen_engine(args, rows):
+def qwen_engine(args, rows, kv=F16):
     """The Qwen2.5-3B-architecture engine of the batch-128 legs (random Q4_0 weights, fp16 KV pages)."""
     from qraf_amd.engine import Engine, model_config
     cfg = model_config(*(QWEN[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq",
                                            "rope_theta", "eps")))
     pages = 128 * (-(-QWEN["max_seq"] // 16)) + 64
-    e = Engine(cfg, kv_dtype=F16, max_batch=rows, num_pages=pages)
+    e = Engine(cfg, kv_dtype=kv, max_batch=rows, num_pages=pages)
     e.generate_weights(Q4, Q4, Q4, True, True, 3)
     e.finalize()
     e.set_graphs(not args.no_graphs)
@@ -432,6 +447,9 @@ def bench_decode_b128(args, rt):
     tbt, streams_t = run(128, 1)
     steady = steady_decode_b128(e, rng, args.decode_steps)
     e.close()
+    e8 = qwen_engine(args, 128, I8)
+    steady["int8_pages"] = steady_decode_b128(e8, np.random.default_rng(3), args.decode_steps)
+    e8.close()
     out = {"model": "Qwen2.5-3B architecture, Q4_0 weights, tied head, QKV bias, fp16 KV pages, random init",
            "requests": args.requests, "max_concurrent": 128}
     out.update(chunked)

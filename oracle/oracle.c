@@ -465,6 +465,11 @@ struct or_model {
     float* emb_f32; /* load_tensor_f32 of the embedding (transformer.cpp:321-334) */
     int kv_cap;
     float *kc, *vc; /* [layer][pos][kv_dim] f32, attention.cpp:14-31 */
+    /* int8 KV mode (or_model_set_kv_int8): QuantizedKVCache in place of the
+     * f32 KVCache, kv_cache_quant.h:16-50 ([layer][pos][kv_dim] int8 and
+     * [layer][pos][kv_heads] scales) */
+    int8_t *k8, *v8;
+    float *ks, *vs;
     float *x, *res, *nrm, *att, *mlp, *q, *k, *v, *ao, *g, *u;
 };
 
@@ -559,6 +564,7 @@ void or_model_free(or_model* m) {
     free(m->wq); free(m->wk); free(m->wv); free(m->wo); free(m->wg); free(m->wu); free(m->wd);
     free(m->bq); free(m->bk); free(m->bv); free(m->an); free(m->fn);
     free(m->emb_f32); free(m->kc); free(m->vc);
+    free(m->k8); free(m->v8); free(m->ks); free(m->vs);
     free(m->x); free(m->res); free(m->nrm); free(m->att); free(m->mlp);
     free(m->q); free(m->k); free(m->v); free(m->ao); free(m->g); free(m->u);
     free(m);
@@ -584,6 +590,28 @@ void or_model_reset(or_model* m) { /* attention.cpp:33-37 */
     size_t n = (size_t)m->c.layers * m->kv_cap * m->c.kv_heads * m->hd;
     memset(m->kc, 0, n * 4);
     memset(m->vc, 0, n * 4);
+    if (m->k8) { /* kv_cache_quant.h:52-58 */
+        size_t ns = (size_t)m->c.layers * m->kv_cap * m->c.kv_heads;
+        memset(m->k8, 0, n); memset(m->v8, 0, n);
+        memset(m->ks, 0, ns * 4); memset(m->vs, 0, ns * 4);
+    }
+}
+
+/* Switch the model's cache to QuantizedKVCache (kv_cache_quant.h:30-50),
+ * emptied.  The reference defines that cache without wiring it into its
+ * Transformer; here it takes the f32 KVCache's two places: the store after
+ * RoPE (attention.cpp:119) quantizes, and the attention reads scores through
+ * dot_with_key and values through dequant_value. */
+int or_model_set_kv_int8(or_model* m) {
+    size_t n = (size_t)m->c.layers * m->kv_cap * m->c.kv_heads * m->hd;
+    size_t ns = (size_t)m->c.layers * m->kv_cap * m->c.kv_heads;
+    if (!m->k8) {
+        m->k8 = (int8_t*)calloc(n, 1); m->v8 = (int8_t*)calloc(n, 1);
+        m->ks = (float*)calloc(ns, 4); m->vs = (float*)calloc(ns, 4);
+        if (!m->k8 || !m->v8 || !m->ks || !m->vs) return -1;
+    }
+    or_model_reset(m);
+    return 0;
 }
 
 /* attention.cpp:56-65 do_matvec */
@@ -612,11 +640,21 @@ int or_model_forward(or_model* m, uint32_t token, int pos, float* logits) {
         if (m->bv[l] >= 0) or_add(m->v, (const float*)m->t[m->bv[l]].data, kvd);
         for (int h = 0; h < H; h++) or_rope(m->q + h * hd, hd, pos, c->rope_theta);
         for (int h = 0; h < Hkv; h++) or_rope(m->k + h * hd, hd, pos, c->rope_theta);
-        float* kl = m->kc + (size_t)l * m->kv_cap * kvd;
-        float* vl = m->vc + (size_t)l * m->kv_cap * kvd;
-        memcpy(kl + (size_t)pos * kvd, m->k, kvd * 4);
-        memcpy(vl + (size_t)pos * kvd, m->v, kvd * 4);
-        or_attention_decode(m->q, kl, vl, pos + 1, H, Hkv, hd, m->ao);
+        if (m->k8) { /* QuantizedKVCache::store (kv_cache_quant.h:61-95) */
+            size_t lo = (size_t)l * m->kv_cap * kvd, so = (size_t)l * m->kv_cap * Hkv;
+            for (int h = 0; h < Hkv; h++) {
+                size_t e = lo + (size_t)pos * kvd + h * hd, sc = so + (size_t)pos * Hkv + h;
+                or_kv_quant_head(m->k + h * hd, hd, m->k8 + e, m->ks + sc);
+                or_kv_quant_head(m->v + h * hd, hd, m->v8 + e, m->vs + sc);
+            }
+            or_attention_decode_i8(m->q, m->k8 + lo, m->ks + so, m->v8 + lo, m->vs + so, pos + 1, H, Hkv, hd, m->ao);
+        } else {
+            float* kl = m->kc + (size_t)l * m->kv_cap * kvd;
+            float* vl = m->vc + (size_t)l * m->kv_cap * kvd;
+            memcpy(kl + (size_t)pos * kvd, m->k, kvd * 4);
+            memcpy(vl + (size_t)pos * kvd, m->v, kvd * 4);
+            or_attention_decode(m->q, kl, vl, pos + 1, H, Hkv, hd, m->ao);
+        }
         mv(m, m->wo[l], D, qd, m->ao, m->att);
         or_add(m->att, m->res, D);
         memcpy(m->res, m->att, D * 4);

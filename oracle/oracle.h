@@ -74,6 +74,7 @@ void or_scale(float* x, float s, int n);
  * out [H*hd].  scores buffer is internal. */
 void or_kv_quant_head(const float* x, int hd, int8_t* q, float* scale);
 float or_kv_dot_key(const int8_t* kq, float scale, const float* query, int hd);
+
 void or_attention_decode_i8(const float* q, const int8_t* K8, const float* Ks, const int8_t* V8, const float* Vs,
                             int ctx, int H, int Hkv, int hd, float* out);
 void or_attention_decode(const float* q, const float* K, const float* V, int ctx,
@@ -117,6 +118,7 @@ int       or_model_num_tensors(const or_model* m);
 int       or_model_tensor(const or_model* m, int i, const char** name, uint32_t* dtype,
                           uint32_t* ndim, uint32_t* shape, const void** data, uint64_t* size);
 void      or_model_reset(or_model* m);                       /* transformer.cpp:641-643 */
+int       or_model_set_kv_int8(or_model* m);                 /* QuantizedKVCache, kv_cache_quant.h */
 int       or_model_forward(or_model* m, uint32_t token, int pos, float* logits); /* :573-639 */
 /* inference.cpp:68-159 with temperature 0 (argmax); eos < 0 disables the stop
  * token; returns the number of generated tokens. */

@@ -12,7 +12,7 @@ import os
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-F32, F16, Q8_0, Q4_0 = 0, 1, 10, 20
+F32, F16, Q8_0, Q4_0, I8 = 0, 1, 10, 20, 102
 
 _fp = C.POINTER(C.c_float)
 _u8p = C.POINTER(C.c_uint8)
@@ -101,6 +101,7 @@ def lib():
         L.or_model_tensor.argtypes = [C.c_void_p, C.c_int, C.POINTER(C.c_char_p), _u32p, _u32p, _u32p,
                                       C.POINTER(C.c_void_p), C.POINTER(C.c_uint64)]
         L.or_model_reset.argtypes = [C.c_void_p]
+        L.or_model_set_kv_int8.argtypes = [C.c_void_p]
         L.or_model_forward.argtypes = [C.c_void_p, C.c_uint32, C.c_int, _fp]
         L.or_generate.argtypes = [C.c_void_p, _u32p, C.c_int, C.c_int, C.c_float, C.c_int, _u32p]
     return _lib
@@ -287,6 +288,11 @@ class Model:
 
     def reset(self):
         lib().or_model_reset(self.h)
+
+    def set_kv_int8(self):
+        """Use QuantizedKVCache (int8 K/V, a scale per position and KV head) from here on."""
+        if lib().or_model_set_kv_int8(self.h) != 0:
+            raise MemoryError("int8 KV cache allocation failed")
 
     def forward(self, token, pos):
         logits = np.zeros(self.cfg.vocab, dtype=np.float32)

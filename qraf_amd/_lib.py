@@ -14,7 +14,7 @@ LIB_PATH = os.path.join(PKG, "libqraf_hip.so")
 
 OK = 0
 ERR_INVALID, ERR_DTYPE, ERR_HIP, ERR_NOMEM, ERR_STATE, ERR_FORMAT = -1, -2, -3, -4, -5, -6
-F32, F16, Q8_0, Q4_0 = 0, 1, 10, 20
+F32, F16, Q8_0, Q4_0, I8 = 0, 1, 10, 20, 102
 
 vp = C.c_void_p
 fp = C.POINTER(C.c_float)

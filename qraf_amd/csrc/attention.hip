@@ -7,6 +7,9 @@
 //     K     : [num_pages][Hkv][page_size][head_dim]   (f32 or f16)
 //     V f32 : [num_pages][Hkv][page_size][head_dim]
 //     V f16 : [num_pages][Hkv][head_dim][page_size]   (dimension-major in a page)
+//     int8  : [num_pages][Hkv] blocks of page_size * (head_dim + 4) bytes,
+//             K block = int8 [page_size][head_dim] then f32 scale [page_size]
+//             V block = int8 [head_dim][page_size] then f32 scale [page_size]
 // and a page table per sequence maps logical page j (positions
 // j*page_size .. +page_size-1) to a physical page.  fp16 V is stored
 // dimension-major so that the matrix-core kernel's V operand (consecutive
@@ -23,16 +26,25 @@
 // second launch, one workgroup per sequence and KV head) combines in chunk
 // order.
 //
-// Two kernels share this decomposition.  attn_mfma_kernel (fp16 pages,
-// head_dim 64 or 128, up to 16 query heads per KV head) runs q.K^T and P.V
-// on v_mfma_f32_16x16x32_f16: K and V enter as stored (fp16, exact), q and the
-// probabilities as fp16 hi + lo pairs (q scaled per head by a power of two so
-// hi + lo carries 22 bits of it), products accumulate in fp32.
+// int8 pages hold the scheme of QuantizedKVCache (kv_cache_quant.h:61-128):
+// per (position, KV head) scale = absmax / 127 and q = clamp(round(x / scale),
+// +-127); a score is (sum_d q_k[d] * query[d]) * k_scale * 1/sqrt(hd) and a
+// value element q_v[d] * v_scale.
+//
+// Two kernels share this decomposition.  attn_mfma_kernel (fp16 or int8
+// pages, head_dim 64 or 128, up to 16 query heads per KV head) runs q.K^T and
+// P.V on v_mfma_f32_16x16x32_f16: K and V enter as stored (fp16, or int8
+// widened to fp16, both exact), q and the probabilities as fp16 hi + lo pairs
+// (q scaled per head by a power of two so hi + lo carries 22 bits of it),
+// products accumulate in fp32.  int8 scales are applied in fp32: a K scale
+// to each position's score, a V scale folded into that position's
+// probability before the P.V product.
 // attn_decode_kernel (the rest) is plain fp32 VALU code: scores with
 // thread = position, output with thread = (head, dimension).
 #include <math.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "common.h"
 
@@ -269,16 +281,37 @@ __device__ __forceinline__ uint2 mask_run(uint2 v, int pos0, int ctx) {
     return make_uint2(v.x & mx, v.y & my);
 }
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+// 4 int8 (one dword, byte i = element i) -> 4 fp16, exactly: the biased byte
+// u = q + 128 goes under the exponent of 1024 (fp16 bits 0x6400 | u encode
+// 1024 + u, spacing 1 in [1024, 2048)), then 1152 = 1024 + 128 is subtracted
+__device__ __forceinline__ uint2 i8x4_to_f16x4(uint32_t w) {
+    const uint32_t u = w ^ 0x80808080u;
+    const uint32_t lo = __builtin_amdgcn_perm(0x64646464u, u, 0x04010400u);  // 0x64,u1,0x64,u0
+    const uint32_t hi = __builtin_amdgcn_perm(0x64646464u, u, 0x04030402u);  // 0x64,u3,0x64,u2
+    const f16x2 off = {(_Float16)1152.0f, (_Float16)1152.0f};
+    const f16x2 a = __builtin_bit_cast(f16x2, lo) - off, b = __builtin_bit_cast(f16x2, hi) - off;
+    return make_uint2(__builtin_bit_cast(uint32_t, a), __builtin_bit_cast(uint32_t, b));
+}
+__device__ __forceinline__ f16x8 i8x8_to_f16x8(uint32_t w0, uint32_t w1) {
+    const uint2 a = i8x4_to_f16x4(w0), b = i8x4_to_f16x4(w1);
+    return __builtin_bit_cast(f16x8, make_uint4(a.x, a.y, b.x, b.y));
+}
+
 // 4 workgroups per CU (at most 128 VGPRs): the K and V loads of one wave
 // already cover its own latency, more resident workgroups cover the
 // prologue and epilogue of the others
-template <int HD>
+template <int HD, bool I8>
 __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
     constexpr int KK = HD / 32;  // MFMA k-steps per score tile
-    // q.K^T k-step kk, lane group s = l/16 covers dimensions 8*(4kk+s) .. +7:
-    // the 4 groups of one step read 64 consecutive bytes of a K row
+    // q.K^T k-step kk, lane group s = l/16 covers 8 dimensions starting at
+    // kdim(kk, s).  fp16: 8*(4kk+s), so the 4 groups of one step read 64
+    // consecutive bytes of a K row; int8: 8*(KK*s+kk), so each lane reads
+    // its 8*KK bytes of the row at once (one or two 16-byte loads)
+    auto kdim = [](int kk, int sg) { return I8 ? 8 * (KK * sg + kk) : 8 * (4 * kk + sg); };
     constexpr int DT = HD / 16;  // 16-dimension output tiles
+    typedef typename std::conditional<I8, uint32_t, uint2>::type VRun;  // one 4-position V run
     constexpr int QS = HD + 8;   // q plane row stride (fp16): 16-byte reads of 16 rows hit distinct banks
     __shared__ __align__(16) _Float16 s_q[2][16][QS];
     __shared__ float s_qs[16];
@@ -306,6 +339,19 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     const int vlast = (ctx - 1) & ~3;
 #pragma unroll
     for (int j = 0; j < 4; j++) vpg[j] = ptab[min(pw + 16 * j + 4 * seg, vlast) / ps];
+    // int8: the K and V scales of the lane's 4-position runs pw + 16j + 4seg
+    // (j = 0..3, the positions of its scores and of its P operand)
+    const size_t blk = (size_t)ps * (HD + 4);  // int8 bytes of one (page, KV head) block
+    float4 ksc[4], vsc[4];
+    if (I8 && active) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int rp = min(pw + 16 * j + 4 * seg, vlast) % ps;
+            const size_t b = ((size_t)vpg[j] * a.Hkv + kvh) * blk + (size_t)ps * HD;
+            ksc[j] = *(const float4*)((const int8_t*)a.kc + b + 4 * rp);
+            vsc[j] = *(const float4*)((const int8_t*)a.vc + b + 4 * rp);
+        }
+    }
 
     // ---- q of the G heads as fp16 hi + lo, scaled per head by 2^e so that
     // max|q| lands in [2^14, 2^15): hi + lo then carries 22 bits of every
@@ -348,19 +394,34 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
         f16x8 qh[KK], ql[KK];
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) {
-            qh[kk] = *(const f16x8*)&s_q[0][l16][8 * (4 * kk + seg)];
-            ql[kk] = *(const f16x8*)&s_q[1][l16][8 * (4 * kk + seg)];
+            qh[kk] = *(const f16x8*)&s_q[0][l16][kdim(kk, seg)];
+            ql[kk] = *(const f16x8*)&s_q[1][l16][kdim(kk, seg)];
         }
 #pragma unroll
         for (int t = 0; t < 4; t++) {
             const int pc = min(pw + 16 * t + l16, ctx - 1);  // clamped: past-ctx scores are masked below
-            const _Float16* kr = kc + (((size_t)kpg[t] * a.Hkv + kvh) * ps + pc % ps) * HD + 8 * seg;
             f32x4a d = {0.f, 0.f, 0.f, 0.f};
+            if constexpr (I8) {
+                const int8_t* kr = (const int8_t*)a.kc + ((size_t)kpg[t] * a.Hkv + kvh) * blk +
+                                   (size_t)(pc % ps) * HD + 8 * KK * seg;
+                uint4 kw[KK / 2];
 #pragma unroll
-            for (int kk = 0; kk < KK; kk++) {
-                const f16x8 kf = *(const f16x8*)(kr + 32 * kk);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[kk], d, 0, 0, 0);
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[kk], d, 0, 0, 0);
+                for (int i = 0; i < KK / 2; i++) kw[i] = *(const uint4*)(kr + 16 * i);
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) {
+                    const uint4 w = kw[kk / 2];
+                    const f16x8 kf = (kk & 1) ? i8x8_to_f16x8(w.z, w.w) : i8x8_to_f16x8(w.x, w.y);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[kk], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[kk], d, 0, 0, 0);
+                }
+            } else {
+                const _Float16* kr = kc + (((size_t)kpg[t] * a.Hkv + kvh) * ps + pc % ps) * HD + 8 * seg;
+#pragma unroll
+                for (int kk = 0; kk < KK; kk++) {
+                    const f16x8 kf = *(const f16x8*)(kr + 32 * kk);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[kk], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[kk], d, 0, 0, 0);
+                }
             }
             sc[t] = d;
         }
@@ -369,18 +430,29 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     // ---- V of the wave's 64 positions, requested before the softmax so its
     // latency overlaps the score phase.  Per lane and 32-position step b: two
     // 4-position runs (b*32 + 4seg and +16) per 16-dimension tile, clamped
-    // into the context (values past it are masked), 4-aligned so a run never
-    // leaves a page.
-    uint2 va0[DT], vb0[DT], va1[DT], vb1[DT];
-    auto vload = [&](int b, uint2 (&ra)[DT], uint2 (&rb)[DT]) {
+    // into the context (fp16 values past it are masked; int8 ones are finite
+    // and meet a zero probability), 4-aligned so a run never leaves a page.
+    VRun va0[DT], vb0[DT], va1[DT], vb1[DT];
+    auto vload = [&](int b, VRun (&ra)[DT], VRun (&rb)[DT]) {
         const int pac = min(pw + 32 * b + 4 * seg, vlast), pbc = min(pw + 32 * b + 16 + 4 * seg, vlast);
-        const _Float16* va = vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * HD * ps + pac % ps;
-        const _Float16* vb = vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * HD * ps + pbc % ps;
+        if constexpr (I8) {
+            const int8_t* va = (const int8_t*)a.vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * blk + pac % ps;
+            const int8_t* vb = (const int8_t*)a.vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * blk + pbc % ps;
 #pragma unroll
-        for (int d = 0; d < DT; d++) {
-            const int dim = 16 * d + l16;
-            ra[d] = *(const uint2*)(va + (size_t)dim * ps);
-            rb[d] = *(const uint2*)(vb + (size_t)dim * ps);
+            for (int d = 0; d < DT; d++) {
+                const int dim = 16 * d + l16;
+                ra[d] = *(const uint32_t*)(va + (size_t)dim * ps);
+                rb[d] = *(const uint32_t*)(vb + (size_t)dim * ps);
+            }
+        } else {
+            const _Float16* va = vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * HD * ps + pac % ps;
+            const _Float16* vb = vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * HD * ps + pbc % ps;
+#pragma unroll
+            for (int d = 0; d < DT; d++) {
+                const int dim = 16 * d + l16;
+                ra[d] = *(const uint2*)(va + (size_t)dim * ps);
+                rb[d] = *(const uint2*)(vb + (size_t)dim * ps);
+            }
         }
     };
     if (active) {
@@ -396,7 +468,8 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const bool ok = active && pw + 16 * t + 4 * seg + r < ctx;
-            sc[t][r] = ok ? sc[t][r] * qs : -INFINITY;
+            if constexpr (I8) sc[t][r] = ok ? (sc[t][r] * ksc[t][r]) * qs : -INFINITY;  // kv_cache_quant.h:127
+            else sc[t][r] = ok ? sc[t][r] * qs : -INFINITY;
             mloc = fmaxf(mloc, sc[t][r]);
         }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
@@ -417,12 +490,43 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     lsum += __shfl_xor(lsum, 32);
     if (seg == 0) s_l[wave][l16] = lsum;
 
+    // ---- int8: fold each position's V scale into its probability, times a
+    // power of two 2^-e per wave that brings the wave's largest V scale into
+    // [1/2, 1), so the fp16 hi + lo split of p * scale neither overflows nor
+    // loses bits to fp16 underflow; the output is multiplied back by 2^e
+    float ounit = 1.f;
+    if constexpr (I8) {
+        float vm = 0.f;
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++)
+                vm = active && pw + 16 * t + 4 * seg + r < ctx ? fmaxf(vm, vsc[t][r]) : vm;
+        vm = fmaxf(vm, __shfl_xor(vm, 16));
+        vm = fmaxf(vm, __shfl_xor(vm, 32));
+        float cw = 1.f;
+        if (vm > 0.f && vm <= 3.0e38f) {
+            int e;
+            frexpf(vm, &e);
+            e = max(-120, min(e, 120));
+            cw = ldexpf(1.f, -e);
+            ounit = ldexpf(1.f, e);
+        }
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const bool ok = active && pw + 16 * t + 4 * seg + r < ctx;
+                sc[t][r] = ok ? sc[t][r] * (vsc[t][r] * cw) : 0.f;
+            }
+    }
+
     // ---- P.V over the wave's 64 positions (two 32-position MFMA steps)
     f32x4a o[DT];
 #pragma unroll
     for (int d = 0; d < DT; d++) o[d] = f32x4a{0.f, 0.f, 0.f, 0.f};
     if (active) {
-        auto pv = [&](int b, const uint2 (&ra)[DT], const uint2 (&rb)[DT]) {
+        auto pv = [&](int b, const VRun (&ra)[DT], const VRun (&rb)[DT]) {
             f16x8 ph, pl;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
@@ -434,8 +538,13 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
             const int pa = pw + 32 * b + 4 * seg, pb = pa + 16;
 #pragma unroll
             for (int d = 0; d < DT; d++) {
-                const uint2 xa = mask_run(ra[d], pa, ctx), xb = mask_run(rb[d], pb, ctx);
-                const f16x8 vf = __builtin_bit_cast(f16x8, make_uint4(xa.x, xa.y, xb.x, xb.y));
+                f16x8 vf;
+                if constexpr (I8) {
+                    vf = i8x8_to_f16x8(ra[d], rb[d]);
+                } else {
+                    const uint2 xa = mask_run(ra[d], pa, ctx), xb = mask_run(rb[d], pb, ctx);
+                    vf = __builtin_bit_cast(f16x8, make_uint4(xa.x, xa.y, xb.x, xb.y));
+                }
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vf, o[d], 0, 0, 0);
                 o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, o[d], 0, 0, 0);
             }
@@ -450,7 +559,7 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const int h = 4 * seg + r;
-            if (h < G) s_o[wave * G + h][16 * d + l16] = o[d][r];
+            if (h < G) s_o[wave * G + h][16 * d + l16] = o[d][r] * ounit;
         }
     __syncthreads();
     const size_t hbase = (size_t)s * a.H + kvh * G;
@@ -561,7 +670,10 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     QH_REQUIRE(Hkv > 0 && H % Hkv == 0, QRAF_HIP_ERR_INVALID, "attention: %d heads not a multiple of %d kv heads", H, Hkv);
     QH_REQUIRE(page_size > 0 && max_pages > 0 && max_ctx > 0 && max_ctx <= max_pages * page_size, QRAF_HIP_ERR_INVALID,
                "attention: bad page geometry");
-    QH_REQUIRE(kv_dtype == DT_F32 || kv_dtype == DT_F16, QRAF_HIP_ERR_DTYPE, "attention: KV dtype %u", kv_dtype);
+    QH_REQUIRE(kv_dtype == DT_F32 || kv_dtype == DT_F16 || kv_dtype == DT_I8, QRAF_HIP_ERR_DTYPE,
+               "attention: KV dtype %u", kv_dtype);
+    QH_REQUIRE(kv_dtype != DT_I8 || ((hd == 64 || hd == 128) && H / Hkv <= 16 && page_size % 4 == 0),
+               QRAF_HIP_ERR_INVALID, "attention: int8 pages need head_dim 64/128, group <= 16, page_size %% 4 == 0");
     QH_REQUIRE(ws_bytes >= attn_workspace_bytes(n, H, Hkv, hd, max_ctx), QRAF_HIP_ERR_INVALID,
                "attention: workspace too small");
     const int items = n * ((max_ctx + ACH - 1) / ACH);
@@ -592,10 +704,14 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
         QH_TRY(launch_attn_t<float>(a, hd, G, items, st));
     } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0) {
         const dim3 grid(items, Hkv);
-        if (hd == 128)
-            hipLaunchKernelGGL(attn_mfma_kernel<128>, grid, dim3(ACH), 4 * G * 128 * sizeof(float), st, a, G);
-        else
-            hipLaunchKernelGGL(attn_mfma_kernel<64>, grid, dim3(ACH), 4 * G * 64 * sizeof(float), st, a, G);
+        const size_t lds = 4 * G * hd * sizeof(float);
+        if (kv_dtype == DT_I8) {
+            if (hd == 128) hipLaunchKernelGGL((attn_mfma_kernel<128, true>), grid, dim3(ACH), lds, st, a, G);
+            else hipLaunchKernelGGL((attn_mfma_kernel<64, true>), grid, dim3(ACH), lds, st, a, G);
+        } else {
+            if (hd == 128) hipLaunchKernelGGL((attn_mfma_kernel<128, false>), grid, dim3(ACH), lds, st, a, G);
+            else hipLaunchKernelGGL((attn_mfma_kernel<64, false>), grid, dim3(ACH), lds, st, a, G);
+        }
         QH_CHECK_HIP(hipGetLastError());
     } else {
         QH_TRY(launch_attn_t<_Float16>(a, hd, G, items, st));
@@ -672,11 +788,92 @@ __global__ void rope_append_kernel(const float* __restrict__ qkv, const float* _
     }
 }
 
+// int8 pages: QuantizedKVCache::store (kv_cache_quant.h:61-95) of the rotated
+// k and the v of each KV head.  One workgroup per sequence: its threads
+// rotate the q pairs, then wave w takes heads j = w, w + 4, ... of the 2*Hkv
+// (K heads, then V heads); lane l holds elements 2l, 2l+1 of a K head (one
+// rotated pair) or l, l+64 of a V head, the wave's absmax is a max-reduction,
+// and scale = absmax / 127, q = clamp(round(x * (1 / scale)), +-127) with
+// the reference's divisions (IEEE, correctly rounded) and rounding (half away
+// from zero).  head_dim <= 128.
+__global__ __launch_bounds__(256) void rope_append_i8_kernel(const float* __restrict__ qkv,
+                                                             const float* __restrict__ bias, int H, int Hkv, int hd,
+                                                             const int32_t* __restrict__ pos,
+                                                             const float* __restrict__ rope, float* __restrict__ q_out,
+                                                             int8_t* __restrict__ kc, int8_t* __restrict__ vc,
+                                                             const int32_t* __restrict__ page_table, int max_pages,
+                                                             int page_size, int S, size_t slice) {
+    const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int qd = H * hd, kvd = Hkv * hd;
+    const size_t rbase = (size_t)s * (qd + 2 * kvd);
+    auto ld = [&](int i) {
+        const float x = sum_slices(qkv, S, slice, rbase + i);
+        return bias ? __fadd_rn(x, bias[i]) : x;
+    };
+    const int p = pos[s];
+    const int page = page_table[(size_t)s * max_pages + p / page_size], off = p % page_size;
+    const float* cs = rope + (size_t)p * hd;
+    // rotated pair (i0, i0 + 1) of the q|k part, as rope_append_kernel
+    auto rot = [&](int i0, float& ra, float& rb) {
+        const int i = i0 % hd;
+        const float x = ld(i0), y = ld(i0 + 1), c = cs[i], sn = cs[i + 1];
+        ra = __fsub_rn(__fmul_rn(x, c), __fmul_rn(y, sn));
+        rb = __fadd_rn(__fmul_rn(x, sn), __fmul_rn(y, c));
+    };
+    for (int e = tid; e < qd / 2; e += 256) {
+        float ra, rb;
+        rot(2 * e, ra, rb);
+        q_out[(size_t)s * qd + 2 * e] = ra;
+        q_out[(size_t)s * qd + 2 * e + 1] = rb;
+    }
+    const size_t blk = (size_t)page_size * (hd + 4);
+    for (int j = wave; j < 2 * Hkv; j += 4) {
+        const bool isk = j < Hkv;
+        const int h = isk ? j : j - Hkv;
+        const int d0 = isk ? 2 * lane : lane, d1 = isk ? 2 * lane + 1 : lane + 64;
+        const bool v0 = d0 < hd, v1 = d1 < hd;
+        float x0 = 0.f, x1 = 0.f;
+        if (isk) {
+            if (v0) rot(qd + h * hd + d0, x0, x1);
+        } else {
+            if (v0) x0 = ld(qd + kvd + h * hd + d0);
+            if (v1) x1 = ld(qd + kvd + h * hd + d1);
+        }
+        float amax = fmaxf(v0 ? fabsf(x0) : 0.f, v1 ? fabsf(x1) : 0.f);  // kv_cache_quant.h:75-78
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o));
+        const float scale = amax / 127.0f;                      // :80
+        const float inv = scale > 0.f ? 1.0f / scale : 0.0f;    // :82
+        auto qz = [&](float x) {                                // :88-91
+            return (int8_t)(int)fmaxf(-127.0f, fminf(127.0f, roundf(x * inv)));
+        };
+        int8_t* b = (isk ? kc : vc) + ((size_t)page * Hkv + h) * blk;
+        if (isk) {
+            if (v0) {
+                b[(size_t)off * hd + d0] = qz(x0);
+                b[(size_t)off * hd + d1] = qz(x1);
+            }
+        } else {  // dimension-major
+            if (v0) b[(size_t)d0 * page_size + off] = qz(x0);
+            if (v1) b[(size_t)d1 * page_size + off] = qz(x1);
+        }
+        if (lane == 0) *(float*)(b + (size_t)page_size * hd + 4 * off) = scale;
+    }
+}
+
 int launch_rope_append(const float* qkv, const float* bias, int n, int H, int Hkv, int hd, const int32_t* pos,
                        const float* rope, float* q_out, void* kc, void* vc, uint32_t kv_dtype,
                        const int32_t* page_table, int max_pages, int page_size, hipStream_t st, int S, size_t slice) {
     QH_REQUIRE(qkv && pos && rope && q_out && kc && vc && page_table && n > 0 && hd % 2 == 0 && S >= 1,
                QRAF_HIP_ERR_INVALID, "rope_append: bad arguments");
+    if (kv_dtype == DT_I8) {
+        QH_REQUIRE(hd <= 128 && hd % 4 == 0 && page_size % 4 == 0, QRAF_HIP_ERR_INVALID,
+                   "rope_append: int8 pages need head_dim <= 128 (multiple of 4) and page_size %% 4 == 0");
+        hipLaunchKernelGGL(rope_append_i8_kernel, dim3(n), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos, rope, q_out,
+                           (int8_t*)kc, (int8_t*)vc, page_table, max_pages, page_size, S, slice);
+        QH_CHECK_HIP(hipGetLastError());
+        return QRAF_HIP_OK;
+    }
     const size_t work = (size_t)n * ((H * hd + Hkv * hd) / 2 + Hkv * hd);
     const int grid = (int)std::min<size_t>((work + 255) / 256, 4096);
     if (kv_dtype == DT_F32)

@@ -12,7 +12,7 @@
 namespace qraf_hip {
 
 // QRAF dtype codes (reference include/core/types.h:27-39).
-constexpr uint32_t DT_F32 = 0, DT_F16 = 1, DT_Q8_0 = 10, DT_Q4_0 = 20;
+constexpr uint32_t DT_F32 = 0, DT_F16 = 1, DT_Q8_0 = 10, DT_Q4_0 = 20, DT_I8 = 102;  // types.h:27-38
 
 // Sets the calling thread's last-error string and returns `code`.
 int set_error(int code, const char* fmt, ...);

@@ -13,7 +13,9 @@
 // SiLU(gate) * up (attention.cpp:172-180) pairs neighbouring outputs.
 //
 // KV cache: a pool of pages per layer, [num_pages][Hkv][page_size][head_dim]
-// (f32 or f16); sequences own page lists handed out by a host-side free list.
+// (f32 or f16), or int8 blocks with a scale per position (the layout of the
+// attention kernels); sequences own page lists handed out by a host-side free
+// list.
 // Each step: embedding row, then per layer RMSNorm -> fused QKV projection
 // -> bias + RoPE + page append -> ragged paged attention -> O projection with
 // the residual add in its epilogue -> RMSNorm -> gate/up projection ->
@@ -446,8 +448,11 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
                "engine: hidden and intermediate sizes must be multiples of 32");
     qraf_engine_options o = opt ? *opt : qraf_engine_options{};
     if (!o.kv_dtype) o.kv_dtype = DT_F32;
-    if (o.kv_dtype != DT_F32 && o.kv_dtype != DT_F16) return set_error(QRAF_HIP_ERR_DTYPE, "engine: KV dtype %u", o.kv_dtype);
+    if (o.kv_dtype != DT_F32 && o.kv_dtype != DT_F16 && o.kv_dtype != DT_I8)
+        return set_error(QRAF_HIP_ERR_DTYPE, "engine: KV dtype %u", o.kv_dtype);
     if (!o.page_size) o.page_size = 16;
+    QH_REQUIRE(o.kv_dtype != DT_I8 || ((hd == 64 || hd == 128) && c.num_heads / kvh <= 16 && o.page_size % 4 == 0),
+               QRAF_HIP_ERR_INVALID, "engine: int8 KV pages need head_dim 64/128, group <= 16, page_size %% 4 == 0");
     if (!o.max_batch) o.max_batch = 1;
     QH_REQUIRE(o.max_batch <= 1024, QRAF_HIP_ERR_INVALID, "engine: max_batch %u > 1024", o.max_batch);
     QH_REQUIRE(o.page_size <= 256 && (256 % o.page_size) == 0, QRAF_HIP_ERR_INVALID,
@@ -476,8 +481,11 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     if (hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking) != hipSuccess)
         return fail(set_error(QRAF_HIP_ERR_HIP, "engine: stream creation failed"));
     const int B = (int)o.max_batch, D = (int)c.hidden_size, F = (int)c.intermediate_size, V = (int)c.vocab_size;
-    const size_t kv_elem = o.kv_dtype == DT_F16 ? 2 : 4;
-    e->layer_kv_bytes = (size_t)o.num_pages * kvh * o.page_size * hd * kv_elem;
+    // a (page, KV head) block: page_size positions x head_dim elements, and
+    // for int8 a f32 scale per position after them
+    const size_t kv_block = o.kv_dtype == DT_I8 ? (size_t)o.page_size * (hd + 4)
+                                                : (size_t)o.page_size * hd * (o.kv_dtype == DT_F16 ? 2 : 4);
+    e->layer_kv_bytes = (size_t)o.num_pages * kvh * kv_block;
     int rc = QRAF_HIP_OK;
 #define A(ptr, bytes)                                           \
     if ((rc = ealloc(e, (void**)&(ptr), (bytes))) != QRAF_HIP_OK) \

@@ -75,3 +75,28 @@ def test_attention_i8_close_to_fp32_on_dequantized_cache():
     # and within int8 rounding of the unquantized attention
     full = po.attention_decode(q, K.reshape(ctx, -1), V.reshape(ctx, -1), H, Hkv, hd)
     assert np.abs(got - full).max() < 0.05
+
+
+def test_model_with_int8_cache_stays_near_f32_cache():
+    """The oracle model with QuantizedKVCache in place of KVCache: position 0
+    attends to itself only, so its attention output is the dequantized V row
+    and its logits move by the V rounding alone; over a prompt the logits stay
+    within the int8 rounding of the f32 cache's (a dropped scale or a
+    transposed cache index would move them by O(1))."""
+    kw = dict(vocab=500, hidden=256, layers=2, heads=4, kv_heads=2, inter=512, max_seq=64, rope_theta=1e4,
+              eps=1e-5, wdtype=po.Q8_0)
+    a, b = po.Model(po.make_config(**kw), 5), po.Model(po.make_config(**kw), 5)
+    b.set_kv_int8()
+    toks = [po.lib().or_gen_token(5, i, kw["vocab"]) for i in range(12)]
+    worst = 0.0
+    for pos, t in enumerate(toks):
+        la, lb = a.forward(t, pos), b.forward(t, pos)
+        assert not np.array_equal(la, lb)
+        worst = max(worst, float(np.abs(la - lb).max() / np.abs(la).max()))
+    assert worst < 0.03, worst
+    b.reset()
+    lb0 = b.forward(toks[0], 0)
+    a.reset()
+    assert np.abs(a.forward(toks[0], 0) - lb0).max() / np.abs(lb0).max() < 0.03
+    a.close()
+    b.close()
