@@ -41,6 +41,7 @@ extern "C" {
 #define QRAF_DTYPE_F16 1u
 #define QRAF_DTYPE_Q8_0 10u
 #define QRAF_DTYPE_Q4_0 20u
+#define QRAF_DTYPE_I8 102u /* KV pages only: the QuantizedKVCache scheme, kv_cache_quant.h:61-128 */
 
 /* ------------------------------------------------------------ runtime */
 
@@ -145,6 +146,12 @@ uint64_t qraf_hip_attention_workspace_bytes(int32_t n_seqs, int32_t n_heads, int
  *   v_cache  F32: [num_pages][n_kv_heads][page_size][head_dim]
  *            F16: [num_pages][n_kv_heads][head_dim][page_size] (dimension-major
  *            in a page, the layout qraf_hip_rope_append_dev writes)
+ *   I8 (both caches): [num_pages][n_kv_heads] blocks of page_size*(head_dim+4)
+ *            bytes; K block = int8 [page_size][head_dim] then f32 scale
+ *            [page_size], V block = int8 [head_dim][page_size] then f32 scale
+ *            [page_size]; a score is (sum q_k[d]*query[d]) * k_scale * scale
+ *            (dot_with_key, kv_cache_quant.h:118-128), a value q_v[d]*v_scale
+ *            (dequant_value, :108-116)
  *   page_table [n_seqs][max_pages_per_seq] physical page of logical page j
  *   ctx_lens [n_seqs] positions attended (1 <= ctx <= max_ctx), on the device
  *   out      [n_seqs][n_heads][head_dim] f32
@@ -152,7 +159,8 @@ uint64_t qraf_hip_attention_workspace_bytes(int32_t n_seqs, int32_t n_heads, int
  * scale is 1/sqrt(head_dim) in the reference (attention.cpp:122).
  * head_dim 64 or 128 with n_heads / n_kv_heads in {1,2,3,4,6,8,12,16}, or
  * head_dim 16 or 32 with n_heads / n_kv_heads in {1,2,4,8}.  F16 pages with
- * head_dim 64/128 and page_size % 4 == 0 run on the matrix cores.  Page
+ * head_dim 64/128 and page_size % 4 == 0 run on the matrix cores; I8 pages
+ * need that shape (QRAF_HIP_ERR_INVALID otherwise) and always do.  Page
  * contents at positions >= ctx are never used (NaN there is harmless). */
 int qraf_hip_paged_attention_dev(const float* q, const void* k_cache, const void* v_cache, uint32_t kv_dtype,
                                  const int32_t* page_table, int32_t max_pages_per_seq, const int32_t* ctx_lens,
@@ -169,7 +177,9 @@ int qraf_hip_rope_table_host(int32_t max_pos, int32_t head_dim, float rope_theta
  * rows of the fused q|k|v projection, bias the matching F32 vector or NULL,
  * rope_table a device copy of the qraf_hip_rope_table_host table covering
  * every position; writes rotated q to q_out [n_seqs][H*hd] and rotated k, v at
- * positions[s] into the paged cache. */
+ * positions[s] into the paged cache.  I8 pages: k and v quantized per KV head
+ * as QuantizedKVCache::store (kv_cache_quant.h:61-95), bytes and scales
+ * bit-identical to it; head_dim <= 128, page_size % 4 == 0. */
 int qraf_hip_rope_append_dev(const float* qkv, const float* bias, int32_t n_seqs, int32_t n_heads,
                              int32_t n_kv_heads, int32_t head_dim, const int32_t* positions, const float* rope_table,
                              float* q_out, void* k_cache, void* v_cache, uint32_t kv_dtype, const int32_t* page_table,
@@ -232,7 +242,8 @@ typedef struct qraf_model_config {
     float rope_theta, rms_norm_eps;
 } qraf_model_config;
 
-/* Engine resources.  kv_dtype F32 (0, the reference's KVCache) or F16;
+/* Engine resources.  kv_dtype F32 (0, the reference's KVCache), F16, or I8
+ * (QuantizedKVCache; head_dim 64/128, page_size % 4 == 0);
  * page_size tokens per KV page (0 -> 16, must divide 256); max_batch rows
  * per step (0 -> 1, at most 1024); num_pages KV pages per layer (0 -> enough
  * for max_batch sequences of min(max_seq_len, 8192) positions). */
