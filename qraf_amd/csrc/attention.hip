@@ -316,6 +316,7 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     __shared__ __align__(16) _Float16 s_q[2][16][QS];
     __shared__ float s_qs[16];
     __shared__ float s_m[4][16], s_l[4][16];
+    __shared__ __align__(16) float s_kvs[2][4][64];  // int8: K, V scale of position pw + lane, per wave
     extern __shared__ float s_odyn[];  // [4][G][HD]: the waves' partial outputs
     float(*s_o)[HD] = (float(*)[HD])s_odyn;  // s_o[wave * G + head][dim]
 
@@ -331,104 +332,72 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     const int pw = chunk * ACH + 64 * wave;  // first position of this wave
     const bool active = pw < ctx;            // wave-uniform
 
-    // ---- page ids of every K row and V run this lane reads, requested first
-    // (clamped into the context, so every read is inside the page table)
+    // Every global read that does not depend on another is requested before
+    // the first wait: q of the G heads with the page ids; for int8 pages then
+    // (page ids known) the K rows, V runs and scales before q is staged, so
+    // the staging and its barrier overlap those loads.
+    constexpr int PER = HD / 64;
+    float qv[4][PER];  // q of head wave + 4j, dimensions lane + 64i
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int h = wave + 4 * j;
+#pragma unroll
+        for (int i = 0; i < PER; i++)
+            qv[j][i] = h < G ? a.q[((size_t)s * a.H + kvh * G + h) * HD + lane + 64 * i] : 0.f;
+    }
+
+    // ---- page ids of every K row and V run this lane reads (clamped into
+    // the context, so every read is inside the page table)
     int kpg[4], vpg[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) kpg[t] = ptab[min(pw + 16 * t + l16, ctx - 1) / ps];
     const int vlast = (ctx - 1) & ~3;
 #pragma unroll
     for (int j = 0; j < 4; j++) vpg[j] = ptab[min(pw + 16 * j + 4 * seg, vlast) / ps];
-    // int8: the K and V scales of the lane's 4-position runs pw + 16j + 4seg
-    // (j = 0..3, the positions of its scores and of its P operand)
+    // int8: lane l loads the K and V scales of position pw + l (clamped like
+    // its K row, whose page is kpg[l / 16]) and stores them to LDS before the
+    // staging barrier; a score's or probability's lane reads its 4-position
+    // run back as a float4.  (Not by shuffle: the compiler may move a shuffle
+    // whose result feeds a select into the branch of the select, where a
+    // source lane outside the branch reads as 0.)
     const size_t blk = (size_t)ps * (HD + 4);  // int8 bytes of one (page, KV head) block
-    float4 ksc[4], vsc[4];
+    float ks_own = 0.f, vs_own = 0.f;
     if (I8 && active) {
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int rp = min(pw + 16 * j + 4 * seg, vlast) % ps;
-            const size_t b = ((size_t)vpg[j] * a.Hkv + kvh) * blk + (size_t)ps * HD;
-            ksc[j] = *(const float4*)((const int8_t*)a.kc + b + 4 * rp);
-            vsc[j] = *(const float4*)((const int8_t*)a.vc + b + 4 * rp);
-        }
+        const int pg = seg == 0 ? kpg[0] : seg == 1 ? kpg[1] : seg == 2 ? kpg[2] : kpg[3];
+        const size_t b = ((size_t)pg * a.Hkv + kvh) * blk + (size_t)ps * HD + 4 * (min(pw + lane, ctx - 1) % ps);
+        ks_own = *(const float*)((const int8_t*)a.kc + b);
+        vs_own = *(const float*)((const int8_t*)a.vc + b);
     }
 
-    // ---- q of the G heads as fp16 hi + lo, scaled per head by 2^e so that
-    // max|q| lands in [2^14, 2^15): hi + lo then carries 22 bits of every
-    // element that matters at fp32 precision
-    for (int h = wave; h < 16; h += 4) {
-        constexpr int PER = HD / 64;
-        float v[PER];
-        float mx = 0.f;
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            v[i] = h < G ? a.q[((size_t)s * a.H + kvh * G + h) * HD + lane + 64 * i] : 0.f;
-            mx = fmaxf(mx, fabsf(v[i]));
-        }
-#pragma unroll
-        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-        float sigma = 1.f;
-        if (mx > 0.f && mx <= 3.0e38f) {
-            int e;
-            frexpf(mx, &e);
-            sigma = ldexpf(1.f, min(15 - e, 120));
-        }
-#pragma unroll
-        for (int i = 0; i < PER; i++) {
-            const float x = v[i] * sigma;
-            const _Float16 hi = (_Float16)x;
-            s_q[0][h][lane + 64 * i] = hi;
-            s_q[1][h][lane + 64 * i] = (_Float16)(x - (float)hi);
-        }
-        if (lane == 0) s_qs[h] = a.scale / sigma;  // attention.cpp:134: dot * scale
-    }
-    __syncthreads();
-
+    // ---- K rows of the wave's 4 score tiles: lane row pw + 16t + l16
+    // (clamped: past-ctx scores are masked later), the lane's 8*KK dimensions
     const _Float16* kc = (const _Float16*)a.kc;
     const _Float16* vc = (const _Float16*)a.vc;
-    // ---- scores of 4 tiles: sc[t][r] = position pw + 16t + 4seg + r, head l16
-    f32x4a sc[4];
-#pragma unroll
-    for (int t = 0; t < 4; t++) sc[t] = f32x4a{0.f, 0.f, 0.f, 0.f};
-    if (active) {
-        f16x8 qh[KK], ql[KK];
-#pragma unroll
-        for (int kk = 0; kk < KK; kk++) {
-            qh[kk] = *(const f16x8*)&s_q[0][l16][kdim(kk, seg)];
-            ql[kk] = *(const f16x8*)&s_q[1][l16][kdim(kk, seg)];
-        }
+    typedef typename std::conditional<I8, uint4[KK / 2], f16x8[KK]>::type KRow;
+    KRow kreg[4];
+    auto kload = [&]() {
 #pragma unroll
         for (int t = 0; t < 4; t++) {
-            const int pc = min(pw + 16 * t + l16, ctx - 1);  // clamped: past-ctx scores are masked below
-            f32x4a d = {0.f, 0.f, 0.f, 0.f};
+            const int pc = min(pw + 16 * t + l16, ctx - 1);
             if constexpr (I8) {
                 const int8_t* kr = (const int8_t*)a.kc + ((size_t)kpg[t] * a.Hkv + kvh) * blk +
                                    (size_t)(pc % ps) * HD + 8 * KK * seg;
-                uint4 kw[KK / 2];
 #pragma unroll
-                for (int i = 0; i < KK / 2; i++) kw[i] = *(const uint4*)(kr + 16 * i);
-#pragma unroll
-                for (int kk = 0; kk < KK; kk++) {
-                    const uint4 w = kw[kk / 2];
-                    const f16x8 kf = (kk & 1) ? i8x8_to_f16x8(w.z, w.w) : i8x8_to_f16x8(w.x, w.y);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[kk], d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[kk], d, 0, 0, 0);
-                }
+                for (int i = 0; i < KK / 2; i++) kreg[t][i] = *(const uint4*)(kr + 16 * i);
             } else {
                 const _Float16* kr = kc + (((size_t)kpg[t] * a.Hkv + kvh) * ps + pc % ps) * HD + 8 * seg;
 #pragma unroll
-                for (int kk = 0; kk < KK; kk++) {
-                    const f16x8 kf = *(const f16x8*)(kr + 32 * kk);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh[kk], d, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql[kk], d, 0, 0, 0);
-                }
+                for (int kk = 0; kk < KK; kk++) kreg[t][kk] = *(const f16x8*)(kr + 32 * kk);
             }
-            sc[t] = d;
         }
-    }
+    };
+    // int8 rows (half the registers) are requested here; fp16 ones after the
+    // staging barrier (holding them across it would spill)
+    if (I8 && active) kload();
 
-    // ---- V of the wave's 64 positions, requested before the softmax so its
-    // latency overlaps the score phase.  Per lane and 32-position step b: two
+    // ---- V of the wave's 64 positions: int8 runs are requested here, with
+    // the K rows; fp16 ones (twice the registers) after the score tiles,
+    // still before the softmax.  Per lane and 32-position step b: two
     // 4-position runs (b*32 + 4seg and +16) per 16-dimension tile, clamped
     // into the context (fp16 values past it are masked; int8 ones are finite
     // and meet a zero probability), 4-aligned so a run never leaves a page.
@@ -455,7 +424,71 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
             }
         }
     };
-    if (active) {
+    if (I8 && active) {
+        vload(0, va0, vb0);
+        vload(1, va1, vb1);
+    }
+
+    if (I8) {
+        s_kvs[0][wave][lane] = ks_own;
+        s_kvs[1][wave][lane] = vs_own;
+    }
+
+    // ---- q of the G heads as fp16 hi + lo, scaled per head by 2^e so that
+    // max|q| lands in [2^14, 2^15): hi + lo then carries 22 bits of every
+    // element that matters at fp32 precision
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int h = wave + 4 * j;
+        float* v = qv[j];
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < PER; i++) mx = fmaxf(mx, fabsf(v[i]));
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        float sigma = 1.f;
+        if (mx > 0.f && mx <= 3.0e38f) {
+            int e;
+            frexpf(mx, &e);
+            sigma = ldexpf(1.f, min(15 - e, 120));
+        }
+#pragma unroll
+        for (int i = 0; i < PER; i++) {
+            const float x = v[i] * sigma;
+            const _Float16 hi = (_Float16)x;
+            s_q[0][h][lane + 64 * i] = hi;
+            s_q[1][h][lane + 64 * i] = (_Float16)(x - (float)hi);
+        }
+        if (lane == 0) s_qs[h] = a.scale / sigma;  // attention.cpp:134: dot * scale
+    }
+    __syncthreads();
+
+    // ---- scores of 4 tiles: sc[t][r] = position pw + 16t + 4seg + r, head l16
+    f32x4a sc[4];
+#pragma unroll
+    for (int t = 0; t < 4; t++) sc[t] = f32x4a{0.f, 0.f, 0.f, 0.f};
+    if (active) {  // k-step outer: one step's q fragments live at a time
+        if (!I8) kload();
+#pragma unroll
+        for (int kk = 0; kk < KK; kk++) {
+            const f16x8 qh = *(const f16x8*)&s_q[0][l16][kdim(kk, seg)];
+            const f16x8 ql = *(const f16x8*)&s_q[1][l16][kdim(kk, seg)];
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                f16x8 kf;
+                if constexpr (I8) {
+                    const uint4 w = kreg[t][kk / 2];
+                    kf = (kk & 1) ? i8x8_to_f16x8(w.z, w.w) : i8x8_to_f16x8(w.x, w.y);
+                } else {
+                    kf = kreg[t][kk];
+                }
+                sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh, sc[t], 0, 0, 0);
+                sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql, sc[t], 0, 0, 0);
+            }
+        }
+    }
+
+    if (!I8 && active) {  // fp16: after the score tiles (their K registers are free again)
         vload(0, va0, vb0);
         vload(1, va1, vb1);
     }
@@ -464,14 +497,17 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     const float qs = s_qs[l16];
     float mloc = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 4; t++)
+    for (int t = 0; t < 4; t++) {
+        const float4 ks4 = I8 ? *(const float4*)&s_kvs[0][wave][16 * t + 4 * seg] : float4{};
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             const bool ok = active && pw + 16 * t + 4 * seg + r < ctx;
-            if constexpr (I8) sc[t][r] = ok ? (sc[t][r] * ksc[t][r]) * qs : -INFINITY;  // kv_cache_quant.h:127
+            const float ks = r == 0 ? ks4.x : r == 1 ? ks4.y : r == 2 ? ks4.z : ks4.w;
+            if constexpr (I8) sc[t][r] = ok ? (sc[t][r] * ks) * qs : -INFINITY;  // kv_cache_quant.h:127
             else sc[t][r] = ok ? sc[t][r] * qs : -INFINITY;
             mloc = fmaxf(mloc, sc[t][r]);
         }
+    }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
     if (seg == 0) s_m[wave][l16] = mloc;
@@ -496,14 +532,10 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     // loses bits to fp16 underflow; the output is multiplied back by 2^e
     float ounit = 1.f;
     if constexpr (I8) {
-        float vm = 0.f;
+        // lane l holds position pw + l's scale: the wave maximum over valid positions
+        float vm = active && pw + lane < ctx ? fmaxf(0.f, vs_own) : 0.f;
 #pragma unroll
-        for (int t = 0; t < 4; t++)
-#pragma unroll
-            for (int r = 0; r < 4; r++)
-                vm = active && pw + 16 * t + 4 * seg + r < ctx ? fmaxf(vm, vsc[t][r]) : vm;
-        vm = fmaxf(vm, __shfl_xor(vm, 16));
-        vm = fmaxf(vm, __shfl_xor(vm, 32));
+        for (int o = 32; o >= 1; o >>= 1) vm = fmaxf(vm, __shfl_xor(vm, o));
         float cw = 1.f;
         if (vm > 0.f && vm <= 3.0e38f) {
             int e;
@@ -513,12 +545,15 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
             ounit = ldexpf(1.f, e);
         }
 #pragma unroll
-        for (int t = 0; t < 4; t++)
+        for (int t = 0; t < 4; t++) {
+            const float4 vs4 = *(const float4*)&s_kvs[1][wave][16 * t + 4 * seg];
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const bool ok = active && pw + 16 * t + 4 * seg + r < ctx;
-                sc[t][r] = ok ? sc[t][r] * (vsc[t][r] * cw) : 0.f;
+                const float vs = r == 0 ? vs4.x : r == 1 ? vs4.y : r == 2 ? vs4.z : vs4.w;
+                sc[t][r] = ok ? sc[t][r] * (vs * cw) : 0.f;
             }
+        }
     }
 
     // ---- P.V over the wave's 64 positions (two 32-position MFMA steps)
