@@ -293,13 +293,22 @@ def bench_attention(args, rt):
     ws = DeviceBuffer(wsb)
     ws.zero()
 
+    def timed(kv, K, V):
+        return graph_time_us(rt, lambda i: call("qraf_hip_paged_attention_dev", q.ptr, K.ptr, V.ptr, kv, dt_.ptr,
+                                                max_pages, dc.ptr, n, H, Hkv, hd, ps, np.float32(1 / math.sqrt(hd)),
+                                                max_ctx, out.ptr, ws.ptr, wsb, stream.h), 50)
+
     def leg(kv, K, V, pos_bytes):
-        us = graph_time_us(rt, lambda i: call("qraf_hip_paged_attention_dev", q.ptr, K.ptr, V.ptr, kv, dt_.ptr,
-                                              max_pages, dc.ptr, n, H, Hkv, hd, ps, np.float32(1 / math.sqrt(hd)),
-                                              max_ctx, out.ptr, ws.ptr, wsb, stream.h), 50)
+        us = timed(kv, K, V)  # balanced split (the default form)
+        call("qraf_hip_set_attention_tuning", 1)
+        try:
+            us_chunk = timed(kv, K, V)  # one workgroup per (sequence, 256-position chunk)
+        finally:
+            call("qraf_hip_set_attention_tuning", 0)
         by = int(ctxs.sum()) * Hkv * pos_bytes * 2 + 2 * n * H * hd * 4
         return {"us": round(us, 2), "sum_ctx": int(ctxs.sum()), "alg_bytes": by,
-                "GB_s": round(by / (us * 1e-6) / 1e9, 1), "frac_hbm_peak": round(by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)}
+                "GB_s": round(by / (us * 1e-6) / 1e9, 1), "frac_hbm_peak": round(by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "us_chunk_grid_form": round(us_chunk, 2)}
 
     # fp16 pages, N(0,1)
     kv_half = num_pages * Hkv * ps * hd

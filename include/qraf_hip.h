@@ -134,8 +134,9 @@ uint64_t qraf_hip_name_hash(const char* name);
 
 /* ------------------------------------------- ragged paged decode attention */
 
-/* Workspace bytes for qraf_hip_paged_attention_dev (chunk partials of long
- * contexts); no initialisation needed.  Calls sharing one must not overlap. */
+/* Workspace bytes for qraf_hip_paged_attention_dev (partials of contexts
+ * split across workgroups); no initialisation needed.  Calls sharing one
+ * must not overlap. */
 uint64_t qraf_hip_attention_workspace_bytes(int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads,
                                             int32_t head_dim, int32_t max_ctx);
 /* The score / softmax / weighted-sum loops of attention_forward
@@ -159,9 +160,15 @@ uint64_t qraf_hip_attention_workspace_bytes(int32_t n_seqs, int32_t n_heads, int
  * scale is 1/sqrt(head_dim) in the reference (attention.cpp:122).
  * head_dim 64 or 128 with n_heads / n_kv_heads in {1,2,3,4,6,8,12,16}, or
  * head_dim 16 or 32 with n_heads / n_kv_heads in {1,2,4,8}.  F16 pages with
- * head_dim 64/128 and page_size % 4 == 0 run on the matrix cores; I8 pages
- * need that shape (QRAF_HIP_ERR_INVALID otherwise) and always do.  Page
+ * head_dim 64/128, at most 16 query heads per KV head and a power-of-two
+ * page_size >= 4 run on the matrix cores; I8 pages need that shape
+ * (QRAF_HIP_ERR_INVALID otherwise) and always do.  Page
  * contents at positions >= ctx are never used (NaN there is harmless). */
+/* Work decomposition of the matrix-core attention (fp16 / int8 pages,
+ * process-wide): 0 = balanced split of the batch's 64-position tiles over
+ * the workgroups (default), 1 = one workgroup per (sequence, 256-position
+ * chunk).  Results agree within the attention tolerance, not bit for bit. */
+int qraf_hip_set_attention_tuning(int32_t form);
 int qraf_hip_paged_attention_dev(const float* q, const void* k_cache, const void* v_cache, uint32_t kv_dtype,
                                  const int32_t* page_table, int32_t max_pages_per_seq, const int32_t* ctx_lens,
                                  int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
@@ -179,7 +186,8 @@ int qraf_hip_rope_table_host(int32_t max_pos, int32_t head_dim, float rope_theta
  * every position; writes rotated q to q_out [n_seqs][H*hd] and rotated k, v at
  * positions[s] into the paged cache.  I8 pages: k and v quantized per KV head
  * as QuantizedKVCache::store (kv_cache_quant.h:61-95), bytes and scales
- * bit-identical to it; head_dim <= 128, page_size % 4 == 0. */
+ * bit-identical to it; head_dim <= 128, page_size % 4 == 0 (attention on
+ * them also needs a power of two). */
 int qraf_hip_rope_append_dev(const float* qkv, const float* bias, int32_t n_seqs, int32_t n_heads,
                              int32_t n_kv_heads, int32_t head_dim, const int32_t* positions, const float* rope_table,
                              float* q_out, void* k_cache, void* v_cache, uint32_t kv_dtype, const int32_t* page_table,

@@ -15,32 +15,38 @@
 // dimension-major so that the matrix-core kernel's V operand (consecutive
 // positions of one dimension) is a contiguous load.
 //
-// Work decomposition: the context of every sequence is cut into chunks of
-// CH = 256 positions; one workgroup handles one (sequence, chunk) item for
-// one KV head and all H/Hkv query heads that share it (GQA).  The grid has
-// ceil(max_ctx / CH) items per sequence (item = s * that + chunk); a
-// workgroup whose chunk starts at or past its sequence's device-resident
+// Work decomposition, chunk grid: the context of every sequence is cut into
+// chunks of CH = 256 positions; one workgroup handles one (sequence, chunk)
+// item for one KV head and all H/Hkv query heads that share it (GQA).  The
+// grid has ceil(max_ctx / CH) items per sequence (item = s * that + chunk);
+// a workgroup whose chunk starts at or past its sequence's device-resident
 // context length exits at once, so the lengths can change on the device
 // between launches with no host round trip.  Sequences with several chunks
 // write (max, sum, unnormalised output) partials, which attn_merge_kernel (a
-// second launch, one workgroup per sequence and KV head) combines in chunk
-// order.
+// second launch, one wave per sequence and query head) combines in chunk
+// order.  Balanced split (the default for the matrix-core kernels, described
+// at attn_split_kernel): the batch's 64-position tiles are divided into
+// equal shares, one per resident workgroup, computed on the device from the
+// same device-resident lengths; a sequence split across shares is merged in
+// share order.
 //
 // int8 pages hold the scheme of QuantizedKVCache (kv_cache_quant.h:61-128):
 // per (position, KV head) scale = absmax / 127 and q = clamp(round(x / scale),
 // +-127); a score is (sum_d q_k[d] * query[d]) * k_scale * 1/sqrt(hd) and a
 // value element q_v[d] * v_scale.
 //
-// Two kernels share this decomposition.  attn_mfma_kernel (fp16 or int8
-// pages, head_dim 64 or 128, up to 16 query heads per KV head) runs q.K^T and
-// P.V on v_mfma_f32_16x16x32_f16: K and V enter as stored (fp16, or int8
-// widened to fp16, both exact), q and the probabilities as fp16 hi + lo pairs
-// (q scaled per head by a power of two so hi + lo carries 22 bits of it),
-// products accumulate in fp32.  int8 scales are applied in fp32: a K scale
-// to each position's score, a V scale folded into that position's
-// probability before the P.V product.
-// attn_decode_kernel (the rest) is plain fp32 VALU code: scores with
-// thread = position, output with thread = (head, dimension).
+// The matrix-core kernels, attn_mfma_kernel (chunk grid) and
+// attn_split_kernel (balanced split), take fp16 or int8 pages, head_dim 64
+// or 128, up to 16 query heads per KV head and a power-of-two page_size
+// (pages addressed by shifts).  They run q.K^T and P.V on
+// v_mfma_f32_16x16x32_f16: K and V enter as stored (fp16, or int8 widened to
+// fp16, both exact), q and the probabilities as fp16 hi + lo pairs (q scaled
+// per head by a power of two so hi + lo carries 22 bits of it), products
+// accumulate in fp32.  int8 scales are applied in fp32: a K scale to each
+// position's score, a V scale folded into that position's probability
+// before the P.V product.  attn_decode_kernel (the rest) is plain fp32 VALU
+// code on the chunk grid: scores with thread = position, output with
+// thread = (head, dimension).
 #include <math.h>
 
 #include <algorithm>
@@ -81,8 +87,11 @@ struct AttnArgs {
     float* part_o;             // [items][H][HD]   (multi-chunk partials)
     float* part_ml;            // [items][H][2]
     uint32_t* counters;        // [n][Hkv]          (reserved)
+    int32_t* pref;             // [n + 1] tile prefix of the split kernel, for its merge
     int n, H, Hkv, page_size, max_pages, max_ctx;
     float scale;
+    int gx;                    // split kernel: workgroups per KV head
+    int ps_log2;               // matrix-core kernels: page_size = 1 << ps_log2
 };
 
 // final output element: f32, or split into the bf16 planes a GEMM consumes
@@ -327,7 +336,7 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     int s, chunk, nchunks;
     int ctx;
     if (!attn_item(a, s, chunk, nchunks, ctx)) return;
-    const int ps = a.page_size;
+    const int ps = a.page_size, psl = a.ps_log2, psm = ps - 1;  // page_size is a power of two here
     const int32_t* ptab = a.page_table + (size_t)s * a.max_pages;
     const int pw = chunk * ACH + 64 * wave;  // first position of this wave
     const bool active = pw < ctx;            // wave-uniform
@@ -350,10 +359,10 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     // the context, so every read is inside the page table)
     int kpg[4], vpg[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) kpg[t] = ptab[min(pw + 16 * t + l16, ctx - 1) / ps];
+    for (int t = 0; t < 4; t++) kpg[t] = ptab[min(pw + 16 * t + l16, ctx - 1) >> psl];
     const int vlast = (ctx - 1) & ~3;
 #pragma unroll
-    for (int j = 0; j < 4; j++) vpg[j] = ptab[min(pw + 16 * j + 4 * seg, vlast) / ps];
+    for (int j = 0; j < 4; j++) vpg[j] = ptab[min(pw + 16 * j + 4 * seg, vlast) >> psl];
     // int8: lane l loads the K and V scales of position pw + l (clamped like
     // its K row, whose page is kpg[l / 16]) and stores them to LDS before the
     // staging barrier; a score's or probability's lane reads its 4-position
@@ -364,7 +373,7 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     float ks_own = 0.f, vs_own = 0.f;
     if (I8 && active) {
         const int pg = seg == 0 ? kpg[0] : seg == 1 ? kpg[1] : seg == 2 ? kpg[2] : kpg[3];
-        const size_t b = ((size_t)pg * a.Hkv + kvh) * blk + (size_t)ps * HD + 4 * (min(pw + lane, ctx - 1) % ps);
+        const size_t b = ((size_t)pg * a.Hkv + kvh) * blk + (size_t)ps * HD + 4 * (min(pw + lane, ctx - 1) & psm);
         ks_own = *(const float*)((const int8_t*)a.kc + b);
         vs_own = *(const float*)((const int8_t*)a.vc + b);
     }
@@ -381,11 +390,11 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
             const int pc = min(pw + 16 * t + l16, ctx - 1);
             if constexpr (I8) {
                 const int8_t* kr = (const int8_t*)a.kc + ((size_t)kpg[t] * a.Hkv + kvh) * blk +
-                                   (size_t)(pc % ps) * HD + 8 * KK * seg;
+                                   (size_t)(pc & psm) * HD + 8 * KK * seg;
 #pragma unroll
                 for (int i = 0; i < KK / 2; i++) kreg[t][i] = *(const uint4*)(kr + 16 * i);
             } else {
-                const _Float16* kr = kc + (((size_t)kpg[t] * a.Hkv + kvh) * ps + pc % ps) * HD + 8 * seg;
+                const _Float16* kr = kc + (((size_t)kpg[t] * a.Hkv + kvh) * ps + (pc & psm)) * HD + 8 * seg;
 #pragma unroll
                 for (int kk = 0; kk < KK; kk++) kreg[t][kk] = *(const f16x8*)(kr + 32 * kk);
             }
@@ -405,8 +414,8 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     auto vload = [&](int b, VRun (&ra)[DT], VRun (&rb)[DT]) {
         const int pac = min(pw + 32 * b + 4 * seg, vlast), pbc = min(pw + 32 * b + 16 + 4 * seg, vlast);
         if constexpr (I8) {
-            const int8_t* va = (const int8_t*)a.vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * blk + pac % ps;
-            const int8_t* vb = (const int8_t*)a.vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * blk + pbc % ps;
+            const int8_t* va = (const int8_t*)a.vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * blk + (pac & psm);
+            const int8_t* vb = (const int8_t*)a.vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * blk + (pbc & psm);
 #pragma unroll
             for (int d = 0; d < DT; d++) {
                 const int dim = 16 * d + l16;
@@ -414,8 +423,8 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
                 rb[d] = *(const uint32_t*)(vb + (size_t)dim * ps);
             }
         } else {
-            const _Float16* va = vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * HD * ps + pac % ps;
-            const _Float16* vb = vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * HD * ps + pbc % ps;
+            const _Float16* va = vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * HD * ps + (pac & psm);
+            const _Float16* vb = vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * HD * ps + (pbc & psm);
 #pragma unroll
             for (int d = 0; d < DT; d++) {
                 const int dim = 16 * d + l16;
@@ -619,20 +628,463 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Balanced split of the whole batch (the default for fp16 and int8 pages).
+// The batch's contexts are cut into 64-position tiles; tiles of sequence s
+// are numbered pref[s] .. pref[s+1]-1 (pref = exclusive prefix of the tile
+// counts, computed by every workgroup from the device-resident context
+// lengths).  Workgroup w of the gx per KV head takes tiles
+// [w*T/g, (w+1)*T/g), T = pref[n], g = min(gx, T): equal non-empty shares
+// of the batch, all resident at once, whatever the lengths.  A share spans one or more
+// sequences; for each sequence segment in it, the 4 waves take its tiles in
+// turn (wave v: tiles a+v, a+v+4, ...), each keeping an online softmax
+// (running max and sum per head, output rows in LDS rescaled per tile), and
+// the 4 wave states are combined at the segment's end.  A segment that is
+// the whole sequence writes the output; otherwise it writes a partial
+// (max, sum, output) to slot w + s (unique: along the staircase of
+// (workgroup, sequence) pairs w + s increases), and attn_merge_kernel<HD,
+// true> combines sequence s's slots in workgroup order, i.e. position order.
+// Per tile the matrix-core arithmetic is the chunk kernel's above.
+// ---------------------------------------------------------------------------
+constexpr int SPLIT_MAXN = 1024;   // sequences per launch (the batch bound)
+// resident workgroups aimed at: 256 CUs x 4 (head_dim 64) or 3 (head_dim
+// 128, whose 148-168 registers per lane leave room for 3)
+constexpr int split_slots(int hd) { return 256 * (hd == 128 ? 3 : 4); }
+
+template <int HD, bool I8>
+__global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(AttnArgs a, int G) {
+    static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    constexpr int KK = HD / 32, DT = HD / 16, QS = HD + 8, PER = HD / 64;
+    auto kdim = [](int kk, int sg) { return I8 ? 8 * (KK * sg + kk) : 8 * (4 * kk + sg); };
+    typedef typename std::conditional<I8, uint32_t, uint2>::type VRun;
+    typedef typename std::conditional<I8, uint4[KK / 2], f16x8[KK]>::type KRow;
+    __shared__ __align__(16) _Float16 s_q[2][16][QS];
+    __shared__ float s_qs[16];
+    __shared__ float s_m[4][16], s_l[4][16], s_alpha[4][16];
+    __shared__ __align__(16) float s_kvs[2][4][64];
+    __shared__ int s_pref[SPLIT_MAXN + 1];
+    __shared__ int s_tsum[64];
+    extern __shared__ float s_odyn[];
+    float(*s_o)[HD] = (float(*)[HD])s_odyn;  // s_o[wave * G + head][dim]: running outputs
+
+    const int tid = threadIdx.x;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    // lane indices are re-derived per tile (see the tile loop)
+    int lane = tid & 63, l16 = lane & 15, seg = lane >> 4;
+    const int kvh = blockIdx.y, w = blockIdx.x, n = a.n, ps = a.page_size, psl = a.ps_log2, psm = ps - 1;
+
+    // ---- tile counts and their exclusive prefix (n <= 1024): wave 0 lane l
+    // sums entries 16l .. 16l+15, then adds the sums of lanes 0 .. l-1 (64
+    // broadcast LDS reads) and writes its entries' prefixes.  Workgroup
+    // barriers between the phases: a value one lane writes to LDS and another
+    // reads needs one (without it the compiler may forward a lane's own
+    // earlier store to its load).
+    for (int i = tid; i < n; i += ACH) s_pref[i] = (min(a.ctx[i], a.max_ctx) + 63) >> 6;
+    __syncthreads();
+    int loc[16];
+    if (wave == 0) {
+        int sum = 0;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int idx = 16 * lane + k;
+            loc[k] = idx < n ? s_pref[idx] : 0;
+            sum += loc[k];
+        }
+        s_tsum[lane] = sum;
+    }
+    __syncthreads();
+    if (wave == 0) {
+        int run = 0, total = 0;
+#pragma unroll 16
+        for (int i = 0; i < 64; i++) {
+            const int v = s_tsum[i];
+            run += i < lane ? v : 0;
+            total += v;
+        }
+        if (lane == 0) s_pref[n] = total;
+#pragma unroll
+        for (int k = 0; k < 16; k++) {
+            const int idx = 16 * lane + k;
+            if (idx < n) s_pref[idx] = run;
+            run += loc[k];
+        }
+    }
+    __syncthreads();
+    if (w == 0 && kvh == 0)
+        for (int i = tid; i <= n; i += ACH) a.pref[i] = s_pref[i];
+    // g = min(workgroups, tiles) shares, each non-empty (floor((w+1)T/g) -
+    // floor(wT/g) >= 1 for g <= T); workgroups past g have no share
+    const int T = s_pref[n];
+    const int g = min((int)gridDim.x, T);
+    if (w >= g) return;
+    const int t0 = (int)(((long long)w * T) / g), t1 = (int)(((long long)(w + 1) * T) / g);
+    // first sequence of the share: the last s with pref[s] <= t0
+    int s = 0;
+    {
+        int lo = 0, hi = n - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (s_pref[mid] <= t0) lo = mid;
+            else hi = mid - 1;
+        }
+        s = __builtin_amdgcn_readfirstlane(lo);
+    }
+
+    for (; s < n; s++) {
+        const int p0 = s_pref[s], p1 = s_pref[s + 1];
+        if (p0 >= t1) break;
+        const int ja = max(t0, p0) - p0, jb = min(t1, p1) - p0;  // the segment: tiles [ja, jb) of s
+        const bool whole = ja == 0 && jb == p1 - p0;
+        const int ctx = min(a.ctx[s], a.max_ctx);
+        const int32_t* ptab = a.page_table + (size_t)s * a.max_pages;
+        const int vlast = (ctx - 1) & ~3;
+        const size_t blk = (size_t)ps * (HD + 4);
+        const _Float16* kc = (const _Float16*)a.kc;
+        const _Float16* vc = (const _Float16*)a.vc;
+
+        // ---- per-tile loads (tile j: positions 64j .. 64j+63 of s)
+        // page ids: kpg/vpg of the tile being loaded; int8 also keeps the
+        // ids of the tile after it (kpg2/vpg2), requested a tile earlier
+        int kpg[4], vpg[4], kpg2[4], vpg2[4];
+        auto ids_to = [&](int j, int (&kp)[4], int (&vp)[4]) {
+            const int pw = 64 * j;
+#pragma unroll
+            for (int t = 0; t < 4; t++) kp[t] = ptab[min(pw + 16 * t + l16, ctx - 1) >> psl];
+#pragma unroll
+            for (int t = 0; t < 4; t++) vp[t] = ptab[min(pw + 16 * t + 4 * seg, vlast) >> psl];
+        };
+        auto ids = [&](int j) { ids_to(j, kpg, vpg); };
+        KRow kreg[4];
+        auto kload = [&](int j) {
+            const int pw = 64 * j;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const int pc = min(pw + 16 * t + l16, ctx - 1);
+                if constexpr (I8) {
+                    const int8_t* kr = (const int8_t*)a.kc + ((size_t)kpg[t] * a.Hkv + kvh) * blk +
+                                       ((pc & psm) * HD + 8 * KK * seg);
+#pragma unroll
+                    for (int i = 0; i < KK / 2; i++) kreg[t][i] = *(const uint4*)(kr + 16 * i);
+                } else {
+                    const _Float16* kr = kc + ((size_t)kpg[t] * a.Hkv + kvh) * ps * HD + ((pc & psm) * HD + 8 * seg);
+#pragma unroll
+                    for (int kk = 0; kk < KK; kk++) kreg[t][kk] = *(const f16x8*)(kr + 32 * kk);
+                }
+            }
+        };
+        VRun va0[DT], vb0[DT], va1[DT], vb1[DT];
+        auto vload = [&](int j, int b, VRun (&ra)[DT], VRun (&rb)[DT]) {
+            const int pw = 64 * j;
+            const int pac = min(pw + 32 * b + 4 * seg, vlast), pbc = min(pw + 32 * b + 16 + 4 * seg, vlast);
+            if constexpr (I8) {
+                const int8_t* va = (const int8_t*)a.vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * blk + (pac & psm);
+                const int8_t* vb = (const int8_t*)a.vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * blk + (pbc & psm);
+#pragma unroll
+                for (int d = 0; d < DT; d++) {
+                    const int off = (16 * d + l16) * ps;  // in-block offsets stay 32-bit
+                    ra[d] = *(const uint32_t*)(va + off);
+                    rb[d] = *(const uint32_t*)(vb + off);
+                }
+            } else {
+                const _Float16* va = vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * HD * ps + (pac & psm);
+                const _Float16* vb = vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * HD * ps + (pbc & psm);
+#pragma unroll
+                for (int d = 0; d < DT; d++) {
+                    const int off = (16 * d + l16) * ps;
+                    ra[d] = *(const uint2*)(va + off);
+                    rb[d] = *(const uint2*)(vb + off);
+                }
+            }
+        };
+        // int8 scales of position 64j + lane (page kpg[lane / 16]), stored to
+        // LDS at the top of the tile's iteration and read back per 4-position run
+        float ks_own = 0.f, vs_own = 0.f;
+        auto sload = [&](int j) {
+            const int pg = seg == 0 ? kpg[0] : seg == 1 ? kpg[1] : seg == 2 ? kpg[2] : kpg[3];
+            const size_t b = ((size_t)pg * a.Hkv + kvh) * blk + (ps * HD + 4 * (min(64 * j + lane, ctx - 1) & psm));
+            ks_own = *(const float*)((const int8_t*)a.kc + b);
+            vs_own = *(const float*)((const int8_t*)a.vc + b);
+        };
+
+        // ---- q of the G heads (requested first), the wave's first tile's
+        // page ids (and int8 K rows and V runs), then q staged as in the
+        // chunk kernel
+        float qv[4][PER];
+#pragma unroll
+        for (int jh = 0; jh < 4; jh++) {
+            const int h = wave + 4 * jh;
+#pragma unroll
+            for (int i = 0; i < PER; i++)
+                qv[jh][i] = h < G ? a.q[((size_t)s * a.H + kvh * G + h) * HD + lane + 64 * i] : 0.f;
+        }
+        int j = ja + wave;
+        if (j < jb) {
+            ids(j);
+            if (I8) {
+                sload(j);
+                kload(j);
+                vload(j, 0, va0, vb0);
+                vload(j, 1, va1, vb1);
+                if (j + 4 < jb) ids_to(j + 4, kpg2, vpg2);
+            }
+        }
+#pragma unroll
+        for (int jh = 0; jh < 4; jh++) {
+            const int h = wave + 4 * jh;
+            float mx = 0.f;
+#pragma unroll
+            for (int i = 0; i < PER; i++) mx = fmaxf(mx, fabsf(qv[jh][i]));
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+            float sigma = 1.f;
+            if (mx > 0.f && mx <= 3.0e38f) {
+                int e;
+                frexpf(mx, &e);
+                sigma = ldexpf(1.f, min(15 - e, 120));
+            }
+#pragma unroll
+            for (int i = 0; i < PER; i++) {
+                const float x = qv[jh][i] * sigma;
+                const _Float16 hi = (_Float16)x;
+                s_q[0][h][lane + 64 * i] = hi;
+                s_q[1][h][lane + 64 * i] = (_Float16)(x - (float)hi);
+            }
+            if (lane == 0) s_qs[h] = a.scale / sigma;  // attention.cpp:134: dot * scale
+        }
+        __syncthreads();
+        const float qs = s_qs[l16];
+
+        // ---- the wave's tiles, online softmax per head (lane: head l16)
+        float m_run = -INFINITY, l_run = 0.f;
+        bool first = true;
+        for (; j < jb; j += 4) {
+            // opaque to the compiler: every lane-derived address below is
+            // recomputed per tile instead of being hoisted out of the loops
+            // and held (spilled) across them
+            asm volatile("" : "+v"(lane));
+            l16 = lane & 15;
+            seg = lane >> 4;
+            const int pw = 64 * j;
+            if (I8) {
+                s_kvs[0][wave][lane] = ks_own;
+                s_kvs[1][wave][lane] = vs_own;
+            }
+            if (!I8) kload(j);
+            f32x4a sc[4];
+#pragma unroll
+            for (int t = 0; t < 4; t++) sc[t] = f32x4a{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int kk = 0; kk < KK; kk++) {
+                const f16x8 qh = *(const f16x8*)&s_q[0][l16][kdim(kk, seg)];
+                const f16x8 ql = *(const f16x8*)&s_q[1][l16][kdim(kk, seg)];
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    f16x8 kf;
+                    if constexpr (I8) {
+                        const uint4 wv = kreg[t][kk / 2];
+                        kf = (kk & 1) ? i8x8_to_f16x8(wv.z, wv.w) : i8x8_to_f16x8(wv.x, wv.y);
+                    } else {
+                        kf = kreg[t][kk];
+                    }
+                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qh, sc[t], 0, 0, 0);
+                    sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql, sc[t], 0, 0, 0);
+                }
+            }
+            if (!I8) {  // fp16: V after the score tiles (K's registers are free again)
+                vload(j, 0, va0, vb0);
+                vload(j, 1, va1, vb1);
+            }
+            // scores (int8: times each position's K scale), tile max per head
+            float mt = -INFINITY;
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const float4 ks4 = I8 ? *(const float4*)&s_kvs[0][wave][16 * t + 4 * seg] : float4{};
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const bool ok = pw + 16 * t + 4 * seg + r < ctx;
+                    const float ks = r == 0 ? ks4.x : r == 1 ? ks4.y : r == 2 ? ks4.z : ks4.w;
+                    if constexpr (I8) sc[t][r] = ok ? (sc[t][r] * ks) * qs : -INFINITY;  // kv_cache_quant.h:127
+                    else sc[t][r] = ok ? sc[t][r] * qs : -INFINITY;
+                    mt = fmaxf(mt, sc[t][r]);
+                }
+            }
+            mt = fmaxf(mt, __shfl_xor(mt, 16));
+            mt = fmaxf(mt, __shfl_xor(mt, 32));
+            const float m_new = fmaxf(m_run, mt);  // finite: a tile holds a position < ctx
+            const float alpha = first ? 0.f : __expf(m_run - m_new);
+            float lsum = 0.f;
+#pragma unroll
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float p = sc[t][r] == -INFINITY ? 0.f : __expf(sc[t][r] - m_new);
+                    sc[t][r] = p;
+                    lsum += p;
+                }
+            lsum += __shfl_xor(lsum, 16);
+            lsum += __shfl_xor(lsum, 32);
+            l_run = l_run * alpha + lsum;
+            m_run = m_new;
+            if (seg == 0) s_alpha[wave][l16] = alpha;
+
+            // int8: fold each position's V scale (times a per-tile power of
+            // two 2^-e) into its probability; the tile's output is scaled by 2^e
+            float ounit = 1.f;
+            if constexpr (I8) {
+                float vm = pw + lane < ctx ? fmaxf(0.f, s_kvs[1][wave][lane]) : 0.f;
+#pragma unroll
+                for (int o = 32; o >= 1; o >>= 1) vm = fmaxf(vm, __shfl_xor(vm, o));
+                float cw = 1.f;
+                if (vm > 0.f && vm <= 3.0e38f) {
+                    int e;
+                    frexpf(vm, &e);
+                    e = max(-120, min(e, 120));
+                    cw = ldexpf(1.f, -e);
+                    ounit = ldexpf(1.f, e);
+                }
+#pragma unroll
+                for (int t = 0; t < 4; t++) {
+                    const float4 vs4 = *(const float4*)&s_kvs[1][wave][16 * t + 4 * seg];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const bool ok = pw + 16 * t + 4 * seg + r < ctx;
+                        const float vs = r == 0 ? vs4.x : r == 1 ? vs4.y : r == 2 ? vs4.z : vs4.w;
+                        sc[t][r] = ok ? sc[t][r] * (vs * cw) : 0.f;
+                    }
+                }
+            }
+
+            // ---- P.V of the tile (two 32-position MFMA steps)
+            f32x4a o[DT];
+#pragma unroll
+            for (int d = 0; d < DT; d++) o[d] = f32x4a{0.f, 0.f, 0.f, 0.f};
+            auto pv = [&](int b, const VRun (&ra)[DT], const VRun (&rb)[DT]) {
+                f16x8 ph, pl;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const float p = sc[2 * b + (i >> 2)][i & 3];
+                    const _Float16 h = (_Float16)p;
+                    ph[i] = h;
+                    pl[i] = (_Float16)(p - (float)h);
+                }
+                const int pa = pw + 32 * b + 4 * seg, pb = pa + 16;
+#pragma unroll
+                for (int d = 0; d < DT; d++) {
+                    f16x8 vf;
+                    if constexpr (I8) {
+                        vf = i8x8_to_f16x8(ra[d], rb[d]);
+                    } else {
+                        const uint2 xa = mask_run(ra[d], pa, ctx), xb = mask_run(rb[d], pb, ctx);
+                        vf = __builtin_bit_cast(f16x8, make_uint4(xa.x, xa.y, xb.x, xb.y));
+                    }
+                    o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ph, vf, o[d], 0, 0, 0);
+                    o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, o[d], 0, 0, 0);
+                }
+            };
+            pv(0, va0, vb0);
+            pv(1, va1, vb1);
+
+            // the next tile's loads in flight while this tile's output is
+            // folded into the wave's rows.  int8: its ids arrived during this
+            // tile, so its scales, rows and runs are requested at once, and
+            // the ids of the tile after it are requested; fp16: its ids (its
+            // rows are requested at its top: holding them here would spill)
+            if (j + 4 < jb) {
+                if (I8) {
+#pragma unroll
+                    for (int t = 0; t < 4; t++) {
+                        kpg[t] = kpg2[t];
+                        vpg[t] = vpg2[t];
+                    }
+                    sload(j + 4);
+                    kload(j + 4);
+                    vload(j + 4, 0, va0, vb0);
+                    vload(j + 4, 1, va1, vb1);
+                    if (j + 8 < jb) ids_to(j + 8, kpg2, vpg2);
+                } else {
+                    ids(j + 4);
+                }
+            }
+            // o[d][r] = O[head 4seg+r][dim 16d+l16]: row = row * alpha(head) + o * 2^e
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int h = 4 * seg + r;
+                if (h < G) {
+                    const float al = s_alpha[wave][h];
+#pragma unroll
+                    for (int d = 0; d < DT; d++) {
+                        float* row = &s_o[wave * G + h][16 * d + l16];
+                        *row = first ? o[d][r] * ounit : __builtin_fmaf(*row, al, o[d][r] * ounit);
+                    }
+                }
+            }
+            first = false;
+        }
+
+        // ---- combine the 4 waves' states of the segment
+        if (seg == 0) {
+            s_m[wave][l16] = m_run;  // -inf for a wave without tiles (its rows are not read)
+            s_l[wave][l16] = l_run;
+        }
+        __syncthreads();
+        const size_t hbase = (size_t)s * a.H + kvh * G;
+        const size_t sbase = ((size_t)w + s) * a.H + kvh * G;  // partial slot w + s
+        for (int i = tid; i < G * HD; i += ACH) {
+            const int h = i / HD, dd = i % HD;
+            const float M = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
+            float O = 0.f, L = 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) {
+                const float mv = s_m[v][h];
+                const float e = mv == -INFINITY ? 0.f : __expf(mv - M);
+                O = mv == -INFINITY ? O : __builtin_fmaf(s_o[v * G + h][dd], e, O);
+                L = __builtin_fmaf(s_l[v][h], e, L);
+            }
+            if (whole) attn_store(a, (hbase + h) * HD + dd, O / L);
+            else a.part_o[(sbase + h) * HD + dd] = O;
+        }
+        if (!whole && tid < G) {
+            const int h = tid;
+            const float M = fmaxf(fmaxf(s_m[0][h], s_m[1][h]), fmaxf(s_m[2][h], s_m[3][h]));
+            float L = 0.f;
+#pragma unroll
+            for (int v = 0; v < 4; v++) L = __builtin_fmaf(s_l[v][h], s_m[v][h] == -INFINITY ? 0.f : __expf(s_m[v][h] - M), L);
+            a.part_ml[(sbase + h) * 2 + 0] = M;
+            a.part_ml[(sbase + h) * 2 + 1] = L;
+        }
+        __syncthreads();  // s_q, s_o, s_m are reused by the next segment
+    }
+}
+
 // Sequences of several chunks: one wave per (sequence, query head) merges
 // the chunk partials (a separate launch: no device-scope fence or atomic,
 // which on a multi-XCD part would write back and invalidate L2 for every
 // workgroup).  Lane c holds chunk c's (m, l) (64 chunks per round), the
 // weights exp(m_c - M) reach every lane by shuffle, and lane d accumulates
 // output dimensions d, d+64, ... over the chunks in chunk order.
-template <int HD>
+// SPLIT: the partials of attn_split_kernel, sequence s's in slots w + s for
+// the workgroups w whose tile range meets its tiles [pref[s], pref[s+1])
+// (tile t lies in workgroup ((t+1)*g - 1) / T, g = min(gx, T): every one of
+// them has a share, so every slot in the range is written).
+template <int HD, bool SPLIT>
 __global__ __launch_bounds__(64) void attn_merge_kernel(AttnArgs a) {
     constexpr int HPL = HD >= 64 ? HD / 64 : 1;  // dimensions per lane
     const int s = blockIdx.x, h = blockIdx.y, lane = threadIdx.x;
     const int dl = min(lane, HD - 1);            // lanes past a head_dim < 64 redo the last dimension, unstored
-    const int nch = (min(a.ctx[s], a.max_ctx) + ACH - 1) / ACH;
+    int nch;
+    size_t base;                                 // partial row of the sequence's first chunk or slot
+    if (SPLIT) {
+        const long long T = a.pref[a.n], P0 = a.pref[s], P1 = a.pref[s + 1];
+        if (T <= 0 || P1 <= P0) return;
+        const long long g = std::min<long long>(a.gx, T);
+        const int wf = (int)(((P0 + 1) * g - 1) / T), wl = (int)((P1 * g - 1) / T);
+        nch = wl - wf + 1;
+        base = ((size_t)wf + s) * a.H + h;
+    } else {
+        nch = (min(a.ctx[s], a.max_ctx) + ACH - 1) / ACH;
+        base = (size_t)s * ((a.max_ctx + ACH - 1) / ACH) * a.H + h;
+    }
     if (nch <= 1) return;
-    const size_t base = (size_t)s * ((a.max_ctx + ACH - 1) / ACH) * a.H + h;  // partial row of chunk 0
     float M = -INFINITY;
     for (int c = lane; c < nch; c += 64) M = fmaxf(M, a.part_ml[(base + (size_t)c * a.H) * 2]);
 #pragma unroll
@@ -690,10 +1142,23 @@ static int launch_attn_t(const AttnArgs& a, int hd, int G, int grid_x, hipStream
     return set_error(QRAF_HIP_ERR_INVALID, "attention: unsupported head_dim %d / group %d", hd, G);
 }
 
-size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx) {
-    const size_t items = (size_t)n * ((max_ctx + ACH - 1) / ACH);
-    return items * H * hd * 4 + items * H * 2 * 4 + (size_t)n * Hkv * 4 + 256;
+// split kernel: workgroups per KV head (at most one 64-position tile each)
+static int split_gx(int n, int Hkv, int hd, int max_ctx) {
+    return (int)std::min<long long>(std::max(1, split_slots(hd) / Hkv), (long long)n * ((max_ctx + 63) / 64));
 }
+
+// partial slots: chunk items of the chunk grid, or gx + n of the split
+static size_t attn_slots(int n, int Hkv, int hd, int max_ctx) {
+    return std::max<size_t>((size_t)n * ((max_ctx + ACH - 1) / ACH), (size_t)split_gx(n, Hkv, hd, max_ctx) + n);
+}
+
+size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx) {
+    const size_t slots = attn_slots(n, Hkv, hd, max_ctx);
+    return ((size_t)n * Hkv * 4 + 255) / 256 * 256 + ((size_t)(n + 1) * 4 + 255) / 256 * 256 + slots * H * 2 * 4 +
+           slots * H * hd * 4;
+}
+
+static int g_attn_form = 0;  // 0: balanced split, 1: chunk grid (fp16 / int8 pages)
 
 int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv_dtype, const int32_t* page_table,
                      int max_pages, const int32_t* ctx, int n, int H, int Hkv, int hd, int page_size, float scale,
@@ -707,11 +1172,14 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
                "attention: bad page geometry");
     QH_REQUIRE(kv_dtype == DT_F32 || kv_dtype == DT_F16 || kv_dtype == DT_I8, QRAF_HIP_ERR_DTYPE,
                "attention: KV dtype %u", kv_dtype);
-    QH_REQUIRE(kv_dtype != DT_I8 || ((hd == 64 || hd == 128) && H / Hkv <= 16 && page_size % 4 == 0),
-               QRAF_HIP_ERR_INVALID, "attention: int8 pages need head_dim 64/128, group <= 16, page_size %% 4 == 0");
+    QH_REQUIRE(kv_dtype != DT_I8 || ((hd == 64 || hd == 128) && H / Hkv <= 16 && page_size % 4 == 0 &&
+                                     (page_size & (page_size - 1)) == 0),
+               QRAF_HIP_ERR_INVALID,
+               "attention: int8 pages need head_dim 64/128, group <= 16, page_size a power of two >= 4");
     QH_REQUIRE(ws_bytes >= attn_workspace_bytes(n, H, Hkv, hd, max_ctx), QRAF_HIP_ERR_INVALID,
                "attention: workspace too small");
     const int items = n * ((max_ctx + ACH - 1) / ACH);
+    const size_t slots = attn_slots(n, Hkv, hd, max_ctx);
     AttnArgs a;
     a.q = q;
     a.kc = kc;
@@ -724,9 +1192,15 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     uint8_t* w = (uint8_t*)ws;
     a.counters = (uint32_t*)w;  // reserved
     w += ((size_t)n * Hkv * 4 + 255) / 256 * 256;
+    a.pref = (int32_t*)w;
+    w += ((size_t)(n + 1) * 4 + 255) / 256 * 256;
     a.part_ml = (float*)w;
-    w += (size_t)items * H * 2 * 4;
+    w += slots * H * 2 * 4;
     a.part_o = (float*)w;
+    a.gx = split_gx(n, Hkv, hd, max_ctx);
+    a.ps_log2 = 0;
+    while ((1 << a.ps_log2) < page_size) a.ps_log2++;
+    const bool ps_pow2 = (1 << a.ps_log2) == page_size;
     a.n = n;
     a.H = H;
     a.Hkv = Hkv;
@@ -735,9 +1209,22 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     a.max_ctx = max_ctx;
     a.scale = scale;
     const int G = H / Hkv;
+    bool split = false;
     if (kv_dtype == DT_F32) {
         QH_TRY(launch_attn_t<float>(a, hd, G, items, st));
-    } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0) {
+    } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0 && ps_pow2 && g_attn_form == 0) {
+        split = true;
+        const dim3 grid(a.gx, Hkv);
+        const size_t lds = 4 * G * hd * sizeof(float);
+        if (kv_dtype == DT_I8) {
+            if (hd == 128) hipLaunchKernelGGL((attn_split_kernel<128, true>), grid, dim3(ACH), lds, st, a, G);
+            else hipLaunchKernelGGL((attn_split_kernel<64, true>), grid, dim3(ACH), lds, st, a, G);
+        } else {
+            if (hd == 128) hipLaunchKernelGGL((attn_split_kernel<128, false>), grid, dim3(ACH), lds, st, a, G);
+            else hipLaunchKernelGGL((attn_split_kernel<64, false>), grid, dim3(ACH), lds, st, a, G);
+        }
+        QH_CHECK_HIP(hipGetLastError());
+    } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0 && ps_pow2) {
         const dim3 grid(items, Hkv);
         const size_t lds = 4 * G * hd * sizeof(float);
         if (kv_dtype == DT_I8) {
@@ -751,12 +1238,17 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     } else {
         QH_TRY(launch_attn_t<_Float16>(a, hd, G, items, st));
     }
-    if (max_ctx > ACH) {  // some sequence may span several chunks
+    if (split) {  // a sequence may span several workgroups' shares
         const dim3 mg(n, H);
-        if (hd == 128) hipLaunchKernelGGL(attn_merge_kernel<128>, mg, dim3(64), 0, st, a);
-        else if (hd == 64) hipLaunchKernelGGL(attn_merge_kernel<64>, mg, dim3(64), 0, st, a);
-        else if (hd == 32) hipLaunchKernelGGL(attn_merge_kernel<32>, mg, dim3(64), 0, st, a);
-        else hipLaunchKernelGGL(attn_merge_kernel<16>, mg, dim3(64), 0, st, a);
+        if (hd == 128) hipLaunchKernelGGL((attn_merge_kernel<128, true>), mg, dim3(64), 0, st, a);
+        else hipLaunchKernelGGL((attn_merge_kernel<64, true>), mg, dim3(64), 0, st, a);
+        QH_CHECK_HIP(hipGetLastError());
+    } else if (max_ctx > ACH) {  // some sequence may span several chunks
+        const dim3 mg(n, H);
+        if (hd == 128) hipLaunchKernelGGL((attn_merge_kernel<128, false>), mg, dim3(64), 0, st, a);
+        else if (hd == 64) hipLaunchKernelGGL((attn_merge_kernel<64, false>), mg, dim3(64), 0, st, a);
+        else if (hd == 32) hipLaunchKernelGGL((attn_merge_kernel<32, false>), mg, dim3(64), 0, st, a);
+        else hipLaunchKernelGGL((attn_merge_kernel<16, false>), mg, dim3(64), 0, st, a);
         QH_CHECK_HIP(hipGetLastError());
     }
     return QRAF_HIP_OK;
@@ -926,6 +1418,13 @@ int launch_rope_append(const float* qkv, const float* bias, int n, int H, int Hk
 }  // namespace qraf_hip
 
 extern "C" {
+
+int qraf_hip_set_attention_tuning(int32_t form) {
+    qraf_hip::clear_error();
+    QH_REQUIRE(form == 0 || form == 1, QRAF_HIP_ERR_INVALID, "attention tuning: form %d", form);
+    qraf_hip::g_attn_form = form;
+    return QRAF_HIP_OK;
+}
 
 uint64_t qraf_hip_attention_workspace_bytes(int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                                             int32_t max_ctx) {

@@ -197,3 +197,51 @@ def test_rope_append_vs_oracle(hip, kv_dtype):
         assert np.array_equal(qo[s].view(np.uint32), q.view(np.uint32))
         assert np.array_equal(Kc[page, :, off, :].reshape(-1), k.astype(np_dt))
         assert np.array_equal(Vc[page, :, off, :].reshape(-1), v.astype(np_dt))
+
+
+@pytest.fixture
+def chunk_form(hip):
+    """The per-(sequence, 256-position chunk) decomposition, restored to the
+    default balanced split afterwards."""
+    hip._lib.call("qraf_hip_set_attention_tuning", 1)
+    yield
+    hip._lib.call("qraf_hip_set_attention_tuning", 0)
+
+
+@pytest.mark.parametrize("H,Hkv,hd", [(16, 2, 128), (9, 3, 64)])
+def test_attention_chunk_form(hip, chunk_form, H, Hkv, hd):
+    rng = np.random.default_rng(H + hd)
+    ctxs = [1, 17, 255, 256, 257, 700, 1000, 3]
+    table, K, V, _ = build_cache(rng, ctxs, Hkv, hd, 16, po.F16, poison=True)
+    q = rng.standard_normal((len(ctxs), H * hd)).astype(np.float32)
+    got = run_attention(hip, q, table, K, V, ctxs, H, Hkv, hd, 16, po.F16, max(ctxs))
+    check(got[0], oracle_attention(q, table, K, V, ctxs, H, Hkv, hd, 16))
+
+
+def test_attention_split_shares_over_many_sequences(hip):
+    """Batches whose 64-position tiles outnumber the workgroups: shares span
+    several sequences and sequences span several shares (merged in order);
+    fewer tiles than workgroups: one tile per share."""
+    for n, lo, hi, Hkv in [(300, 1, 700, 2), (40, 128, 4096, 2), (7, 1, 90, 16)]:
+        rng = np.random.default_rng(n + lo)
+        ctxs = rng.integers(lo, hi + 1, n).tolist()
+        H, hd = 8 * Hkv if Hkv < 16 else 16, 128 if Hkv < 16 else 64
+        print(f"split n={n} ctx {lo}..{hi} Hkv={Hkv}", flush=True)
+        table, K, V, _ = build_cache(rng, ctxs, Hkv, hd, 16, po.F16, poison=True)
+        q = rng.standard_normal((n, H * hd)).astype(np.float32)
+        got = run_attention(hip, q, table, K, V, ctxs, H, Hkv, hd, 16, po.F16, max(ctxs), repeats=2)
+        assert np.array_equal(got[0], got[1])
+        check(got[0], oracle_attention(q, table, K, V, ctxs, H, Hkv, hd, 16))
+
+
+@pytest.mark.parametrize("ps", [12, 20])
+def test_attention_page_size_not_power_of_two(hip, ps):
+    """fp16 pages of such sizes take the VALU kernel (the matrix-core ones
+    address pages by shifts)."""
+    rng = np.random.default_rng(ps)
+    ctxs = [1, 13, 100, 300]
+    H, Hkv, hd = 8, 2, 128
+    table, K, V, _ = build_cache(rng, ctxs, Hkv, hd, ps, po.F16, poison=True)
+    q = rng.standard_normal((len(ctxs), H * hd)).astype(np.float32)
+    got = run_attention(hip, q, table, K, V, ctxs, H, Hkv, hd, ps, po.F16, max(ctxs))
+    check(got[0], oracle_attention(q, table, K, V, ctxs, H, Hkv, hd, ps))

@@ -171,6 +171,26 @@ def test_attention_i8_refuses_unsupported_shapes(hip):
     with pytest.raises(HipError) as e:
         run_i8(hip, q, table, K8, Ks, V8, Vs, [5], 2, 1, 32, 16)
     assert e.value.code == ERR_INVALID
+    table, K8, Ks, V8, Vs, _ = build_i8_cache(rng, [5], 1, 64, 12)  # page size not a power of two
+    q = rng.standard_normal((1, 2 * 64)).astype(np.float32)
+    with pytest.raises(HipError) as e:
+        run_i8(hip, q, table, K8, Ks, V8, Vs, [5], 2, 1, 64, 12)
+    assert e.value.code == ERR_INVALID
+
+
+@pytest.mark.parametrize("form", [0, 1], ids=["split", "chunk"])
+def test_attention_i8_both_forms_many_sequences(hip, form):
+    rng = np.random.default_rng(77)
+    ctxs = rng.integers(1, 900, 200).tolist()
+    H, Hkv, hd = 16, 2, 128
+    table, K8, Ks, V8, Vs, _ = build_i8_cache(rng, ctxs, Hkv, hd, 16)
+    q = rng.standard_normal((len(ctxs), H * hd)).astype(np.float32)
+    hip._lib.call("qraf_hip_set_attention_tuning", form)
+    try:
+        got = run_i8(hip, q, table, K8, Ks, V8, Vs, ctxs, H, Hkv, hd, 16)
+    finally:
+        hip._lib.call("qraf_hip_set_attention_tuning", 0)
+    check(got[0], oracle_i8(q, table, K8, Ks, V8, Vs, ctxs, H, Hkv, hd, 16))
 
 
 @pytest.mark.parametrize("Hkv,hd,bias,kind", [(2, 128, True, "normal"), (3, 64, False, "normal"), (2, 128, False, "special"),
