@@ -165,9 +165,11 @@ uint64_t qraf_hip_attention_workspace_bytes(int32_t n_seqs, int32_t n_heads, int
  * (QRAF_HIP_ERR_INVALID otherwise) and always do.  Page
  * contents at positions >= ctx are never used (NaN there is harmless). */
 /* Work decomposition of the matrix-core attention (fp16 / int8 pages,
- * process-wide): 0 = balanced split of the batch's 64-position tiles over
- * the workgroups (default), 1 = one workgroup per (sequence, 256-position
- * chunk).  Results agree within the attention tolerance, not bit for bit. */
+ * process-wide): 1 = one workgroup per (sequence, 256-position chunk),
+ * 2 = balanced split of the batch's 64-position tiles over the resident
+ * workgroups, 0 = automatic (default: the split when n_seqs *
+ * ceil(max_ctx / 256) exceeds 1024, else the chunk grid).  Results agree
+ * within the attention tolerance, not bit for bit. */
 int qraf_hip_set_attention_tuning(int32_t form);
 int qraf_hip_paged_attention_dev(const float* q, const void* k_cache, const void* v_cache, uint32_t kv_dtype,
                                  const int32_t* page_table, int32_t max_pages_per_seq, const int32_t* ctx_lens,

@@ -1158,7 +1158,11 @@ size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx) {
            slots * H * hd * 4;
 }
 
-static int g_attn_form = 0;  // 0: balanced split, 1: chunk grid (fp16 / int8 pages)
+// 0: automatic (the balanced split when the chunk grid would need more than
+// one round of resident workgroups, 4 per CU x 256 CUs, at the host-known
+// bound n x ceil(max_ctx / 256); below that the chunk grid, whose per-chunk
+// workgroups carry no share bookkeeping), 1: chunk grid, 2: balanced split
+static int g_attn_form = 0;
 
 int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv_dtype, const int32_t* page_table,
                      int max_pages, const int32_t* ctx, int n, int H, int Hkv, int hd, int page_size, float scale,
@@ -1212,7 +1216,8 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     bool split = false;
     if (kv_dtype == DT_F32) {
         QH_TRY(launch_attn_t<float>(a, hd, G, items, st));
-    } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0 && ps_pow2 && g_attn_form == 0) {
+    } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0 && ps_pow2 &&
+               (g_attn_form == 2 || (g_attn_form == 0 && items > 1024))) {
         split = true;
         const dim3 grid(a.gx, Hkv);
         const size_t lds = 4 * G * hd * sizeof(float);
@@ -1316,8 +1321,8 @@ __global__ void rope_append_kernel(const float* __restrict__ qkv, const float* _
 }
 
 // int8 pages: QuantizedKVCache::store (kv_cache_quant.h:61-95) of the rotated
-// k and the v of each KV head.  One workgroup per sequence: its threads
-// rotate the q pairs, then wave w takes heads j = w, w + 4, ... of the 2*Hkv
+// k and the v of each KV head.  Per sequence, workgroups y >= 1 rotate the q
+// pairs and workgroup 0's wave w takes heads j = w, w + 4, ... of the 2*Hkv
 // (K heads, then V heads); lane l holds elements 2l, 2l+1 of a K head (one
 // rotated pair) or l, l+64 of a V head, the wave's absmax is a max-reduction,
 // and scale = absmax / 127, q = clamp(round(x * (1 / scale)), +-127) with
@@ -1332,6 +1337,7 @@ __global__ __launch_bounds__(256) void rope_append_i8_kernel(const float* __rest
                                                              int page_size, int S, size_t slice) {
     const int s = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int qd = H * hd, kvd = Hkv * hd;
+    // blockIdx.y 0: the K and V heads; y >= 1: q pairs (y-1)*256 + tid, ...
     const size_t rbase = (size_t)s * (qd + 2 * kvd);
     auto ld = [&](int i) {
         const float x = sum_slices(qkv, S, slice, rbase + i);
@@ -1347,11 +1353,14 @@ __global__ __launch_bounds__(256) void rope_append_i8_kernel(const float* __rest
         ra = __fsub_rn(__fmul_rn(x, c), __fmul_rn(y, sn));
         rb = __fadd_rn(__fmul_rn(x, sn), __fmul_rn(y, c));
     };
-    for (int e = tid; e < qd / 2; e += 256) {
-        float ra, rb;
-        rot(2 * e, ra, rb);
-        q_out[(size_t)s * qd + 2 * e] = ra;
-        q_out[(size_t)s * qd + 2 * e + 1] = rb;
+    if (blockIdx.y > 0) {
+        for (int e = (blockIdx.y - 1) * 256 + tid; e < qd / 2; e += (gridDim.y - 1) * 256) {
+            float ra, rb;
+            rot(2 * e, ra, rb);
+            q_out[(size_t)s * qd + 2 * e] = ra;
+            q_out[(size_t)s * qd + 2 * e + 1] = rb;
+        }
+        return;
     }
     const size_t blk = (size_t)page_size * (hd + 4);
     for (int j = wave; j < 2 * Hkv; j += 4) {
@@ -1396,8 +1405,9 @@ int launch_rope_append(const float* qkv, const float* bias, int n, int H, int Hk
     if (kv_dtype == DT_I8) {
         QH_REQUIRE(hd <= 128 && hd % 4 == 0 && page_size % 4 == 0, QRAF_HIP_ERR_INVALID,
                    "rope_append: int8 pages need head_dim <= 128 (multiple of 4) and page_size %% 4 == 0");
-        hipLaunchKernelGGL(rope_append_i8_kernel, dim3(n), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos, rope, q_out,
-                           (int8_t*)kc, (int8_t*)vc, page_table, max_pages, page_size, S, slice);
+        const int qblocks = std::min(8, (H * hd / 2 + 255) / 256);
+        hipLaunchKernelGGL(rope_append_i8_kernel, dim3(n, 1 + qblocks), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos,
+                           rope, q_out, (int8_t*)kc, (int8_t*)vc, page_table, max_pages, page_size, S, slice);
         QH_CHECK_HIP(hipGetLastError());
         return QRAF_HIP_OK;
     }
@@ -1421,7 +1431,7 @@ extern "C" {
 
 int qraf_hip_set_attention_tuning(int32_t form) {
     qraf_hip::clear_error();
-    QH_REQUIRE(form == 0 || form == 1, QRAF_HIP_ERR_INVALID, "attention tuning: form %d", form);
+    QH_REQUIRE(form >= 0 && form <= 2, QRAF_HIP_ERR_INVALID, "attention tuning: form %d", form);
     qraf_hip::g_attn_form = form;
     return QRAF_HIP_OK;
 }

@@ -21,6 +21,16 @@ from oracle import pyoracle as po
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(params=[1, 2], ids=["chunk", "split"])
+def form(request, hip):
+    """Both work decompositions of the matrix-core kernels (1: one workgroup
+    per 256-position chunk, 2: balanced split); the automatic choice is
+    restored afterwards."""
+    hip._lib.call("qraf_hip_set_attention_tuning", request.param)
+    yield request.param
+    hip._lib.call("qraf_hip_set_attention_tuning", 0)
+
+
 def build_cache(rng, ctxs, Hkv, hd, page_size, kv_dtype, extra_pages=7, poison=False):
     """Logical [page][kv head][position][dim] K and V.  poison: positions at
     or past each sequence's context in its last page hold NaN, which the
@@ -94,7 +104,7 @@ def check(got, want):
 
 
 @pytest.mark.parametrize("kv_dtype", [po.F16, po.F32])
-def test_attention_ragged_batch_config(hip, kv_dtype):
+def test_attention_ragged_batch_config(hip, form, kv_dtype):
     # 128 sequences, context lengths U[128, 4096] from a seed, 16 q / 2 kv
     # heads, head_dim 128, fp16 (and f32) K/V ~ N(0,1), one query per sequence
     rng = np.random.default_rng(2024)
@@ -111,7 +121,7 @@ def test_attention_ragged_batch_config(hip, kv_dtype):
 @pytest.mark.parametrize("H,Hkv,hd", [(9, 3, 64), (16, 16, 64), (4, 1, 128), (32, 4, 128), (12, 2, 64), (16, 1, 128),
                                      (4, 1, 16), (8, 2, 32)])
 @pytest.mark.parametrize("kv_dtype", [po.F16, po.F32])
-def test_attention_edge_lengths(hip, H, Hkv, hd, kv_dtype):
+def test_attention_edge_lengths(hip, form, H, Hkv, hd, kv_dtype):
     # head_dim 16 and 32 take the VALU kernel for fp16 pages too
     rng = np.random.default_rng(H * 7 + hd)
     ctxs = [1, 2, 15, 16, 17, 255, 256, 257, 511, 512, 513, 1000, 3]
@@ -124,7 +134,7 @@ def test_attention_edge_lengths(hip, H, Hkv, hd, kv_dtype):
 
 @pytest.mark.parametrize("ps", [4, 8, 32, 64])
 @pytest.mark.parametrize("kv_dtype", [po.F16, po.F32])
-def test_attention_page_sizes(hip, ps, kv_dtype):
+def test_attention_page_sizes(hip, form, ps, kv_dtype):
     rng = np.random.default_rng(ps)
     ctxs = [1, 5, 33, 64, 100, 257, 700]
     H, Hkv, hd = 16, 2, 128
@@ -199,26 +209,8 @@ def test_rope_append_vs_oracle(hip, kv_dtype):
         assert np.array_equal(Vc[page, :, off, :].reshape(-1), v.astype(np_dt))
 
 
-@pytest.fixture
-def chunk_form(hip):
-    """The per-(sequence, 256-position chunk) decomposition, restored to the
-    default balanced split afterwards."""
-    hip._lib.call("qraf_hip_set_attention_tuning", 1)
-    yield
-    hip._lib.call("qraf_hip_set_attention_tuning", 0)
 
-
-@pytest.mark.parametrize("H,Hkv,hd", [(16, 2, 128), (9, 3, 64)])
-def test_attention_chunk_form(hip, chunk_form, H, Hkv, hd):
-    rng = np.random.default_rng(H + hd)
-    ctxs = [1, 17, 255, 256, 257, 700, 1000, 3]
-    table, K, V, _ = build_cache(rng, ctxs, Hkv, hd, 16, po.F16, poison=True)
-    q = rng.standard_normal((len(ctxs), H * hd)).astype(np.float32)
-    got = run_attention(hip, q, table, K, V, ctxs, H, Hkv, hd, 16, po.F16, max(ctxs))
-    check(got[0], oracle_attention(q, table, K, V, ctxs, H, Hkv, hd, 16))
-
-
-def test_attention_split_shares_over_many_sequences(hip):
+def test_attention_split_shares_over_many_sequences(hip, form):
     """Batches whose 64-position tiles outnumber the workgroups: shares span
     several sequences and sequences span several shares (merged in order);
     fewer tiles than workgroups: one tile per share."""

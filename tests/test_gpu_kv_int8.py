@@ -30,6 +30,15 @@ from tests.test_gpu_engine import SMALL, engine_config, oracle_model
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(params=[1, 2], ids=["chunk", "split"])
+def form(request, hip):
+    """Both work decompositions (1: chunk grid, 2: balanced split); the
+    automatic choice is restored afterwards."""
+    hip._lib.call("qraf_hip_set_attention_tuning", request.param)
+    yield request.param
+    hip._lib.call("qraf_hip_set_attention_tuning", 0)
+
+
 def blocks(K8, Ks, V8, Vs):
     """Logical int8 [pages][Hkv][ps][hd] + f32 [pages][Hkv][ps] -> device pools (uint8)."""
     P, Hkv, ps, hd = K8.shape
@@ -111,7 +120,7 @@ def check(got, want):
     assert np.all(err <= tol), f"max err {err.max():.3e}, worst ratio {(err / tol).max():.2f}"
 
 
-def test_attention_i8_ragged_batch(hip):
+def test_attention_i8_ragged_batch(hip, form):
     # 128 sequences, context lengths U[128, 4096], 16 q / 2 kv heads, head_dim 128
     rng = np.random.default_rng(2024)
     ctxs = rng.integers(128, 4097, 128).tolist()
@@ -125,7 +134,7 @@ def test_attention_i8_ragged_batch(hip):
 
 
 @pytest.mark.parametrize("H,Hkv,hd", [(9, 3, 64), (16, 16, 64), (4, 1, 128), (32, 4, 128), (12, 2, 64), (16, 1, 128)])
-def test_attention_i8_edge_lengths(hip, H, Hkv, hd):
+def test_attention_i8_edge_lengths(hip, form, H, Hkv, hd):
     rng = np.random.default_rng(H * 7 + hd)
     ctxs = [1, 2, 15, 16, 17, 255, 256, 257, 511, 512, 513, 1000, 3]
     print(f"int8 attention H={H} Hkv={Hkv} hd={hd}", flush=True)
@@ -136,7 +145,7 @@ def test_attention_i8_edge_lengths(hip, H, Hkv, hd):
 
 
 @pytest.mark.parametrize("ps", [4, 8, 32, 64, 256])
-def test_attention_i8_page_sizes(hip, ps):
+def test_attention_i8_page_sizes(hip, form, ps):
     rng = np.random.default_rng(ps)
     ctxs = [1, 5, 33, 64, 100, 257, 700]
     H, Hkv, hd = 16, 2, 128
@@ -149,7 +158,7 @@ def test_attention_i8_page_sizes(hip, ps):
 
 @pytest.mark.parametrize("ks,vs", [(1e-20, 1e7), (2.5 / 127, 1e-25), (2.5 / 127, 3e30)],
                          ids=["tinyK_hugeV", "tinyV", "V3e30"])
-def test_attention_i8_scale_range(hip, ks, vs):
+def test_attention_i8_scale_range(hip, form, ks, vs):
     """Value scales far outside fp16's range: the per-wave power of two keeps
     the probability x scale operand finite and normal."""
     rng = np.random.default_rng(5)
@@ -178,18 +187,13 @@ def test_attention_i8_refuses_unsupported_shapes(hip):
     assert e.value.code == ERR_INVALID
 
 
-@pytest.mark.parametrize("form", [0, 1], ids=["split", "chunk"])
 def test_attention_i8_both_forms_many_sequences(hip, form):
     rng = np.random.default_rng(77)
     ctxs = rng.integers(1, 900, 200).tolist()
     H, Hkv, hd = 16, 2, 128
     table, K8, Ks, V8, Vs, _ = build_i8_cache(rng, ctxs, Hkv, hd, 16)
     q = rng.standard_normal((len(ctxs), H * hd)).astype(np.float32)
-    hip._lib.call("qraf_hip_set_attention_tuning", form)
-    try:
-        got = run_i8(hip, q, table, K8, Ks, V8, Vs, ctxs, H, Hkv, hd, 16)
-    finally:
-        hip._lib.call("qraf_hip_set_attention_tuning", 0)
+    got = run_i8(hip, q, table, K8, Ks, V8, Vs, ctxs, H, Hkv, hd, 16)
     check(got[0], oracle_i8(q, table, K8, Ks, V8, Vs, ctxs, H, Hkv, hd, 16))
 
 
