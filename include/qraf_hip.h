@@ -288,8 +288,7 @@ int qraf_engine_finalize(qraf_engine* engine);
 /* Sampler on the device (src/sampling/sampler.cpp).  Parameters as in
  * SamplingConfig (include/sampling/sampler.h:10-17): temperature <= 0 is
  * greedy (Sampler::argmax, :25-35); otherwise p = logit / temperature, the
- * top_k largest (all when top_k <= 0 or >= vocab; at most 1024 candidates
- * on the device), softmax over them, the top_p nucleus when 0 < top_p < 1,
+ * top_k largest (all when top_k <= 0 or >= vocab), softmax over them, the top_p nucleus when 0 < top_p < 1,
  * and the first candidate whose cumulative probability reaches the row's
  * uniform (Sampler::sample, :57-128).  repetition_penalty != 1 first applies
  * Sampler::apply_repetition_penalty (:37-49) in place to each row with that
@@ -307,7 +306,13 @@ typedef struct qraf_sampling_params {
  * place), recent [rows][recent_stride] with recent_count [rows] valid
  * entries (may be NULL when repetition_penalty is 1), uniforms [rows] (may
  * be NULL when greedy), tokens [rows] out.  No device scope synchronisation
- * and no allocation. */
+ * and no allocation.  top_k of at most 4096, or the whole vocabulary
+ * (top_k <= 0 or >= vocab; QRAF_HIP_ERR_INVALID for 4096 < top_k < vocab).
+ * The whole vocabulary is reproduced exactly from the tokens whose
+ * exp(p - max) terms are not absorbed by the reference's sequential fp32
+ * sums (at most 4096 of them per row, else that row's token is
+ * QRAF_SAMPLE_TOO_MANY). */
+#define QRAF_SAMPLE_TOO_MANY 0xFFFFFFFFu
 int qraf_hip_sample_dev(float* logits, int32_t rows, int32_t vocab, const qraf_sampling_params* params,
                         const uint32_t* recent, const int32_t* recent_count, int32_t recent_stride,
                         const float* uniforms, uint32_t* tokens, void* stream);

@@ -1129,6 +1129,9 @@ int qraf_engine_sample(qraf_engine* e, int32_t row0, int32_t rows, const qraf_sa
                          pen ? d_rec : nullptr, pen ? d_cnt : nullptr, stride, greedy ? nullptr : d_uni, d_tok, s));
     QH_CHECK_HIP(hipMemcpyAsync(tokens, d_tok, (size_t)rows * 4, hipMemcpyDeviceToHost, s));
     QH_CHECK_HIP(hipStreamSynchronize(s));
+    for (int i = 0; i < rows; i++)
+        QH_REQUIRE(tokens[i] != QRAF_SAMPLE_TOO_MANY, QRAF_HIP_ERR_INVALID,
+                   "sample: row %d: more than 4096 tokens carry weight for the whole-vocabulary softmax", row0 + i);
     return QRAF_HIP_OK;
 }
 

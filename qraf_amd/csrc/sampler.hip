@@ -17,19 +17,33 @@
 //      LDS by (p descending, index ascending).  The reference's std::sort
 //      leaves the order of equal p unspecified; this order is one of its
 //      possible results.
-//   4. One thread runs the reference's arithmetic on the sorted candidates
-//      in the reference's order: exp(p - max), sequential sum, divide, top-p
-//      prefix, renormalise, cumulative sum against the uniform.
-// cutoff = top_k when 0 < top_k < vocab, else vocab (sampler.cpp:73-77); it
-// must be at most SAMPLE_MAX_CUTOFF.
+//   4. The reference's arithmetic on the sorted candidates in its order:
+//      exp(p - max) and the divisions elementwise (all threads), the
+//      sequential sums, top-p prefix, renormalisation and the cumulative sum
+//      against the uniform by one thread.
+// cutoff = top_k when 0 < top_k < vocab, else vocab (sampler.cpp:73-77).
+// cutoff <= SAMPLE_MAX_CUTOFF takes the steps above.  cutoff = vocab > that
+// (top_k 0, the whole vocabulary) takes the absorbed-tail path: in the
+// reference's descending order the running sum only grows, so once a term
+// exp(p - max) is below half an ulp of the running sum it and every later
+// term leave every sum unchanged.  With S = sum_i exp(p_i - max) (a parallel
+// estimate), every token with exp(p - max) >= S * 2^-28 is gathered (the
+// terms that can change a sum, with a 2^3 margin: a term below S * 2^-25 is
+// below half an ulp of a running sum >= S / 2 ... and the running sum there
+// is >= S (1 - V 2^-28)); the reference's loops over the vocabulary then
+// equal the same loops over the gathered candidates, except that its
+// fallback (no cumulative sum reaches the uniform) is its last sorted token,
+// the smallest p (largest index among equal p in this order).  A row whose
+// gathered set exceeds CAND_CAP gets token SAMPLE_TOO_MANY.
 #include <math.h>
 
 #include "common.h"
 
 namespace qraf_hip {
 
-constexpr int SAMPLE_MAX_CUTOFF = 1024;
-constexpr int CAND_CAP = 4096;  // candidates the fast path gathers at most
+constexpr int SAMPLE_MAX_CUTOFF = 4096;
+constexpr int CAND_CAP = 4096;  // candidates gathered and sorted at most
+constexpr uint32_t SAMPLE_TOO_MANY = QRAF_SAMPLE_TOO_MANY;
 
 constexpr int SNT = 1024;  // threads per row (16 waves)
 
@@ -186,13 +200,79 @@ __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restric
         return;
     }
 
+    // ---- the whole vocabulary (cutoff = V > CAND_CAP): gather the tokens
+    // whose terms are not absorbed (see the file comment)
+    const bool trunc = cutoff > CAND_CAP;
+    __shared__ uint32_t s_last;  // trunc: the reference's last sorted token
+    int nsort = cutoff;
+    bool fast = cutoff == V;  // every token a candidate
+    float t = -INFINITY;
+    if (trunc) {
+        float mx = -INFINITY, mn = INFINITY;
+        int imn = -1;
+        for_row(l, V, tid, [&](int i, float v) {  // increasing i per thread
+            const float p = v / T;
+            mx = fmaxf(mx, p);
+            if (imn < 0 || p <= mn) {  // the smallest p, largest index among equal
+                mn = p;
+                imn = i;
+            }
+        });
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) {
+            mx = fmaxf(mx, __shfl_xor(mx, o));
+            const float omn = __shfl_xor(mn, o);
+            const int oi = __shfl_xor(imn, o);
+            if (omn < mn || (omn == mn && oi > imn)) {
+                mn = omn;
+                imn = oi;
+            }
+        }
+        __shared__ float wmn[NW];
+        __shared__ int wimn[NW];
+        if ((tid & 63) == 0) {
+            s_red[0][tid >> 6] = mx;
+            wmn[tid >> 6] = mn;
+            wimn[tid >> 6] = imn;
+        }
+        __syncthreads();
+        for (int w = 0; w < NW; w++) {
+            mx = fmaxf(mx, s_red[0][w]);
+            if (wmn[w] < mn || (wmn[w] == mn && wimn[w] > imn)) {
+                mn = wmn[w];
+                imn = wimn[w];
+            }
+        }
+        if (tid == 0) s_last = (uint32_t)imn;
+        float S = 0.f;
+        for_row(l, V, tid, [&](int, float v) { S += __expf(v / T - mx); });
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) S += __shfl_xor(S, o);
+        __syncthreads();  // the reads of s_red above are done
+        if ((tid & 63) == 0) s_red[1][tid >> 6] = S;
+        __syncthreads();
+        S = 0.f;
+        for (int w = 0; w < NW; w++) S += s_red[1][w];
+        t = mx + logf(S) - 28.0f * 0.69314718f;  // exp(p - max) >= S * 2^-28
+        int c = 0;
+        for_row(l, V, tid, [&](int, float v) { c += v / T >= t; });
+#pragma unroll
+        for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o);
+        if ((tid & 63) == 0) s_cnt[tid >> 6][0] = c;
+        __syncthreads();
+        c = 0;
+        for (int w = 0; w < NW; w++) c += s_cnt[w][0];
+        if (c > CAND_CAP) {
+            if (tid == 0) out[row] = SAMPLE_TOO_MANY;
+            return;
+        }
+        fast = true;  // gather p >= t below
+    }
+
     // ---- fast path: a threshold t with cutoff <= #{p >= t} <= CAND_CAP, by an
     // 8-way search between the row's smallest and largest p; then every
     // p >= t is gathered and sorted.  The sort makes the result independent
     // of the gather order, and equal to the radix path's.
-    int nsort = cutoff;
-    bool fast = cutoff == V;  // every token a candidate
-    float t = -INFINITY;
     if (!fast) {
         float mx = -INFINITY, mn = INFINITY;
         for_row(l, V, tid, [&](int, float v) {
@@ -375,34 +455,57 @@ __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restric
         }
     }
 
-    // ---- the reference's arithmetic, in its order (sampler.cpp:79-127)
+    // ---- the reference's arithmetic, in its order (sampler.cpp:79-127);
+    // exponentials and divisions are elementwise, so all threads take them
+    const int nc = trunc ? nsort : cutoff;  // the candidates the loops run over
+    __shared__ float s_sum;
+    __shared__ int s_nucleus;
+    const float max_val = cval[0];
+    __syncthreads();
+    for (int i = tid; i < nc; i += SNT) cval[i] = expf(cval[i] - max_val);
+    __syncthreads();
     if (tid == 0) {
-        const float max_val = cval[0];
         float sum = 0.f;
-        for (int i = 0; i < cutoff; i++) {
-            cval[i] = expf(cval[i] - max_val);
-            sum += cval[i];
-        }
-        for (int i = 0; i < cutoff; i++) cval[i] /= sum;
-        int n = cutoff;
-        if (top_p > 0.f && top_p < 1.f) {
-            float cs = 0.f;
-            int nucleus = cutoff;
-            for (int i = 0; i < cutoff; i++) {
-                cs += cval[i];
-                if (cs >= top_p) {
-                    nucleus = i + 1;
-                    break;
-                }
+        for (int i = 0; i < nc; i++) sum += cval[i];
+        s_sum = sum;
+    }
+    __syncthreads();
+    const float sum = s_sum;
+    for (int i = tid; i < nc; i += SNT) cval[i] /= sum;
+    __syncthreads();
+    const bool topp = top_p > 0.f && top_p < 1.f;
+    if (topp && tid == 0) {
+        float cs = 0.f;
+        int nucleus = -1;  // -1: the prefix never reaches top_p (the whole list)
+        for (int i = 0; i < nc; i++) {
+            cs += cval[i];
+            if (cs >= top_p) {
+                nucleus = i + 1;
+                break;
             }
-            float ns = 0.f;
-            for (int i = 0; i < nucleus; i++) ns += cval[i];
-            for (int i = 0; i < nucleus; i++) cval[i] /= ns;
-            n = nucleus;
         }
+        const int m = nucleus < 0 ? nc : nucleus;
+        float ns = 0.f;
+        for (int i = 0; i < m; i++) ns += cval[i];
+        s_sum = ns;
+        s_nucleus = nucleus;
+    }
+    __syncthreads();
+    int nucleus = -1;
+    if (topp) {
+        nucleus = s_nucleus;
+        const int m = nucleus < 0 ? nc : nucleus;
+        const float ns = s_sum;
+        for (int i = tid; i < m; i += SNT) cval[i] /= ns;
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const int n = nucleus < 0 ? nc : nucleus;
         const float r = uniforms[row];
         float cs = 0.f;
-        uint32_t pick = (uint32_t)cidx[n - 1];  // fallback: the last candidate
+        // fallback: the reference's last candidate; with an absorbed tail and
+        // no nucleus that is its last sorted token of the whole vocabulary
+        uint32_t pick = trunc && nucleus < 0 ? s_last : (uint32_t)cidx[n - 1];
         for (int i = 0; i < n; i++) {
             cs += cval[i];
             if (r <= cs) {
@@ -419,9 +522,9 @@ int launch_sample(float* logits, int rows, int V, const qraf_sampling_params& sp
     QH_REQUIRE(logits && out && rows > 0 && V > 0, QRAF_HIP_ERR_INVALID, "sample: bad arguments");
     const bool greedy = !(sp.temperature > 0.f);
     const int cutoff = (sp.top_k > 0 && sp.top_k < V) ? sp.top_k : V;
-    QH_REQUIRE(greedy || cutoff <= SAMPLE_MAX_CUTOFF, QRAF_HIP_ERR_INVALID,
-               "sample: %d candidates (top_k %d, vocab %d); the device sampler takes at most %d", cutoff, sp.top_k,
-               V, SAMPLE_MAX_CUTOFF);
+    QH_REQUIRE(greedy || cutoff <= SAMPLE_MAX_CUTOFF || cutoff == V, QRAF_HIP_ERR_INVALID,
+               "sample: top_k %d of vocab %d; the device sampler takes top_k <= %d or the whole vocabulary",
+               sp.top_k, V, SAMPLE_MAX_CUTOFF);
     QH_REQUIRE(greedy || uniforms, QRAF_HIP_ERR_INVALID, "sample: temperature %g needs uniforms", sp.temperature);
     if (sp.repetition_penalty != 1.0f) {  // sampler.cpp:39
         QH_REQUIRE(!recent || (counts && stride > 0), QRAF_HIP_ERR_INVALID, "sample: recent tokens need counts");

@@ -63,8 +63,9 @@ def ref_sample(logits, T, k, p, seed, n):
 def test_sampling_equals_reference_sampler(hip, V, cfg):
     from qraf_amd.engine import Sampler, SamplingConfig
     T, k, p = cfg
-    if k == 0 and V > 1024:
-        pytest.skip("every token a candidate: over the device sampler's 1024")
+    if k == 0 and V > 4096:
+        pytest.skip("N(0,3) logits weigh too many tokens for the whole-vocabulary path "
+                    "(test_whole_vocabulary_equals_reference_sampler covers it)")
     rng = np.random.default_rng(V + int(T * 10) + k)
     n = 96
     logits = (rng.standard_normal(V) * 3.0).astype(np.float32)
@@ -104,12 +105,65 @@ def test_first_index_of_equal_maxima(hip):
     assert got.tolist() == [7, 4094]
 
 
-def test_too_many_candidates_is_refused(hip):
+def test_top_k_between_limit_and_vocab_is_refused(hip):
     from qraf_amd._lib import ERR_INVALID, HipError
-    L = np.zeros((1, 4096), np.float32)
+    L = np.zeros((1, 8192), np.float32)
     with pytest.raises(HipError) as e:
-        device_sample(hip, L, (0.8, 0, 0.9, 1.0), uniforms=[0.5])
+        device_sample(hip, L, (0.8, 5000, 0.9, 1.0), uniforms=[0.5])
     assert e.value.code == ERR_INVALID
+
+
+def zipf_logits(rng, V, exponent, scale=1.0, head=20.0):
+    """log of a Zipf-like law over a random permutation of the vocabulary:
+    p ~ (1 + rank / head)^-exponent (a flat head of about `head` tokens)."""
+    rank = rng.permutation(V).astype(np.float64)
+    return (-exponent * np.log1p(rank / head) * scale + rng.standard_normal(V) * 1e-3).astype(np.float32)
+
+
+@pytest.mark.parametrize("kind,T,p", [("zipf6", 1.0, 0.9), ("zipf6", 0.8, 0.0), ("zipf8", 1.3, 0.95),
+                                      ("masked", 0.8, 0.9), ("masked", 1.0, 0.0)])
+def test_whole_vocabulary_equals_reference_sampler(hip, kind, T, p):
+    """top_k 0 over 151,936 tokens: the device gathers the tokens whose terms
+    survive the reference's sequential sums (file comment of sampler.hip) and
+    must pick the reference's token for every draw; "masked" rows hold 2,000
+    N(0,3) logits and -inf elsewhere (the reference sorts those last)."""
+    from qraf_amd.engine import Sampler, SamplingConfig
+    V, n = 151936, 96
+    rng = np.random.default_rng(hash(kind) % 1000 + int(T * 10))
+    if kind == "masked":
+        logits = np.full(V, -np.inf, np.float32)
+        logits[rng.choice(V, 2000, replace=False)] = (rng.standard_normal(2000) * 3).astype(np.float32)
+    else:
+        logits = zipf_logits(rng, V, 6.0 if kind == "zipf6" else 8.0, T)
+    seed = 77
+    print(f"whole vocabulary {kind} T={T} top_p={p}", flush=True)
+    want = ref_sample(logits, T, 0, p, seed, n)
+    uni = Sampler(SamplingConfig(seed=seed)).uniforms(n)
+    got, _ = device_sample(hip, np.tile(logits, (n, 1)), (T, 0, p, 1.0), uniforms=uni)
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {n} draws differ"
+    assert len(set(want.tolist())) > 3
+
+
+def test_whole_vocabulary_too_many_weighted_tokens(hip):
+    """Rows whose weight spreads over more than 4096 tokens get
+    QRAF_SAMPLE_TOO_MANY (the engine's call turns it into an error)."""
+    V = 20000
+    rng = np.random.default_rng(5)
+    flat = rng.standard_normal((2, V)).astype(np.float32) * 0.1
+    got, _ = device_sample(hip, flat, (1.0, 0, 0.9, 1.0), uniforms=[0.5, 0.5])
+    assert got.tolist() == [0xFFFFFFFF, 0xFFFFFFFF]
+
+
+@pytest.mark.parametrize("k", [1500, 3000, 4096])
+def test_top_k_up_to_4096_equals_reference_sampler(hip, k):
+    from qraf_amd.engine import Sampler, SamplingConfig
+    V, n = 151936, 64
+    rng = np.random.default_rng(k)
+    logits = (rng.standard_normal(V) * 3.0).astype(np.float32)
+    want = ref_sample(logits, 0.9, k, 0.95, 11, n)
+    uni = Sampler(SamplingConfig(seed=11)).uniforms(n)
+    got, _ = device_sample(hip, np.tile(logits, (n, 1)), (0.9, k, 0.95, 1.0), uniforms=uni)
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {n} draws differ"
 
 
 @pytest.mark.parametrize("cfg", [(0.8, 40, 0.9, 1.1, 7), (1.0, 10, 1.0, 1.0, 3), (0.0, 40, 0.9, 1.3, 1)],
