@@ -197,9 +197,11 @@ int qraf_hip_rope_append_dev(const float* qkv, const float* bias, int32_t n_seqs
 
 /* ------------------------------------------------- batched quantized GEMM */
 
-/* Split fp32 activations into bf16 planes x = hi + lo + r, |r| <= 2^-17 |x|
- * (round-to-nearest-even at both steps), the operand form of
- * qraf_hip_qgemm_dev.  rows x cols elements, row-major. */
+/* Split fp32 activations into two 16-bit planes, the operand form of
+ * qraf_hip_qgemm_dev: x_hi = bf16 of x, x_lo = fp16 of x - x_hi (clamped to
+ * +-65504), both round-to-nearest-even; x = hi + lo + r with
+ * |r| <= 2^-20 |x| + 2^-25 for |x| < 2^24 (|r| <= 2^-8 |x| beyond).  rows x
+ * cols elements, row-major. */
 int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int32_t rows, int32_t cols,
                             void* stream);
 /* Tuning of the batched GEMM for batches over 32 rows: waves 4 or 8 per
@@ -222,7 +224,8 @@ uint64_t qraf_hip_qgemm_workspace_bytes(uint32_t dtype, uint32_t out_dim, uint32
  * qraf_hip_qgemm_workspace_bytes enables the split-K path; NULL runs one
  * split.  The split-K sum is taken in a fixed order: results are
  * deterministic.  Calls that share a workspace must not overlap.
- * Error bound per output: (2^-17 + (in_dim+2) 2^-24) sum_k |w_k x_k|. */
+ * Error bound per output: sum_k |w_k| (2^-20 |x_k| + 2^-25)
+ * + (in_dim+2) 2^-24 sum_k |w_k x_k|, for |x_k| < 2^24. */
 int qraf_hip_qgemm_dev(const void* w, uint32_t dtype, uint32_t block_size, uint32_t out_dim, uint32_t in_dim,
                        const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, float* y, const float* add,
                        void* workspace, uint64_t workspace_bytes, void* stream);

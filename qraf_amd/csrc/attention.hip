@@ -94,7 +94,7 @@ struct AttnArgs {
     int ps_log2;               // matrix-core kernels: page_size = 1 << ps_log2
 };
 
-// final output element: f32, or split into the bf16 planes a GEMM consumes
+// final output element: f32, or split into the two planes a GEMM consumes
 __device__ __forceinline__ void attn_store(const AttnArgs& a, size_t i, float v) {
     if (a.out_hi) split_bf16(v, &a.out_hi[i], &a.out_lo[i]);
     else a.out[i] = v;

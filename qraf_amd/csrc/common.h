@@ -80,15 +80,21 @@ int launch_dot(const float* a, const float* b, int n, float* out, hipStream_t s)
 // op: 0 silu, 1 add, 2 mul, 3 scale
 int launch_ew(int op, float* x, const float* y, float sc, int n, hipStream_t s);
 
-// x = hi + lo + r, |r| <= 2^-17 |x|: round-to-nearest-even bf16 of x, then of the rest
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
     const uint32_t b = __builtin_bit_cast(uint32_t, f);
     return (b + 0x7FFFu + ((b >> 16) & 1u)) >> 16;
 }
+// The two activation planes of the GEMM: hi = round-to-nearest-even bf16 of
+// x (fp32's range), lo = round-to-nearest-even fp16 of the exact rest x - hi
+// (|x - hi| <= 2^-8 |x|), clamped to the finite fp16 range.  x = hi + lo + r
+// with |r| <= 2^-20 |x| + 2^-25 while |x| < 2^24 (lo normal: 2^-20 |x|; lo
+// subnormal, |x| below about 2^-5: at most half the fp16 subnormal step);
+// beyond 2^24 the clamp leaves |r| <= 2^-8 |x|.
 __device__ __forceinline__ void split_bf16(float v, uint16_t* hi, uint16_t* lo) {
     const uint32_t h = f32_to_bf16_rne(v);
     *hi = (uint16_t)h;
-    *lo = (uint16_t)f32_to_bf16_rne(v - __builtin_bit_cast(float, h << 16));
+    const float rest = v - __builtin_bit_cast(float, h << 16);  // exact
+    *lo = __builtin_bit_cast(uint16_t, (_Float16)__builtin_fminf(__builtin_fmaxf(rest, -65504.0f), 65504.0f));
 }
 
 // SiLU-gate of one gate/up pair (ops.cpp:218-222 then :275-279): silu(g) * u

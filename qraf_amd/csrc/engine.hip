@@ -85,7 +85,7 @@ __global__ __launch_bounds__(256) void rmsnorm_rows_kernel(const float* __restri
 }
 
 // Residual add of a projection's split-K partials, then the next RMSNorm into
-// the bf16 planes the following GEMM reads (one 1024-thread workgroup per
+// the two planes (bf16 hi, fp16 lo) the following GEMM reads (one 1024-thread workgroup per
 // row, J elements per thread):
 //     h += (part[0] + ... + part[S-1])        (transformer.cpp:593 / :601)
 //     xh + xl = rms_norm(h) * w               (ops.cpp:107-118)

@@ -6,13 +6,15 @@
 // reference has no batched product: this is dispatch_matvec_q
 // (backend.cpp:131-199) applied to M vectors at once.
 //
-// Exactness: each quant block is one K=32 step of v_mfma_f32_16x16x32_bf16.
-// Weights enter as bf16 copies of the block integers (exact: |q| <= 127), X
-// as two bf16 planes hi + lo with x = hi + lo + r, |r| <= 2^-17 |x| (split
-// once per activation by split_bf16_kernel).  The two MFMAs of a block
-// accumulate sum_k q (x_hi + x_lo) in fp32 (products exact), then the block
-// is scaled by its fp32 (Q8) or fp16 (Q4) scale with one FMA per output:
-//     |y - y_exact| <= (2^-17 + (K + 2) 2^-24) sum_k |w_k x_k|.
+// Exactness: each quant block is one K=32 step of two matrix-core products,
+// v_mfma_f32_16x16x32_bf16 then _f16.  Weights enter as bf16 and fp16 copies
+// of the block integers (exact: |q| <= 127), X as two planes: hi = the bf16 of
+// x, lo = the fp16 of the rest, x = hi + lo + r with |r| <= 2^-20 |x| + 2^-25
+// for |x| < 2^24 (split once per activation by split_bf16_kernel).  The two
+// MFMAs of a block accumulate sum_k q (x_hi + x_lo) in fp32 (products exact),
+// then the block is scaled by its fp32 (Q8) or fp16 (Q4) scale with one FMA
+// per output:
+//     |y - y_exact| <= sum_k |w_k| (2^-20 |x_k| + 2^-25) + (K + 2) 2^-24 sum_k |w_k x_k|.
 //
 // Tiling.  A workgroup (4 waves) owns a tile of MW batch rows x 128 weight
 // rows over a range of quant blocks.  For MW > 32 the waves form a 2 x 2
@@ -38,6 +40,7 @@
 namespace qraf_hip {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2), aligned(4)));
@@ -45,7 +48,7 @@ typedef uint32_t u32a2 __attribute__((aligned(2)));
 
 constexpr int QG_MCHUNK = 128;         // batch rows per workgroup at most
 
-// X fp32 [M][K] -> hi, lo bf16 planes [M][K] (hi = rne(x), lo = rne(x - hi)).
+// X fp32 [M][K] -> hi (bf16), lo (fp16) planes [M][K] (hi = rne(x), lo = rne(x - hi)).
 // op 0: x as given; op 1: x = silu(g) * u from an interleaved gate/up row
 // [M][2K] (g = even columns, u = odd columns), ops.cpp:218-222 then :275-279.
 // x may be S slices (GEMM split-K partials) of `slice` floats, summed in order.
@@ -167,31 +170,47 @@ __device__ __forceinline__ uint32_t bf16_pair(float even, float odd) {
     return __builtin_amdgcn_perm(__builtin_bit_cast(uint32_t, odd), __builtin_bit_cast(uint32_t, even), 0x07060302u);
 }
 
+__device__ __forceinline__ uint32_t f16_pair(float even, float odd) {
+    // exact small integers: round-toward-zero packing loses nothing
+    return __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(even, odd));
+}
+
+// One lane's 8 quants of a block as the bf16 operand (for the hi plane) and
+// the fp16 operand (for the lo plane) of the block's two MFMAs, and its scale.
 template <int FMT>
-__device__ __forceinline__ void convert(const WRaw<FMT>& r, bf16x8& w, float& scale);
+__device__ __forceinline__ void convert(const WRaw<FMT>& r, bf16x8& w, f16x8& wh, float& scale);
 template <>
-__device__ __forceinline__ void convert<8>(const WRaw<8>& r, bf16x8& w, float& scale) {
+__device__ __forceinline__ void convert<8>(const WRaw<8>& r, bf16x8& w, f16x8& wh, float& scale) {
     scale = __builtin_bit_cast(float, r.scale);
-    u32x4 p;
+    u32x4 p, ph;
 #pragma unroll
     for (int j = 0; j < 2; j++) {
         const uint32_t d = j ? r.q1 : r.q0;
-        p[2 * j] = bf16_pair((float)(int8_t)(d), (float)(int8_t)(d >> 8));
-        p[2 * j + 1] = bf16_pair((float)(int8_t)(d >> 16), (float)(int8_t)(d >> 24));
+        const float f0 = (float)(int8_t)(d), f1 = (float)(int8_t)(d >> 8);
+        const float f2 = (float)(int8_t)(d >> 16), f3 = (float)(int8_t)(d >> 24);
+        p[2 * j] = bf16_pair(f0, f1);
+        p[2 * j + 1] = bf16_pair(f2, f3);
+        ph[2 * j] = f16_pair(f0, f1);
+        ph[2 * j + 1] = f16_pair(f2, f3);
     }
     w = __builtin_bit_cast(bf16x8, p);
+    wh = __builtin_bit_cast(f16x8, ph);
 }
 template <>
-__device__ __forceinline__ void convert<4>(const WRaw<4>& r, bf16x8& w, float& scale) {
+__device__ __forceinline__ void convert<4>(const WRaw<4>& r, bf16x8& w, f16x8& wh, float& scale) {
     scale = (float)__builtin_bit_cast(_Float16, (uint16_t)r.scale);
     // nibble u -> signed byte u - 8: (u + 0x78) ^ 0x80, no carry between bytes
     const uint32_t lo = ((r.q & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
     const uint32_t hi = (((r.q >> 4) & 0x0F0F0F0Fu) + 0x78787878u) ^ 0x80808080u;
-    u32x4 p;
+    u32x4 p, ph;
 #pragma unroll
-    for (int j = 0; j < 4; j++)
-        p[j] = bf16_pair((float)(int8_t)(lo >> (8 * j)), (float)(int8_t)(hi >> (8 * j)));
+    for (int j = 0; j < 4; j++) {
+        const float f0 = (float)(int8_t)(lo >> (8 * j)), f1 = (float)(int8_t)(hi >> (8 * j));
+        p[j] = bf16_pair(f0, f1);
+        ph[j] = f16_pair(f0, f1);
+    }
     w = __builtin_bit_cast(bf16x8, p);
+    wh = __builtin_bit_cast(f16x8, ph);
 }
 
 // WM x WN waves (batch x weight rows); TM: 16-row batch tiles per wave; TN:
@@ -295,22 +314,23 @@ __global__ __launch_bounds__(64 * WM * WNW, 512 / (64 * WM * WNW)) void qgemm_ke
         for (int j = 0; j < KC; j++) {
             const bool valid = cb + j < b_end;  // uniform; an invalid block's scale is 0 (its data is finite)
             bf16x8 wf[TN];
+            f16x8 wh[TN];
             float sc[TN];
 #pragma unroll
             for (int u = 0; u < TN; u++) {
                 WRaw<FMT> r = wc[j][u];
                 r.scale = valid ? r.scale : 0u;
-                convert<FMT>(r, wf[u], sc[u]);
+                convert<FMT>(r, wf[u], wh[u], sc[u]);
             }
 #pragma unroll
             for (int t = 0; t < TM; t++) {
                 const int row = (wm * TM + t) * 16 + l16;
                 const bf16x8 ah = *(const bf16x8*)&sx[(buf * 2 + 0) * PLANE + row * XS + j * 32 + seg * 8];
-                const bf16x8 al = *(const bf16x8*)&sx[(buf * 2 + 1) * PLANE + row * XS + j * 32 + seg * 8];
+                const f16x8 al = *(const f16x8*)&sx[(buf * 2 + 1) * PLANE + row * XS + j * 32 + seg * 8];
 #pragma unroll
                 for (int u = 0; u < TN; u++) {
                     f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[u], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[u], d, 0, 0, 0);
+                    d = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, wh[u], d, 0, 0, 0);
 #pragma unroll
                     for (int r = 0; r < 4; r++) acc[t][u][r] = __builtin_fmaf(d[r], sc[u], acc[t][u][r]);
                 }
@@ -370,7 +390,7 @@ __global__ __launch_bounds__(64 * WM * WNW, 512 / (64 * WM * WNW)) void qgemm_ke
 //
 // Workgroup tile: MW = 32*TM batch rows x NW = 32*TN weight rows, 4 waves in
 // a 2 x 2 grid, each wave TM x TN MFMA tiles of 16 x 16.  Three LDS stage
-// buffers, each holding KC quant blocks of X (both bf16 planes) and of W, are
+// buffers, each holding KC quant blocks of X (both planes) and of W, are
 // filled by direct-to-LDS buffer loads (buffer_load_dwordx4 ... lds): while
 // stage c computes, stages c+1 and c+2 are in flight.  One raw s_barrier per
 // stage, after the wave's own loads of stage c have landed (explicit vmcnt
@@ -561,6 +581,7 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
                 continue;
             }
             bf16x8 wf[TN];
+            f16x8 wh[TN];
             float sc[TN];
 #pragma unroll
             for (int u = 0; u < TN; u++) {
@@ -575,20 +596,20 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
                     r.scale = *(const uint16_t*)(tb + 2 * l16);
                     reinterpret_cast<uint32_t*>(&r)[1] = *(const uint32_t*)(tb + 32 + 16 * l16 + 4 * seg);
                 }
-                convert<FMT>(r, wf[u], sc[u]);
+                convert<FMT>(r, wf[u], wh[u], sc[u]);
             }
 #pragma unroll
             for (int t = 0; t < TM; t++) {
                 const int row = (wm * TM + t) * 16 + l16;
                 const int slot = (4 * j + seg) ^ (row & 7);
                 const bf16x8 ah = *(const bf16x8*)(buf + row * G::XROW + 16 * slot);
-                const bf16x8 al = *(const bf16x8*)(buf + G::XPL + row * G::XROW + 16 * slot);
+                const f16x8 al = *(const f16x8*)(buf + G::XPL + row * G::XROW + 16 * slot);
                 const int q = (j * TM + t) & 3, pq = (q + 2) & 3;  // this step's slot, the pending one's
                 const int pt = t >= 2 ? t - 2 : TM - 2 + t;         // pending tile
 #pragma unroll
                 for (int u = 0; u < TN; u++) {
                     const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[u], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-                    dR[q][u] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, wf[u], d, 0, 0, 0);
+                    dR[q][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, wh[u], d, 0, 0, 0);
                     const float ps = t >= 2 ? sc[u] : sP[u];
 #pragma unroll
                     for (int r = 0; r < 4; r++) acc[pt][u][r] = __builtin_fmaf(dR[pq][u][r], ps, acc[pt][u][r]);

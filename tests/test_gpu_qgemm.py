@@ -1,9 +1,13 @@
 """GPU parity of the batched Q8_0/Q4_0 GEMM (matrix cores) against the
 oracle's dispatch_matvec_q applied to every batch row.
 
-Tolerance per output (floating point): the GEMM's activation split leaves
-|r| <= 2^-17 |x| per element and both sides accumulate in fp32, so
-    |y_gpu - y_oracle| <= (2^-17 + 2 (K + 2) 2^-24) sum_k |w_k x_k|.
+Tolerance per output (floating point): the GEMM's activation split (bf16 hi,
+fp16 lo) leaves |r| <= 2^-20 |x| + 2^-25 per element and both sides
+accumulate in fp32, so
+    |y_gpu - y_oracle| <= sum_k |w_k| (2^-20 |x_k| + 2^-25) + 2 (K + 2) 2^-24 sum_k |w_k x_k|.
+The split itself is pinned bit-exactly (numpy's correctly rounded bf16 and
+fp16 conversions), and single-product GEMMs pin that the matrix cores add
+the two planes exactly, fp16 subnormals included.
 """
 import numpy as np
 import pytest
@@ -57,7 +61,8 @@ def check(Y, wq, dt, N, K, X, add=None):
         y_ref = po.matvec_q(wq, dt, N, K, X[m]).astype(np.float64)
         if add is not None:
             y_ref = y_ref + add[m]
-        tol = (2.0 ** -17 + 2 * (K + 2) * 2.0 ** -24) * (absw @ np.abs(X[m].astype(np.float64))) + 1e-30
+        ax = np.abs(X[m].astype(np.float64))
+        tol = 2.0 ** -20 * (absw @ ax) + 2.0 ** -25 * absw.sum(1) + 2 * (K + 2) * 2.0 ** -24 * (absw @ ax) + 1e-30
         if add is not None:
             tol += 2.0 ** -23 * np.abs(y_ref)
         err = np.abs(Y[m] - y_ref)
@@ -167,15 +172,48 @@ def test_qgemm_residual_epilogue(hip, split, in_place, tiled):
     check(Y, wq, po.Q8_0, N, K, X, add)
 
 
+def split_planes(X):
+    """The planes the split must produce: hi = round-to-nearest-even bf16 of
+    x, lo = round-to-nearest-even fp16 of x - hi clamped to +-65504."""
+    b = X.view(np.uint32).astype(np.uint64)
+    hi = ((b + 0x7FFF + ((b >> 16) & 1)) >> 16).astype(np.uint16)
+    hv = (hi.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    lo = np.clip(X.astype(np.float64) - hv, -65504, 65504).astype(np.float16)
+    return hi, lo
+
+
 def test_split_bf16_reconstruction(hip):
     rng = np.random.default_rng(6)
     X = (rng.standard_normal((7, 4096)) * np.exp(rng.uniform(-30, 30, (7, 4096)))).astype(np.float32)
     X[0, :4] = [0.0, -0.0, 1.0, -3.0]
     _, h, l = run_gemm(hip, np.zeros(36 * 4096 // 32, np.uint8), po.Q8_0, 1, 4096, X)
-    hi = (h.astype(np.uint32) << 16).view(np.float32).reshape(X.shape).astype(np.float64)
-    lo = (l.astype(np.uint32) << 16).view(np.float32).reshape(X.shape).astype(np.float64)
-    assert np.all(np.abs(hi + lo - X) <= 2.0 ** -17 * np.abs(X))
-    # hi is the round-to-nearest-even bf16 of x
-    ref_hi = X.view(np.uint32).astype(np.uint64)
-    ref_hi = ((ref_hi + 0x7FFF + ((ref_hi >> 16) & 1)) >> 16).astype(np.uint16)
+    ref_hi, ref_lo = split_planes(X)
     assert np.array_equal(h.reshape(X.shape), ref_hi)
+    assert np.array_equal(l.reshape(X.shape), ref_lo.view(np.uint16))
+    hi = (h.astype(np.uint32) << 16).view(np.float32).reshape(X.shape).astype(np.float64)
+    lo = l.view(np.float16).reshape(X.shape).astype(np.float64)
+    ax = np.abs(X.astype(np.float64))
+    err = np.abs(hi + lo - X)
+    small = ax < 2.0 ** 24
+    assert np.all(err[small] <= 2.0 ** -20 * ax[small] + 2.0 ** -25)
+    assert np.all(err[~small] <= 2.0 ** -8 * ax[~small])
+
+
+@pytest.mark.parametrize("N,M,tiled", [(16, 5, False), (8192, 128, True)])
+def test_planes_added_exactly(hip, N, M, tiled):
+    """One product per output: weight row n is 1 at k = n % 32 (Q8_0, scale
+    1), so y[m][n] = hi + lo of x[m][n % 32] exactly, for x from 1e-7 (fp16
+    subnormal lo) to 1e6; N = 8192 at 128 rows runs the pipelined kernel."""
+    K = 32
+    rng = np.random.default_rng(N + M)
+    X = (rng.choice([-1.0, 1.0], (M, K)) * 10.0 ** rng.uniform(-7, 6, (M, K))).astype(np.float32)
+    wq = np.zeros((N, 36), np.uint8)
+    wq[:, :4] = np.frombuffer(np.float32(1.0).tobytes(), np.uint8)
+    wq[np.arange(N), 4 + np.arange(N) % K] = 1
+    Y, h, l = run_gemm(hip, wq.reshape(-1), po.Q8_0, N, K, X, tiled=tiled)
+    hi = (h.astype(np.uint32) << 16).view(np.float32).reshape(M, K).astype(np.float64)
+    lo = l.view(np.float16).reshape(M, K).astype(np.float64)
+    want = (hi + lo).astype(np.float32)[:, np.arange(N) % K]
+    assert np.array_equal(Y.view(np.uint32), want.view(np.uint32))
+    ax = np.abs(X.astype(np.float64))[:, np.arange(N) % K]
+    assert np.all(np.abs(Y - X[:, np.arange(N) % K].astype(np.float64)) <= 2.0 ** -20 * ax + 2.0 ** -25)
