@@ -176,6 +176,16 @@ def bench_matvec(args, rt):
         total_bytes += b * args.steps
     for g in graphs:
         g.destroy()
+    # plain-read ceiling: a streaming read of the same bytes from the same rotated pool copies
+    rp_out = DeviceBuffer(lib.qraf_hip_read_probe_out_bytes())
+    for c, p in zip(cases, per_case):
+        b = mv_bytes(c["dt"], c["n"], c["k"])
+        us = graph_time_us(rt, lambda i: call("qraf_hip_read_probe_dev", c["pool"].ptr + (i % c["copies"]) * c["wbytes"],
+                                              c["wbytes"], rp_out.ptr, stream.h), args.steps)
+        p["plain_read_us"] = round(us, 3)
+        p["plain_read_GB_s"] = round(c["wbytes"] / (us * 1e-6) / 1e9, 1)
+        p["frac_of_plain_read"] = round(us / p["us_per_launch"], 4)  # plain-read time / matvec time
+    rp_out.free()
     # cache-resident reference point (same weight copy every launch), labelled as such
     cache_res = []
     for c in cases:
@@ -749,7 +759,8 @@ def main():
                 "traffic_source": "profiles/qmv_matvec_isolated.md (FETCH_SIZE, WRITE_SIZE scaled by a copy kernel)"
                 if traffic else None,
                 "kernel": kname,
-                "case": dom["case"], "alg_bytes_per_launch": dom["alg_bytes"]}
+                "case": dom["case"], "alg_bytes_per_launch": dom["alg_bytes"],
+                "plain_read_GB_s": dom.get("plain_read_GB_s"), "frac_of_plain_read": dom.get("frac_of_plain_read")}
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_matvec(hosts, args.cpu_seconds)

@@ -61,6 +61,13 @@ int qraf_hip_memcpy_h2d(void* dst_dev, const void* src_host, uint64_t bytes);
 int qraf_hip_memcpy_d2h(void* dst_host, const void* src_dev, uint64_t bytes);
 int qraf_hip_memcpy_d2d(void* dst_dev, const void* src_dev, uint64_t bytes, void* stream);
 int qraf_hip_memset(void* dev_ptr, int value, uint64_t bytes);
+/* Streaming read of `bytes` (a positive multiple of 16, 16-byte aligned) in
+ * the device's best plain-read launch shape: the HBM ceiling a memory-bound
+ * kernel moving the same bytes is measured against.  Writes partial sums of
+ * the data to `out` (qraf_hip_read_probe_out_bytes bytes).  No counterpart in
+ * the reference (a measurement aid). */
+int qraf_hip_read_probe_dev(const void* dev_ptr, uint64_t bytes, float* out, void* stream);
+uint64_t qraf_hip_read_probe_out_bytes(void);
 int qraf_hip_stream_create(void** stream);
 int qraf_hip_stream_destroy(void* stream);
 int qraf_hip_stream_synchronize(void* stream);

@@ -137,6 +137,10 @@ int qraf_hip_memcpy_d2d(void* dst, const void* src, uint64_t n, void* stream) {
     if (n) QH_CHECK_HIP(hipMemcpyAsync(dst, src, n, hipMemcpyDeviceToDevice, as_stream(stream)));
     return QRAF_HIP_OK;
 }
+int qraf_hip_read_probe_dev(const void* p, uint64_t bytes, float* out, void* stream) {
+    return qraf_hip::launch_read_probe(p, bytes, out, as_stream(stream));
+}
+uint64_t qraf_hip_read_probe_out_bytes(void) { return qraf_hip::read_probe_out_floats() * sizeof(float); }
 int qraf_hip_memset(void* p, int v, uint64_t n) {
     if (n) QH_CHECK_HIP(hipMemset(p, v, n));
     return QRAF_HIP_OK;

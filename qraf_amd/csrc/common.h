@@ -79,6 +79,9 @@ int launch_softmax(float* x, int n, hipStream_t s);
 int launch_dot(const float* a, const float* b, int n, float* out, hipStream_t s);
 // op: 0 silu, 1 add, 2 mul, 3 scale
 int launch_ew(int op, float* x, const float* y, float sc, int n, hipStream_t s);
+// streaming read of `bytes` (the plain-read ceiling); out: read_probe_out_floats() floats
+int launch_read_probe(const void* p, size_t bytes, float* out, hipStream_t s);
+size_t read_probe_out_floats();
 
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {
     const uint32_t b = __builtin_bit_cast(uint32_t, f);
