@@ -117,7 +117,9 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     constexpr int NOUT = G * HD;                 // outputs of this workgroup
     constexpr int HPT = (NOUT + ACH - 1) / ACH;  // outputs per thread at the end
     constexpr int NG = ACH / HD;                 // position groups of the PV phase
-    constexpr int PADP = 8 * NG;                 // past-the-end slots its unrolled loop may touch
+    constexpr int PVU = 16;                      // V loads in flight per thread in the PV phase
+    constexpr int PADP = PVU * NG;               // past-the-end slots its unrolled loop may touch
+    static_assert(PADP <= ACH, "padding is written by the first PADP threads");
     __shared__ float s_q[G][HD];
     __shared__ float s_p[G][ACH + PADP];         // probabilities (zero past the end); then PV partials
     __shared__ uint32_t s_voff[ACH + PADP];      // element offset of each position's V row in the layer pages
@@ -207,7 +209,7 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
 
     // ---- weighted sum of V.  Thread (dimension d = tid % HD, group g = tid /
     // HD) sums positions g, g + NG, ... of the chunk for all G heads at once
-    // (each V element is loaded once for the heads that share it), with 8
+    // (each V element is loaded once for the heads that share it), with PVU
     // independent loads in flight; the NG group sums are then added in group
     // order.  For f32 pages and head_dim >= 64 a wave reads one V row.
     const int dd = tid % HD, grp = tid / HD;
@@ -216,12 +218,12 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     float acc[G];
 #pragma unroll
     for (int h = 0; h < G; h++) acc[h] = 0.f;
-    for (int tt = grp; tt < tend; tt += NG * 8) {
-        float v[8];
+    for (int tt = grp; tt < tend; tt += NG * PVU) {
+        float v[PVU];
 #pragma unroll
-        for (int u = 0; u < 8; u++) v[u] = kv_load(vd + s_voff[tt + NG * u]);
+        for (int u = 0; u < PVU; u++) v[u] = kv_load(vd + s_voff[tt + NG * u]);
 #pragma unroll
-        for (int u = 0; u < 8; u++)
+        for (int u = 0; u < PVU; u++)
 #pragma unroll
             for (int h = 0; h < G; h++) acc[h] = __builtin_fmaf(s_p[h][tt + NG * u], v[u], acc[h]);
     }
