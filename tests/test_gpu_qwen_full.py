@@ -10,7 +10,7 @@ and v by 2^-11, which 36 layers carry past the logit bar at this depth).
 The weights are the engine's device-generated ones, written to a .qraf file
 in the reference's format; the reference's own QrafModel + Transformer load
 it (oracle/_ref) and decode sequence 0 on the host (one sequence: a
-4-token prompt, then 4 greedy tokens).  The
+4-token prompt, then 32 greedy tokens).  The
 engine's logits for sequence 0 at every position must be within the engine
 bar of the reference's (1e-3 relative + 1e-4 absolute), and its greedy
 tokens equal.
@@ -20,6 +20,8 @@ import pytest
 
 from oracle import pyoracle as po
 from tests.test_gpu_engine import check_logits
+
+GEN = 32  # greedy tokens of sequence 0 compared with the reference's
 
 pytestmark = [pytest.mark.gpu,
               pytest.mark.skipif(po.ref() is None, reason="oracle/_ref (the compiled reference) is not built")]
@@ -48,7 +50,7 @@ def test_qwen25_3b_q4_sequence_matches_reference(hip, tmp_path, n):
     want_logits = np.zeros(n, np.uint8)
     want_logits[0] = 1
     try:
-        for pos in range(8):
+        for pos in range(len(tok0) - 1 + GEN):
             t0 = tok0[pos]
             toks = [t0] + rng.integers(0, V, n - 1).tolist()
             lg, nx = e.step(seqs, toks, [pos] * n, want_logits=want_logits, logits=True, argmax=True)
