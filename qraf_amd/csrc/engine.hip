@@ -944,7 +944,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
             // Batched layer on the matrix cores, 9 launches: each projection writes
             // split-K partials that the next kernel sums (with the bias, residual,
             // norm or SiLU-gate it applies anyway), and every kernel that feeds a
-            // projection writes its input as the bf16 hi/lo planes directly.
+            // projection writes its input as the hi (bf16) and lo (fp16) planes directly.
             QH_TRY(launch_residual_norm_split(nullptr, 0, 0, e->h, e->layers[0].an, D, c.rms_norm_eps, e->xh, e->xl, n, s));
             for (uint32_t l = 0; l < c.num_layers; l++) {
                 qraf_engine::Layer& L = e->layers[l];
