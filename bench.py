@@ -15,10 +15,12 @@ over the total timed time.  Algorithmic bytes per launch = weight bytes +
 The same JSON line also reports the other configurations of the metric:
   decode_b1    SmolLM2-135M architecture, Q8_0, batch 1: seeded 32-token
                prompt, 128 greedy tokens (decode-only and prefill+decode tok/s)
-  decode_b128  Qwen2.5-3B architecture, Q4_0, tied head, QKV bias, fp16 KV
-               pages: 128 concurrent sequences, prompts U[16,512], outputs
-               U[64,256], new requests admitted as others finish; aggregate
-               generated tok/s
+  decode_b128  Qwen2.5-3B architecture, Q4_0, tied head, QKV bias, f32 KV
+               pages (the reference's KVCache): 128 concurrent sequences,
+               prompts U[16,512], outputs U[64,256], new requests admitted as
+               others finish; aggregate generated tok/s; fp16 and int8 pages
+               reported beside it with their streams' agreement with the f32
+               run
   gemm         batched Q-GEMM, B in {8,32,64,128}, Qwen2.5-3B projection shapes
   attention    ragged paged decode attention: 128 sequences, context U[128,4096],
                16 q / 2 kv heads, head_dim 128, fp16 K/V
@@ -78,8 +80,20 @@ def host_cpu():
 
 def graph_time_us(rt, body, iters):
     """Capture `iters` calls of body(i) in one graph; replay once untimed, then
-    time one replay with events on the stream; microseconds per call."""
+    time one replay with events on the stream; microseconds per call.  With
+    rt["eager"] (--no-graphs): the calls are launched directly, once untimed
+    and once between the events."""
     stream, Graph, Event = rt["stream"], rt["Graph"], rt["Event"]
+    if rt.get("eager"):
+        for i in range(iters):
+            body(i)
+        stream.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(stream)
+        for i in range(iters):
+            body(i)
+        e1.record(stream)
+        return e0.elapsed_ms(e1) * 1e3 / iters
     g = Graph(stream)
     with g:
         for i in range(iters):
@@ -147,20 +161,25 @@ def bench_matvec(args, rt):
             launch(c, i)
     stream.synchronize()
     graphs = []
-    for c in cases:
-        g = Graph(stream)
-        with g:
-            for i in range(args.steps):
-                launch(c, args.warmup + i)
-        graphs.append(g)
-    for g in graphs:  # one untimed replay: graph upload stays out of the timed region
-        g.launch()
-    stream.synchronize()
+    if not rt.get("eager"):
+        for c in cases:
+            g = Graph(stream)
+            with g:
+                for i in range(args.steps):
+                    launch(c, args.warmup + i)
+            graphs.append(g)
+        for g in graphs:  # one untimed replay: graph upload stays out of the timed region
+            g.launch()
+        stream.synchronize()
     ev = [Event() for _ in range(len(cases) + 1)]
     call("qraf_hip_device_synchronize")
     ev[0].record(stream)
-    for i, g in enumerate(graphs):
-        g.launch()
+    for i, c in enumerate(cases):
+        if graphs:
+            graphs[i].launch()
+        else:
+            for j in range(args.steps):
+                launch(c, args.warmup + j)
         ev[i + 1].record(stream)
     stream.synchronize()
     call("qraf_hip_device_synchronize")
@@ -415,12 +434,55 @@ def cpu_decode_b1(n_tokens=8):
 
 # --------------------------------------------------------------------------- decode, batch 128
 
+def cpu_decode_qwen(rt, n_prompt=4, n_gen=4):
+    """The Qwen2.5-3B-architecture Q4 decode on the host with the reference's
+    own QrafModel + Transformer (oracle/_ref), one core, on the same weights
+    (written to a .qraf file from the device generator): one sequence, an
+    n_prompt-token prompt fed token by token, then n_gen greedy tokens.  The
+    reference decodes sequences one at a time (its scheduler calls forward
+    per request), so its aggregate rate over 128 sequences is this rate."""
+    import tempfile
+    from oracle import pyoracle as po
+    if po.ref() is None:
+        return None
+    tmp = tempfile.mkdtemp()
+    path = os.path.join(tmp, "qwen3b_q4.qraf")
+    try:
+        write_qraf_synthetic(path, QWEN, Q4, 3, rt)
+        ref = po.RefModel(path, QWEN["vocab"])
+        try:
+            toks = np.random.default_rng(9).integers(0, QWEN["vocab"], n_prompt).tolist()
+            t0 = time.perf_counter()
+            for pos in range(n_prompt + n_gen - 1):
+                lg = ref.forward(toks[pos], pos)
+                if pos >= n_prompt - 1:
+                    toks.append(int(np.argmax(lg)))
+            el = time.perf_counter() - t0
+        finally:
+            ref.close()
+    finally:
+        if os.path.exists(path):
+            os.remove(path)
+        os.rmdir(tmp)
+    fwd = n_prompt + n_gen - 1
+    return {"value": round(fwd / el, 4), "unit": "tok/s (forward passes per second, one sequence)", "cores": 1,
+            "kind": "reference", "s_per_token": round(el / fwd, 3),
+            "sample": f"Transformer::forward of the Qwen2.5-3B architecture (Q4_0, tied f32 head as the reference "
+                      f"builds it): {n_prompt}-token prompt + {n_gen} greedy tokens, {fwd} forwards in {el:.1f} s, "
+                      f"host CPU {host_cpu()}"}
+
+
 QWEN = dict(vocab=151936, hidden=2048, layers=36, heads=16, kv_heads=2, inter=11008, max_seq=1024, rope_theta=1e6,
             eps=1e-6)
 
 
-def qwen_engine(args, rows, kv=F16):
-    """The Qwen2.5-3B-architecture engine of the batch-128 legs (random Q4_0 weights, fp16 KV pages)."""
+KV_NAMES = {F32: "f32", F16: "fp16", I8: "int8"}
+KV_POS_BYTES = {F32: 2 * 36 * 2 * 128 * 4, F16: 2 * 36 * 2 * 128 * 2, I8: 2 * 36 * 2 * (128 + 4)}  # K+V, all layers
+
+
+def qwen_engine(args, rows, kv=F32):
+    """The Qwen2.5-3B-architecture engine of the batch-128 legs (random Q4_0
+    weights; f32 KV pages by default, the reference's KVCache)."""
     from qraf_amd.engine import Engine, model_config
     cfg = model_config(*(QWEN[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq",
                                            "rope_theta", "eps")))
@@ -451,33 +513,57 @@ def bench_decode_b128(args, rt):
         work.append((rng.integers(0, QWEN["vocab"], plen).tolist(), olen))
 
     def run(max_rows, chunk):
-        sched = BatchScheduler(e, max_batch=128, max_rows=max_rows, prefill_chunk=chunk)
-        for p, o in work:
-            sched.submit(p, o)
-        t0 = time.perf_counter()
-        done = sched.run()
-        el = time.perf_counter() - t0
-        gen = sum(len(r.generated) for r in done)
-        return {"generated_tokens": gen, "steps": sched.steps, "rows_processed": sched.rows, "wall_s": round(el, 3),
-                "generated_tok_s": round(gen / el, 1), "rows_per_s": round(sched.rows / el, 1),
-                "ms_per_step": round(el / sched.steps * 1e3, 3)}, [r.generated for r in sorted(done, key=lambda r: r.id)]
+        return run_schedule(e, work, max_rows, chunk)
 
+    e.stats(reset=True)
     chunked, streams_c = run(rows, args.prefill_chunk)
     tbt, streams_t = run(128, 1)
-    steady = steady_decode_b128(e, rng, args.decode_steps)
+    steady = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, F32)
     e.close()
-    e8 = qwen_engine(args, 128, I8)
-    steady["int8_pages"] = steady_decode_b128(e8, np.random.default_rng(3), args.decode_steps)
-    e8.close()
-    out = {"model": "Qwen2.5-3B architecture, Q4_0 weights, tied head, QKV bias, fp16 KV pages, random init",
+    extras = {}
+    for kv in (F16, I8):  # narrower pages: not the reference's values; agreement with the f32 streams beside them
+        ek = qwen_engine(args, rows, kv)
+        res, streams_k = run_schedule(ek, work, rows, args.prefill_chunk)
+        res["stream_agreement_with_f32_pages"] = stream_agreement(streams_c, streams_k)
+        res["steady_decode"] = steady_decode_b128(ek, np.random.default_rng(3), args.decode_steps, kv)
+        ek.close()
+        extras[f"{KV_NAMES[kv]}_pages"] = res
+    out = {"model": "Qwen2.5-3B architecture, Q4_0 weights, tied head, QKV bias, f32 KV pages, random init",
            "requests": args.requests, "max_concurrent": 128}
     out.update(chunked)
     out.update({"row_budget": rows, "prefill_chunk": args.prefill_chunk,
                 "note": "continuous batching, requests admitted as others finish; each step feeds every decoding "
-                        "request's last token, then prompt chunks within the row budget",
+                        "request's last token, then prompt chunks within the row budget; f32 KV pages hold the "
+                        "reference's KVCache values",
                 "token_by_token": tbt, "stream_agreement": stream_agreement(streams_c, streams_t),
                 "steady_decode": steady})
+    out.update(extras)
     return out
+
+
+def run_schedule(e, work, max_rows, chunk):
+    """One continuous-batching run of `work` [(prompt, max tokens)] through 128
+    slots; aggregate generated tok/s, and the host's share of the wall time:
+    the scheduler's own Python work plus the engine's host-side preparation of
+    each step (the device idles meanwhile: every step ends in a synchronisation)."""
+    from qraf_amd.engine import BatchScheduler
+    sched = BatchScheduler(e, max_batch=128, max_rows=max_rows, prefill_chunk=chunk)
+    for p, o in work:
+        sched.submit(p, o)
+    e.stats(reset=True)
+    t0 = time.perf_counter()
+    done = sched.run()
+    el = time.perf_counter() - t0
+    st = e.stats(reset=True)
+    gen = sum(len(r.generated) for r in done)
+    host_ms = (sched.host_s * 1e3 + st["host_us"] * 1e-3) / sched.steps
+    return {"generated_tokens": gen, "steps": sched.steps, "rows_processed": sched.rows, "wall_s": round(el, 3),
+            "generated_tok_s": round(gen / el, 1), "rows_per_s": round(sched.rows / el, 1),
+            "ms_per_step": round(el / sched.steps * 1e3, 3),
+            "host_ms_per_step": round(host_ms, 3), "host_share": round(host_ms / (el / sched.steps * 1e3), 4),
+            "scheduler_python_ms_per_step": round(sched.host_s * 1e3 / sched.steps, 3),
+            "engine_host_prep_ms_per_step": round(st["host_us"] * 1e-3 / sched.steps, 3)}, \
+        [r.generated for r in sorted(done, key=lambda r: r.id)]
 
 
 def fnv1a(name: str) -> int:
@@ -655,8 +741,9 @@ def cpu_sampler():
 
 def bench_steady_b128(args, rt):
     """The steady 128-sequence decode alone (every GEMM at 128 rows), for profiling."""
-    e = qwen_engine(args, 128)
-    out = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps)
+    kv = {"f32": F32, "fp16": F16, "int8": I8}[args.kv]
+    e = qwen_engine(args, 128, kv)
+    out = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, kv)
     e.close()
     return out
 
@@ -672,7 +759,11 @@ def stream_agreement(a, b):
             "median_first_difference": int(np.median(first))}
 
 
-def steady_decode_b128(e, rng, steps):
+QWEN_LAYER_WEIGHT_BYTES = 1560674304  # 36 layers of Q4_0 q/k/v/o/gate/up/down
+QWEN_HEAD_BYTES = 175030272           # the tied Q4_0 embedding read as the head
+
+
+def steady_decode_b128(e, rng, steps, kv):
     """128 concurrent sequences at ragged contexts (prompt U[16,512] plus U[0,255] generated, the run above's
     distribution), prefilled in 128-row steps; then `steps` decode steps of 128 rows, every row generating
     (greedy, device argmax).  Timed: the decode steps only."""
@@ -696,9 +787,14 @@ def steady_decode_b128(e, rng, steps):
     el = time.perf_counter() - t0
     for s in seqs:
         e.seq_release(s)
-    return {"sequences": n, "context_mean_at_start": round(float(ctx.mean()) + 3, 1),
-            "context_max_at_end": int(pos.max()), "decode_steps": steps, "ms_per_step": round(el / steps * 1e3, 3),
-            "decode_tok_s": round(n * steps / el, 1)}
+    # HBM bytes per step: every layer weight, the head, and every cached K/V position read once
+    mean_ctx = float(ctx.mean()) + 3 + (steps + 1) / 2
+    by = QWEN_LAYER_WEIGHT_BYTES + QWEN_HEAD_BYTES + KV_POS_BYTES[kv] * mean_ctx * n
+    ms = el / steps * 1e3
+    return {"kv_pages": KV_NAMES[kv], "sequences": n, "context_mean_at_start": round(float(ctx.mean()) + 3, 1),
+            "context_max_at_end": int(pos.max()), "decode_steps": steps, "ms_per_step": round(ms, 3),
+            "decode_tok_s": round(n * steps / el, 1), "alg_bytes_per_step": int(by),
+            "GB_s": round(by / (ms * 1e-3) / 1e9, 1), "frac_hbm_peak": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
 # --------------------------------------------------------------------------- main
@@ -721,7 +817,9 @@ def main():
     ap.add_argument("--gemm-cases", default="",
                     help="restrict the GEMM leg to these cases, e.g. 'q4_0 11008x2048 B=128' (comma-separated)")
     ap.add_argument("--no-graphs", action="store_true",
-                    help="decode legs launch every step's kernels eagerly instead of replaying step graphs")
+                    help="launch every kernel eagerly (timed with events) instead of replaying captured graphs, "
+                         "in every leg")
+    ap.add_argument("--kv", default="f32", choices=["f32", "fp16", "int8"], help="KV pages of the steady_b128 leg")
     ap.add_argument("--rows-per-wave", type=int, default=0)
     ap.add_argument("--kernel", type=int, default=0,
                     help="matvec kernel: 0 auto, 1 one-shot, 2 persistent, 3 ring (8-wave groups), 4 ring (4-wave groups)")
@@ -739,7 +837,8 @@ def main():
 
     qraf_amd.backend.backend_init(0)
     call("qraf_hip_set_matvec_tuning", args.kernel, args.rows_per_wave, args.wgs_per_cu)
-    rt = dict(call=call, DeviceBuffer=DeviceBuffer, Event=Event, Graph=Graph, stream=Stream(), lib=qraf_amd.lib)
+    rt = dict(call=call, DeviceBuffer=DeviceBuffer, Event=Event, Graph=Graph, stream=Stream(), lib=qraf_amd.lib,
+              eager=args.no_graphs)
 
     value, total_ms, per_case, cache_res, hosts = bench_matvec(args, rt)
     print(f"# matvec done: {value:.1f} GB/s", file=sys.stderr, flush=True)
@@ -768,6 +867,8 @@ def main():
             extra["cpu_decode_b1"] = cpu_decode_b1()
         if "sampler" in only:
             extra["cpu_sampler"] = cpu_sampler()
+        if "decode_b128" in only:
+            extra["cpu_decode_b128"] = cpu_decode_qwen(rt)
         print("# cpu baseline done", file=sys.stderr, flush=True)
 
     out = {"metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,

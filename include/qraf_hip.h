@@ -91,18 +91,18 @@ int qraf_hip_graph_destroy(void* graph_exec);
 int qraf_hip_register_weights(const void* host_ptr, uint64_t bytes);
 int qraf_hip_unregister_weights(const void* host_ptr);
 
-/* dispatch_matvec_q (backend.h:35-38, backend.cpp:131-199):
+/* dispatch_matvec_q (backend.h:31-34, backend.cpp:131-199):
  * y[i] = dot(row_i(w), x) for i < out_dim; w in the reference's Q8_0/Q4_0
  * block layout with `block_size` (0 means 32, as backend.cpp:135).
  * w_size may be 0 (unchecked, as the reference) or the buffer size. */
 int qraf_hip_matvec_q(const void* w, uint64_t w_size, uint32_t dtype, uint32_t block_size,
                       uint32_t out_dim, uint32_t in_dim, const float* x, float* y);
-/* dispatch_matvec_opt (backend.h:31-32, backend.cpp:62-105). */
+/* dispatch_matvec_opt (backend.h:27-28, backend.cpp:62-105). */
 int qraf_hip_matvec_f32(const float* W, const float* x, float* y, uint32_t out_dim, uint32_t in_dim);
-/* dispatch_dot_f32 (backend.h:41, backend.cpp:109-127). */
+/* dispatch_dot_f32 (backend.h:37, backend.cpp:109-127). */
 int qraf_hip_dot_f32(const float* a, const float* b, int n, float* result);
 /* dispatch_rms_norm / softmax / silu / add / mul / scale
- * (backend.h:44-49, backend.cpp:203-320). */
+ * (backend.h:40-45, backend.cpp:203-320). */
 int qraf_hip_rms_norm(float* x, const float* weight, int size, float eps);
 int qraf_hip_softmax(float* x, int size);
 int qraf_hip_silu(float* x, int size);
@@ -379,6 +379,22 @@ int qraf_engine_set_graphs(qraf_engine* engine, int32_t on);
 int qraf_engine_sample(qraf_engine* engine, int32_t row0, int32_t rows, const qraf_sampling_params* params,
                        const uint32_t* recent, const int32_t* recent_count, int32_t recent_stride,
                        const float* uniforms, uint32_t* tokens);
+/* The last step's logit rows row0 .. row0+rows-1 (the rows it returned
+ * logits or argmax for, in order) copied from HBM to out [rows][vocab]: a
+ * step can keep its logits on the device and a caller read back only the
+ * rows it inspects.  No reference counterpart (Transformer::forward returns
+ * every logit by value, transformer.cpp:622-639). */
+int qraf_engine_read_logits(qraf_engine* engine, int32_t row0, int32_t rows, float* out);
+/* Host-side cost of qraf_engine_step, accumulated since the last reset:
+ * host_us = time from entry until every launch and copy of the step was
+ * issued (validation, page bookkeeping, staging, graph launch), wait_us =
+ * time blocked in the step's final stream synchronisation.  No reference
+ * counterpart (a measurement aid). */
+typedef struct qraf_engine_stats {
+    uint64_t steps, rows;
+    double host_us, wait_us;
+} qraf_engine_stats;
+int qraf_engine_get_stats(qraf_engine* engine, qraf_engine_stats* stats, int32_t reset);
 /* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)
  * on the engine's default sequence, and Transformer::reset() (:641-643). */
 int qraf_engine_forward(qraf_engine* engine, uint32_t token, int32_t pos, float* logits);

@@ -96,6 +96,11 @@ class EngineOptions(C.Structure):
     _fields_ = [(n, C.c_uint32) for n in ("kv_dtype", "page_size", "max_batch", "num_pages")]
 
 
+class EngineStats(C.Structure):
+    """qraf_engine_stats (include/qraf_hip.h)."""
+    _fields_ = [("steps", C.c_uint64), ("rows", C.c_uint64), ("host_us", C.c_double), ("wait_us", C.c_double)]
+
+
 class SamplingParams(C.Structure):
     """qraf_sampling_params (include/qraf_hip.h)."""
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_int32), ("top_p", C.c_float),
@@ -120,6 +125,8 @@ SIGNATURES.update({
     "qraf_engine_step": (C.c_int, [vp, C.c_int32, i32p, u32p, i32p, C.POINTER(C.c_uint8), fp, u32p]),
     "qraf_engine_set_graphs": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_forward": (C.c_int, [vp, C.c_uint32, C.c_int32, fp]),
+    "qraf_engine_read_logits": (C.c_int, [vp, C.c_int32, C.c_int32, fp]),
+    "qraf_engine_get_stats": (C.c_int, [vp, vp, C.c_int32]),
     "qraf_engine_reset": (C.c_int, [vp]),
     "qraf_file_read_config": (C.c_int, [C.c_char_p, C.POINTER(ModelConfig), u32p]),
     "qraf_engine_create_from_file": (C.c_int, [C.c_char_p, C.POINTER(EngineOptions), C.POINTER(vp)]),

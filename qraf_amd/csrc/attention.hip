@@ -1434,7 +1434,10 @@ extern "C" {
 int qraf_hip_set_attention_tuning(int32_t form) {
     qraf_hip::clear_error();
     QH_REQUIRE(form >= 0 && form <= 2, QRAF_HIP_ERR_INVALID, "attention tuning: form %d", form);
-    qraf_hip::g_attn_form = form;
+    if (qraf_hip::g_attn_form != form) {
+        qraf_hip::g_attn_form = form;
+        qraf_hip::bump_tuning_generation();  // captured engine steps are rebuilt with the new form
+    }
     return QRAF_HIP_OK;
 }
 

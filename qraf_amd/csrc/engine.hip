@@ -27,6 +27,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <chrono>
 #include <string>
 #include <vector>
 
@@ -334,6 +335,7 @@ struct qraf_engine {
     std::vector<Seq> seqs;
     int32_t default_seq = -1;
     int last_logit_rows = 0;          // logit rows the last step left in `logits`
+    qraf_engine_stats stats{};        // host-side time of qraf_engine_step
     uint8_t* samp = nullptr;          // sampling staging: recent tokens, counts, uniforms, tokens
     size_t samp_cap = 0;
 
@@ -832,9 +834,14 @@ int qraf_engine_free_pages(qraf_engine* e, int32_t* n) {
     return QRAF_HIP_OK;
 }
 
+static double now_us() {
+    return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
 int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const uint32_t* tokens,
                      const int32_t* positions, const uint8_t* want_logits, float* logits, uint32_t* next_tokens) {
     clear_error();
+    const double t_enter = now_us();
     QH_REQUIRE(e && seq_ids && tokens && positions, QRAF_HIP_ERR_INVALID, "step: null argument");
     QH_REQUIRE(e->finalized, QRAF_HIP_ERR_STATE, "step: engine not finalized");
     QH_REQUIRE(n > 0 && n <= (int32_t)e->o.max_batch, QRAF_HIP_ERR_INVALID, "step: %d rows (max_batch %u)", n,
@@ -1088,9 +1095,39 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
     e->last_logit_rows = head ? n_logit_rows : 0;
     if (head && logits)
         QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_rows * V * 4, hipMemcpyDeviceToHost, s));
+    // tokens come back through pinned staging: an async copy into pageable
+    // memory would block the host until the whole step has run
     if (head && next_tokens)
-        QH_CHECK_HIP(hipMemcpyAsync(next_tokens, e->amax, (size_t)n_logit_rows * 4, hipMemcpyDeviceToHost, s));
+        QH_CHECK_HIP(hipMemcpyAsync(e->h_amax, e->amax, (size_t)n_logit_rows * 4, hipMemcpyDeviceToHost, s));
+    const double t_issued = now_us();
     QH_CHECK_HIP(hipStreamSynchronize(s));
+    const double t_done = now_us();
+    if (head && next_tokens) memcpy(next_tokens, e->h_amax, (size_t)n_logit_rows * 4);
+    e->stats.steps += 1;
+    e->stats.rows += (uint64_t)n;
+    e->stats.host_us += t_issued - t_enter;
+    e->stats.wait_us += t_done - t_issued;
+    return QRAF_HIP_OK;
+}
+
+// The logit rows the last step left in HBM (rows row0 .. row0+rows-1 of them) -> host.
+int qraf_engine_read_logits(qraf_engine* e, int32_t row0, int32_t rows, float* out) {
+    clear_error();
+    QH_REQUIRE(e && out && rows > 0 && row0 >= 0, QRAF_HIP_ERR_INVALID, "read_logits: bad arguments");
+    QH_REQUIRE(row0 + rows <= e->last_logit_rows, QRAF_HIP_ERR_STATE,
+               "read_logits: rows %d..%d, the last step left %d logit rows", row0, row0 + rows - 1, e->last_logit_rows);
+    const size_t V = e->c.vocab_size;
+    QH_CHECK_HIP(hipMemcpyAsync(out, e->logits + (size_t)row0 * V, (size_t)rows * V * 4, hipMemcpyDeviceToHost,
+                                e->stream));
+    QH_CHECK_HIP(hipStreamSynchronize(e->stream));
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_get_stats(qraf_engine* e, qraf_engine_stats* out, int32_t reset) {
+    clear_error();
+    QH_REQUIRE(e && out, QRAF_HIP_ERR_INVALID, "get_stats: null argument");
+    *out = e->stats;
+    if (reset) e->stats = qraf_engine_stats{};
     return QRAF_HIP_OK;
 }
 

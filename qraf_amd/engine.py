@@ -23,12 +23,14 @@ from __future__ import annotations
 import ctypes as C
 import os
 import random
+import time
 from collections import deque
 from dataclasses import dataclass, field
 
 import numpy as np
 
-from ._lib import F16, F32, Q4_0, Q8_0, EngineOptions, ModelConfig, SamplingParams, call, fp, i32p, lib, u32p
+from ._lib import (F16, F32, Q4_0, Q8_0, EngineOptions, EngineStats, ModelConfig, SamplingParams, call, fp, i32p, lib,
+                   u32p)
 
 __all__ = ["Engine", "Transformer", "InferenceEngine", "BatchScheduler", "Request", "model_config",
            "read_file_config", "SamplingConfig", "Sampler"]
@@ -191,6 +193,20 @@ class Engine:
         return lg, nx
 
 
+    def read_logits(self, row0: int, rows: int = 1) -> np.ndarray:
+        """Logit rows row0 .. row0+rows-1 of the last step (in the order of the
+        rows that wanted logits), read back from HBM."""
+        out = np.empty((rows, self.vocab), np.float32)
+        call("qraf_engine_read_logits", self.h, row0, rows, out.ctypes.data_as(fp))
+        return out
+
+    def stats(self, reset: bool = False) -> dict:
+        """Host-side time of the steps so far: host_us until every launch was
+        issued, wait_us blocked on the device at the step's end."""
+        st = EngineStats()
+        call("qraf_engine_get_stats", self.h, C.byref(st), int(bool(reset)))
+        return {"steps": st.steps, "rows": st.rows, "host_us": st.host_us, "wait_us": st.wait_us}
+
     def sample(self, params: SamplingParams, recent=None, uniforms=None, row0=0, rows=None) -> np.ndarray:
         """Sampler::apply_repetition_penalty + Sampler::sample on rows row0.. of
         the last step's logit rows, on the device.  recent: one token list per
@@ -331,6 +347,7 @@ class Request:
     state: str = "QUEUED"  # QUEUED -> PREFILLING -> DECODING -> DONE
     seq: int = -1
     next_prompt: int = 0
+    admit_step: int = -1  # scheduler step at which the request took a slot
 
 
 class BatchScheduler:
@@ -369,6 +386,9 @@ class BatchScheduler:
         self._next_id = 1
         self.steps = 0
         self.rows = 0
+        self.host_s = 0.0    # time in step() outside the engine's calls (admission, row building, retirement)
+        self.engine_s = 0.0  # time inside the engine's step and sample calls
+        self.observer = None  # observer(scheduler, requests of this step's logit rows, next tokens) after each step
 
     def submit(self, prompt_tokens, max_tokens, repetition_penalty=1.0, eos=None) -> int:
         if len(prompt_tokens) == 0:
@@ -383,6 +403,7 @@ class BatchScheduler:
             r = self.pending.popleft()
             r.seq = self.engine.seq_create()
             r.state = "PREFILLING"
+            r.admit_step = self.steps
             self.active.append(r)
 
     def _finish(self, r):
@@ -392,6 +413,7 @@ class BatchScheduler:
 
     def step(self) -> bool:
         """One scheduler iteration (process_step, batch_scheduler.h:239-273)."""
+        t_start = time.perf_counter()
         self._admit()
         if not self.active:
             return False
@@ -409,6 +431,7 @@ class BatchScheduler:
                 rows.append((r, r.prompt[i], i, i == len(r.prompt) - 1))
             budget -= c
         want = np.array([w for (_, _, _, w) in rows], np.uint8)
+        t_eng = time.perf_counter()
         lg, nx = self.engine.step([r.seq for (r, _, _, _) in rows], [t for (_, t, _, _) in rows],
                                   [p for (_, _, p, _) in rows], want_logits=want, logits=False, argmax=True)
         # rows with a repetition penalty: penalty + argmax again on the device,
@@ -423,6 +446,11 @@ class BatchScheduler:
                 gp = SamplingParams(0.0, 0, 1.0, lrows[i].penalty)
                 nx[i:j] = self.engine.sample(gp, [r.prompt + r.generated for r in lrows[i:j]], row0=i)
             i = j
+        t_eng_end = time.perf_counter()
+        self.engine_s += t_eng_end - t_eng
+        if self.observer is not None:
+            self.observer(self, lrows, nx)
+        t_obs = time.perf_counter() - t_eng_end
         self.steps += 1
         self.rows += len(rows)
         k = 0
@@ -445,6 +473,7 @@ class BatchScheduler:
         for r in retire:
             self.active.remove(r)
             self._finish(r)
+        self.host_s += time.perf_counter() - t_start - (t_eng_end - t_eng) - t_obs
         return True
 
     def run(self):

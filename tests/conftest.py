@@ -39,3 +39,15 @@ def hip():
     import qraf_amd
     qraf_amd.backend.backend_init(0)
     return qraf_amd
+
+
+@pytest.fixture(scope="session")
+def reference():
+    """The compiled reference (oracle/_ref/libqraf_ref.so).  GPU parity tests
+    that need it fail, not skip, when it is missing: it is built by
+    `make -C oracle all` where the reference checkout exists and travels with
+    the working tree."""
+    from oracle import pyoracle as po
+    if po.ref() is None:
+        pytest.fail("oracle/_ref/libqraf_ref.so (the compiled reference) is missing; build it with `make -C oracle all`")
+    return po.ref()

@@ -12,7 +12,7 @@ from oracle import pyoracle as po
 from tests.test_gpu_engine import SMALL, check_logits, upload
 
 pytestmark = [pytest.mark.gpu,
-              pytest.mark.skipif(po.ref() is None, reason="oracle/_ref (the compiled reference) is not built")]
+              pytest.mark.usefixtures("reference")]
 
 
 @pytest.mark.parametrize("name", ["q8_llama", "q4_qwen2_tied_bias", "f32_llama", "q8_hd64_gqa3"])

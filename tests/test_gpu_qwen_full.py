@@ -24,7 +24,7 @@ from tests.test_gpu_engine import check_logits
 GEN = 32  # greedy tokens of sequence 0 compared with the reference's
 
 pytestmark = [pytest.mark.gpu,
-              pytest.mark.skipif(po.ref() is None, reason="oracle/_ref (the compiled reference) is not built")]
+              pytest.mark.usefixtures("reference")]
 
 
 @pytest.mark.parametrize("n", [1, 128])

@@ -19,7 +19,7 @@ import pytest
 from oracle import pyoracle as po
 
 pytestmark = [pytest.mark.gpu,
-              pytest.mark.skipif(po.ref() is None, reason="oracle/_ref (the compiled reference) is not built")]
+              pytest.mark.usefixtures("reference")]
 
 u32p = C.POINTER(C.c_uint32)
 fp = C.POINTER(C.c_float)
