@@ -183,6 +183,21 @@ int qraf_hip_paged_attention_dev(const float* q, const void* k_cache, const void
                                  int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
                                  int32_t page_size, float scale, int32_t max_ctx, float* out, void* workspace,
                                  uint64_t workspace_bytes, void* stream);
+/* qraf_hip_paged_attention_dev without a workspace argument, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  No counterpart in the
+ * reference.  The workspace is a file-scope device array of
+ * qraf_hip_attention_noalloc_max_bytes() bytes (32 MiB) per GPU, resolved by
+ * qraf_hip_init (QRAF_HIP_ERR_STATE if that was not called on the current
+ * device); a shape whose qraf_hip_attention_workspace_bytes exceeds it is
+ * refused with QRAF_HIP_ERR_INVALID.  The call allocates nothing.  Every call
+ * on one GPU uses the same array: calls that overlap on one GPU (other
+ * streams, other threads) race. */
+int qraf_hip_paged_attention_noalloc_dev(const float* q, const void* k_cache, const void* v_cache, uint32_t kv_dtype,
+                                         const int32_t* page_table, int32_t max_pages_per_seq, const int32_t* ctx_lens,
+                                         int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                         int32_t page_size, float scale, int32_t max_ctx, float* out, void* stream);
+uint64_t qraf_hip_attention_noalloc_max_bytes(void);
 /* RoPE angle table, RopeCache::init (ops.cpp:179-193) computed on the host
  * with the host libm: table[pos*head_dim + i] = cos(pos*f_i),
  * table[pos*head_dim + i + 1] = sin(pos*f_i), f_i = 1/powf(theta, i/head_dim)

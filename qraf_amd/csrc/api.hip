@@ -98,7 +98,8 @@ int qraf_hip_init(int device) {
     QH_CHECK_HIP(hipGetDeviceCount(&n));
     QH_REQUIRE(device >= 0 && device < n, QRAF_HIP_ERR_INVALID, "device %d out of range (%d devices)", device, n);
     QH_CHECK_HIP(hipSetDevice(device));
-    return ensure_init();
+    QH_TRY(ensure_init());
+    return attn_scratch_init(device);
 }
 
 int qraf_hip_device_count(int* count) {

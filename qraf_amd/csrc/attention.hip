@@ -50,6 +50,7 @@
 #include <math.h>
 
 #include <algorithm>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -1427,9 +1428,67 @@ int launch_rope_append(const float* qkv, const float* bias, int n, int H, int Hk
     return QRAF_HIP_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Workspace of the no-allocation entry point (qraf_hip_paged_attention_noalloc_dev):
+// a file-scope device array, one copy per GPU, held until the process ends.
+// Host code never passes the array's name to a kernel (on the host it names a
+// stand-in, not device memory): qraf_hip_init resolves the array's device
+// address once per device with hipGetSymbolAddress, and only that address is
+// used afterwards.  Every call on one GPU shares the array; it keeps the last
+// call's contents, and nothing in it must start at zero (every partial a
+// merge reads is written earlier in the same call).
+// ---------------------------------------------------------------------------
+constexpr size_t ATTN_SCRATCH_BYTES = (size_t)32 << 20;
+static __device__ __align__(256) uint8_t scratch[ATTN_SCRATCH_BYTES];
+constexpr int ATTN_SCRATCH_DEVICES = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[ATTN_SCRATCH_DEVICES];
+
+int attn_scratch_init(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    QH_REQUIRE(device >= 0 && device < ATTN_SCRATCH_DEVICES, QRAF_HIP_ERR_INVALID,
+               "attention scratch: device %d beyond %d", device, ATTN_SCRATCH_DEVICES);
+    if (g_scratch_ptr[device]) return QRAF_HIP_OK;
+    void* p = nullptr;
+    QH_CHECK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    QH_REQUIRE(p, QRAF_HIP_ERR_HIP, "attention scratch: no device address on device %d", device);
+    g_scratch_ptr[device] = p;
+    return QRAF_HIP_OK;
+}
+
+static void* attn_scratch(int device) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    return device >= 0 && device < ATTN_SCRATCH_DEVICES ? g_scratch_ptr[device] : nullptr;
+}
+
 }  // namespace qraf_hip
 
 extern "C" {
+
+int qraf_hip_paged_attention_noalloc_dev(const float* q, const void* k_cache, const void* v_cache, uint32_t kv_dtype,
+                                         const int32_t* page_table, int32_t max_pages_per_seq, const int32_t* ctx_lens,
+                                         int32_t n_seqs, int32_t n_heads, int32_t n_kv_heads, int32_t head_dim,
+                                         int32_t page_size, float scale, int32_t max_ctx, float* out, void* stream) {
+    qraf_hip::clear_error();
+    QH_REQUIRE(n_seqs > 0 && n_seqs <= 1024 && n_heads > 0 && n_kv_heads > 0 && head_dim > 0 && max_ctx > 0,
+               QRAF_HIP_ERR_INVALID, "attention: bad shape (n_seqs %d, heads %d / %d, head_dim %d, max_ctx %d)",
+               n_seqs, n_heads, n_kv_heads, head_dim, max_ctx);
+    const size_t need = qraf_hip::attn_workspace_bytes(n_seqs, n_heads, n_kv_heads, head_dim, max_ctx);
+    QH_REQUIRE(need <= qraf_hip::ATTN_SCRATCH_BYTES, QRAF_HIP_ERR_INVALID,
+               "attention (no-allocation form): this shape needs %zu bytes of workspace, the scratch holds %zu "
+               "(n_seqs %d, heads %d, head_dim %d, max_ctx %d)",
+               need, qraf_hip::ATTN_SCRATCH_BYTES, n_seqs, n_heads, head_dim, max_ctx);
+    int dev = 0;
+    QH_CHECK_HIP(hipGetDevice(&dev));
+    void* ws = qraf_hip::attn_scratch(dev);
+    QH_REQUIRE(ws, QRAF_HIP_ERR_STATE, "attention (no-allocation form): qraf_hip_init was not called on device %d",
+               dev);
+    return qraf_hip::launch_attention(q, k_cache, v_cache, kv_dtype, page_table, max_pages_per_seq, ctx_lens, n_seqs,
+                                      n_heads, n_kv_heads, head_dim, page_size, scale, max_ctx, out, ws,
+                                      qraf_hip::ATTN_SCRATCH_BYTES, qraf_hip::as_stream(stream));
+}
+
+uint64_t qraf_hip_attention_noalloc_max_bytes(void) { return qraf_hip::ATTN_SCRATCH_BYTES; }
 
 int qraf_hip_set_attention_tuning(int32_t form) {
     qraf_hip::clear_error();

@@ -158,6 +158,9 @@ size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M, bool tiled = fa
 size_t tiled_weight_bytes(uint32_t dtype, int N, int K);
 int launch_repack_tiles(const void* W, uint32_t dtype, int N, int K, void* dst, hipStream_t s);
 size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx);
+// resolves the device address of the no-allocation attention workspace on
+// `device` (current); called once per device by qraf_hip_init
+int attn_scratch_init(int device);
 int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv_dtype, const int32_t* page_table,
                      int max_pages, const int32_t* ctx, int n, int H, int Hkv, int hd, int page_size, float scale,
                      int max_ctx, float* out, void* ws, size_t ws_bytes, hipStream_t st, uint16_t* out_hi = nullptr,

@@ -49,3 +49,16 @@ def test_argument_validation_without_device():
 def test_version_names_gfx950():
     from qraf_amd._lib import lib
     assert lib.qraf_hip_version().startswith(b"gfx950")
+
+
+def test_noalloc_attention_refuses_shapes_beyond_its_scratch():
+    """The no-allocation attention checks the workspace a shape needs against
+    its fixed scratch on the host, before it touches the device: a shape
+    beyond it is refused (no GPU needed)."""
+    from qraf_amd._lib import ERR_INVALID, lib
+    n, H, Hkv, hd, max_ctx = 1024, 64, 8, 128, 8192
+    assert lib.qraf_hip_attention_workspace_bytes(n, H, Hkv, hd, max_ctx) > lib.qraf_hip_attention_noalloc_max_bytes()
+    rc = lib.qraf_hip_paged_attention_noalloc_dev(None, None, None, 1, None, max_ctx // 16, None, n, H, Hkv, hd, 16,
+                                                  0.1, max_ctx, None, None)
+    assert rc == ERR_INVALID
+    assert b"scratch holds" in lib.qraf_hip_last_error()
