@@ -157,6 +157,16 @@ size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M, bool tiled = fa
 // tile-major copy of a Q8_0/Q4_0 matrix for launch_qgemm(..., tiled = true)
 size_t tiled_weight_bytes(uint32_t dtype, int N, int K);
 int launch_repack_tiles(const void* W, uint32_t dtype, int N, int K, void* dst, hipStream_t s);
+// Y = sum of S slices [S][MN] (+ add), in slice order
+int launch_reduce_slices(const float* part, int S, size_t MN, float* Y, const float* add, hipStream_t s);
+// MFMA-ready ("mx") weight copy and the large-batch GEMM on it (qgemm_mx.hip)
+size_t mx_weight_bytes(uint32_t dtype, int N, int K);
+int launch_repack_mx(const void* W, uint32_t dtype, int N, int K, void* dst, hipStream_t s);
+size_t qgemm_mx_partials_bytes(uint32_t dtype, int N, int K, int M);
+int launch_qgemm_mx(const void* W, uint32_t dtype, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
+                    float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, int* slices,
+                    uint16_t* silu_hi, uint16_t* silu_lo);
+int set_mx_tuning(int shape, int splits);
 size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx);
 // resolves the device address of the no-allocation attention workspace on
 // `device` (current); called once per device by qraf_hip_init
@@ -172,6 +182,35 @@ int launch_rope_append(const float* qkv, const float* bias, int n, int H, int Hk
 int launch_gen_weights(void* dst, uint32_t dtype, uint64_t count, uint64_t seed, uint64_t stream_id, float stddev,
                        hipStream_t s);
 int launch_quantize(const float* src, uint64_t count, uint32_t dtype, void* dst, hipStream_t s);
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+// ---------------------------------------------------------------- LDS staging
+// Direct-to-LDS 16-byte load: lane i writes LDS [lds + 16 i, +16) from its
+// own voffset.  Issued as inline asm so that the compiler tracks none of these
+// loads (it would otherwise wait for all of them before every LDS read it
+// cannot prove disjoint): the kernel counts them itself (vmcnt) and every
+// other vector memory access of the kernel happens after the final drain.
+__device__ __forceinline__ v4i make_rsrc_words(const void* p, uint32_t bytes) {
+    const uint64_t a = (uint64_t)p;
+    return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
+}
+__device__ __forceinline__ void dma16(v4i rsrc, uint32_t voff, const void* lds) {
+    const uint32_t m0v = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
+    __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
+                     :
+                     : "v"(voff), "s"(rsrc), "s"(m0v)
+                     : "memory", "m0");
+}
+
+__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_barrier" ::: "memory"); }
+
+// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14)
+template <int N>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
+}
+
 
 // Library default stream of the current device (created by qraf_hip_init).
 hipStream_t default_stream();

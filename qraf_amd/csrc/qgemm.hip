@@ -401,33 +401,6 @@ __global__ __launch_bounds__(64 * WM * WNW, 512 / (64 * WM * WNW)) void qgemm_ke
 // Blocks past the split's range (stage padding) are read from wherever the
 // clamped or out-of-range address points and not computed.
 // ---------------------------------------------------------------------------
-// Direct-to-LDS 16-byte load: lane i writes LDS [lds + 16 i, +16) from its
-// own voffset.  Issued as inline asm so that the compiler tracks none of these
-// loads (it would otherwise wait for all of them before every LDS read it
-// cannot prove disjoint): the kernel counts them itself (vmcnt) and every
-// other vector memory access of the kernel happens after the final drain.
-typedef int v4i __attribute__((ext_vector_type(4)));
-__device__ __forceinline__ v4i make_rsrc_words(const void* p, uint32_t bytes) {
-    const uint64_t a = (uint64_t)p;
-    return v4i{(int)(uint32_t)a, (int)(uint32_t)(a >> 32), (int)bytes, 0x00020000};
-}
-__device__ __forceinline__ void dma16(v4i rsrc, uint32_t voff, const void* lds) {
-    const uint32_t m0v = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds;
-    __asm__ volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, 0 offen lds"
-                     :
-                     : "v"(voff), "s"(rsrc), "s"(m0v)
-                     : "memory", "m0");
-}
-
-__device__ __forceinline__ void lds_barrier() { __asm__ volatile("s_barrier" ::: "memory"); }
-
-// s_waitcnt vmcnt(N) lgkmcnt(0) (gfx9 encoding: vmcnt bits 3:0 and 15:14)
-template <int N>
-__device__ __forceinline__ void wait_vm_lgkm0() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (0 << 8));
-}
-
 // The three stage buffers are file-scope LDS objects reached through
 // compile-time accessors: the compiler then sees that a DMA into one buffer
 // does not alias reads of another and inserts no waits of its own.
@@ -697,6 +670,13 @@ __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float* __restri
         if (add) v += add[i];
         Y[i] = v;
     }
+}
+
+int launch_reduce_slices(const float* part, int S, size_t MN, float* Y, const float* add, hipStream_t s) {
+    const int rgrid = (int)min((MN / 4 + 255) / 256 + 1, (size_t)2048);
+    hipLaunchKernelGGL(qgemm_reduce_kernel, dim3(rgrid), dim3(256), 0, s, part, S, MN, Y, add);
+    QH_CHECK_HIP(hipGetLastError());
+    return QRAF_HIP_OK;
 }
 
 struct QgPlan {
