@@ -327,17 +327,22 @@ def bench_attention(args, rt):
                                                 max_pages, dc.ptr, n, H, Hkv, hd, ps, np.float32(1 / math.sqrt(hd)),
                                                 max_ctx, out.ptr, ws.ptr, wsb, stream.h), 50)
 
-    def leg(kv, K, V, pos_bytes):
+    def leg(kv, K, V, pos_bytes, valu=False):
         us = timed(kv, K, V)  # balanced split (the default form)
-        call("qraf_hip_set_attention_tuning", 1)
+        forms = {"us_chunk_grid_form": 1}  # one workgroup per (sequence, 256-position chunk)
+        if valu:
+            forms["us_valu_kernel"] = 3  # the plain fp32 VALU kernel
+        other = {}
         try:
-            us_chunk = timed(kv, K, V)  # one workgroup per (sequence, 256-position chunk)
+            for name, f in forms.items():
+                call("qraf_hip_set_attention_tuning", f)
+                other[name] = round(timed(kv, K, V), 2)
         finally:
             call("qraf_hip_set_attention_tuning", 0)
         by = int(ctxs.sum()) * Hkv * pos_bytes * 2 + 2 * n * H * hd * 4
         return {"us": round(us, 2), "sum_ctx": int(ctxs.sum()), "alg_bytes": by,
                 "GB_s": round(by / (us * 1e-6) / 1e9, 1), "frac_hbm_peak": round(by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                "us_chunk_grid_form": round(us_chunk, 2)}
+                **other}
 
     # fp16 pages, N(0,1)
     kv_half = num_pages * Hkv * ps * hd
@@ -355,6 +360,12 @@ def bench_attention(args, rt):
         blocks[:, ps * hd:] = np.full((num_pages * Hkv, ps), 0.02, np.float32).view(np.uint8)
         buf.upload(blocks)
     res["int8_pages"] = leg(I8, K8, V8, hd + 4)
+    del K8, V8
+    # f32 pages (the reference's own KV precision), N(0,1)
+    K, V = DeviceBuffer(kv_half * 4), DeviceBuffer(kv_half * 4)
+    K.upload(rng.standard_normal(kv_half, dtype=np.float32))
+    V.upload(rng.standard_normal(kv_half, dtype=np.float32))
+    res["f32_pages"] = leg(F32, K, V, hd * 4, valu=True)
     return res
 
 

@@ -166,17 +166,19 @@ uint64_t qraf_hip_attention_workspace_bytes(int32_t n_seqs, int32_t n_heads, int
  * Query head h reads KV head h / (n_heads / n_kv_heads) (attention.cpp:127);
  * scale is 1/sqrt(head_dim) in the reference (attention.cpp:122).
  * head_dim 64 or 128 with n_heads / n_kv_heads in {1,2,3,4,6,8,12,16}, or
- * head_dim 16 or 32 with n_heads / n_kv_heads in {1,2,4,8}.  F16 pages with
- * head_dim 64/128, at most 16 query heads per KV head and a power-of-two
- * page_size >= 4 run on the matrix cores; I8 pages need that shape
- * (QRAF_HIP_ERR_INVALID otherwise) and always do.  Page
+ * head_dim 16 or 32 with n_heads / n_kv_heads in {1,2,4,8}.  F32 and F16
+ * pages with head_dim 64/128, at most 16 query heads per KV head and a
+ * power-of-two page_size >= 4 run on the matrix cores (F32 pages in fp32
+ * arithmetic throughout); I8 pages need that shape (QRAF_HIP_ERR_INVALID
+ * otherwise) and always do.  Page
  * contents at positions >= ctx are never used (NaN there is harmless). */
-/* Work decomposition of the matrix-core attention (fp16 / int8 pages,
- * process-wide): 1 = one workgroup per (sequence, 256-position chunk),
- * 2 = balanced split of the batch's 64-position tiles over the resident
- * workgroups, 0 = automatic (default: the split when n_seqs *
- * ceil(max_ctx / 256) exceeds 1024, else the chunk grid).  Results agree
- * within the attention tolerance, not bit for bit. */
+/* Work decomposition of the matrix-core attention (process-wide):
+ * 1 = one workgroup per (sequence, 256-position chunk), 2 = balanced split
+ * of the batch's 64-position tiles over the resident workgroups,
+ * 0 = automatic (default: the split when n_seqs * ceil(max_ctx / 256)
+ * exceeds 1024, else the chunk grid), 3 = the plain fp32 VALU kernel for F32
+ * and F16 pages (I8 pages: automatic).  Results agree within the attention
+ * tolerance, not bit for bit. */
 int qraf_hip_set_attention_tuning(int32_t form);
 int qraf_hip_paged_attention_dev(const float* q, const void* k_cache, const void* v_cache, uint32_t kv_dtype,
                                  const int32_t* page_table, int32_t max_pages_per_seq, const int32_t* ctx_lens,

@@ -36,17 +36,18 @@
 // value element q_v[d] * v_scale.
 //
 // The matrix-core kernels, attn_mfma_kernel (chunk grid) and
-// attn_split_kernel (balanced split), take fp16 or int8 pages, head_dim 64
-// or 128, up to 16 query heads per KV head and a power-of-two page_size
-// (pages addressed by shifts).  They run q.K^T and P.V on
+// attn_split_kernel (balanced split), take f32, fp16 or int8 pages, head_dim
+// 64 or 128, up to 16 query heads per KV head and a power-of-two page_size
+// (pages addressed by shifts).  fp16 and int8 pages run q.K^T and P.V on
 // v_mfma_f32_16x16x32_f16: K and V enter as stored (fp16, or int8 widened to
 // fp16, both exact), q and the probabilities as fp16 hi + lo pairs (q scaled
 // per head by a power of two so hi + lo carries 22 bits of it), products
 // accumulate in fp32.  int8 scales are applied in fp32: a K scale to each
 // position's score, a V scale folded into that position's probability
-// before the P.V product.  attn_decode_kernel (the rest) is plain fp32 VALU
-// code on the chunk grid: scores with thread = position, output with
-// thread = (head, dimension).
+// before the P.V product.  f32 pages run on v_mfma_f32_16x16x4_f32 with
+// every operand in fp32 as it is.  attn_decode_kernel (the other shapes, and
+// f32 / fp16 pages on request) is plain fp32 VALU code on the chunk grid:
+// scores with thread = position, output with thread = (head, dimension).
 #include <math.h>
 
 #include <algorithm>
@@ -285,6 +286,82 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4a __attribute__((ext_vector_type(4)));
 
+// page types of the matrix-core kernels
+enum : int { KV_F16 = 0, KV_I8 = 1, KV_F32 = 2 };
+
+// f32 pages (KV_F32) run q.K^T and P.V on v_mfma_f32_16x16x4_f32: K, V, q
+// and the probabilities enter as they are (fp32 products, fp32 sums), so no
+// split or range scaling is involved.  The tile decomposition is the fp16
+// one, with k = 4 per instruction:
+//   q.K^T k-step 4c+e: lane (l%16, s = l/16) gives K[position l%16][dim
+//     16c + 4s + e] and q[head l%16][same dim]; a lane's K operands of one
+//     tile are HD/16 float4 loads (the 4 lane groups read 64 contiguous
+//     bytes of each row per load);
+//   P.V k-step (tile t, r): lane gives P[head l%16][position 16t + 4s + r]
+//     (its own score register sc[t][r]) and V[that position][dim
+//     dvf(l%16, d)] for output tile d, dvf(j, d) = 4j + 64(d/4) + d%4, so a
+//     lane's V operands of one position are HD/64 float4 loads (16 lanes
+//     read 256 contiguous bytes of the row).
+// Output tile d, register r of lane (j, s) is O[head 4s + r][dvf(j, d)].
+__device__ __forceinline__ constexpr int dvf(int j, int d) { return 4 * j + 64 * (d >> 2) + (d & 3); }
+
+// K operands of one f32 score tile: position pc of page pg, the lane group's dims
+template <int HD>
+__device__ __forceinline__ void kload_f32(const AttnArgs& a, int pg, int kvh, int row, int seg,
+                                          float4 (&kb)[HD / 16]) {
+    const float* kr = (const float*)a.kc + (((size_t)pg * a.Hkv + kvh) * a.page_size + row) * HD + 4 * seg;
+#pragma unroll
+    for (int c = 0; c < HD / 16; c++) kb[c] = *(const float4*)(kr + 16 * c);
+}
+
+// V operands of one f32 P.V tile: 4 positions (rows r0 .. of page pg, each
+// clamped by the caller) x the lane's HD/16 dims
+template <int HD>
+__device__ __forceinline__ void vload_f32(const AttnArgs& a, int pg, int kvh, const int (&rows)[4], int l16,
+                                          float4 (&vb)[4][HD / 64]) {
+    const float* vp = (const float*)a.vc + ((size_t)pg * a.Hkv + kvh) * a.page_size * HD + 4 * l16;
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int i = 0; i < HD / 64; i++) vb[r][i] = *(const float4*)(vp + (size_t)rows[r] * HD + 64 * i);
+}
+
+// one f32 score tile: sc += K . q^T over all HD dims (q from LDS, row stride HD + 4)
+template <int HD>
+__device__ __forceinline__ void score_f32(const float* s_qrow, int seg, const float4 (&kb)[HD / 16], f32x4a& sc) {
+#pragma unroll
+    for (int c = 0; c < HD / 16; c++) {
+        const float4 qf = *(const float4*)(s_qrow + 16 * c + 4 * seg);
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kb[c].x, qf.x, sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kb[c].y, qf.y, sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kb[c].z, qf.z, sc, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_f32_16x16x4f32(kb[c].w, qf.w, sc, 0, 0, 0);
+    }
+}
+
+// one f32 P.V tile: o[d] += P[., 16t + 4s + r] V[16t + 4s + r, dvf(., d)], r = 0..3
+template <int HD>
+__device__ __forceinline__ void pv_f32(const f32x4a& p, const float4 (&vb)[4][HD / 64], f32x4a (&o)[HD / 16]) {
+#pragma unroll
+    for (int r = 0; r < 4; r++)
+#pragma unroll
+        for (int d = 0; d < HD / 16; d++) {
+            const float4 v = vb[r][d >> 2];
+            const float x = (d & 3) == 0 ? v.x : (d & 3) == 1 ? v.y : (d & 3) == 2 ? v.z : v.w;
+            o[d] = __builtin_amdgcn_mfma_f32_16x16x4f32(p[r], x, o[d], 0, 0, 0);
+        }
+}
+
+// f32 page rows of a lane's V operands for tile t of the 64 positions from
+// pw: positions pw + 16t + 4s + r, each clamped to ctx - 1.  The 4-position
+// group starts at a = min(pw + 16t + 4s, vlast), vlast = (ctx - 1) & ~3, so
+// every clamped row lies in a's page (page_size % 4 == 0).
+__device__ __forceinline__ void vrows_f32(int pw, int t, int seg, int ctx, int vlast, int psm, int (&rows)[4]) {
+    const int pa = min(pw + 16 * t + 4 * seg, vlast);
+#pragma unroll
+    for (int r = 0; r < 4; r++) rows[r] = min(pa + r, ctx - 1) & psm;
+}
+
 // zero the fp16 lanes of a 4-position run (2 dwords) at or past ctx
 __device__ __forceinline__ uint2 mask_run(uint2 v, int pos0, int ctx) {
     const int k = ctx - pos0;  // valid positions in the run (selects, no branches)
@@ -313,9 +390,10 @@ __device__ __forceinline__ f16x8 i8x8_to_f16x8(uint32_t w0, uint32_t w1) {
 // 4 workgroups per CU (at most 128 VGPRs): the K and V loads of one wave
 // already cover its own latency, more resident workgroups cover the
 // prologue and epilogue of the others
-template <int HD, bool I8>
+template <int HD, int KV>
 __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    constexpr bool I8 = KV == KV_I8, F32 = KV == KV_F32;
     constexpr int KK = HD / 32;  // MFMA k-steps per score tile
     // q.K^T k-step kk, lane group s = l/16 covers 8 dimensions starting at
     // kdim(kk, s).  fp16: 8*(4kk+s), so the 4 groups of one step read 64
@@ -325,11 +403,14 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     constexpr int DT = HD / 16;  // 16-dimension output tiles
     typedef typename std::conditional<I8, uint32_t, uint2>::type VRun;  // one 4-position V run
     constexpr int QS = HD + 8;   // q plane row stride (fp16): 16-byte reads of 16 rows hit distinct banks
-    __shared__ __align__(16) _Float16 s_q[2][16][QS];
+    // q: fp16 hi/lo planes [2][16][QS], or (f32 pages) f32 rows [16][HD + 4]
+    __shared__ __align__(16) float s_qbuf[16 * QS];
+    _Float16(*s_q)[16][QS] = (_Float16(*)[16][QS])s_qbuf;
+    float(*s_qf)[HD + 4] = (float(*)[HD + 4])s_qbuf;
     __shared__ float s_qs[16];
     __shared__ float s_m[4][16], s_l[4][16];
     __shared__ __align__(16) float s_kvs[2][4][64];  // int8: K, V scale of position pw + lane, per wave
-    extern __shared__ float s_odyn[];  // [4][G][HD]: the waves' partial outputs
+    extern __shared__ __align__(16) float s_odyn[];  // [4][G][HD]: the waves' partial outputs
     float(*s_o)[HD] = (float(*)[HD])s_odyn;  // s_o[wave * G + head][dim]
 
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -446,9 +527,18 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
         s_kvs[1][wave][lane] = vs_own;
     }
 
-    // ---- q of the G heads as fp16 hi + lo, scaled per head by 2^e so that
-    // max|q| lands in [2^14, 2^15): hi + lo then carries 22 bits of every
-    // element that matters at fp32 precision
+    // ---- q of the G heads: f32 rows for f32 pages; otherwise fp16 hi + lo,
+    // scaled per head by 2^e so that max|q| lands in [2^14, 2^15): hi + lo
+    // then carries 22 bits of every element that matters at fp32 precision
+    if constexpr (F32) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int h = wave + 4 * j;
+#pragma unroll
+            for (int i = 0; i < PER; i++) s_qf[h][lane + 64 * i] = qv[j][i];
+            if (lane == 0) s_qs[h] = a.scale;  // attention.cpp:134: dot * scale
+        }
+    } else {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int h = wave + 4 * j;
@@ -473,13 +563,35 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
         }
         if (lane == 0) s_qs[h] = a.scale / sigma;  // attention.cpp:134: dot * scale
     }
+    }
     __syncthreads();
 
     // ---- scores of 4 tiles: sc[t][r] = position pw + 16t + 4seg + r, head l16
     f32x4a sc[4];
 #pragma unroll
     for (int t = 0; t < 4; t++) sc[t] = f32x4a{0.f, 0.f, 0.f, 0.f};
-    if (active) {  // k-step outer: one step's q fragments live at a time
+    // f32 pages: K of two score tiles in flight, then V of the first two P.V
+    // tiles requested behind the last score tiles (their K registers free)
+    float4 vf0[4][HD / 64], vf1[4][HD / 64];
+    if constexpr (F32) {
+        if (active) {
+            float4 k0[HD / 16], k1[HD / 16];
+            auto krow = [&](int t) { return min(pw + 16 * t + l16, ctx - 1) & psm; };
+            kload_f32<HD>(a, kpg[0], kvh, krow(0), seg, k0);
+            kload_f32<HD>(a, kpg[1], kvh, krow(1), seg, k1);
+            score_f32<HD>(s_qf[l16], seg, k0, sc[0]);
+            kload_f32<HD>(a, kpg[2], kvh, krow(2), seg, k0);
+            score_f32<HD>(s_qf[l16], seg, k1, sc[1]);
+            kload_f32<HD>(a, kpg[3], kvh, krow(3), seg, k1);
+            score_f32<HD>(s_qf[l16], seg, k0, sc[2]);
+            int rows[4];
+            vrows_f32(pw, 0, seg, ctx, vlast, psm, rows);
+            vload_f32<HD>(a, vpg[0], kvh, rows, l16, vf0);
+            score_f32<HD>(s_qf[l16], seg, k1, sc[3]);
+            vrows_f32(pw, 1, seg, ctx, vlast, psm, rows);
+            vload_f32<HD>(a, vpg[1], kvh, rows, l16, vf1);
+        }
+    } else if (active) {  // k-step outer: one step's q fragments live at a time
         if (!I8) kload();
 #pragma unroll
         for (int kk = 0; kk < KK; kk++) {
@@ -500,7 +612,7 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
         }
     }
 
-    if (!I8 && active) {  // fp16: after the score tiles (their K registers are free again)
+    if (!I8 && !F32 && active) {  // fp16: after the score tiles (their K registers are free again)
         vload(0, va0, vb0);
         vload(1, va1, vb1);
     }
@@ -572,7 +684,19 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     f32x4a o[DT];
 #pragma unroll
     for (int d = 0; d < DT; d++) o[d] = f32x4a{0.f, 0.f, 0.f, 0.f};
-    if (active) {
+    if constexpr (F32) {
+        if (active) {
+            int rows[4];
+            pv_f32<HD>(sc[0], vf0, o);
+            vrows_f32(pw, 2, seg, ctx, vlast, psm, rows);
+            vload_f32<HD>(a, vpg[2], kvh, rows, l16, vf0);
+            pv_f32<HD>(sc[1], vf1, o);
+            vrows_f32(pw, 3, seg, ctx, vlast, psm, rows);
+            vload_f32<HD>(a, vpg[3], kvh, rows, l16, vf1);
+            pv_f32<HD>(sc[2], vf0, o);
+            pv_f32<HD>(sc[3], vf1, o);
+        }
+    } else if (active) {
         auto pv = [&](int b, const VRun (&ra)[DT], const VRun (&rb)[DT]) {
             f16x8 ph, pl;
 #pragma unroll
@@ -601,6 +725,18 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     }
 
     // ---- combine the 4 waves: o[d][r] = O[head 4seg+r][dim 16d+l16]
+    // (f32 pages: dim dvf(l16, d), four consecutive dims per float4)
+    if constexpr (F32) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int h = 4 * seg + r;
+            if (h < G)
+#pragma unroll
+                for (int i = 0; i < DT / 4; i++)
+                    *(float4*)&s_o[wave * G + h][dvf(l16, 4 * i)] =
+                        float4{o[4 * i][r], o[4 * i + 1][r], o[4 * i + 2][r], o[4 * i + 3][r]};
+        }
+    } else {
 #pragma unroll
     for (int d = 0; d < DT; d++)
 #pragma unroll
@@ -608,6 +744,7 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
             const int h = 4 * seg + r;
             if (h < G) s_o[wave * G + h][16 * d + l16] = o[d][r] * ounit;
         }
+    }
     __syncthreads();
     const size_t hbase = (size_t)s * a.H + kvh * G;
     if (nchunks == 1) {
@@ -654,20 +791,23 @@ constexpr int SPLIT_MAXN = 1024;   // sequences per launch (the batch bound)
 // 128, whose 148-168 registers per lane leave room for 3)
 constexpr int split_slots(int hd) { return 256 * (hd == 128 ? 3 : 4); }
 
-template <int HD, bool I8>
+template <int HD, int KV>
 __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(AttnArgs a, int G) {
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
+    constexpr bool I8 = KV == KV_I8, F32 = KV == KV_F32;
     constexpr int KK = HD / 32, DT = HD / 16, QS = HD + 8, PER = HD / 64;
     auto kdim = [](int kk, int sg) { return I8 ? 8 * (KK * sg + kk) : 8 * (4 * kk + sg); };
     typedef typename std::conditional<I8, uint32_t, uint2>::type VRun;
     typedef typename std::conditional<I8, uint4[KK / 2], f16x8[KK]>::type KRow;
-    __shared__ __align__(16) _Float16 s_q[2][16][QS];
+    __shared__ __align__(16) float s_qbuf[16 * QS];  // as in attn_mfma_kernel
+    _Float16(*s_q)[16][QS] = (_Float16(*)[16][QS])s_qbuf;
+    float(*s_qf)[HD + 4] = (float(*)[HD + 4])s_qbuf;
     __shared__ float s_qs[16];
     __shared__ float s_m[4][16], s_l[4][16], s_alpha[4][16];
     __shared__ __align__(16) float s_kvs[2][4][64];
     __shared__ int s_pref[SPLIT_MAXN + 1];
     __shared__ int s_tsum[64];
-    extern __shared__ float s_odyn[];
+    extern __shared__ __align__(16) float s_odyn[];
     float(*s_o)[HD] = (float(*)[HD])s_odyn;  // s_o[wave * G + head][dim]: running outputs
 
     const int tid = threadIdx.x;
@@ -831,6 +971,15 @@ __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(Attn
                 if (j + 4 < jb) ids_to(j + 4, kpg2, vpg2);
             }
         }
+        if constexpr (F32) {
+#pragma unroll
+            for (int jh = 0; jh < 4; jh++) {
+                const int h = wave + 4 * jh;
+#pragma unroll
+                for (int i = 0; i < PER; i++) s_qf[h][lane + 64 * i] = qv[jh][i];
+                if (lane == 0) s_qs[h] = a.scale;  // attention.cpp:134: dot * scale
+            }
+        } else {
 #pragma unroll
         for (int jh = 0; jh < 4; jh++) {
             const int h = wave + 4 * jh;
@@ -854,6 +1003,7 @@ __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(Attn
             }
             if (lane == 0) s_qs[h] = a.scale / sigma;  // attention.cpp:134: dot * scale
         }
+        }
         __syncthreads();
         const float qs = s_qs[l16];
 
@@ -872,10 +1022,30 @@ __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(Attn
                 s_kvs[0][wave][lane] = ks_own;
                 s_kvs[1][wave][lane] = vs_own;
             }
-            if (!I8) kload(j);
+            if (!I8 && !F32) kload(j);
             f32x4a sc[4];
 #pragma unroll
             for (int t = 0; t < 4; t++) sc[t] = f32x4a{0.f, 0.f, 0.f, 0.f};
+            // f32 pages: the chunk kernel's pipeline (K of two score tiles in
+            // flight, V of the first two P.V tiles behind the last score tiles)
+            float4 vf0[4][HD / 64], vf1[4][HD / 64];
+            if constexpr (F32) {
+                float4 k0[HD / 16], k1[HD / 16];
+                auto krow = [&](int t) { return min(pw + 16 * t + l16, ctx - 1) & psm; };
+                kload_f32<HD>(a, kpg[0], kvh, krow(0), seg, k0);
+                kload_f32<HD>(a, kpg[1], kvh, krow(1), seg, k1);
+                score_f32<HD>(s_qf[l16], seg, k0, sc[0]);
+                kload_f32<HD>(a, kpg[2], kvh, krow(2), seg, k0);
+                score_f32<HD>(s_qf[l16], seg, k1, sc[1]);
+                kload_f32<HD>(a, kpg[3], kvh, krow(3), seg, k1);
+                score_f32<HD>(s_qf[l16], seg, k0, sc[2]);
+                int rows[4];
+                vrows_f32(pw, 0, seg, ctx, vlast, psm, rows);
+                vload_f32<HD>(a, vpg[0], kvh, rows, l16, vf0);
+                score_f32<HD>(s_qf[l16], seg, k1, sc[3]);
+                vrows_f32(pw, 1, seg, ctx, vlast, psm, rows);
+                vload_f32<HD>(a, vpg[1], kvh, rows, l16, vf1);
+            } else
 #pragma unroll
             for (int kk = 0; kk < KK; kk++) {
                 const f16x8 qh = *(const f16x8*)&s_q[0][l16][kdim(kk, seg)];
@@ -893,7 +1063,7 @@ __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(Attn
                     sc[t] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, ql, sc[t], 0, 0, 0);
                 }
             }
-            if (!I8) {  // fp16: V after the score tiles (K's registers are free again)
+            if (!I8 && !F32) {  // fp16: V after the score tiles (K's registers are free again)
                 vload(j, 0, va0, vb0);
                 vload(j, 1, va1, vb1);
             }
@@ -984,8 +1154,20 @@ __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(Attn
                     o[d] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pl, vf, o[d], 0, 0, 0);
                 }
             };
-            pv(0, va0, vb0);
-            pv(1, va1, vb1);
+            if constexpr (F32) {
+                int rows[4];
+                pv_f32<HD>(sc[0], vf0, o);
+                vrows_f32(pw, 2, seg, ctx, vlast, psm, rows);
+                vload_f32<HD>(a, vpg[2], kvh, rows, l16, vf0);
+                pv_f32<HD>(sc[1], vf1, o);
+                vrows_f32(pw, 3, seg, ctx, vlast, psm, rows);
+                vload_f32<HD>(a, vpg[3], kvh, rows, l16, vf1);
+                pv_f32<HD>(sc[2], vf0, o);
+                pv_f32<HD>(sc[3], vf1, o);
+            } else {
+                pv(0, va0, vb0);
+                pv(1, va1, vb1);
+            }
 
             // the next tile's loads in flight while this tile's output is
             // folded into the wave's rows.  int8: its ids arrived during this
@@ -1009,6 +1191,28 @@ __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(Attn
                 }
             }
             // o[d][r] = O[head 4seg+r][dim 16d+l16]: row = row * alpha(head) + o * 2^e
+            // (f32 pages: dim dvf(l16, d), four consecutive dims per float4)
+            if constexpr (F32) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int h = 4 * seg + r;
+                    if (h < G) {
+                        const float al = s_alpha[wave][h];
+#pragma unroll
+                        for (int i = 0; i < DT / 4; i++) {
+                            float4* row = (float4*)&s_o[wave * G + h][dvf(l16, 4 * i)];
+                            const float4 x{o[4 * i][r], o[4 * i + 1][r], o[4 * i + 2][r], o[4 * i + 3][r]};
+                            if (first) {
+                                *row = x;
+                            } else {
+                                const float4 y = *row;
+                                *row = float4{__builtin_fmaf(y.x, al, x.x), __builtin_fmaf(y.y, al, x.y),
+                                              __builtin_fmaf(y.z, al, x.z), __builtin_fmaf(y.w, al, x.w)};
+                            }
+                        }
+                    }
+                }
+            } else
 #pragma unroll
             for (int r = 0; r < 4; r++) {
                 const int h = 4 * seg + r;
@@ -1164,7 +1368,8 @@ size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx) {
 // 0: automatic (the balanced split when the chunk grid would need more than
 // one round of resident workgroups, 4 per CU x 256 CUs, at the host-known
 // bound n x ceil(max_ctx / 256); below that the chunk grid, whose per-chunk
-// workgroups carry no share bookkeeping), 1: chunk grid, 2: balanced split
+// workgroups carry no share bookkeeping), 1: chunk grid, 2: balanced split,
+// 3: the plain fp32 VALU kernel for f32 and fp16 pages (int8 pages: automatic)
 static int g_attn_form = 0;
 
 int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv_dtype, const int32_t* page_table,
@@ -1216,35 +1421,29 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     a.max_ctx = max_ctx;
     a.scale = scale;
     const int G = H / Hkv;
-    bool split = false;
-    if (kv_dtype == DT_F32) {
-        QH_TRY(launch_attn_t<float>(a, hd, G, items, st));
-    } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0 && ps_pow2 &&
-               (g_attn_form == 2 || (g_attn_form == 0 && items > 1024))) {
-        split = true;
-        const dim3 grid(a.gx, Hkv);
-        const size_t lds = 4 * G * hd * sizeof(float);
-        if (kv_dtype == DT_I8) {
-            if (hd == 128) hipLaunchKernelGGL((attn_split_kernel<128, true>), grid, dim3(ACH), lds, st, a, G);
-            else hipLaunchKernelGGL((attn_split_kernel<64, true>), grid, dim3(ACH), lds, st, a, G);
-        } else {
-            if (hd == 128) hipLaunchKernelGGL((attn_split_kernel<128, false>), grid, dim3(ACH), lds, st, a, G);
-            else hipLaunchKernelGGL((attn_split_kernel<64, false>), grid, dim3(ACH), lds, st, a, G);
-        }
-        QH_CHECK_HIP(hipGetLastError());
-    } else if ((hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0 && ps_pow2) {
-        const dim3 grid(items, Hkv);
-        const size_t lds = 4 * G * hd * sizeof(float);
-        if (kv_dtype == DT_I8) {
-            if (hd == 128) hipLaunchKernelGGL((attn_mfma_kernel<128, true>), grid, dim3(ACH), lds, st, a, G);
-            else hipLaunchKernelGGL((attn_mfma_kernel<64, true>), grid, dim3(ACH), lds, st, a, G);
-        } else {
-            if (hd == 128) hipLaunchKernelGGL((attn_mfma_kernel<128, false>), grid, dim3(ACH), lds, st, a, G);
-            else hipLaunchKernelGGL((attn_mfma_kernel<64, false>), grid, dim3(ACH), lds, st, a, G);
-        }
-        QH_CHECK_HIP(hipGetLastError());
+    const bool mfma_shape = (hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0 && ps_pow2;
+    const bool valu = !mfma_shape || (g_attn_form == 3 && kv_dtype != DT_I8);
+    const bool split = !valu && (g_attn_form == 2 || (g_attn_form != 1 && items > 1024));
+    if (valu) {  // the plain fp32 VALU kernel
+        if (kv_dtype == DT_F32) QH_TRY(launch_attn_t<float>(a, hd, G, items, st));
+        else QH_TRY(launch_attn_t<_Float16>(a, hd, G, items, st));
     } else {
-        QH_TRY(launch_attn_t<_Float16>(a, hd, G, items, st));
+        const int kind = kv_dtype == DT_I8 ? KV_I8 : kv_dtype == DT_F32 ? KV_F32 : KV_F16;
+        const dim3 grid(split ? a.gx : items, Hkv);
+        const size_t lds = 4 * G * hd * sizeof(float);
+#define QH_ATTN_MFMA(K, HDv, KINDv)                                                     \
+    if (kind == KINDv && hd == HDv) hipLaunchKernelGGL((K<HDv, KINDv>), grid, dim3(ACH), lds, st, a, G);
+        if (split) {
+            QH_ATTN_MFMA(attn_split_kernel, 128, KV_F16) QH_ATTN_MFMA(attn_split_kernel, 64, KV_F16)
+            QH_ATTN_MFMA(attn_split_kernel, 128, KV_I8) QH_ATTN_MFMA(attn_split_kernel, 64, KV_I8)
+            QH_ATTN_MFMA(attn_split_kernel, 128, KV_F32) QH_ATTN_MFMA(attn_split_kernel, 64, KV_F32)
+        } else {
+            QH_ATTN_MFMA(attn_mfma_kernel, 128, KV_F16) QH_ATTN_MFMA(attn_mfma_kernel, 64, KV_F16)
+            QH_ATTN_MFMA(attn_mfma_kernel, 128, KV_I8) QH_ATTN_MFMA(attn_mfma_kernel, 64, KV_I8)
+            QH_ATTN_MFMA(attn_mfma_kernel, 128, KV_F32) QH_ATTN_MFMA(attn_mfma_kernel, 64, KV_F32)
+        }
+#undef QH_ATTN_MFMA
+        QH_CHECK_HIP(hipGetLastError());
     }
     if (split) {  // a sequence may span several workgroups' shares
         const dim3 mg(n, H);
@@ -1492,7 +1691,7 @@ uint64_t qraf_hip_attention_noalloc_max_bytes(void) { return qraf_hip::ATTN_SCRA
 
 int qraf_hip_set_attention_tuning(int32_t form) {
     qraf_hip::clear_error();
-    QH_REQUIRE(form >= 0 && form <= 2, QRAF_HIP_ERR_INVALID, "attention tuning: form %d", form);
+    QH_REQUIRE(form >= 0 && form <= 3, QRAF_HIP_ERR_INVALID, "attention tuning: form %d", form);
     if (qraf_hip::g_attn_form != form) {
         qraf_hip::g_attn_form = form;
         qraf_hip::bump_tuning_generation();  // captured engine steps are rebuilt with the new form

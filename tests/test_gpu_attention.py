@@ -21,11 +21,11 @@ from oracle import pyoracle as po
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(params=[1, 2], ids=["chunk", "split"])
+@pytest.fixture(params=[1, 2, 3], ids=["chunk", "split", "valu"])
 def form(request, hip):
     """Both work decompositions of the matrix-core kernels (1: one workgroup
-    per 256-position chunk, 2: balanced split); the automatic choice is
-    restored afterwards."""
+    per 256-position chunk, 2: balanced split) and the plain VALU kernel (3);
+    the automatic choice is restored afterwards."""
     hip._lib.call("qraf_hip_set_attention_tuning", request.param)
     yield request.param
     hip._lib.call("qraf_hip_set_attention_tuning", 0)
