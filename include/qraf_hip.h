@@ -364,14 +364,16 @@ typedef struct qraf_sampling_params {
 /* Device pointers, stream-ordered: logits [rows][vocab] (penalised in
  * place), recent [rows][recent_stride] with recent_count [rows] valid
  * entries (may be NULL when repetition_penalty is 1), uniforms [rows] (may
- * be NULL when greedy), tokens [rows] out.  No device scope synchronisation
- * and no allocation.  top_k of at most 4096, or the whole vocabulary
- * (top_k <= 0 or >= vocab; QRAF_HIP_ERR_INVALID for 4096 < top_k < vocab).
- * The whole vocabulary is reproduced exactly from the tokens whose
- * exp(p - max) terms are not absorbed by the reference's sequential fp32
- * sums (at most 4096 of them per row, else that row's token is
- * QRAF_SAMPLE_TOO_MANY). */
-#define QRAF_SAMPLE_TOO_MANY 0xFFFFFFFFu
+ * be NULL when greedy), tokens [rows] out.  No device scope synchronisation.
+ * Every top_k (<= 0 or >= vocab: the whole vocabulary).  Candidate lists of
+ * at most 4096 tokens are sorted in on-chip memory; a whole-vocabulary row
+ * is reproduced exactly from the tokens whose exp(p - max) terms are not
+ * absorbed by the reference's sequential fp32 sums.  Larger candidate lists
+ * (4096 < top_k < vocab, or more than 4096 unabsorbed tokens) are sorted in
+ * sort storage of rows * vocab * 16 bytes that the library allocates on the
+ * device's first such call (temperature > 0 and top_k outside 1..4096),
+ * grows as needed and holds until the process ends; that first call must
+ * not be made under stream capture (QRAF_HIP_ERR_STATE). */
 int qraf_hip_sample_dev(float* logits, int32_t rows, int32_t vocab, const qraf_sampling_params* params,
                         const uint32_t* recent, const int32_t* recent_count, int32_t recent_stride,
                         const float* uniforms, uint32_t* tokens, void* stream);

@@ -141,8 +141,12 @@ __device__ __forceinline__ float sum_slices(const float* __restrict__ p, int S, 
     return acc;
 }
 
+// sort storage a sampling call needs (0: none): rows whose candidates may
+// exceed the in-LDS limit keep rows * V (p, index) pairs twice
+size_t sample_sort_bytes(int rows, int V, const qraf_sampling_params& sp);
 int launch_sample(float* logits, int rows, int V, const qraf_sampling_params& sp, const uint32_t* recent,
-                  const int32_t* counts, int stride, const float* uniforms, uint32_t* out, hipStream_t s);
+                  const int32_t* counts, int stride, const float* uniforms, uint32_t* out, void* sort_ws,
+                  size_t sort_bytes, hipStream_t s);
 
 // x may be S slices of `slice` floats each (GEMM partials), summed in slice order
 int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s,

@@ -338,6 +338,8 @@ struct qraf_engine {
     qraf_engine_stats stats{};        // host-side time of qraf_engine_step
     uint8_t* samp = nullptr;          // sampling staging: recent tokens, counts, uniforms, tokens
     size_t samp_cap = 0;
+    void* sort_ws = nullptr;          // sampling sort storage (large top_k, flat whole-vocabulary rows)
+    size_t sort_cap = 0;
 
     // activations (max_batch rows)
     float *h = nullptr, *xn = nullptr, *qkv = nullptr, *q = nullptr, *att = nullptr, *gu = nullptr, *act = nullptr,
@@ -1152,6 +1154,11 @@ int qraf_engine_sample(qraf_engine* e, int32_t row0, int32_t rows, const qraf_sa
         QH_TRY(ealloc(e, (void**)&e->samp, cap));  // held until the engine is destroyed
         e->samp_cap = cap;
     }
+    const size_t sort_need = sample_sort_bytes(rows, (int)e->c.vocab_size, *p);
+    if (sort_need > e->sort_cap) {
+        QH_TRY(ealloc(e, &e->sort_ws, sort_need));  // held until the engine is destroyed
+        e->sort_cap = sort_need;
+    }
     hipStream_t s = e->stream;
     uint32_t* d_tok = (uint32_t*)e->samp;
     float* d_uni = (float*)(e->samp + rb);
@@ -1163,12 +1170,10 @@ int qraf_engine_sample(qraf_engine* e, int32_t row0, int32_t rows, const qraf_sa
         QH_CHECK_HIP(hipMemcpyAsync(d_rec, recent, (size_t)rows * stride * 4, hipMemcpyHostToDevice, s));
     }
     QH_TRY(launch_sample(e->logits + (size_t)row0 * e->c.vocab_size, rows, (int)e->c.vocab_size, *p,
-                         pen ? d_rec : nullptr, pen ? d_cnt : nullptr, stride, greedy ? nullptr : d_uni, d_tok, s));
+                         pen ? d_rec : nullptr, pen ? d_cnt : nullptr, stride, greedy ? nullptr : d_uni, d_tok,
+                         e->sort_ws, e->sort_cap, s));
     QH_CHECK_HIP(hipMemcpyAsync(tokens, d_tok, (size_t)rows * 4, hipMemcpyDeviceToHost, s));
     QH_CHECK_HIP(hipStreamSynchronize(s));
-    for (int i = 0; i < rows; i++)
-        QH_REQUIRE(tokens[i] != QRAF_SAMPLE_TOO_MANY, QRAF_HIP_ERR_INVALID,
-                   "sample: row %d: more than 4096 tokens carry weight for the whole-vocabulary softmax", row0 + i);
     return QRAF_HIP_OK;
 }
 

@@ -22,7 +22,7 @@
 //      sequential sums, top-p prefix, renormalisation and the cumulative sum
 //      against the uniform by one thread.
 // cutoff = top_k when 0 < top_k < vocab, else vocab (sampler.cpp:73-77).
-// cutoff <= SAMPLE_MAX_CUTOFF takes the steps above.  cutoff = vocab > that
+// cutoff <= CAND_CAP takes the steps above.  cutoff = vocab > that
 // (top_k 0, the whole vocabulary) takes the absorbed-tail path: in the
 // reference's descending order the running sum only grows, so once a term
 // exp(p - max) is below half an ulp of the running sum it and every later
@@ -33,17 +33,26 @@
 // is >= S (1 - V 2^-28)); the reference's loops over the vocabulary then
 // equal the same loops over the gathered candidates, except that its
 // fallback (no cumulative sum reaches the uniform) is its last sorted token,
-// the smallest p (largest index among equal p in this order).  A row whose
-// gathered set exceeds CAND_CAP gets token SAMPLE_TOO_MANY.
+// the smallest p (largest index among equal p in this order).
+//
+// Rows whose candidates do not fit in LDS (a whole-vocabulary row whose
+// gathered set exceeds CAND_CAP, or CAND_CAP < top_k < vocab) keep their
+// (p, index) pairs in a per-row region of global sort storage: every pair
+// of the row (whole vocabulary), or the top_k pairs of step 2 gathered in
+// index order.  A stable LSD radix sort over the order-preserving keys (4
+// passes of 8 bits, descending digit order) sorts them by p descending with
+// equal p in index order, the LDS path's order; the reference's loops then
+// run over the sorted pairs, staged through LDS CAND_CAP at a time for the
+// sequential sums.
 #include <math.h>
+
+#include <mutex>
 
 #include "common.h"
 
 namespace qraf_hip {
 
-constexpr int SAMPLE_MAX_CUTOFF = 4096;
-constexpr int CAND_CAP = 4096;  // candidates gathered and sorted at most
-constexpr uint32_t SAMPLE_TOO_MANY = QRAF_SAMPLE_TOO_MANY;
+constexpr int CAND_CAP = 4096;  // candidates gathered and sorted in LDS at most
 
 constexpr int SNT = 1024;  // threads per row (16 waves)
 
@@ -149,9 +158,150 @@ __global__ __launch_bounds__(256) void penalty_rows_lds_kernel(float* __restrict
     }
 }
 
+// Stable LSD radix sort of n (p, index) pairs in global memory by p
+// descending, one workgroup: 4 passes of 8 key bits, each a histogram, an
+// exclusive scan and a scatter of SNT-pair tiles in pair order.  Within a
+// tile, a pair's rank among the earlier pairs of its digit is its rank among
+// its wave's lanes of that digit (lanes with the same digit found by 8
+// ballots, one per digit bit) plus the counts of that digit in the earlier
+// waves.  The pairs end in (pa, ia); (pb, ib) is the other buffer.
+// Waves of one workgroup share the CU's write-through L1, so a barrier
+// orders their global stores and loads.
+__device__ void radix_sort_pairs(float* pa, int* ia, float* pb, int* ib, int n, uint32_t* hist, int (*wcnt)[256],
+                                 int (*base)[256]) {
+    constexpr int NW = SNT / 64;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint64_t below = (1ull << lane) - 1;
+    float* sp = pa;
+    int* si = ia;
+    float* dp = pb;
+    int* di = ib;
+    for (int shift = 0; shift < 32; shift += 8) {
+        if (tid < 256) hist[tid] = 0;
+        __syncthreads();
+        for (int i = tid; i < n; i += SNT) atomicAdd(&hist[255u - ((order_key(sp[i]) >> shift) & 255u)], 1u);
+        __syncthreads();
+        if (tid == 0) {
+            int acc = 0;
+            for (int d = 0; d < 256; d++) {
+                base[0][d] = acc;
+                acc += (int)hist[d];
+            }
+        }
+        __syncthreads();
+        int cur = 0;
+        float np_ = tid < n ? sp[tid] : 0.f;  // the next tile's pair, requested a tile ahead
+        int ni = tid < n ? si[tid] : 0;
+        for (int t0 = 0; t0 < n; t0 += SNT) {
+            const int i = t0 + tid;
+            const bool ok = i < n;
+            const float p = np_;
+            const int ix = ni;
+            if (t0 + SNT + tid < n) {
+                np_ = sp[t0 + SNT + tid];
+                ni = si[t0 + SNT + tid];
+            }
+            const uint32_t d = 255u - ((order_key(p) >> shift) & 255u);
+            uint64_t peers = __ballot(ok);
+#pragma unroll
+            for (int b = 0; b < 8; b++) {
+                const uint64_t m = __ballot((d >> b) & 1u);
+                peers &= ((d >> b) & 1u) ? m : ~m;
+            }
+#pragma unroll
+            for (int k = 0; k < 4; k++) wcnt[wave][lane + 64 * k] = 0;  // the wave's own row: no barrier
+            if (ok && (peers & below) == 0) wcnt[wave][d] = __popcll(peers);
+            __syncthreads();
+            if (ok) {
+                int off = base[cur][d] + __popcll(peers & below);
+                for (int w = 0; w < wave; w++) off += wcnt[w][d];
+                dp[off] = p;
+                di[off] = ix;
+            }
+            if (tid < 256) {
+                int c = 0;
+#pragma unroll
+                for (int w = 0; w < NW; w++) c += wcnt[w][tid];
+                base[cur ^ 1][tid] = base[cur][tid] + c;
+            }
+            cur ^= 1;
+            __syncthreads();
+        }
+        float* tp = sp;
+        sp = dp;
+        dp = tp;
+        int* ti = si;
+        si = di;
+        di = ti;
+    }
+}
+
+// The reference's loops (sampler.cpp:79-127) over n sorted pairs in global
+// memory: exponentials and divisions elementwise by all threads, the
+// sequential sums by thread 0 over LDS-staged chunks of CAND_CAP, stopping
+// at the chunk where a cumulative sum reaches its bound.  Returns the token
+// (thread 0's value is the one used).
+__device__ uint32_t sorted_pairs_pick(float* pv, const int* iv, int n, float top_p, float r, float* stage,
+                                      float* s_val, int* s_pos) {
+    const int tid = threadIdx.x;
+    const float max_val = pv[0];
+    __syncthreads();
+    for (int i = tid; i < n; i += SNT) pv[i] = expf(pv[i] - max_val);
+    __syncthreads();
+    // sequential sum (or first reach of `bound`) over pv[0..m): thread 0's
+    // running sum over staged chunks; pos = index where cs >= bound, or -1
+    auto scan = [&](int m, float bound, bool stop_ge, float& total, int& pos) {
+        float cs = 0.f;
+        int at = -1;
+        for (int c0 = 0; c0 < m; c0 += CAND_CAP) {
+            const int cn = min(CAND_CAP, m - c0);
+            for (int j = tid; j < cn; j += SNT) stage[j] = pv[c0 + j];
+            __syncthreads();
+            if (tid == 0) {
+                for (int j = 0; j < cn; j++) {
+                    cs += stage[j];
+                    if (stop_ge ? cs >= bound : bound <= cs) {
+                        at = c0 + j;
+                        break;
+                    }
+                }
+                *s_val = cs;
+                *s_pos = at;
+            }
+            __syncthreads();
+            cs = *s_val;
+            at = *s_pos;
+            __syncthreads();
+            if (at >= 0) break;
+        }
+        total = cs;
+        pos = at;
+    };
+    float sum;
+    int unused;
+    scan(n, INFINITY, true, sum, unused);  // cs >= inf never holds: the whole sum
+    for (int i = tid; i < n; i += SNT) pv[i] /= sum;
+    __syncthreads();
+    int m = n;
+    if (top_p > 0.f && top_p < 1.f) {
+        // the nucleus sum is the same additions as the cumulative sum up to
+        // and including the nucleus' last term (both start from 0)
+        float ns;
+        int at;
+        scan(n, top_p, true, ns, at);
+        m = at < 0 ? n : at + 1;
+        for (int i = tid; i < m; i += SNT) pv[i] /= ns;
+        __syncthreads();
+    }
+    float cs;
+    int at;
+    scan(m, r, false, cs, at);
+    return (uint32_t)iv[at < 0 ? m - 1 : at];
+}
+
 __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restrict__ logits, int V, float T, int cutoff,
                                                           float top_p, const float* __restrict__ uniforms,
-                                                          uint32_t* __restrict__ out) {
+                                                          uint32_t* __restrict__ out, float* __restrict__ sort_ws) {
     const int tid = threadIdx.x, row = blockIdx.x;
     const float* l = logits + (size_t)row * V;
     __shared__ uint32_t hist[256];
@@ -163,6 +313,9 @@ __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restric
     __shared__ float s_red[2][NW];
     __shared__ int s_cnt[NW][8];
     __shared__ int s_n;
+    __shared__ int s_wcnt[NW][256], s_base[2][256];  // the global sort
+    __shared__ float s_sv;
+    __shared__ int s_sp;
 
     if (!(T > 0.f)) {  // Sampler::argmax (sampler.cpp:25-35): first index of the maximum
         float best = -INFINITY;
@@ -201,12 +354,19 @@ __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restric
     }
 
     // ---- the whole vocabulary (cutoff = V > CAND_CAP): gather the tokens
-    // whose terms are not absorbed (see the file comment)
-    const bool trunc = cutoff > CAND_CAP;
+    // whose terms are not absorbed (see the file comment); more than
+    // CAND_CAP of them, or CAND_CAP < top_k < V: the global sort
+    const bool trunc = cutoff == V && cutoff > CAND_CAP;
+    bool big = cutoff != V && cutoff > CAND_CAP;
     __shared__ uint32_t s_last;  // trunc: the reference's last sorted token
     int nsort = cutoff;
     bool fast = cutoff == V;  // every token a candidate
     float t = -INFINITY;
+    // the row's sort storage: pairs (pa, ia), the radix sort's other buffer (pb, ib)
+    float* pa = sort_ws + (size_t)row * 4 * V;
+    int* ia = (int*)(pa + V);
+    float* pb = pa + 2 * (size_t)V;
+    int* ib = (int*)(pa + 3 * (size_t)V);
     if (trunc) {
         float mx = -INFINITY, mn = INFINITY;
         int imn = -1;
@@ -262,18 +422,15 @@ __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restric
         __syncthreads();
         c = 0;
         for (int w = 0; w < NW; w++) c += s_cnt[w][0];
-        if (c > CAND_CAP) {
-            if (tid == 0) out[row] = SAMPLE_TOO_MANY;
-            return;
-        }
-        fast = true;  // gather p >= t below
+        big = c > CAND_CAP;
+        fast = !big;  // gather p >= t below, or sort every pair
     }
 
     // ---- fast path: a threshold t with cutoff <= #{p >= t} <= CAND_CAP, by an
     // 8-way search between the row's smallest and largest p; then every
     // p >= t is gathered and sorted.  The sort makes the result independent
     // of the gather order, and equal to the radix path's.
-    if (!fast) {
+    if (!fast && !big) {
         float mx = -INFINITY, mn = INFINITY;
         for_row(l, V, tid, [&](int, float v) {
             const float p = v / T;
@@ -355,6 +512,12 @@ __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restric
         });
         __syncthreads();
         nsort = s_n;
+    } else if (big && trunc) {  // every pair of the row, in index order
+        for (int i = tid; i < V; i += SNT) {
+            pa[i] = l[i] / T;
+            ia[i] = i;
+        }
+        nsort = V;
     } else {
     // ---- radix select of the cutoff-th largest key
     uint32_t prefix = 0, mask = 0, need = (uint32_t)cutoff;
@@ -385,7 +548,10 @@ __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restric
     const uint32_t tau = prefix;          // key of the cutoff-th largest p
     const int n_gt = cutoff - (int)need;  // candidates strictly above it
 
-    // ---- gather in index order: thread t owns [t*ch, (t+1)*ch)
+    // ---- gather in index order: thread t owns [t*ch, (t+1)*ch); into LDS,
+    // or the row's sort storage
+    float* gv = big ? pa : cval;
+    int* gi = big ? ia : cidx;
     const int ch = (V + SNT - 1) / SNT;
     const int lo = min(V, tid * ch), hi = min(V, lo + ch);
     int gt = 0, eq = 0;
@@ -413,18 +579,25 @@ __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restric
         const float p = l[i] / T;
         const uint32_t k = order_key(p);
         if (k > tau) {
-            cval[pg] = p;
-            cidx[pg] = i;
+            gv[pg] = p;
+            gi[pg] = i;
             pg++;
         } else if (k == tau) {
             if (pe < (int)need) {
-                cval[n_gt + pe] = p;
-                cidx[n_gt + pe] = i;
+                gv[n_gt + pe] = p;
+                gi[n_gt + pe] = i;
             }
             pe++;
         }
     }
     }  // radix path
+    if (big) {  // global sort, then the reference's loops over the sorted pairs
+        __syncthreads();
+        radix_sort_pairs(pa, ia, pb, ib, nsort, hist, s_wcnt, s_base);
+        const uint32_t pick = sorted_pairs_pick(pa, ia, nsort, top_p, uniforms[row], cval, &s_sv, &s_sp);
+        if (tid == 0) out[row] = pick;
+        return;
+    }
     int P = 1;
     while (P < nsort) P <<= 1;
     for (int i = nsort + tid; i < P; i += SNT) {
@@ -517,15 +690,23 @@ __global__ __launch_bounds__(SNT) void sample_rows_kernel(const float* __restric
     }
 }
 
+size_t sample_sort_bytes(int rows, int V, const qraf_sampling_params& sp) {
+    const bool greedy = !(sp.temperature > 0.f);
+    const int cutoff = (sp.top_k > 0 && sp.top_k < V) ? sp.top_k : V;
+    return greedy || cutoff <= CAND_CAP ? 0 : (size_t)rows * V * 16;
+}
+
 int launch_sample(float* logits, int rows, int V, const qraf_sampling_params& sp, const uint32_t* recent,
-                  const int32_t* counts, int stride, const float* uniforms, uint32_t* out, hipStream_t s) {
+                  const int32_t* counts, int stride, const float* uniforms, uint32_t* out, void* sort_ws,
+                  size_t sort_bytes, hipStream_t s) {
     QH_REQUIRE(logits && out && rows > 0 && V > 0, QRAF_HIP_ERR_INVALID, "sample: bad arguments");
     const bool greedy = !(sp.temperature > 0.f);
     const int cutoff = (sp.top_k > 0 && sp.top_k < V) ? sp.top_k : V;
-    QH_REQUIRE(greedy || cutoff <= SAMPLE_MAX_CUTOFF || cutoff == V, QRAF_HIP_ERR_INVALID,
-               "sample: top_k %d of vocab %d; the device sampler takes top_k <= %d or the whole vocabulary",
-               sp.top_k, V, SAMPLE_MAX_CUTOFF);
     QH_REQUIRE(greedy || uniforms, QRAF_HIP_ERR_INVALID, "sample: temperature %g needs uniforms", sp.temperature);
+    QH_REQUIRE(sort_bytes >= sample_sort_bytes(rows, V, sp) && (sort_ws || !sample_sort_bytes(rows, V, sp)),
+               QRAF_HIP_ERR_INVALID, "sample: sort storage of %zu bytes, %zu needed", sort_bytes,
+               sample_sort_bytes(rows, V, sp));
+    (void)cutoff;
     if (sp.repetition_penalty != 1.0f) {  // sampler.cpp:39
         QH_REQUIRE(!recent || (counts && stride > 0), QRAF_HIP_ERR_INVALID, "sample: recent tokens need counts");
         if (recent) {
@@ -539,7 +720,7 @@ int launch_sample(float* logits, int rows, int V, const qraf_sampling_params& sp
         }
     }
     hipLaunchKernelGGL(sample_rows_kernel, dim3(rows), dim3(SNT), 0, s, logits, V, sp.temperature, cutoff, sp.top_p,
-                       uniforms, out);
+                       uniforms, out, (float*)sort_ws);
     QH_CHECK_HIP(hipGetLastError());
     return QRAF_HIP_OK;
 }
@@ -548,11 +729,40 @@ int launch_sample(float* logits, int rows, int V, const qraf_sampling_params& sp
 
 using namespace qraf_hip;
 
+// Sort storage of qraf_hip_sample_dev, per device, grown on demand and held
+// until the process ends.
+namespace {
+std::mutex g_sort_mu;
+void* g_sort_ws[64];
+size_t g_sort_bytes[64];
+}  // namespace
+
 extern "C" int qraf_hip_sample_dev(float* logits, int32_t rows, int32_t vocab, const qraf_sampling_params* params,
                                    const uint32_t* recent, const int32_t* recent_count, int32_t recent_stride,
                                    const float* uniforms, uint32_t* tokens, void* stream) {
     clear_error();
-    QH_REQUIRE(params, QRAF_HIP_ERR_INVALID, "sample: null params");
-    return launch_sample(logits, rows, vocab, *params, recent, recent_count, recent_stride, uniforms, tokens,
-                         as_stream(stream));
+    QH_REQUIRE(params && rows > 0 && vocab > 0, QRAF_HIP_ERR_INVALID, "sample: bad arguments");
+    const size_t need = sample_sort_bytes(rows, vocab, *params);
+    void* ws = nullptr;
+    if (need) {
+        int dev = 0;
+        QH_CHECK_HIP(hipGetDevice(&dev));
+        QH_REQUIRE(dev >= 0 && dev < 64, QRAF_HIP_ERR_INVALID, "sample: device %d", dev);
+        std::lock_guard<std::mutex> lk(g_sort_mu);
+        if (g_sort_bytes[dev] < need) {
+            hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+            QH_CHECK_HIP(hipStreamIsCapturing(as_stream(stream), &cs));
+            QH_REQUIRE(cs == hipStreamCaptureStatusNone, QRAF_HIP_ERR_STATE,
+                       "sample: the sort storage (%zu bytes) is allocated by a first call outside stream capture",
+                       need);
+            if (g_sort_ws[dev]) QH_CHECK_HIP(hipFree(g_sort_ws[dev]));  // waits for work that may use it
+            g_sort_ws[dev] = nullptr;
+            g_sort_bytes[dev] = 0;
+            QH_CHECK_HIP(hipMalloc(&g_sort_ws[dev], need));
+            g_sort_bytes[dev] = need;
+        }
+        ws = g_sort_ws[dev];
+    }
+    return launch_sample(logits, rows, vocab, *params, recent, recent_count, recent_stride, uniforms, tokens, ws,
+                         need, as_stream(stream));
 }

@@ -9,7 +9,7 @@ Sampling parity is exact on the same logits unless a uniform lands within a
 rounding of a cumulative-probability boundary (device expf against glibc's
 expf); with continuous random logits that has probability of order 1e-6 per
 draw.  Ties between equal probabilities are not ordered by the reference
-(std::sort), so the inputs here have none.
+(std::sort), so the inputs here have none (tie_free).
 """
 import ctypes as C
 
@@ -50,6 +50,22 @@ def device_sample(hip, logits_rows, params, recent=None, uniforms=None):
     return out.download(np.uint32, rows), dl.download(np.float32, rows * V).reshape(rows, V)
 
 
+def tie_free(logits, T):
+    """The logits with every p = logit / T (float32, as both samplers
+    compute it) distinct: duplicates are moved up one ulp at a time.  The
+    reference's std::sort leaves equal p in an unspecified order, which a
+    large candidate list would otherwise reach."""
+    x = np.array(logits, np.float32)
+    for _ in range(64):
+        q = x / np.float32(T)
+        order = np.argsort(q, kind="stable")
+        dup = order[1:][q[order[1:]] == q[order[:-1]]]
+        if dup.size == 0:
+            return x
+        x[dup] = np.nextafter(x[dup], np.float32(np.inf))
+    raise AssertionError("could not separate equal probabilities")
+
+
 def ref_sample(logits, T, k, p, seed, n):
     out = np.zeros(n, np.uint32)
     l = np.ascontiguousarray(logits, np.float32)
@@ -63,12 +79,9 @@ def ref_sample(logits, T, k, p, seed, n):
 def test_sampling_equals_reference_sampler(hip, V, cfg):
     from qraf_amd.engine import Sampler, SamplingConfig
     T, k, p = cfg
-    if k == 0 and V > 4096:
-        pytest.skip("N(0,3) logits weigh too many tokens for the whole-vocabulary path "
-                    "(test_whole_vocabulary_equals_reference_sampler covers it)")
     rng = np.random.default_rng(V + int(T * 10) + k)
     n = 96
-    logits = (rng.standard_normal(V) * 3.0).astype(np.float32)
+    logits = tie_free((rng.standard_normal(V) * 3.0).astype(np.float32), T)
     seed = 1000 + k
     print(f"sampler V={V} T={T} top_k={k} top_p={p}", flush=True)
     want = ref_sample(logits, T, k, p, seed, n)
@@ -105,12 +118,22 @@ def test_first_index_of_equal_maxima(hip):
     assert got.tolist() == [7, 4094]
 
 
-def test_top_k_between_limit_and_vocab_is_refused(hip):
-    from qraf_amd._lib import ERR_INVALID, HipError
-    L = np.zeros((1, 8192), np.float32)
-    with pytest.raises(HipError) as e:
-        device_sample(hip, L, (0.8, 5000, 0.9, 1.0), uniforms=[0.5])
-    assert e.value.code == ERR_INVALID
+@pytest.mark.parametrize("V,k,T,p", [(8192, 5000, 0.8, 0.9), (151936, 4097, 0.9, 0.95), (151936, 60000, 1.5, 0.0),
+                                     (151936, 151935, 2.0, 0.8), (20000, 19999, 1.0, 0.999)])
+def test_top_k_above_lds_limit_equals_reference_sampler(hip, V, k, T, p):
+    """4096 < top_k < vocab: the top_k candidates are gathered and sorted in
+    global sort storage (radix sort), then the reference's loops run over
+    all of them."""
+    from qraf_amd.engine import Sampler, SamplingConfig
+    n = 24
+    rng = np.random.default_rng(V + k)
+    logits = tie_free((rng.standard_normal(V) * 3.0).astype(np.float32), T)
+    print(f"sampler V={V} top_k={k} T={T} top_p={p}", flush=True)
+    want = ref_sample(logits, T, k, p, 5 + k, n)
+    uni = Sampler(SamplingConfig(seed=5 + k)).uniforms(n)
+    got, _ = device_sample(hip, np.tile(logits, (n, 1)), (T, k, p, 1.0), uniforms=uni)
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {n} draws differ"
+    assert len(set(want.tolist())) > 3
 
 
 def zipf_logits(rng, V, exponent, scale=1.0, head=20.0):
@@ -144,14 +167,22 @@ def test_whole_vocabulary_equals_reference_sampler(hip, kind, T, p):
     assert len(set(want.tolist())) > 3
 
 
-def test_whole_vocabulary_too_many_weighted_tokens(hip):
-    """Rows whose weight spreads over more than 4096 tokens get
-    QRAF_SAMPLE_TOO_MANY (the engine's call turns it into an error)."""
-    V = 20000
-    rng = np.random.default_rng(5)
-    flat = rng.standard_normal((2, V)).astype(np.float32) * 0.1
-    got, _ = device_sample(hip, flat, (1.0, 0, 0.9, 1.0), uniforms=[0.5, 0.5])
-    assert got.tolist() == [0xFFFFFFFF, 0xFFFFFFFF]
+@pytest.mark.parametrize("V,p", [(20000, 0.9), (20000, 0.0), (151936, 0.5)])
+def test_flat_whole_vocabulary_equals_reference_sampler(hip, V, p):
+    """Rows whose weight spreads over more than 4096 tokens (nearly flat
+    logits): every pair of the row is sorted in global sort storage; the
+    uniforms include values near 1, where the cumulative sum runs to the
+    row's tail."""
+    from qraf_amd.engine import Sampler, SamplingConfig
+    n = 16
+    rng = np.random.default_rng(V + int(p * 10))
+    logits = tie_free((rng.standard_normal(V) * 0.1).astype(np.float32), 1.0)
+    print(f"sampler flat V={V} top_p={p}", flush=True)
+    want = ref_sample(logits, 1.0, 0, p, 9, n)
+    uni = Sampler(SamplingConfig(seed=9)).uniforms(n)
+    got, _ = device_sample(hip, np.tile(logits, (n, 1)), (1.0, 0, p, 1.0), uniforms=uni)
+    assert np.array_equal(got, want), f"{np.count_nonzero(got != want)} of {n} draws differ"
+    assert len(set(want.tolist())) > 3
 
 
 @pytest.mark.parametrize("k", [1500, 3000, 4096])
