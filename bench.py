@@ -338,7 +338,7 @@ def bench_attention(args, rt):
                 call("qraf_hip_set_attention_tuning", f)
                 other[name] = round(timed(kv, K, V), 2)
         finally:
-            call("qraf_hip_set_attention_tuning", 0)
+            call("qraf_hip_set_attention_tuning", rt["attn_form"])
         by = int(ctxs.sum()) * Hkv * pos_bytes * 2 + 2 * n * H * hd * 4
         return {"us": round(us, 2), "sum_ctx": int(ctxs.sum()), "alg_bytes": by,
                 "GB_s": round(by / (us * 1e-6) / 1e9, 1), "frac_hbm_peak": round(by / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
@@ -835,6 +835,8 @@ def main():
     ap.add_argument("--kernel", type=int, default=0,
                     help="matvec kernel: 0 auto, 1 one-shot, 2 persistent, 3 ring (8-wave groups), 4 ring (4-wave groups)")
     ap.add_argument("--wgs-per-cu", type=int, default=0)
+    ap.add_argument("--attn-form", type=int, default=0,
+                    help="attention work form for every leg: 0 auto, 1 chunk grid, 2 balanced split, 3 VALU kernel")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
@@ -848,8 +850,9 @@ def main():
 
     qraf_amd.backend.backend_init(0)
     call("qraf_hip_set_matvec_tuning", args.kernel, args.rows_per_wave, args.wgs_per_cu)
+    call("qraf_hip_set_attention_tuning", args.attn_form)
     rt = dict(call=call, DeviceBuffer=DeviceBuffer, Event=Event, Graph=Graph, stream=Stream(), lib=qraf_amd.lib,
-              eager=args.no_graphs)
+              eager=args.no_graphs, attn_form=args.attn_form)
 
     value, total_ms, per_case, cache_res, hosts = bench_matvec(args, rt)
     print(f"# matvec done: {value:.1f} GB/s", file=sys.stderr, flush=True)

@@ -7,6 +7,8 @@
 // hidden-size or context-length long) with a fixed tree order, so results
 // are deterministic run to run; they differ from the reference's sequential
 // fp32 sums only by summation order.
+#include <algorithm>
+
 #include "common.h"
 
 namespace qraf_hip {
@@ -115,23 +117,27 @@ int launch_ew(int op, float* x, const float* y, float sc, int n, hipStream_t s) 
     return QRAF_HIP_OK;
 }
 
-// Streaming read of a buffer (16-byte loads, grid-stride, two loads in flight
-// per thread): the plain-read ceiling a memory-bound kernel of the same bytes
-// is measured against.  Each wave writes the sum of what it read, so no load
-// is dead.  1024 workgroups of 256 threads: the best plain-read shape on
-// MI355X for 9-270 MB.
+// Streaming read of a buffer: the plain-read ceiling a memory-bound kernel of
+// the same bytes is measured against.  Grid-stride over 16-byte
+// nontemporal loads, 8 in flight per thread, 2048 workgroups of 256 threads
+// (one pass for buffers up to 64 MB).  Of the read shapes
+// swept on MI355X for one launch over 19-51 MB (grid-stride and contiguous
+// chunk per workgroup, 4-16 loads in flight per thread, 256-1024 threads,
+// 256 workgroups to one per chunk, plain and nontemporal loads) this one was
+// the fastest or within 1% of it.  Each wave writes the sum of what it read,
+// so no load is dead.
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-constexpr int RP_WGS = 1024, RP_WG = 256;
+constexpr int RP_WGS = 2048, RP_WG = 256, RP_U = 8;
 __global__ __launch_bounds__(RP_WG) void read_probe_kernel(const f32x4* __restrict__ p, size_t n4, float* out) {
-    f32x4 a = {0.f, 0.f, 0.f, 0.f}, b = {0.f, 0.f, 0.f, 0.f};
-    const size_t st = (size_t)gridDim.x * blockDim.x;
-    size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    for (; i + st < n4; i += 2 * st) {
-        a += __builtin_nontemporal_load(p + i);
-        b += __builtin_nontemporal_load(p + i + st);
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    const size_t step = (size_t)gridDim.x * RP_WG * RP_U;
+    for (size_t base = (size_t)blockIdx.x * RP_WG * RP_U + threadIdx.x; base < n4; base += step) {
+        f32x4 v[RP_U];
+#pragma unroll
+        for (int u = 0; u < RP_U; u++) v[u] = __builtin_nontemporal_load(p + std::min(base + (size_t)u * RP_WG, n4 - 1));
+#pragma unroll
+        for (int u = 0; u < RP_U; u++) a += base + (size_t)u * RP_WG < n4 ? v[u] : f32x4{0.f, 0.f, 0.f, 0.f};
     }
-    if (i < n4) a += p[i];
-    a += b;
     float v = (a[0] + a[1]) + (a[2] + a[3]);
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
@@ -143,6 +149,7 @@ size_t read_probe_out_floats() { return (size_t)RP_WGS * (RP_WG / 64); }
 int launch_read_probe(const void* p, size_t bytes, float* out, hipStream_t s) {
     QH_REQUIRE(p && out && bytes > 0 && bytes % 16 == 0 && ((uintptr_t)p & 15) == 0, QRAF_HIP_ERR_INVALID,
                "read probe: null or misaligned pointer, or bytes not a positive multiple of 16");
+    // always RP_WGS workgroups, so that every output slot is written (those past the data write 0)
     hipLaunchKernelGGL(read_probe_kernel, dim3(RP_WGS), dim3(RP_WG), 0, s, (const f32x4*)p, bytes / 16, out);
     QH_CHECK_HIP(hipGetLastError());
     return QRAF_HIP_OK;
