@@ -502,6 +502,7 @@ def qwen_engine(args, rows, kv=F32):
     e.generate_weights(Q4, Q4, Q4, True, True, 3)
     e.finalize()
     e.set_graphs(not args.no_graphs)
+    e.set_row_padding(args.row_padding)
     return e
 
 
@@ -573,7 +574,10 @@ def run_schedule(e, work, max_rows, chunk):
             "ms_per_step": round(el / sched.steps * 1e3, 3),
             "host_ms_per_step": round(host_ms, 3), "host_share": round(host_ms / (el / sched.steps * 1e3), 4),
             "scheduler_python_ms_per_step": round(sched.host_s * 1e3 / sched.steps, 3),
-            "engine_host_prep_ms_per_step": round(st["host_us"] * 1e-3 / sched.steps, 3)}, \
+            "engine_host_prep_ms_per_step": round(st["host_us"] * 1e-3 / sched.steps, 3),
+            "step_launches": {"eager": st["eager_steps"], "graph_captures": st["graph_captures"],
+                              "graph_launches": st["graph_launches"]},
+            "pad_rows": st["pad_rows"]}, \
         [r.generated for r in sorted(done, key=lambda r: r.id)]
 
 
@@ -835,6 +839,8 @@ def main():
     ap.add_argument("--kernel", type=int, default=0,
                     help="matvec kernel: 0 auto, 1 one-shot, 2 persistent, 3 ring (8-wave groups), 4 ring (4-wave groups)")
     ap.add_argument("--wgs-per-cu", type=int, default=0)
+    ap.add_argument("--row-padding", type=int, default=32,
+                    help="batched engine steps of more than 8 rows run padded to a multiple of this (1: off)")
     ap.add_argument("--attn-form", type=int, default=0,
                     help="attention work form for every leg: 0 auto, 1 chunk grid, 2 balanced split, 3 VALU kernel")
     args = ap.parse_args()

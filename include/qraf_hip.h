@@ -444,8 +444,18 @@ int qraf_engine_read_logits(qraf_engine* engine, int32_t row0, int32_t rows, flo
 typedef struct qraf_engine_stats {
     uint64_t steps, rows;
     double host_us, wait_us;
+    /* steps launched eagerly, step graphs captured (each also launched),
+     * step graph launches, and pad rows run (row padding, below) */
+    uint64_t eager_steps, graph_captures, graph_launches, pad_rows;
 } qraf_engine_stats;
 int qraf_engine_get_stats(qraf_engine* engine, qraf_engine_stats* stats, int32_t reset);
+/* Row padding of steps with step graphs on: a step of more than 8 rows runs
+ * padded to a multiple of `rows` (at most max_batch), its logit rows too, so
+ * that steps of nearby sizes replay one graph.  Pad rows use a scratch KV
+ * page of their own and return nothing; results of real rows are the same
+ * whatever the padding.  rows 1: off; default 32.  No reference counterpart
+ * (a launch-cost measure). */
+int qraf_engine_set_row_padding(qraf_engine* engine, int32_t rows);
 /* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)
  * on the engine's default sequence, and Transformer::reset() (:641-643). */
 int qraf_engine_forward(qraf_engine* engine, uint32_t token, int32_t pos, float* logits);

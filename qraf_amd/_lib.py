@@ -108,7 +108,9 @@ class EngineOptions(C.Structure):
 
 class EngineStats(C.Structure):
     """qraf_engine_stats (include/qraf_hip.h)."""
-    _fields_ = [("steps", C.c_uint64), ("rows", C.c_uint64), ("host_us", C.c_double), ("wait_us", C.c_double)]
+    _fields_ = [("steps", C.c_uint64), ("rows", C.c_uint64), ("host_us", C.c_double), ("wait_us", C.c_double),
+                ("eager_steps", C.c_uint64), ("graph_captures", C.c_uint64), ("graph_launches", C.c_uint64),
+                ("pad_rows", C.c_uint64)]
 
 
 class SamplingParams(C.Structure):
@@ -134,6 +136,7 @@ SIGNATURES.update({
     "qraf_engine_free_pages": (C.c_int, [vp, i32p]),
     "qraf_engine_step": (C.c_int, [vp, C.c_int32, i32p, u32p, i32p, C.POINTER(C.c_uint8), fp, u32p]),
     "qraf_engine_set_graphs": (C.c_int, [vp, C.c_int32]),
+    "qraf_engine_set_row_padding": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_forward": (C.c_int, [vp, C.c_uint32, C.c_int32, fp]),
     "qraf_engine_read_logits": (C.c_int, [vp, C.c_int32, C.c_int32, fp]),
     "qraf_engine_get_stats": (C.c_int, [vp, vp, C.c_int32]),

@@ -425,12 +425,17 @@ struct qraf_engine {
     uint8_t* vpool = nullptr;
     size_t layer_kv_bytes = 0;
     std::vector<int32_t> free_pages;
+    int32_t scratch_page = 0;         // one page past the pool's num_pages: written and read by pad rows only
     struct Seq {
         bool live = false;
         int len = 0;
         std::vector<int32_t> pages;
+        uint64_t stamp = 0;           // the step that last validated this sequence
+        int step_len = 0, step_pages = 0;
     };
     std::vector<Seq> seqs;
+    uint64_t step_stamp = 0;
+    int row_pad = 32;                 // steps of more than 8 rows are padded to a multiple of this (graphs on)
     int32_t default_seq = -1;
     int last_logit_rows = 0;          // logit rows the last step left in `logits`
     qraf_engine_stats stats{};        // host-side time of qraf_engine_step
@@ -587,7 +592,8 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     // for int8 a f32 scale per position after them
     const size_t kv_block = o.kv_dtype == DT_I8 ? (size_t)o.page_size * (hd + 4)
                                                 : (size_t)o.page_size * hd * (o.kv_dtype == DT_F16 ? 2 : 4);
-    e->layer_kv_bytes = (size_t)o.num_pages * kvh * kv_block;
+    e->layer_kv_bytes = (size_t)(o.num_pages + 1) * kvh * kv_block;  // + the scratch page
+    e->scratch_page = (int32_t)o.num_pages;
     int rc = QRAF_HIP_OK;
 #define A(ptr, bytes)                                           \
     if ((rc = ealloc(e, (void**)&(ptr), (bytes))) != QRAF_HIP_OK) \
@@ -948,8 +954,9 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
                e->o.max_batch);
     const qraf_model_config& c = e->c;
     const int ps = (int)e->o.page_size, MP = e->max_pages;
-    // validate, and count the pages each sequence needs (before allocating any)
-    std::vector<std::pair<int32_t, int>> target;  // (sequence, pages after this step)
+    // validate, and count the pages each sequence needs (before allocating
+    // any): per sequence, the length and page count so far in this step
+    const uint64_t stamp = ++e->step_stamp;
     int need_pages = 0;
     for (int i = 0; i < n; i++) {
         const int32_t id = seq_ids[i], p = positions[i];
@@ -958,28 +965,39 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         QH_REQUIRE(tokens[i] < c.vocab_size, QRAF_HIP_ERR_INVALID, "Token %u >= vocab %u", tokens[i], c.vocab_size);
         QH_REQUIRE(p >= 0 && p < e->capacity, QRAF_HIP_ERR_INVALID, "step: position %d outside the cache (%d)", p,
                    e->capacity);
-        // rows of one sequence add positions without gaps (earlier rows count)
-        int len = e->seqs[id].len;
-        for (int j = 0; j < i; j++)
-            if (seq_ids[j] == id) len = std::max(len, positions[j] + 1);
-        QH_REQUIRE(p <= len, QRAF_HIP_ERR_INVALID, "step: sequence %d position %d skips past its length %d", id, p,
-                   len);
-        auto it = std::find_if(target.begin(), target.end(), [&](const std::pair<int32_t, int>& t) { return t.first == id; });
-        if (it == target.end()) {
-            target.push_back({id, (int)e->seqs[id].pages.size()});
-            it = target.end() - 1;
+        qraf_engine::Seq& sq = e->seqs[id];
+        if (sq.stamp != stamp) {
+            sq.stamp = stamp;
+            sq.step_len = sq.len;
+            sq.step_pages = (int)sq.pages.size();
         }
-        it->second = std::max(it->second, p / ps + 1);
+        // rows of one sequence add positions without gaps (earlier rows count)
+        QH_REQUIRE(p <= sq.step_len, QRAF_HIP_ERR_INVALID, "step: sequence %d position %d skips past its length %d",
+                   id, p, sq.step_len);
+        sq.step_len = std::max(sq.step_len, p + 1);
+        const int pages = std::max(sq.step_pages, p / ps + 1);
+        need_pages += pages - sq.step_pages;
+        sq.step_pages = pages;
     }
-    for (auto& t : target) need_pages += t.second - (int)e->seqs[t.first].pages.size();
     QH_REQUIRE(need_pages <= (int)e->free_pages.size(), QRAF_HIP_ERR_NOMEM,
                "step: KV page pool exhausted (%d pages needed, %zu free)", need_pages, e->free_pages.size());
+    // With step graphs, a step of more than 8 rows runs padded to a multiple
+    // of row_pad rows (at most max_batch), and its logit rows likewise, so
+    // that steps of nearby sizes share one graph: a pad row is token 0 at
+    // position 0 of the scratch page (context 1), which only pad rows write
+    // and read, and it wants no logits; a pad logit row repeats the last real
+    // one (whose logits are computed twice).  Every kernel's result for a row
+    // depends on that row alone.
+    const int n_real = n;
+    const int n_pad = e->use_graphs && e->row_pad > 1 && n > 8
+                          ? std::min((n + e->row_pad - 1) / e->row_pad * e->row_pad, (int)e->o.max_batch)
+                          : n;
     int n_logit_rows = 0;
     int32_t* tok = e->h_in;
-    int32_t* pos = tok + n;
-    int32_t* ctx = pos + n;
-    int32_t* lrows = ctx + n;
-    int32_t* ptab = lrows + n;
+    int32_t* pos = tok + n_pad;
+    int32_t* ctx = pos + n_pad;
+    int32_t* lrows = ctx + n_pad;
+    int32_t* ptab = lrows + n_pad;
     int step_ctx = 1;  // longest context of this step: sizes the attention grid (and skips the merge)
     for (int i = 0; i < n; i++) {
         qraf_engine::Seq& sq = e->seqs[seq_ids[i]];
@@ -995,6 +1013,19 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         if (!want_logits || want_logits[i]) lrows[n_logit_rows++] = i;
         for (int j = 0; j < MP; j++) ptab[(size_t)i * MP + j] = j < (int)sq.pages.size() ? sq.pages[j] : 0;
     }
+    for (int i = n; i < n_pad; i++) {
+        tok[i] = 0;
+        pos[i] = 0;
+        ctx[i] = 1;
+        for (int j = 0; j < MP; j++) ptab[(size_t)i * MP + j] = j == 0 ? e->scratch_page : 0;
+    }
+    const int n_logit_real = n_logit_rows;
+    if (n_pad != n && n_logit_rows > 0) {
+        const int nl = std::min((n_logit_rows + e->row_pad - 1) / e->row_pad * e->row_pad, n_pad);
+        for (int i = n_logit_rows; i < nl; i++) lrows[i] = lrows[n_logit_real - 1];
+        n_logit_rows = nl;
+    }
+    n = n_pad;
     hipStream_t s = e->stream;
     const size_t words = (size_t)n * (4 + MP);
     const bool head = n_logit_rows > 0 && (logits || next_tokens);
@@ -1153,8 +1184,10 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         }
         if (!g && !second) {
             QH_TRY(enqueue(ctx_grid));  // first sighting: eager
+            e->stats.eager_steps += 1;
         } else if (!g) {
             hipGraph_t graph = nullptr;
+            e->stats.graph_captures += 1;
             QH_CHECK_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
             const int rc = enqueue(ctx_grid);
             const hipError_t ec = hipStreamEndCapture(s, &graph);
@@ -1188,23 +1221,26 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         if (g) {
             g->used = ++e->graph_clock;
             QH_CHECK_HIP(hipGraphLaunch(g->exec, s));
+            e->stats.graph_launches += 1;
         }
     } else {
         QH_TRY(enqueue(step_ctx));
+        e->stats.eager_steps += 1;
     }
-    e->last_logit_rows = head ? n_logit_rows : 0;
+    e->last_logit_rows = head ? n_logit_real : 0;
     if (head && logits)
-        QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_rows * V * 4, hipMemcpyDeviceToHost, s));
+        QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_real * V * 4, hipMemcpyDeviceToHost, s));
     // tokens come back through pinned staging: an async copy into pageable
     // memory would block the host until the whole step has run
     if (head && next_tokens)
-        QH_CHECK_HIP(hipMemcpyAsync(e->h_amax, e->amax, (size_t)n_logit_rows * 4, hipMemcpyDeviceToHost, s));
+        QH_CHECK_HIP(hipMemcpyAsync(e->h_amax, e->amax, (size_t)n_logit_real * 4, hipMemcpyDeviceToHost, s));
     const double t_issued = now_us();
     QH_CHECK_HIP(hipStreamSynchronize(s));
     const double t_done = now_us();
-    if (head && next_tokens) memcpy(next_tokens, e->h_amax, (size_t)n_logit_rows * 4);
+    if (head && next_tokens) memcpy(next_tokens, e->h_amax, (size_t)n_logit_real * 4);
     e->stats.steps += 1;
-    e->stats.rows += (uint64_t)n;
+    e->stats.rows += (uint64_t)n_real;
+    e->stats.pad_rows += (uint64_t)(n - n_real);
     e->stats.host_us += t_issued - t_enter;
     e->stats.wait_us += t_done - t_issued;
     return QRAF_HIP_OK;
@@ -1220,6 +1256,13 @@ int qraf_engine_read_logits(qraf_engine* e, int32_t row0, int32_t rows, float* o
     QH_CHECK_HIP(hipMemcpyAsync(out, e->logits + (size_t)row0 * V, (size_t)rows * V * 4, hipMemcpyDeviceToHost,
                                 e->stream));
     QH_CHECK_HIP(hipStreamSynchronize(e->stream));
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_set_row_padding(qraf_engine* e, int32_t rows) {
+    clear_error();
+    QH_REQUIRE(e && rows >= 1 && rows <= 256, QRAF_HIP_ERR_INVALID, "set_row_padding: rows %d outside 1..256", rows);
+    e->row_pad = rows;
     return QRAF_HIP_OK;
 }
 

@@ -202,10 +202,16 @@ class Engine:
 
     def stats(self, reset: bool = False) -> dict:
         """Host-side time of the steps so far: host_us until every launch was
-        issued, wait_us blocked on the device at the step's end."""
+        issued, wait_us blocked on the device at the step's end; and how the
+        steps ran (eager, captured, graph launches; pad rows)."""
         st = EngineStats()
         call("qraf_engine_get_stats", self.h, C.byref(st), int(bool(reset)))
-        return {"steps": st.steps, "rows": st.rows, "host_us": st.host_us, "wait_us": st.wait_us}
+        return {k: getattr(st, k) for k, _ in EngineStats._fields_}
+
+    def set_row_padding(self, rows: int) -> None:
+        """Steps of more than 8 rows run padded to a multiple of `rows` (with
+        step graphs on), so nearby step sizes share a graph; 1 turns it off."""
+        call("qraf_engine_set_row_padding", self.h, int(rows))
 
     def sample(self, params: SamplingParams, recent=None, uniforms=None, row0=0, rows=None) -> np.ndarray:
         """Sampler::apply_repetition_penalty + Sampler::sample on rows row0.. of
