@@ -133,107 +133,9 @@ __global__ __launch_bounds__(1024) void residual_norm_split_kernel(const float* 
     }
 }
 
-// The same on 16-byte vectors (D % 4 == 0, 16-byte aligned rows): 256 threads
-// per row, thread t holding float4s t, t + 256, ...  Every load of the row,
-// the slices' and the norm weights' included, is issued before the first
-// use, so the kernel waits for memory once before its reduction.
-typedef float f32x4e __attribute__((ext_vector_type(4)));
-template <int S>
-__device__ __forceinline__ f32x4e sum_slices4_n(const float* __restrict__ p, size_t slice, size_t e) {
-    f32x4e t[S];
-#pragma unroll
-    for (int u = 0; u < S; u++) t[u] = *(const f32x4e*)(p + (size_t)u * slice + e);
-    f32x4e acc = t[0];
-#pragma unroll
-    for (int u = 1; u < S; u++) acc += t[u];
-    return acc;
-}
-__device__ __forceinline__ f32x4e sum_slices4(const float* __restrict__ p, int S, size_t slice, size_t e) {
-    switch (S) {
-        case 1: return sum_slices4_n<1>(p, slice, e);
-        case 2: return sum_slices4_n<2>(p, slice, e);
-        case 3: return sum_slices4_n<3>(p, slice, e);
-        case 4: return sum_slices4_n<4>(p, slice, e);
-        case 5: return sum_slices4_n<5>(p, slice, e);
-        case 6: return sum_slices4_n<6>(p, slice, e);
-        case 7: return sum_slices4_n<7>(p, slice, e);
-        case 8: return sum_slices4_n<8>(p, slice, e);
-        default: break;
-    }
-    f32x4e acc = *(const f32x4e*)(p + e);
-    for (int k = 1; k < S; k++) acc += *(const f32x4e*)(p + (size_t)k * slice + e);
-    return acc;
-}
-template <int J4>
-__global__ __launch_bounds__(256) void residual_norm_split4_kernel(const float* __restrict__ part, int S, size_t slice,
-                                                                   float* __restrict__ h, const float* __restrict__ w,
-                                                                   int D, float eps, uint16_t* __restrict__ xh,
-                                                                   uint16_t* __restrict__ xl) {
-    __shared__ float red[4];
-    const int m = blockIdx.x, tid = threadIdx.x, D4 = D >> 2;
-    float* hr = h + (size_t)m * D;
-    f32x4e v[J4], wv[J4];
-#pragma unroll
-    for (int j = 0; j < J4; j++) {
-        const int q = min(tid + 256 * j, D4 - 1);  // lanes past the row redo its last vector, unstored
-        v[j] = *(const f32x4e*)(hr + 4 * q);
-        wv[j] = w ? *(const f32x4e*)(w + 4 * q) : f32x4e{0.f, 0.f, 0.f, 0.f};
-    }
-    if (S > 0) {
-#pragma unroll
-        for (int j = 0; j < J4; j++) {
-            const int q = min(tid + 256 * j, D4 - 1);
-            v[j] = sum_slices4(part, S, slice, (size_t)m * D + 4 * q) + v[j];
-        }
-#pragma unroll
-        for (int j = 0; j < J4; j++)
-            if (tid + 256 * j < D4) *(f32x4e*)(hr + 4 * (tid + 256 * j)) = v[j];
-    }
-    if (!w) return;
-    float ss = 0.f;
-#pragma unroll
-    for (int j = 0; j < J4; j++)
-        if (tid + 256 * j < D4)
-#pragma unroll
-            for (int e = 0; e < 4; e++) ss = __builtin_fmaf(v[j][e], v[j][e], ss);
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-    if ((tid & 63) == 0) red[tid >> 6] = ss;
-    __syncthreads();
-    ss = (red[0] + red[1]) + (red[2] + red[3]);
-    const float r = 1.0f / sqrtf(ss / (float)D + eps);
-#pragma unroll
-    for (int j = 0; j < J4; j++) {
-        const int q = tid + 256 * j;
-        if (q < D4) {
-            uint16_t hb[4], lb[4];
-#pragma unroll
-            for (int e = 0; e < 4; e++) split_bf16(__fmul_rn(__fmul_rn(v[j][e], r), wv[j][e]), &hb[e], &lb[e]);
-            const size_t o = (size_t)m * D + 4 * q;
-            *(uint2*)(xh + o) = make_uint2(hb[0] | ((uint32_t)hb[1] << 16), hb[2] | ((uint32_t)hb[3] << 16));
-            *(uint2*)(xl + o) = make_uint2(lb[0] | ((uint32_t)lb[1] << 16), lb[2] | ((uint32_t)lb[3] << 16));
-        }
-    }
-}
-
 static int launch_residual_norm_split(const float* part, int S, size_t slice, float* h, const float* w, int D, float eps,
                                       uint16_t* xh, uint16_t* xl, int rows, hipStream_t s) {
     QH_REQUIRE(D <= 8192, QRAF_HIP_ERR_INVALID, "residual/norm: hidden size %d > 8192", D);
-    const bool vec = D % 4 == 0 && (slice % 4) == 0 && ((uintptr_t)part & 15) == 0 && ((uintptr_t)h & 15) == 0 &&
-                     ((uintptr_t)w & 15) == 0 && ((uintptr_t)xh & 7) == 0 && ((uintptr_t)xl & 7) == 0;
-    if (vec) {
-#define QH_RNS4(Jv)                                                                                             \
-    hipLaunchKernelGGL(residual_norm_split4_kernel<Jv>, dim3(rows), dim3(256), 0, s, part, S, slice, h, w, D, eps, \
-                       xh, xl)
-        const int D4 = D / 4;
-        if (D4 <= 256) QH_RNS4(1);
-        else if (D4 <= 512) QH_RNS4(2);
-        else if (D4 <= 1024) QH_RNS4(4);
-        else QH_RNS4(8);
-#undef QH_RNS4
-        QH_CHECK_HIP(hipGetLastError());
-        return QRAF_HIP_OK;
-    }
 #define QH_RNS(Jv) hipLaunchKernelGGL(residual_norm_split_kernel<Jv>, dim3(rows), dim3(1024), 0, s, part, S, slice, h, w, \
                                       D, eps, xh, xl)
     if (D <= 1024) QH_RNS(1);
