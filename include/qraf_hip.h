@@ -456,6 +456,12 @@ int qraf_engine_get_stats(qraf_engine* engine, qraf_engine_stats* stats, int32_t
  * whatever the padding.  rows 1: off; default 32.  No reference counterpart
  * (a launch-cost measure). */
 int qraf_engine_set_row_padding(qraf_engine* engine, int32_t rows);
+/* Fusions that change how a step runs, not what it computes (results are
+ * bit-identical either way): bit 0 (default on) = one-row steps apply the
+ * QKV bias, RoPE and the K/V store inside the QKV matvec (its one-shot form;
+ * f32 and fp16 pages) instead of a separate launch.  No reference
+ * counterpart (a launch-count measure). */
+int qraf_engine_set_fusion(qraf_engine* engine, int32_t flags);
 /* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)
  * on the engine's default sequence, and Transformer::reset() (:641-643). */
 int qraf_engine_forward(qraf_engine* engine, uint32_t token, int32_t pos, float* logits);

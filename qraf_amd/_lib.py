@@ -137,6 +137,7 @@ SIGNATURES.update({
     "qraf_engine_step": (C.c_int, [vp, C.c_int32, i32p, u32p, i32p, C.POINTER(C.c_uint8), fp, u32p]),
     "qraf_engine_set_graphs": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_set_row_padding": (C.c_int, [vp, C.c_int32]),
+    "qraf_engine_set_fusion": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_forward": (C.c_int, [vp, C.c_uint32, C.c_int32, fp]),
     "qraf_engine_read_logits": (C.c_int, [vp, C.c_int32, C.c_int32, fp]),
     "qraf_engine_get_stats": (C.c_int, [vp, vp, C.c_int32]),

@@ -65,8 +65,26 @@ struct MvPrep {
     float eps = 0.f;           // XP_NORM epsilon
     float* xbuf = nullptr;     // scratch for the prep-kernel fallback
 };
+// Epilogue of a one-token QKV projection (y = [q | k | v]): the bias, RoPE
+// of q and k, and the store of k and v at the token's position in its KV
+// page (rope_append_kernel's arithmetic), so no y is written.  f32 and fp16
+// pages.
+struct MvRope {
+    const float* bias = nullptr;          // [qd + 2 kvd] F32 bias, or null
+    const int32_t* pos = nullptr;         // device: the token's position
+    const float* rope = nullptr;          // [positions][hd]: (cos, sin) of pair i/2 at [i], [i + 1]
+    float* q_out = nullptr;               // [qd]
+    void* kc = nullptr;                   // the layer's K pages
+    void* vc = nullptr;                   // the layer's V pages
+    const int32_t* page_table = nullptr;  // the sequence's page ids
+    int H = 0, Hkv = 0, hd = 0, page_size = 0;
+    uint32_t kv_dtype = 0;                // DT_F32 or DT_F16
+};
+// rope (optional): fuse that epilogue when the chosen kernel is the one-shot
+// form; *fused says whether it was (else y holds the projection as usual)
 int launch_matvec_q(const void* W, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x,
-                    float* y, hipStream_t s, const float* add = nullptr, const MvPrep* prep = nullptr);
+                    float* y, hipStream_t s, const float* add = nullptr, const MvPrep* prep = nullptr,
+                    const MvRope* rope = nullptr, bool* fused = nullptr);
 int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s,
                       const float* add = nullptr);
 int set_matvec_tuning(int kernel, int rows, int wgs_per_cu);

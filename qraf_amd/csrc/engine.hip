@@ -338,6 +338,7 @@ struct qraf_engine {
     std::vector<Seq> seqs;
     uint64_t step_stamp = 0;
     int row_pad = 32;                 // steps of more than 8 rows are padded to a multiple of this (graphs on)
+    bool fuse_rope = true;            // one-row steps: RoPE/append fused into the QKV matvec
     int32_t default_seq = -1;
     int last_logit_rows = 0;          // logit rows the last step left in `logits`
     qraf_engine_stats stats{};        // host-side time of qraf_engine_step
@@ -945,8 +946,12 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
     // Wt: the tile-major copy (batched steps); K not a multiple of 32: one matvec per row
     // prep (optional): x is formed from its source first (norm or SiLU-gate):
     // inside the matvec at batch 1, else by a kernel writing prep->xbuf
+    // rope (one row only): the QKV epilogue fused into the matvec when its
+    // one-shot form runs; *fused says whether it did
     auto proj = [&](const uint8_t* W, const uint8_t* Wt, uint32_t dt, int N, int K, const float* x, int rows, float* y,
-                    const float* add, const MvPrep* prep = nullptr) -> int {
+                    const float* add, const MvPrep* prep = nullptr, const MvRope* rope = nullptr,
+                    bool* fused = nullptr) -> int {
+        if (fused) *fused = false;
         if (prep && (dt == DT_F32 || rows != 1)) {
             if (prep->op == XP_NORM)
                 hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, s, x, prep->w, K, prep->eps,
@@ -964,6 +969,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
                                          add ? add + (size_t)r * N : nullptr));
             return QRAF_HIP_OK;
         }
+        if (rows == 1 && rope) return launch_matvec_q(W, dt, 32, N, K, x, y, s, add, prep, rope, fused);
         if (rows == 1 || !Wt) {
             for (int r = 0; r < rows; r++)
                 QH_TRY(launch_matvec_q(W, dt, 32, N, K, x + (size_t)r * K, y + (size_t)r * N, s,
@@ -1015,9 +1021,26 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
             uint8_t* kc = e->kpool + (size_t)l * e->layer_kv_bytes;
             uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;
             const MvPrep attn_norm{XP_NORM, L.an, c.rms_norm_eps, e->xn};  // transformer.cpp:586
-            QH_TRY(proj(L.wqkv, L.wqkv_t, L.dt_attn, e->qkvd, D, e->h, n, e->qkv, nullptr, &attn_norm));
-            QH_TRY(launch_rope_append(e->qkv, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q, kc, vc,
-                                      e->o.kv_dtype, d_ptab, MP, ps, s));
+            // one row: bias, RoPE and the K/V store fused into the QKV matvec where its one-shot form runs
+            MvRope rope;
+            rope.bias = L.has_bias ? L.bqkv : nullptr;
+            rope.pos = d_pos;
+            rope.rope = e->rope;
+            rope.q_out = e->q;
+            rope.kc = kc;
+            rope.vc = vc;
+            rope.page_table = d_ptab;
+            rope.H = H;
+            rope.Hkv = Hkv;
+            rope.hd = hd;
+            rope.page_size = ps;
+            rope.kv_dtype = e->o.kv_dtype;
+            bool fused = false;
+            QH_TRY(proj(L.wqkv, L.wqkv_t, L.dt_attn, e->qkvd, D, e->h, n, e->qkv, nullptr, &attn_norm,
+                        e->fuse_rope && e->o.kv_dtype != DT_I8 ? &rope : nullptr, &fused));
+            if (!fused)
+                QH_TRY(launch_rope_append(e->qkv, L.has_bias ? L.bqkv : nullptr, n, H, Hkv, hd, d_pos, e->rope, e->q,
+                                          kc, vc, e->o.kv_dtype, d_ptab, MP, ps, s));
             QH_TRY(launch_attention(e->q, kc, vc, e->o.kv_dtype, d_ptab, MP, d_ctx, n, H, Hkv, hd, ps, scale, ctx_grid,
                                     e->att, e->attn_ws, e->attn_ws_bytes, s));
             QH_TRY(proj(L.wo, L.wo_t, L.dt_attn, D, e->qd, e->att, n, e->h, e->h));  // + residual (transformer.cpp:593)
@@ -1158,6 +1181,14 @@ int qraf_engine_read_logits(qraf_engine* e, int32_t row0, int32_t rows, float* o
     QH_CHECK_HIP(hipMemcpyAsync(out, e->logits + (size_t)row0 * V, (size_t)rows * V * 4, hipMemcpyDeviceToHost,
                                 e->stream));
     QH_CHECK_HIP(hipStreamSynchronize(e->stream));
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_set_fusion(qraf_engine* e, int32_t flags) {
+    clear_error();
+    QH_REQUIRE(e && (flags & ~1) == 0, QRAF_HIP_ERR_INVALID, "set_fusion: flags %d", flags);
+    e->fuse_rope = (flags & 1) != 0;
+    e->drop_graphs();  // captured steps hold the other form
     return QRAF_HIP_OK;
 }
 

@@ -291,14 +291,12 @@ __global__ __launch_bounds__(WG) void qmv_stream_kernel(const uint8_t* __restric
 // few microseconds long, and a load -> use -> load chain per wave would pay
 // the HBM latency several times.
 // ----------------------------------------------------------------------------
-template <int FMT, int R, int J, int XP = XP_NONE>
-__global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
-                                                        int K, int nb, const float* __restrict__ x,
-                                                        float* __restrict__ y, const float* __restrict__ add,
-                                                        const float* __restrict__ xw, float eps) {
-    extern __shared__ __align__(16) float sx[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int row0 = (blockIdx.x * 4 + wave) * R;
+// The rows of one wave: returns row row0 + *rr's sum on the lanes with
+// (lane & (64/R - 1)) == 0 (sx: the workgroup's x staging).
+template <int FMT, int R, int J, int XP>
+__device__ __forceinline__ float oneshot_rows(const uint8_t* __restrict__ W, uint32_t row_bytes, int N, int K, int nb,
+                                              const float* __restrict__ x, const float* __restrict__ xw, float eps,
+                                              float* sx, int row0, int lane, int* rr) {
     const int U = FMT == 8 ? nb : nb >> 1;
 
     const uint8_t* rowp[R];
@@ -323,9 +321,79 @@ __global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restri
             else q4_compute<R>(w[j], sx + u * XS4, acc);
         }
     }
+    return wave_reduce_rows<R>(acc, lane, rr);
+}
+
+template <int FMT, int R, int J, int XP = XP_NONE>
+__global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
+                                                        int K, int nb, const float* __restrict__ x,
+                                                        float* __restrict__ y, const float* __restrict__ add,
+                                                        const float* __restrict__ xw, float eps) {
+    extern __shared__ __align__(16) float sx[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * 4 + wave) * R;
     int rr;
-    float v = wave_reduce_rows<R>(acc, lane, &rr);
+    const float v = oneshot_rows<FMT, R, J, XP>(W, row_bytes, N, K, nb, x, xw, eps, sx, row0, lane, &rr);
     if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = add ? v + add[row0 + rr] : v;
+}
+
+// The one-shot kernel with the QKV epilogue (MvRope): a workgroup's 4R rows
+// (an even count starting at an even row, so whole RoPE pairs) pass through
+// LDS, and thread t < 2R takes the pair 2t, 2t+1: bias, rotation of q and k
+// pairs (unfused products, the host-libm table), stores of q, k and v.
+template <int FMT, int R, int J, int XP>
+__global__ __launch_bounds__(WG) void qmv_oneshot_rope_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes,
+                                                             int N, int K, int nb, const float* __restrict__ x,
+                                                             const float* __restrict__ xw, float eps, MvRope rp) {
+    extern __shared__ __align__(16) float sx[];
+    __shared__ float s_y[4 * R];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int row0 = (blockIdx.x * 4 + wave) * R;
+    int rr;
+    const float v = oneshot_rows<FMT, R, J, XP>(W, row_bytes, N, K, nb, x, xw, eps, sx, row0, lane, &rr);
+    if ((lane & (64 / R - 1)) == 0) s_y[wave * R + rr] = v;
+    __syncthreads();
+    const int t = threadIdx.x, r = blockIdx.x * 4 * R + 2 * t;
+    if (t >= 2 * R || r >= N) return;
+    float a = s_y[2 * t], b = s_y[2 * t + 1];
+    if (rp.bias) {
+        a = __fadd_rn(a, rp.bias[r]);
+        b = __fadd_rn(b, rp.bias[r + 1]);
+    }
+    const int hd = rp.hd, qd = rp.H * hd, kvd = rp.Hkv * hd, ps = rp.page_size;
+    const int p = *rp.pos;
+    const int page = rp.page_table[p / ps], off = p % ps;
+    if (r < qd + kvd) {
+        const int i = r % hd;  // even index inside the head
+        const float* cs = rp.rope + (size_t)p * hd;
+        const float c = cs[i], sn = cs[i + 1];
+        const float ra = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn));
+        const float rb = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, c));
+        if (r < qd) {
+            rp.q_out[r] = ra;
+            rp.q_out[r + 1] = rb;
+        } else {
+            const size_t o = (((size_t)page * rp.Hkv + (r - qd) / hd) * ps + off) * hd + i;
+            if (rp.kv_dtype == DT_F16) {
+                ((_Float16*)rp.kc)[o] = (_Float16)ra;
+                ((_Float16*)rp.kc)[o + 1] = (_Float16)rb;
+            } else {
+                ((float*)rp.kc)[o] = ra;
+                ((float*)rp.kc)[o + 1] = rb;
+            }
+        }
+    } else {
+        const int j = r - qd - kvd, vh = j / hd, dd = j % hd;
+        if (rp.kv_dtype == DT_F16) {  // fp16 pages keep V dimension-major
+            const size_t o = (((size_t)page * rp.Hkv + vh) * hd + dd) * ps + off;
+            ((_Float16*)rp.vc)[o] = (_Float16)a;
+            ((_Float16*)rp.vc)[o + ps] = (_Float16)b;
+        } else {
+            const size_t o = (((size_t)page * rp.Hkv + vh) * ps + off) * hd + dd;
+            ((float*)rp.vc)[o] = a;
+            ((float*)rp.vc)[o + 1] = b;
+        }
+    }
 }
 
 // ----------------------------------------------------------------------------
@@ -794,6 +862,34 @@ static qmv_fn pick_oneshot_xp(int R, int J, int xp) {
     if (xp == XP_SILU_GATE) return pick_oneshot_r<FMT, XP_SILU_GATE>(R, J);
     return pick_oneshot_r<FMT, XP_NONE>(R, J);
 }
+// one-shot instances with the QKV epilogue: x formed as RMSNorm(x) * w in
+// staging (the layer's attention norm), R * J <= 8, J <= 4
+typedef void (*qmv_rope_fn)(const uint8_t*, uint32_t, int, int, int, const float*, const float*, float, MvRope);
+template <int FMT, int R, int J>
+static qmv_rope_fn rope_if_valid() {
+    if constexpr (R * J <= 8 && J <= 4) return qmv_oneshot_rope_kernel<FMT, R, J, XP_NORM>;
+    else return nullptr;
+}
+template <int FMT, int R>
+static qmv_rope_fn pick_rope_j(int J) {
+    switch (J) {
+        case 1: return rope_if_valid<FMT, R, 1>();
+        case 2: return rope_if_valid<FMT, R, 2>();
+        case 3: return rope_if_valid<FMT, R, 3>();
+        case 4: return rope_if_valid<FMT, R, 4>();
+        default: return nullptr;
+    }
+}
+template <int FMT>
+static qmv_rope_fn pick_rope(int R, int J) {
+    switch (R) {
+        case 1: return pick_rope_j<FMT, 1>(J);
+        case 2: return pick_rope_j<FMT, 2>(J);
+        case 4: return pick_rope_j<FMT, 4>(J);
+        default: return pick_rope_j<FMT, 8>(J);
+    }
+}
+
 template <int FMT>
 static qmv_fn pick_stream(int R) {
     switch (R) {
@@ -854,7 +950,8 @@ static int launch_xprep(const float* x, const MvPrep& p, int K, hipStream_t s) {
 }
 
 int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t K, const float* x, float* y,
-                    hipStream_t s, const float* add, const MvPrep* prep) {
+                    hipStream_t s, const float* add, const MvPrep* prep, const MvRope* rope, bool* fused) {
+    if (fused) *fused = false;
     QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "unsupported weight dtype %u", dtype);
     QH_REQUIRE(bs > 0 && bs <= 4096, QRAF_HIP_ERR_INVALID, "bad block size %d", bs);
     QH_REQUIRE(K > 0 && N > 0, QRAF_HIP_ERR_INVALID, "empty matvec (%u x %u)", N, K);
@@ -951,6 +1048,21 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
             while (R > 1 && (R * J > 8 || (N + 4 * R - 1) / (4 * R) < 256)) R >>= 1;
         } else {
             while (R > 1 && R * J > 8) R >>= 1;
+        }
+        if (rope && fused && xp == XP_NORM && !add && (N % 2) == 0 && rope->hd % 2 == 0 &&
+            (int)N == (rope->H + 2 * rope->Hkv) * rope->hd &&
+            (rope->kv_dtype == DT_F32 || rope->kv_dtype == DT_F16)) {
+            const qmv_rope_fn kr = dtype == DT_Q8_0 ? pick_rope<8>(R, J) : pick_rope<4>(R, J);
+            if (kr) {
+                if (lds > 65536)
+                    QH_CHECK_HIP(hipFuncSetAttribute((const void*)kr, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                     (int)lds));
+                hipLaunchKernelGGL(kr, dim3((N + 4 * R - 1) / (4 * R)), dim3(WG), lds, s, W, (uint32_t)rb, (int)N,
+                                   (int)K, nb, x, xw, eps, *rope);
+                QH_CHECK_HIP(hipGetLastError());
+                *fused = true;
+                return QRAF_HIP_OK;
+            }
         }
         qmv_fn k = dtype == DT_Q8_0 ? pick_oneshot_xp<8>(R, J, xp) : pick_oneshot_xp<4>(R, J, xp);
         if (!k) {  // no one-shot instance forms this x (J > 4): prepare it separately

@@ -208,6 +208,11 @@ class Engine:
         call("qraf_engine_get_stats", self.h, C.byref(st), int(bool(reset)))
         return {k: getattr(st, k) for k, _ in EngineStats._fields_}
 
+    def set_fusion(self, flags: int) -> None:
+        """Bit 0: one-row steps fuse the QKV bias, RoPE and K/V store into the
+        QKV matvec (default on); results are bit-identical either way."""
+        call("qraf_engine_set_fusion", self.h, int(flags))
+
     def set_row_padding(self, rows: int) -> None:
         """Steps of more than 8 rows run padded to a multiple of `rows` (with
         step graphs on), so nearby step sizes share a graph; 1 turns it off."""

@@ -224,6 +224,32 @@ def test_batched_logits_and_chunked_prefill(hip):
     e.close()
 
 
+@pytest.mark.parametrize("name,kv", [("q8_llama", "F32"), ("q4_qwen2_tied_bias", "F32"), ("q8_hd64_gqa3", "F16"),
+                                     ("q4_gqa8_hd128", "F16")])
+def test_fused_qkv_epilogue_equals_separate_launch(hip, name, kv):
+    """One-row steps with the QKV bias, RoPE and K/V store fused into the QKV
+    matvec (the default) against the separate RoPE/append launch: logits
+    bit-identical at every position, so the pages hold the same values."""
+    from qraf_amd.engine import Engine
+    kw, seed = SMALL[name]
+    m = oracle_model(kw, seed)
+    L = po.lib()
+    toks = [L.or_gen_token(seed + 9, i, kw["vocab"]) for i in range(40)]
+    runs = []
+    for flags in (1, 0):
+        e = Engine(engine_config(kw), kv_dtype=getattr(po, kv), max_batch=4)
+        for tname, dt, shape, data in m.tensors():
+            e.set_tensor(tname, dt, shape, data)
+        e.finalize()
+        e.set_fusion(flags)
+        a = e.seq_create()
+        runs.append([e.step([a], [toks[p]], [p], logits=True, argmax=False)[0].copy() for p in range(40)])
+        e.close()
+    for p, (x, y) in enumerate(zip(*runs)):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), f"position {p}"
+    m.close()
+
+
 @pytest.mark.parametrize("name", ["q8_hd64_gqa3", "q4_gqa8_hd128"])
 def test_step_graph_replay_equals_eager(hip, name):
     """Captured step graphs (the default) against eager launches of the same
