@@ -1422,7 +1422,13 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
     a.scale = scale;
     const int G = H / Hkv;
     const bool mfma_shape = (hd == 64 || hd == 128) && G <= 16 && page_size % 4 == 0 && ps_pow2;
-    const bool valu = !mfma_shape || (g_attn_form == 3 && kv_dtype != DT_I8);
+    // One sequence of at most one 256-position chunk on f32 pages at
+    // head_dim 64 (batch-1 decode of a small model): the VALU kernel, whose
+    // one round of K/V loads beats the matrix-core kernel's pipelined tiles
+    // when a single workgroup per KV head is all there is (SmolLM2-135M
+    // architecture decode on MI355X: 1,373 against 1,296 tok/s)
+    const bool single_f32 = kv_dtype == DT_F32 && hd == 64 && n == 1 && max_ctx <= ACH && g_attn_form == 0;
+    const bool valu = !mfma_shape || (g_attn_form == 3 && kv_dtype != DT_I8) || single_f32;
     const bool split = !valu && (g_attn_form == 2 || (g_attn_form != 1 && items > 1024));
     if (valu) {  // the plain fp32 VALU kernel
         if (kv_dtype == DT_F32) QH_TRY(launch_attn_t<float>(a, hd, G, items, st));
