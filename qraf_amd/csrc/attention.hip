@@ -130,49 +130,70 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int kvh = blockIdx.y;
     const int item = blockIdx.x;
-    int s, chunk, nchunks;
-    int ctx;
-    if (!attn_item(a, s, chunk, nchunks, ctx)) return;
+    // Requested together, before any of them is used: the context length, q
+    // of the G heads, and the page id of this thread's position (its table
+    // index clamped into the table; used only for positions inside the
+    // context).  Then the K row of the position, and after one barrier the
+    // first round of V loads of the PV phase, both in flight while the scores
+    // and the softmax are formed.
+    const int per = (a.max_ctx + ACH - 1) / ACH;
+    const int s = item / per, chunk = item - s * per;
     const int t0 = chunk * ACH;
-
-    // ---- q of the G heads sharing this KV head
+    const int t = t0 + tid;
+    const int ctx_raw = a.ctx[s];
     for (int i = tid; i < G * HD; i += ACH) s_q[i / HD][i % HD] = a.q[((size_t)s * a.H + kvh * G) * HD + i];
-    __syncthreads();
+    const int page_t = a.page_table[(size_t)s * a.max_pages + min(t, a.max_ctx - 1) / a.page_size];
+    const int ctx = min(ctx_raw, a.max_ctx);
+    const int nchunks = (ctx + ACH - 1) / ACH;
+    if (chunk >= nchunks) return;  // the whole workgroup
 
-    // ---- scores: thread = position t0 + tid
     const KT* kc = (const KT*)a.kc;
     const KT* vc = (const KT*)a.vc;
-    const int t = t0 + tid;
-    {
-        // V row of position t (positions past the end read position t0's row,
-        // which exists, with probability 0)
-        const int tv = t < ctx ? t : t0;
-        const uint32_t page = (uint32_t)a.page_table[(size_t)s * a.max_pages + tv / a.page_size];
-        const uint32_t row = (page * a.Hkv + kvh) * a.page_size;
-        const uint32_t off = sizeof(KT) == 4 ? (row + tv % a.page_size) * HD : row * HD + tv % a.page_size;
-        s_voff[tid] = off;
-        if (tid < PADP) s_voff[ACH + tid] = off;  // any existing row: its probability is 0
+    float kv[HD];
+    if (t < ctx) {
+        const KT* kr = kc + (((size_t)page_t * a.Hkv + kvh) * a.page_size + t % a.page_size) * HD;
+#pragma unroll
+        for (int d = 0; d < HD; d += 8) {
+            float k8[8];
+            load8(kr + d, k8);
+#pragma unroll
+            for (int i = 0; i < 8; i++) kv[d + i] = k8[i];
+        }
+        const uint32_t row = ((uint32_t)page_t * a.Hkv + kvh) * a.page_size;
+        s_voff[tid] = sizeof(KT) == 4 ? (row + t % a.page_size) * HD : row * HD + t % a.page_size;
     }
+    __syncthreads();
+    // V row offsets of positions past the end (and of the padding the PV
+    // loop may touch): position t0's row, which exists; its probability is 0
+    if (t >= ctx) s_voff[tid] = s_voff[0];
+    if (tid < PADP) s_voff[ACH + tid] = s_voff[0];
+    __syncthreads();
+
+    const int dd = tid % HD, grp = tid / HD;
+    const int tend = min(ACH, ctx - t0);
+    const KT* vd = vc + (sizeof(KT) == 4 ? (size_t)dd : (size_t)dd * a.page_size);
+    float vpre[PVU];  // the PV loop's first round, requested before the scores
+#pragma unroll
+    for (int u = 0; u < PVU; u++) vpre[u] = kv_load(vd + s_voff[grp + NG * u]);
+
+    // ---- scores: thread = position t0 + tid
     float sc[G];
 #pragma unroll
     for (int h = 0; h < G; h++) sc[h] = 0.f;
     if (t < ctx) {
-        const int page = a.page_table[(size_t)s * a.max_pages + t / a.page_size];
-        const KT* kr = kc + (((size_t)page * a.Hkv + kvh) * a.page_size + t % a.page_size) * HD;
+#pragma unroll
         for (int d = 0; d < HD; d += 8) {
-            float kv[8];
-            load8(kr + d, kv);
 #pragma unroll
             for (int h = 0; h < G; h++) {
                 const float4 qa = *(const float4*)&s_q[h][d], qb = *(const float4*)&s_q[h][d + 4];
-                sc[h] = __builtin_fmaf(qa.x, kv[0], sc[h]);
-                sc[h] = __builtin_fmaf(qa.y, kv[1], sc[h]);
-                sc[h] = __builtin_fmaf(qa.z, kv[2], sc[h]);
-                sc[h] = __builtin_fmaf(qa.w, kv[3], sc[h]);
-                sc[h] = __builtin_fmaf(qb.x, kv[4], sc[h]);
-                sc[h] = __builtin_fmaf(qb.y, kv[5], sc[h]);
-                sc[h] = __builtin_fmaf(qb.z, kv[6], sc[h]);
-                sc[h] = __builtin_fmaf(qb.w, kv[7], sc[h]);
+                sc[h] = __builtin_fmaf(qa.x, kv[d + 0], sc[h]);
+                sc[h] = __builtin_fmaf(qa.y, kv[d + 1], sc[h]);
+                sc[h] = __builtin_fmaf(qa.z, kv[d + 2], sc[h]);
+                sc[h] = __builtin_fmaf(qa.w, kv[d + 3], sc[h]);
+                sc[h] = __builtin_fmaf(qb.x, kv[d + 4], sc[h]);
+                sc[h] = __builtin_fmaf(qb.y, kv[d + 5], sc[h]);
+                sc[h] = __builtin_fmaf(qb.z, kv[d + 6], sc[h]);
+                sc[h] = __builtin_fmaf(qb.w, kv[d + 7], sc[h]);
             }
         }
 #pragma unroll
@@ -214,13 +235,14 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     // (each V element is loaded once for the heads that share it), with PVU
     // independent loads in flight; the NG group sums are then added in group
     // order.  For f32 pages and head_dim >= 64 a wave reads one V row.
-    const int dd = tid % HD, grp = tid / HD;
-    const int tend = min(ACH, ctx - t0);
-    const KT* vd = vc + (sizeof(KT) == 4 ? (size_t)dd : (size_t)dd * a.page_size);
     float acc[G];
 #pragma unroll
     for (int h = 0; h < G; h++) acc[h] = 0.f;
-    for (int tt = grp; tt < tend; tt += NG * PVU) {
+#pragma unroll
+    for (int u = 0; u < PVU; u++)  // the first round (grp < tend always: tend >= 1, grp < NG <= PVU * NG)
+#pragma unroll
+        for (int h = 0; h < G; h++) acc[h] = __builtin_fmaf(s_p[h][grp + NG * u], vpre[u], acc[h]);
+    for (int tt = grp + NG * PVU; tt < tend; tt += NG * PVU) {
         float v[PVU];
 #pragma unroll
         for (int u = 0; u < PVU; u++) v[u] = kv_load(vd + s_voff[tt + NG * u]);
