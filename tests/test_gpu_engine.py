@@ -250,6 +250,43 @@ def test_fused_qkv_epilogue_equals_separate_launch(hip, name, kv):
     m.close()
 
 
+def test_attention_form_change_reaches_captured_steps(hip):
+    """Changing the attention form (qraf_hip_set_attention_tuning) between
+    replayed step graphs: the engine captures new graphs in the new form, so
+    every step's logits equal an eager run that changes the form at the same
+    steps, bit for bit (the forms themselves round differently)."""
+    from qraf_amd.engine import Engine
+    kw, seed = SMALL["q4_gqa8_hd128"]
+    m = oracle_model(kw, seed)
+    L = po.lib()
+    toks = [L.or_gen_token(seed + 3, i, kw["vocab"]) for i in range(40)]
+    runs = []
+    try:
+        # graphs with the form switched, eager with the form switched, eager in form 1 throughout
+        for graphs, switch in ((True, True), (False, True), (False, False)):
+            e = Engine(engine_config(kw), kv_dtype=po.F16, max_batch=4)
+            for tname, dt, shape, data in m.tensors():
+                e.set_tensor(tname, dt, shape, data)
+            e.finalize()
+            e.set_graphs(graphs)
+            a, b = e.seq_create(), e.seq_create()
+            out = []
+            for form, steps in ((1, range(0, 12)), (2, range(12, 24)), (3, range(24, 36))):
+                hip._lib.call("qraf_hip_set_attention_tuning", form if switch else 1)
+                for i in steps:
+                    lg, _ = e.step([a, b], [toks[i], toks[i + 1]], [i, i], logits=True, argmax=False)
+                    out.append(lg.copy())
+            runs.append(out)
+            e.close()
+    finally:
+        hip._lib.call("qraf_hip_set_attention_tuning", 0)
+    for i, (x, y) in enumerate(zip(runs[0], runs[1])):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32)), f"step {i}"
+    # the forms do round differently, so a graph left in form 1 would have failed above
+    assert any(not np.array_equal(x, y) for x, y in zip(runs[1][12:], runs[2][12:]))
+    m.close()
+
+
 @pytest.mark.parametrize("name", ["q8_hd64_gqa3", "q4_gqa8_hd128"])
 def test_step_graph_replay_equals_eager(hip, name):
     """Captured step graphs (the default) against eager launches of the same
