@@ -524,42 +524,50 @@ def bench_decode_b128(args, rt):
         plen, olen = int(rng.integers(16, 513)), int(rng.integers(64, 257))
         work.append((rng.integers(0, QWEN["vocab"], plen).tolist(), olen))
 
-    def run(max_rows, chunk):
-        return run_schedule(e, work, max_rows, chunk)
+    pipe = not args.no_pipeline
+
+    def run(max_rows, chunk, pipeline=pipe):
+        return run_schedule(e, work, max_rows, chunk, pipeline)
 
     e.stats(reset=True)
     chunked, streams_c = run(rows, args.prefill_chunk)
+    unpiped, streams_u = run(rows, args.prefill_chunk, False)
     tbt, streams_t = run(128, 1)
-    steady = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, F32)
+    steady = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, F32, pipe)
     e.close()
     extras = {}
     for kv in (F16, I8):  # narrower pages: not the reference's values; agreement with the f32 streams beside them
         ek = qwen_engine(args, rows, kv)
-        res, streams_k = run_schedule(ek, work, rows, args.prefill_chunk)
+        res, streams_k = run_schedule(ek, work, rows, args.prefill_chunk, pipe)
         res["stream_agreement_with_f32_pages"] = stream_agreement(streams_c, streams_k)
-        res["steady_decode"] = steady_decode_b128(ek, np.random.default_rng(3), args.decode_steps, kv)
+        res["steady_decode"] = steady_decode_b128(ek, np.random.default_rng(3), args.decode_steps, kv, pipe)
         ek.close()
         extras[f"{KV_NAMES[kv]}_pages"] = res
     out = {"model": "Qwen2.5-3B architecture, Q4_0 weights, tied head, QKV bias, f32 KV pages, random init",
            "requests": args.requests, "max_concurrent": 128}
     out.update(chunked)
-    out.update({"row_budget": rows, "prefill_chunk": args.prefill_chunk,
+    unpiped["streams_equal_pipelined"] = streams_u == streams_c
+    out.update({"row_budget": rows, "prefill_chunk": args.prefill_chunk, "pipelined": pipe,
                 "note": "continuous batching, requests admitted as others finish; each step feeds every decoding "
                         "request's last token, then prompt chunks within the row budget; f32 KV pages hold the "
-                        "reference's KVCache values",
+                        "reference's KVCache values; pipelined: step N+1 is issued before step N's tokens reach "
+                        "the host, its decode rows taking them from step N's argmax on the device",
+                "unpipelined": unpiped,
                 "token_by_token": tbt, "stream_agreement": stream_agreement(streams_c, streams_t),
                 "steady_decode": steady})
     out.update(extras)
     return out
 
 
-def run_schedule(e, work, max_rows, chunk):
+def run_schedule(e, work, max_rows, chunk, pipeline=False):
     """One continuous-batching run of `work` [(prompt, max tokens)] through 128
     slots; aggregate generated tok/s, and the host's share of the wall time:
     the scheduler's own Python work plus the engine's host-side preparation of
-    each step (the device idles meanwhile: every step ends in a synchronisation)."""
+    each step (unpipelined, the device idles meanwhile, as every step ends in a
+    synchronisation; pipelined, that work overlaps the previous step's run and
+    device_wait_ms_per_step is the time the host waited for the device)."""
     from qraf_amd.engine import BatchScheduler
-    sched = BatchScheduler(e, max_batch=128, max_rows=max_rows, prefill_chunk=chunk)
+    sched = BatchScheduler(e, max_batch=128, max_rows=max_rows, prefill_chunk=chunk, pipeline=pipeline)
     for p, o in work:
         sched.submit(p, o)
     e.stats(reset=True)
@@ -575,6 +583,7 @@ def run_schedule(e, work, max_rows, chunk):
             "host_ms_per_step": round(host_ms, 3), "host_share": round(host_ms / (el / sched.steps * 1e3), 4),
             "scheduler_python_ms_per_step": round(sched.host_s * 1e3 / sched.steps, 3),
             "engine_host_prep_ms_per_step": round(st["host_us"] * 1e-3 / sched.steps, 3),
+            "device_wait_ms_per_step": round(st["wait_us"] * 1e-3 / sched.steps, 3),
             "step_launches": {"eager": st["eager_steps"], "graph_captures": st["graph_captures"],
                               "graph_launches": st["graph_launches"]},
             "pad_rows": st["pad_rows"]}, \
@@ -758,7 +767,7 @@ def bench_steady_b128(args, rt):
     """The steady 128-sequence decode alone (every GEMM at 128 rows), for profiling."""
     kv = {"f32": F32, "fp16": F16, "int8": I8}[args.kv]
     e = qwen_engine(args, 128, kv)
-    out = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, kv)
+    out = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, kv, not args.no_pipeline)
     e.close()
     return out
 
@@ -778,10 +787,11 @@ QWEN_LAYER_WEIGHT_BYTES = 1560674304  # 36 layers of Q4_0 q/k/v/o/gate/up/down
 QWEN_HEAD_BYTES = 175030272           # the tied Q4_0 embedding read as the head
 
 
-def steady_decode_b128(e, rng, steps, kv):
+def steady_decode_b128(e, rng, steps, kv, pipeline=False):
     """128 concurrent sequences at ragged contexts (prompt U[16,512] plus U[0,255] generated, the run above's
     distribution), prefilled in 128-row steps; then `steps` decode steps of 128 rows, every row generating
-    (greedy, device argmax).  Timed: the decode steps only."""
+    (greedy, device argmax).  Timed: the decode steps only.  Pipelined: each step is issued before the previous
+    one's tokens are collected, its rows taking them from the previous step's argmax on the device."""
     n, V = 128, QWEN["vocab"]
     seqs = [e.seq_create() for _ in range(n)]
     ctx = rng.integers(16, 513, n) + rng.integers(0, 256, n)
@@ -796,9 +806,19 @@ def steady_decode_b128(e, rng, steps, kv):
         _, nx = e.step(seqs, toks, pos.tolist())
         toks, pos = nx.tolist(), pos + 1
     t0 = time.perf_counter()
-    for _ in range(steps):
-        _, nx = e.step(seqs, toks, pos.tolist())
-        toks, pos = nx.tolist(), pos + 1
+    if pipeline:
+        src = np.arange(n, dtype=np.int32)
+        e.step_async(seqs, toks, pos.tolist())
+        pos = pos + 1
+        for _ in range(steps - 1):
+            e.step_async(seqs, toks, pos.tolist(), token_src=src)
+            pos = pos + 1
+            e.collect()
+        nx = e.collect()
+    else:
+        for _ in range(steps):
+            _, nx = e.step(seqs, toks, pos.tolist())
+            toks, pos = nx.tolist(), pos + 1
     el = time.perf_counter() - t0
     for s in seqs:
         e.seq_release(s)
@@ -808,7 +828,7 @@ def steady_decode_b128(e, rng, steps, kv):
     ms = el / steps * 1e3
     return {"kv_pages": KV_NAMES[kv], "sequences": n, "context_mean_at_start": round(float(ctx.mean()) + 3, 1),
             "context_max_at_end": int(pos.max()), "decode_steps": steps, "ms_per_step": round(ms, 3),
-            "decode_tok_s": round(n * steps / el, 1), "alg_bytes_per_step": int(by),
+            "decode_tok_s": round(n * steps / el, 1), "pipelined": pipeline, "alg_bytes_per_step": int(by),
             "GB_s": round(by / (ms * 1e-3) / 1e9, 1), "frac_hbm_peak": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
@@ -834,6 +854,8 @@ def main():
     ap.add_argument("--no-graphs", action="store_true",
                     help="launch every kernel eagerly (timed with events) instead of replaying captured graphs, "
                          "in every leg")
+    ap.add_argument("--no-pipeline", action="store_true",
+                    help="batch-128 legs: wait for every step's tokens before issuing the next")
     ap.add_argument("--kv", default="f32", choices=["f32", "fp16", "int8"], help="KV pages of the steady_b128 leg")
     ap.add_argument("--rows-per-wave", type=int, default=0)
     ap.add_argument("--kernel", type=int, default=0,

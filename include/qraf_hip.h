@@ -415,6 +415,25 @@ int qraf_engine_free_pages(qraf_engine* engine, int32_t* free_pages);
  * Transformer::forward (transformer.cpp:573-639) for many sequences at once. */
 int qraf_engine_step(qraf_engine* engine, int32_t n_rows, const int32_t* seq_ids, const uint32_t* tokens,
                      const int32_t* positions, const uint8_t* want_logits, float* logits, uint32_t* next_tokens);
+/* Pipelined greedy steps.  qraf_engine_step_async validates and issues one
+ * step as qraf_engine_step does (argmax of the rows that want logits; their
+ * logits stay in HBM) and returns without waiting for it.  Row i feeds
+ * tokens[i], or, where token_src != NULL and token_src[i] >= 0, the greedy
+ * token of logit row token_src[i] of the step issued just before this one,
+ * taken on the device: a decode row need not wait for its previous token to
+ * reach the host, so the host builds step N+1 while step N runs.  At most two
+ * steps are in flight (QRAF_HIP_ERR_STATE for a third);
+ * qraf_engine_step_collect waits for the oldest and writes its greedy tokens
+ * to next_tokens [k] (k = its rows that wanted logits, returned in *n_tokens;
+ * either may be NULL).  qraf_engine_step and qraf_engine_forward return
+ * QRAF_HIP_ERR_STATE while steps are in flight; qraf_engine_sample and
+ * qraf_engine_read_logits wait for every issued step and read the latest's
+ * logits.  No reference counterpart: InferenceEngine::generate_tokens
+ * (inference.cpp:68-159) and the scheduler feed each sampled token back from
+ * the host, one step at a time. */
+int qraf_engine_step_async(qraf_engine* engine, int32_t n_rows, const int32_t* seq_ids, const uint32_t* tokens,
+                           const int32_t* token_src, const int32_t* positions, const uint8_t* want_logits);
+int qraf_engine_step_collect(qraf_engine* engine, uint32_t* next_tokens, int32_t* n_tokens);
 /* Steps are captured once per shape (rows, logit rows, head, context bound
  * rounded up to a power of two, kernel tuning) into a HIP graph and replayed
  * (on = 1, the default); on = 0 launches every step's kernels eagerly.  No
@@ -436,10 +455,11 @@ int qraf_engine_sample(qraf_engine* engine, int32_t row0, int32_t rows, const qr
  * rows it inspects.  No reference counterpart (Transformer::forward returns
  * every logit by value, transformer.cpp:622-639). */
 int qraf_engine_read_logits(qraf_engine* engine, int32_t row0, int32_t rows, float* out);
-/* Host-side cost of qraf_engine_step, accumulated since the last reset:
- * host_us = time from entry until every launch and copy of the step was
- * issued (validation, page bookkeeping, staging, graph launch), wait_us =
- * time blocked in the step's final stream synchronisation.  No reference
+/* Host-side cost of qraf_engine_step / _step_async, accumulated since the last
+ * reset: host_us = time from entry until every launch and copy of the step
+ * was issued (validation, page bookkeeping, staging, graph launch), wait_us =
+ * time blocked waiting for steps (qraf_engine_step's final synchronisation,
+ * qraf_engine_step_collect).  No reference
  * counterpart (a measurement aid). */
 typedef struct qraf_engine_stats {
     uint64_t steps, rows;

@@ -135,6 +135,8 @@ SIGNATURES.update({
     "qraf_engine_seq_length": (C.c_int, [vp, C.c_int32, i32p]),
     "qraf_engine_free_pages": (C.c_int, [vp, i32p]),
     "qraf_engine_step": (C.c_int, [vp, C.c_int32, i32p, u32p, i32p, C.POINTER(C.c_uint8), fp, u32p]),
+    "qraf_engine_step_async": (C.c_int, [vp, C.c_int32, i32p, u32p, i32p, i32p, C.POINTER(C.c_uint8)]),
+    "qraf_engine_step_collect": (C.c_int, [vp, u32p, i32p]),
     "qraf_engine_set_graphs": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_set_row_padding": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_set_fusion": (C.c_int, [vp, C.c_int32]),

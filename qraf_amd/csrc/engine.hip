@@ -37,12 +37,16 @@ namespace qraf_hip {
 
 // ---------------------------------------------------------------- kernels
 
-// embedding row of token tok[s] (load_tensor_f32 + Tensor::row,
-// transformer.cpp:34-39, :577): dequantised values (f32)q * scale
+// embedding row of row s's token (load_tensor_f32 + Tensor::row,
+// transformer.cpp:34-39, :577): dequantised values (f32)q * scale.  The token
+// is tok[s], or, where src[s] >= 0, the previous step's greedy token of its
+// logit row src[s] (prev, still in HBM: the token never visits the host).
 __global__ void embed_kernel(const uint8_t* __restrict__ emb, uint32_t dtype, int bs, int D,
-                             const int32_t* __restrict__ tok, float* __restrict__ h) {
+                             const int32_t* __restrict__ tok, const int32_t* __restrict__ src,
+                             const uint32_t* __restrict__ prev, float* __restrict__ h) {
     const int s = blockIdx.x;
-    const size_t row = (size_t)tok[s];
+    const int32_t from = src[s];
+    const size_t row = from >= 0 ? (size_t)prev[from] : (size_t)tok[s];
     for (int i = threadIdx.x; i < D; i += blockDim.x) {
         const size_t e = row * D + i;
         float v;
@@ -352,9 +356,19 @@ struct qraf_engine {
           *logits = nullptr, *xhead = nullptr, *rope = nullptr;
     uint16_t *xh = nullptr, *xl = nullptr;
     uint32_t* amax = nullptr;
-    int32_t* d_in = nullptr;  // tokens | positions | ctx | logit rows | page table rows
-    int32_t* h_in = nullptr;  // pinned staging of the same
-    uint32_t* h_amax = nullptr;
+    int32_t* d_in = nullptr;  // tokens | positions | ctx | logit rows | token sources | page table rows
+    // Pinned staging, one slot per step in flight: a step's inputs are written
+    // into slot `slot` while the previous step (the other slot) may still be
+    // queued; its tokens come back into h_amax of the same slot.
+    int32_t* h_in[2] = {nullptr, nullptr};
+    uint32_t* h_amax[2] = {nullptr, nullptr};
+    hipEvent_t done_ev[2] = {nullptr, nullptr};  // recorded after a step's last copy
+    int slot = 0;
+    struct Pending {
+        int slot = 0, n_tok = 0;
+    };
+    Pending pending[2];  // issued, not yet collected steps, oldest first
+    int n_pending = 0;
     void* attn_ws = nullptr;
     size_t attn_ws_bytes = 0;
     void* gemm_ws = nullptr;  // split-K partial tiles of the batched projections
@@ -482,8 +496,11 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     e->layers.resize(c.num_layers);
     auto fail = [&](int rc) {
         for (void* p : e->allocs) hipFree(p);
-        if (e->h_in) hipHostFree(e->h_in);
-        if (e->h_amax) hipHostFree(e->h_amax);
+        for (int k = 0; k < 2; k++) {
+            if (e->h_in[k]) hipHostFree(e->h_in[k]);
+            if (e->h_amax[k]) hipHostFree(e->h_amax[k]);
+            if (e->done_ev[k]) hipEventDestroy(e->done_ev[k]);
+        }
         if (e->stream) hipStreamDestroy(e->stream);
         delete e;
         return rc;
@@ -518,7 +535,7 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     A(e->amax, (size_t)B * 4);
     A(e->am_val, (size_t)B * ARGMAX_CHUNKS * 4);
     A(e->am_idx, (size_t)B * ARGMAX_CHUNKS * 4);
-    e->in_words = (size_t)B * (4 + e->max_pages);
+    e->in_words = (size_t)B * (5 + e->max_pages);
     A(e->d_in, e->in_words * 4);
     e->attn_ws_bytes = attn_workspace_bytes(B, (int)c.num_heads, (int)kvh, hd, e->capacity);
     A(e->attn_ws, e->attn_ws_bytes);
@@ -541,10 +558,13 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     }
     if (e->part_ws_bytes) A(e->part_ws, e->part_ws_bytes);
 #undef A
-    if (hipMemset(e->attn_ws, 0, e->attn_ws_bytes) != hipSuccess ||
-        hipHostMalloc((void**)&e->h_in, e->in_words * 4, hipHostMallocDefault) != hipSuccess ||
-        hipHostMalloc((void**)&e->h_amax, (size_t)B * 4, hipHostMallocDefault) != hipSuccess)
+    if (hipMemset(e->attn_ws, 0, e->attn_ws_bytes) != hipSuccess)
         return fail(set_error(QRAF_HIP_ERR_HIP, "engine: workspace set-up failed"));
+    for (int k = 0; k < 2; k++)
+        if (hipHostMalloc((void**)&e->h_in[k], e->in_words * 4, hipHostMallocDefault) != hipSuccess ||
+            hipHostMalloc((void**)&e->h_amax[k], (size_t)B * 4, hipHostMallocDefault) != hipSuccess ||
+            hipEventCreateWithFlags(&e->done_ev[k], hipEventDisableTiming) != hipSuccess)
+            return fail(set_error(QRAF_HIP_ERR_HIP, "engine: staging set-up failed"));
     // RoPE table from the host libm (RopeCache::init, ops.cpp:179-193)
     {
         std::vector<float> tab((size_t)e->capacity * hd);
@@ -563,8 +583,11 @@ int qraf_engine_destroy(qraf_engine* e) {
     hipStreamSynchronize(e->stream);
     e->drop_graphs();
     for (void* p : e->allocs) hipFree(p);
-    if (e->h_in) hipHostFree(e->h_in);
-    if (e->h_amax) hipHostFree(e->h_amax);
+    for (int k = 0; k < 2; k++) {
+        if (e->h_in[k]) hipHostFree(e->h_in[k]);
+        if (e->h_amax[k]) hipHostFree(e->h_amax[k]);
+        if (e->done_ev[k]) hipEventDestroy(e->done_ev[k]);
+    }
     hipStreamDestroy(e->stream);
     delete e;
     return QRAF_HIP_OK;
@@ -847,12 +870,17 @@ static double now_us() {
     return std::chrono::duration<double, std::micro>(std::chrono::steady_clock::now().time_since_epoch()).count();
 }
 
-int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const uint32_t* tokens,
-                     const int32_t* positions, const uint8_t* want_logits, float* logits, uint32_t* next_tokens) {
-    clear_error();
+// Validates one step and issues it on the engine's stream: its inputs into
+// staging slot e->slot, the staging copy, the captured (or eager) launches,
+// the logits copy (logits != null) and the greedy tokens' copy into the
+// slot's h_amax (tok_out), then the slot's event.  The step joins e->pending.
+static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const uint32_t* tokens,
+                      const int32_t* token_src, const int32_t* positions, const uint8_t* want_logits, float* logits,
+                      bool tok_out) {
     const double t_enter = now_us();
     QH_REQUIRE(e && seq_ids && tokens && positions, QRAF_HIP_ERR_INVALID, "step: null argument");
     QH_REQUIRE(e->finalized, QRAF_HIP_ERR_STATE, "step: engine not finalized");
+    QH_REQUIRE(e->n_pending < 2, QRAF_HIP_ERR_STATE, "step: two steps in flight; collect one first");
     QH_REQUIRE(n > 0 && n <= (int32_t)e->o.max_batch, QRAF_HIP_ERR_INVALID, "step: %d rows (max_batch %u)", n,
                e->o.max_batch);
     const qraf_model_config& c = e->c;
@@ -865,7 +893,12 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         const int32_t id = seq_ids[i], p = positions[i];
         QH_REQUIRE(id >= 0 && id < (int32_t)e->seqs.size() && e->seqs[id].live, QRAF_HIP_ERR_INVALID,
                    "step: unknown sequence %d", id);
-        QH_REQUIRE(tokens[i] < c.vocab_size, QRAF_HIP_ERR_INVALID, "Token %u >= vocab %u", tokens[i], c.vocab_size);
+        const int32_t from = token_src ? token_src[i] : -1;
+        QH_REQUIRE(from < e->last_logit_rows, QRAF_HIP_ERR_INVALID,
+                   "step: row %d takes the token of logit row %d of the previous step, which left %d", i, from,
+                   e->last_logit_rows);
+        QH_REQUIRE(from >= 0 || tokens[i] < c.vocab_size, QRAF_HIP_ERR_INVALID, "Token %u >= vocab %u", tokens[i],
+                   c.vocab_size);
         QH_REQUIRE(p >= 0 && p < e->capacity, QRAF_HIP_ERR_INVALID, "step: position %d outside the cache (%d)", p,
                    e->capacity);
         qraf_engine::Seq& sq = e->seqs[id];
@@ -884,6 +917,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
     }
     QH_REQUIRE(need_pages <= (int)e->free_pages.size(), QRAF_HIP_ERR_NOMEM,
                "step: KV page pool exhausted (%d pages needed, %zu free)", need_pages, e->free_pages.size());
+    e->last_logit_rows = 0;  // set again once this step's launches are issued
     // With step graphs, a step of more than 8 rows runs padded to a multiple
     // of row_pad rows (at most max_batch), and its logit rows likewise, so
     // that steps of nearby sizes share one graph: a pad row is token 0 at
@@ -896,11 +930,12 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
                           ? std::min((n + e->row_pad - 1) / e->row_pad * e->row_pad, (int)e->o.max_batch)
                           : n;
     int n_logit_rows = 0;
-    int32_t* tok = e->h_in;
+    int32_t* tok = e->h_in[e->slot];
     int32_t* pos = tok + n_pad;
     int32_t* ctx = pos + n_pad;
     int32_t* lrows = ctx + n_pad;
-    int32_t* ptab = lrows + n_pad;
+    int32_t* src = lrows + n_pad;
+    int32_t* ptab = src + n_pad;
     int step_ctx = 1;  // longest context of this step: sizes the attention grid (and skips the merge)
     for (int i = 0; i < n; i++) {
         qraf_engine::Seq& sq = e->seqs[seq_ids[i]];
@@ -909,7 +944,8 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
             e->free_pages.pop_back();
         }
         sq.len = std::max(sq.len, positions[i] + 1);
-        tok[i] = (int32_t)tokens[i];
+        src[i] = token_src ? token_src[i] : -1;
+        tok[i] = src[i] >= 0 ? 0 : (int32_t)tokens[i];
         pos[i] = positions[i];
         ctx[i] = positions[i] + 1;
         step_ctx = std::max(step_ctx, ctx[i]);
@@ -920,6 +956,7 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         tok[i] = 0;
         pos[i] = 0;
         ctx[i] = 1;
+        src[i] = -1;
         for (int j = 0; j < MP; j++) ptab[(size_t)i * MP + j] = j == 0 ? e->scratch_page : 0;
     }
     const int n_logit_real = n_logit_rows;
@@ -930,13 +967,14 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
     }
     n = n_pad;
     hipStream_t s = e->stream;
-    const size_t words = (size_t)n * (4 + MP);
-    const bool head = n_logit_rows > 0 && (logits || next_tokens);
+    const size_t words = (size_t)n * (5 + MP);
+    const bool head = n_logit_rows > 0 && (logits || tok_out);
     const int32_t* d_tok = e->d_in;
     const int32_t* d_pos = d_tok + n;
     const int32_t* d_ctx = d_pos + n;
     const int32_t* d_lrows = d_ctx + n;
-    const int32_t* d_ptab = d_lrows + n;
+    const int32_t* d_src = d_lrows + n;
+    const int32_t* d_ptab = d_src + n;
 
     const int D = (int)c.hidden_size, F = (int)c.intermediate_size, V = (int)c.vocab_size;
     const int H = (int)c.num_heads, Hkv = (int)c.num_kv_heads, hd = e->hd;
@@ -980,11 +1018,11 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         return launch_qgemm(Wt, dt, 32, N, K, e->xh, e->xl, rows, y, add, e->gemm_ws, e->gemm_ws_bytes, s, true);
     };
 
-    // The whole step, stream-ordered: staging copy, embedding, layers, head and
-    // argmax.  ctx_grid >= every row's context sizes the attention grid.
+    // The step's launches, stream-ordered: embedding, layers, head and argmax.
+    // ctx_grid >= every row's context sizes the attention grid.
     auto enqueue = [&](int ctx_grid) -> int {
-        QH_CHECK_HIP(hipMemcpyAsync(e->d_in, e->h_in, words * 4, hipMemcpyHostToDevice, s));
-        hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, 32, D, d_tok, e->h);
+        hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, 32, D, d_tok, d_src, e->amax,
+                           e->h);
         QH_CHECK_HIP(hipGetLastError());
         if (n > 1 && e->fused) {
             // Batched layer on the matrix cores, 9 launches: each projection writes
@@ -1076,6 +1114,9 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         return QRAF_HIP_OK;
     };
 
+    // the staging copy stays outside the captured launches: its source is the
+    // slot's pinned buffer, which alternates between steps
+    QH_CHECK_HIP(hipMemcpyAsync(e->d_in, e->h_in[e->slot], words * 4, hipMemcpyHostToDevice, s));
     if (e->use_graphs) {
         // context bound rounded up to a power of two (>= one attention chunk) so
         // that a decode reuses one graph for many steps
@@ -1157,17 +1198,59 @@ int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const ui
         QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_real * V * 4, hipMemcpyDeviceToHost, s));
     // tokens come back through pinned staging: an async copy into pageable
     // memory would block the host until the whole step has run
-    if (head && next_tokens)
-        QH_CHECK_HIP(hipMemcpyAsync(e->h_amax, e->amax, (size_t)n_logit_real * 4, hipMemcpyDeviceToHost, s));
-    const double t_issued = now_us();
-    QH_CHECK_HIP(hipStreamSynchronize(s));
-    const double t_done = now_us();
-    if (head && next_tokens) memcpy(next_tokens, e->h_amax, (size_t)n_logit_real * 4);
+    const int slot = e->slot;
+    const bool toks = head && tok_out;
+    if (toks) QH_CHECK_HIP(hipMemcpyAsync(e->h_amax[slot], e->amax, (size_t)n_logit_real * 4, hipMemcpyDeviceToHost, s));
+    QH_CHECK_HIP(hipEventRecord(e->done_ev[slot], s));
+    e->pending[e->n_pending].slot = slot;
+    e->pending[e->n_pending].n_tok = toks ? n_logit_real : 0;
+    e->n_pending += 1;
+    e->slot ^= 1;
     e->stats.steps += 1;
     e->stats.rows += (uint64_t)n_real;
     e->stats.pad_rows += (uint64_t)(n - n_real);
-    e->stats.host_us += t_issued - t_enter;
-    e->stats.wait_us += t_done - t_issued;
+    e->stats.host_us += now_us() - t_enter;
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_step(qraf_engine* e, int32_t n, const int32_t* seq_ids, const uint32_t* tokens,
+                     const int32_t* positions, const uint8_t* want_logits, float* logits, uint32_t* next_tokens) {
+    clear_error();
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "step: null engine");
+    QH_REQUIRE(e->n_pending == 0, QRAF_HIP_ERR_STATE, "step: %d asynchronous steps not collected", e->n_pending);
+    QH_TRY(step_issue(e, n, seq_ids, tokens, nullptr, positions, want_logits, logits, next_tokens != nullptr));
+    const qraf_engine::Pending p = e->pending[0];
+    e->n_pending = 0;
+    const double t0 = now_us();
+    QH_CHECK_HIP(hipStreamSynchronize(e->stream));  // also completes a logits copy into pageable memory
+    e->stats.wait_us += now_us() - t0;
+    if (next_tokens && p.n_tok) memcpy(next_tokens, e->h_amax[p.slot], (size_t)p.n_tok * 4);
+    return QRAF_HIP_OK;
+}
+
+// One step issued without waiting for it: row i's token is tokens[i], or,
+// where token_src[i] >= 0, the greedy token of logit row token_src[i] of the
+// step issued just before (taken on the device).  At most two steps are in
+// flight; qraf_engine_step_collect returns them in order.
+int qraf_engine_step_async(qraf_engine* e, int32_t n, const int32_t* seq_ids, const uint32_t* tokens,
+                           const int32_t* token_src, const int32_t* positions, const uint8_t* want_logits) {
+    clear_error();
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "step_async: null engine");
+    return step_issue(e, n, seq_ids, tokens, token_src, positions, want_logits, nullptr, true);
+}
+
+int qraf_engine_step_collect(qraf_engine* e, uint32_t* next_tokens, int32_t* n_tokens) {
+    clear_error();
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "step_collect: null engine");
+    QH_REQUIRE(e->n_pending > 0, QRAF_HIP_ERR_STATE, "step_collect: no step in flight");
+    const qraf_engine::Pending p = e->pending[0];
+    e->pending[0] = e->pending[1];
+    e->n_pending -= 1;
+    const double t0 = now_us();
+    QH_CHECK_HIP(hipEventSynchronize(e->done_ev[p.slot]));
+    e->stats.wait_us += now_us() - t0;
+    if (next_tokens && p.n_tok) memcpy(next_tokens, e->h_amax[p.slot], (size_t)p.n_tok * 4);
+    if (n_tokens) *n_tokens = p.n_tok;
     return QRAF_HIP_OK;
 }
 
@@ -1187,6 +1270,7 @@ int qraf_engine_read_logits(qraf_engine* e, int32_t row0, int32_t rows, float* o
 int qraf_engine_set_fusion(qraf_engine* e, int32_t flags) {
     clear_error();
     QH_REQUIRE(e && (flags & ~1) == 0, QRAF_HIP_ERR_INVALID, "set_fusion: flags %d", flags);
+    QH_CHECK_HIP(hipStreamSynchronize(e->stream));  // no captured step still in flight
     e->fuse_rope = (flags & 1) != 0;
     e->drop_graphs();  // captured steps hold the other form
     return QRAF_HIP_OK;

@@ -192,6 +192,27 @@ class Engine:
              lg.ctypes.data_as(fp) if lg is not None else None, nx.ctypes.data_as(u32p) if nx is not None else None)
         return lg, nx
 
+    def step_async(self, seq_ids, tokens, positions, want_logits=None, token_src=None):
+        """Issue one greedy step without waiting for it (at most two in
+        flight).  token_src[i] >= 0: row i feeds the greedy token of logit
+        row token_src[i] of the step issued just before, taken on the device
+        (tokens[i] is then ignored).  collect() returns the steps' tokens in
+        issue order."""
+        sid = np.ascontiguousarray(seq_ids, dtype=np.int32)
+        tok = np.ascontiguousarray(tokens, dtype=np.uint32)
+        pos = np.ascontiguousarray(positions, dtype=np.int32)
+        src = None if token_src is None else np.ascontiguousarray(token_src, dtype=np.int32)
+        wl = None if want_logits is None else np.ascontiguousarray(want_logits, dtype=np.uint8)
+        call("qraf_engine_step_async", self.h, sid.size, sid.ctypes.data_as(i32p), tok.ctypes.data_as(u32p),
+             src.ctypes.data_as(i32p) if src is not None else None, pos.ctypes.data_as(i32p),
+             wl.ctypes.data_as(C.POINTER(C.c_uint8)) if wl is not None else None)
+
+    def collect(self) -> np.ndarray:
+        """Wait for the oldest step in flight; its greedy tokens [k]."""
+        out = np.empty(self.max_batch, np.uint32)
+        k = C.c_int32()
+        call("qraf_engine_step_collect", self.h, out.ctypes.data_as(u32p), C.byref(k))
+        return out[:k.value]
 
     def read_logits(self, row0: int, rows: int = 1) -> np.ndarray:
         """Logit rows row0 .. row0+rows-1 of the last step (in the order of the
@@ -359,6 +380,9 @@ class Request:
     seq: int = -1
     next_prompt: int = 0
     admit_step: int = -1  # scheduler step at which the request took a slot
+    inflight: int = 0     # pipelined runs: tokens issued and not yet collected
+    lrow: int = -1        # its logit row in step lrow_step (the source of its next decode row's token)
+    lrow_step: int = -1
 
 
 class BatchScheduler:
@@ -378,10 +402,23 @@ class BatchScheduler:
     reference's scheduler runs requests one at a time over one shared cache,
     F3 in the survey, so it offers no batched numerics to mirror).  With the
     defaults (prefill_chunk 1, max_rows = max_batch) every active request
-    feeds exactly one token per step."""
+    feeds exactly one token per step.
+
+    pipeline=True (when no request has a repetition penalty): run() issues
+    step N+1 before it collects step N's tokens (Engine.step_async), each
+    decode row taking its token from step N's argmax on the device, so the
+    host builds the next step while the device runs this one.  A request
+    whose last token (by max_tokens) is in flight gets no further row and its
+    slot goes to the next queued request at once, as the unpipelined run
+    retires it before building that step: without EOS both runs issue the
+    same steps, row for row.  A request that emits EOS is found a step late:
+    the row it had in the next step is dropped (its cache writes land in
+    pages it then releases, which later steps, ordered after it on the
+    stream, may reuse) and its slot is refilled a step later.  The observer
+    sees tokens only (the logits in HBM already belong to the next step)."""
 
     def __init__(self, engine: Engine, max_batch: int | None = None, max_rows: int | None = None,
-                 prefill_chunk: int = 1):
+                 prefill_chunk: int = 1, pipeline: bool = False):
         self.engine = engine
         self.max_batch = max_batch or engine.max_batch
         self.max_rows = min(max_rows or self.max_batch, engine.max_batch)
@@ -391,6 +428,7 @@ class BatchScheduler:
         if prefill_chunk < 1:
             raise ValueError("prefill_chunk must be >= 1")
         self.prefill_chunk = prefill_chunk
+        self.pipeline = pipeline
         self.pending = deque()
         self.active = []
         self.done = []
@@ -488,6 +526,106 @@ class BatchScheduler:
         return True
 
     def run(self):
+        if self.pipeline and all(r.penalty == 1.0 for r in list(self.pending) + self.active):
+            self._run_pipelined()
         while self.step():
             pass
         return self.done
+
+    def _run_pipelined(self):
+        inflight = deque()  # per issued step: the requests of its logit rows
+        while True:
+            lrows = self._issue()
+            if lrows is not None:
+                inflight.append(lrows)
+                if len(inflight) < 2:
+                    continue
+            if not inflight:
+                if self.active:
+                    raise RuntimeError("scheduler: active requests but no rows to run")
+                return
+            self._collect(inflight.popleft())
+
+    def _issue(self):
+        """Build and issue the next step without waiting; the requests of its
+        logit rows, or None when there is nothing to run."""
+        t_start = time.perf_counter()
+        # a request whose last token is in flight no longer holds its slot
+        held = sum(1 for r in self.active
+                   if r.state != "DECODING" or len(r.generated) + r.inflight < r.max_tokens)
+        while self.pending and held < self.max_batch:
+            r = self.pending.popleft()
+            r.seq = self.engine.seq_create()
+            r.state = "PREFILLING"
+            r.admit_step = self.steps
+            self.active.append(r)
+            held += 1
+        rows = []  # (request, token, position, wants logits, token source)
+        for r in self.active:
+            if r.state != "DECODING":
+                continue
+            g = len(r.generated) + r.inflight
+            if g >= r.max_tokens:
+                continue  # its last token is in flight
+            if r.inflight:
+                assert r.lrow_step == self.steps - 1, "decode row without a token in the previous step"
+                rows.append((r, 0, len(r.prompt) + g - 1, True, r.lrow))
+            else:
+                rows.append((r, r.generated[-1], len(r.prompt) + g - 1, True, -1))
+        budget = self.max_rows - len(rows)
+        for r in self.active:
+            if r.state != "PREFILLING" or budget <= 0:
+                continue
+            c = min(self.prefill_chunk, len(r.prompt) - r.next_prompt, budget)
+            for i in range(r.next_prompt, r.next_prompt + c):
+                rows.append((r, r.prompt[i], i, i == len(r.prompt) - 1, -1))
+            budget -= c
+        if not rows:
+            self.host_s += time.perf_counter() - t_start
+            return None
+        t_eng = time.perf_counter()
+        self.engine.step_async([r.seq for (r, *_) in rows], [t for (_, t, *_) in rows], [p for (_, _, p, _, _) in rows],
+                               want_logits=np.array([w for (_, _, _, w, _) in rows], np.uint8),
+                               token_src=[s for (*_, s) in rows])
+        t_eng_end = time.perf_counter()
+        lrows = []
+        for (r, _, _, w, _) in rows:
+            if r.state == "PREFILLING":
+                r.next_prompt += 1
+                if r.next_prompt == len(r.prompt):
+                    r.state = "DECODING"
+            if w:
+                r.lrow, r.lrow_step = len(lrows), self.steps
+                r.inflight += 1
+                lrows.append(r)
+        self.steps += 1
+        self.rows += len(rows)
+        self.engine_s += t_eng_end - t_eng
+        self.host_s += time.perf_counter() - t_start - (t_eng_end - t_eng)
+        return lrows
+
+    def _collect(self, lrows):
+        """Wait for the oldest issued step and apply its tokens."""
+        t_eng = time.perf_counter()
+        nx = self.engine.collect()
+        t_eng_end = time.perf_counter()
+        self.engine_s += t_eng_end - t_eng
+        if self.observer is not None:
+            self.observer(self, lrows, nx)
+        t_obs = time.perf_counter()
+        retire = []
+        for k, r in enumerate(lrows):
+            r.inflight -= 1
+            if r.state == "DONE":
+                continue  # retired on EOS a step ago: this row ran past it
+            t = int(nx[k])
+            if (r.eos is not None and t == r.eos) or len(r.generated) >= r.max_tokens:
+                retire.append(r)
+                continue
+            r.generated.append(t)
+            if len(r.generated) >= r.max_tokens:
+                retire.append(r)
+        for r in retire:
+            self.active.remove(r)
+            self._finish(r)
+        self.host_s += time.perf_counter() - t_obs

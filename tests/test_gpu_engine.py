@@ -145,10 +145,12 @@ def test_greedy_streams_32_tokens(hip, kv):
     tf.engine.close()
 
 
-def test_batched_step_equals_single_sequence_decode(hip):
+@pytest.mark.parametrize("pipeline", [False, True])
+def test_batched_step_equals_single_sequence_decode(hip, pipeline):
     """Several sequences of different lengths advanced together (GEMM path,
     several rows per step) produce each sequence's own greedy stream, and
-    logits within tolerance of the oracle."""
+    logits within tolerance of the oracle; pipelined (step N+1 issued before
+    step N's tokens reach the host) or not."""
     from qraf_amd.engine import BatchScheduler, Engine
     kw, seed = SMALL["q4_gqa8_hd128"]
     m = oracle_model(kw, seed)
@@ -159,7 +161,7 @@ def test_batched_step_equals_single_sequence_decode(hip):
     e.finalize()
     pool = e.free_pages()
     prompts = [[L.or_gen_token(100 + r, i, kw["vocab"]) for i in range(3 + 5 * r)] for r in range(6)]
-    sched = BatchScheduler(e, max_batch=4)  # 6 requests, 4 slots: admission as others finish
+    sched = BatchScheduler(e, max_batch=4, pipeline=pipeline)  # 6 requests, 4 slots: admission as others finish
     ids = [sched.submit(p, 10 + 3 * r) for r, p in enumerate(prompts)]
     done = {r.id: r for r in sched.run()}
     for r, (i, p) in enumerate(zip(ids, prompts)):
@@ -168,8 +170,9 @@ def test_batched_step_equals_single_sequence_decode(hip):
     e.close()
 
 
+@pytest.mark.parametrize("pipeline", [False, True])
 @pytest.mark.parametrize("chunk,max_rows,plen", [(7, 32, 9), (64, 40, 9), (3, 4, 9), (512, 512, 31), (300, 300, 33)])
-def test_scheduler_chunked_prefill_streams(hip, chunk, max_rows, plen):
+def test_scheduler_chunked_prefill_streams(hip, chunk, max_rows, plen, pipeline):
     """Continuous batching with prompts entering in chunks of up to `chunk`
     tokens per step within a `max_rows` row budget (decode rows first; the
     last two cases run steps of several hundred rows, over the GEMM's
@@ -185,7 +188,7 @@ def test_scheduler_chunked_prefill_streams(hip, chunk, max_rows, plen):
     e.finalize()
     pool = e.free_pages()
     prompts = [[L.or_gen_token(300 + r, i, kw["vocab"]) for i in range(2 + plen * r)] for r in range(7)]
-    sched = BatchScheduler(e, max_batch=4, max_rows=max_rows, prefill_chunk=chunk)
+    sched = BatchScheduler(e, max_batch=4, max_rows=max_rows, prefill_chunk=chunk, pipeline=pipeline)
     ids = [sched.submit(p, 6 + 2 * r) for r, p in enumerate(prompts)]
     done = {r.id: r for r in sched.run()}
     for r, (i, p) in enumerate(zip(ids, prompts)):
@@ -195,6 +198,97 @@ def test_scheduler_chunked_prefill_streams(hip, chunk, max_rows, plen):
     if chunk > 1 and max_rows > 4:
         assert sched.steps < 25 + 6 * plen  # prompts entered in chunks
     assert e.free_pages() == pool
+    e.close()
+
+
+def test_pipelined_scheduler_eos_retirement(hip):
+    """Requests that stop on EOS: the pipelined run finds EOS a step late and
+    drops the row it had issued past it; every stream equals the unpipelined
+    run's (and each request's independent greedy decode cut at EOS), and
+    every page comes back."""
+    from qraf_amd.engine import BatchScheduler, Engine
+    kw, seed = SMALL["q8_llama"]
+    m = oracle_model(kw, seed)
+    L = po.lib()
+    prompts = [[L.or_gen_token(500 + r, i, kw["vocab"]) for i in range(3 + 4 * r)] for r in range(8)]
+    full = [m.generate(p, 24, 1.0, eos=-1) for p in prompts]
+    # an EOS id that cuts several streams early: the token (past the first)
+    # found in the most streams
+    streams = {}
+    for k, f in enumerate(full):
+        for t in set(f[1:]):
+            streams.setdefault(t, set()).add(k)
+    eos = max(sorted(streams), key=lambda t: len(streams[t]))
+    want = [f[:f.index(eos)] if eos in f else f for f in full]
+    assert sum(len(w) < 24 for w in want) >= 2, "the EOS id should end at least two streams early"
+    runs = {}
+    for stop in (None, eos):
+        for pipeline in (False, True):
+            e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=16)
+            for name, dt, shape, data in m.tensors():
+                e.set_tensor(name, dt, shape, data)
+            e.finalize()
+            pool = e.free_pages()
+            sched = BatchScheduler(e, max_batch=3, max_rows=16, prefill_chunk=4, pipeline=pipeline)
+            ids = [sched.submit(p, 24, eos=stop) for p in prompts]
+            done = {r.id: r for r in sched.run()}
+            runs[stop, pipeline] = ([done[i].generated for i in ids], sched.steps, sched.rows)
+            assert e.free_pages() == pool
+            assert all(r.inflight == 0 for r in done.values())
+            e.close()
+    # without EOS the pipelined run issues the same steps, row for row
+    assert runs[None, True] == runs[None, False]
+    assert runs[None, True][0] == full
+    assert runs[eos, False][0] == want
+    assert runs[eos, True][0] == want
+    # with EOS it runs one dropped row per request that stopped on it before
+    # its last allowed token (a row past the EOS it had not yet seen)
+    dropped = sum(len(w) < 23 for w in want)
+    assert runs[eos, True][2] == runs[eos, False][2] + dropped
+
+
+def test_async_step_token_sources_and_states(hip):
+    """Engine.step_async / collect: decode rows fed from the previous step's
+    argmax on the device give the host-fed greedy streams; a third step in
+    flight, a synchronous step while steps are in flight and a token source
+    past the previous step's logit rows are refused."""
+    from qraf_amd._lib import HipError
+    from qraf_amd.engine import Engine
+    kw, seed = SMALL["q4_qwen2_tied_bias"]
+    m = oracle_model(kw, seed)
+    L = po.lib()
+    e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=32)
+    for name, dt, shape, data in m.tensors():
+        e.set_tensor(name, dt, shape, data)
+    e.finalize()
+    prompts = [[L.or_gen_token(700 + r, i, kw["vocab"]) for i in range(5 + 3 * r)] for r in range(3)]
+    want = [m.generate(p, 12, 1.0, eos=-1) for p in prompts]
+    seqs = [e.seq_create() for _ in prompts]
+    # prefill: every prompt in one step, the last row of each wants logits
+    rows = [(s, t, i, i == len(p) - 1) for s, p in zip(seqs, prompts) for i, t in enumerate(p)]
+    e.step_async([r[0] for r in rows], [r[1] for r in rows], [r[2] for r in rows], want_logits=[r[3] for r in rows])
+    got = [[] for _ in prompts]
+    src = list(range(len(prompts)))
+    for k in range(11):
+        pos = [len(p) + k for p in prompts]
+        e.step_async(seqs, [0] * len(seqs), pos, token_src=src)
+        if k == 0:
+            with pytest.raises(HipError):
+                e.step_async(seqs, [0] * len(seqs), [x + 1 for x in pos], token_src=src)
+            with pytest.raises(HipError):
+                e.step(seqs, [0] * len(seqs), [x + 1 for x in pos])
+        for j, t in enumerate(e.collect()):
+            got[j].append(int(t))
+    for j, t in enumerate(e.collect()):
+        got[j].append(int(t))
+    assert got == want
+    with pytest.raises(HipError):
+        e.collect()  # nothing in flight
+    with pytest.raises(HipError):  # the last step left 3 logit rows
+        e.step_async(seqs, [0] * 3, [len(p) + 11 for p in prompts], token_src=[0, 1, 3])
+    # a synchronous step works again once everything is collected
+    _, nx = e.step(seqs, [w[-1] for w in want], [len(p) + 11 for p in prompts])
+    assert len(nx) == 3
     e.close()
 
 
