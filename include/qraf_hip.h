@@ -235,6 +235,18 @@ int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int3
  * automatic choice.  Affects the workspace queries too.  No counterpart in
  * the reference (a performance knob). */
 int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe, int batch_chunk);
+/* Work schedule of the pipelined GEMM (batches over 32 rows, tile-major
+ * weights): mode 1 = stream-K (each resident workgroup takes an equal share
+ * of the (weight tile, quant block) pairs, at least min_blocks blocks (0:
+ * 16), crossing tile boundaries; a tile's segments are summed in segment
+ * order, so results stay deterministic), 2 and 0 (the default) = the
+ * uniform split-K grid, which measured faster at the continuous-batch
+ * shapes (shares of 11-21 blocks pay a pipeline prologue per segment).  A
+ * forced split count
+ * (qraf_hip_set_qgemm_tuning) selects the uniform grid.  Affects the
+ * workspace queries too.  No counterpart in the reference (a performance
+ * knob). */
+int qraf_hip_set_qgemm_schedule(int32_t mode, int32_t min_blocks);
 /* Workspace (bytes) that lets qraf_hip_qgemm_dev split the in_dim range of an
  * out_dim x in_dim product at this batch across workgroups; 0 when it does
  * not split. */

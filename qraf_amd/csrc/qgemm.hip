@@ -443,12 +443,21 @@ struct PipeGeom {
     static constexpr int MINB = SMALL ? 2 : 1;
 };
 
+// Stream-K schedule: workgroup w of G owns blocks [w T / G, (w+1) T / G) of the T = units x nb
+// (tile, quant block) pairs, units in tile-major order; the workgroup that owns pair x:
+__host__ __device__ inline int sk_owner(long long x, long long T, int G) {
+    int w = (int)(x * G / T);
+    while (w + 1 < G && (long long)(w + 1) * T / G <= x) w++;
+    return w;
+}
+
 template <int FMT, int TM, int TN, int KC, int WN, int WMN>
 __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>::MINB)) void qgemm_pipe_kernel(const uint8_t* __restrict__ Wt, int N, int nb,
                                                                  const uint16_t* __restrict__ xh,
                                                                  const uint16_t* __restrict__ xl, int K, int M,
                                                                  float* Y, const float* add, int bps,
-                                                                 float* __restrict__ part) {
+                                                                 float* __restrict__ part, int skG, int sk_ntiles,
+                                                                 int skS) {
     using G = PipeGeom<FMT, TM, TN, KC, WN, WMN>;
     constexpr int MW = G::MW, NW = G::NW, TB = G::TB, NWV = G::NWV;
 
@@ -457,18 +466,18 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
     const int wm = wave / WN, wn = wave % WN;
     const bool wextra = wave < G::WEXTRA;  // this wave issues one more W instruction per stage
     const int seg = lane >> 4, l16 = lane & 15;
-    const int m0 = blockIdx.z * MW;
-    const int n0 = blockIdx.x * NW;
-    const int b_begin = blockIdx.y * bps;  // bps: a positive multiple of KC
-    const int b_end = min(nb, b_begin + bps);
-    const int nstages = (bps / KC + 2) / 3 * 3;  // whole trips of the 3-stage loop
-
-    // ---- DMA source offsets (bytes), fixed per lane and instruction; the
-    // stage's first block adds cb*64 (X) or cb*TB (W)
     const uint32_t xbytes = (uint32_t)((size_t)M * K * 2);
     const v4i xrs[2] = {make_rsrc_words(xh, xbytes), make_rsrc_words(xl, xbytes)};
     const int ntile16 = (N + 15) / 16;
     const v4i wrs = make_rsrc_words(Wt, (uint32_t)min((size_t)ntile16 * nb * TB, (size_t)0xFFFFFFFFu));
+
+    // One segment: weight rows [n0, n0 + NW) x batch rows [m0, m0 + MW) over
+    // quant blocks [b_begin, b_end), written to dst (+ add when given).
+    auto segment = [&](const int n0, const int m0, const int b_begin, const int b_end, float* dst, const float* addp) {
+    const int nstages = ((b_end - b_begin + KC - 1) / KC + 2) / 3 * 3;  // whole trips of the 3-stage loop
+
+    // ---- DMA source offsets (bytes), fixed per lane and instruction; the
+    // stage's first block adds cb*64 (X) or cb*TB (W)
     uint32_t xo[G::XI], wo[G::WIH];
 #pragma unroll
     for (int q = 0; q < G::XI; q++) {
@@ -621,8 +630,7 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
             acc[TM - 1][u][r] = __builtin_fmaf(dR[3][u][r], sP[u], acc[TM - 1][u][r]);
         }
 
-    // epilogue: direct (+ residual) or this split's partial tile
-    float* dst = part ? part + (size_t)blockIdx.y * M * N : Y;
+    // epilogue: direct (+ residual) or a partial tile
 #pragma unroll
     for (int t = 0; t < TM; t++) {
 #pragma unroll
@@ -633,11 +641,58 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
                 const int m = m0 + (wm * TM + t) * 16 + seg * 4 + r;
                 if (m < M && n < N) {
                     float v = acc[t][u][r];
-                    if (!part && add) v += add[(size_t)m * N + n];
+                    if (addp) v += addp[(size_t)m * N + n];
                     dst[(size_t)m * N + n] = v;
                 }
             }
         }
+    }
+    };  // segment
+
+    if (skG == 0) {  // uniform split: workgroup (tile, split, batch chunk)
+        const int b_begin = blockIdx.y * bps;  // bps: a positive multiple of KC
+        segment(blockIdx.x * NW, blockIdx.z * MW, b_begin, min(nb, b_begin + bps),
+                part ? part + (size_t)blockIdx.y * M * N : Y, part ? nullptr : add);
+        return;
+    }
+    // stream-K: this workgroup's equal share of the (tile, block) pairs, one
+    // segment per tile it touches; segment k of a tile writes partial slice k
+    // (or Y itself when no tile is shared, skS == 1), and the tile's last
+    // segment zeroes the slices past the tile's segment count
+    const long long T = (long long)sk_ntiles * ((M + MW - 1) / MW) * nb;
+    const int w = blockIdx.x;
+    long long lo = (long long)w * T / skG;
+    const long long hi = (long long)(w + 1) * T / skG;
+    while (lo < hi) {
+        const long long u = lo / nb;
+        const int b0 = (int)(lo % nb);
+        const int b1 = (int)min((long long)nb, b0 + (hi - lo));
+        const int tile = (int)(u % sk_ntiles), mc = (int)(u / sk_ntiles);
+        const int first = sk_owner(u * nb, T, skG);
+        const int k = w - first, nseg = sk_owner(u * nb + nb - 1, T, skG) - first + 1;
+        lds_barrier();  // every wave is done with the stage buffers of the previous segment
+        if (!part) {  // no tile is shared (skS == 1)
+            segment(tile * NW, mc * MW, b0, b1, Y, add);
+        } else {
+            segment(tile * NW, mc * MW, b0, b1, part + (size_t)k * M * N, nullptr);
+            if (k == nseg - 1) {
+                for (int sl = nseg; sl < skS; sl++) {
+                    float* z = part + (size_t)sl * M * N;
+#pragma unroll
+                    for (int t = 0; t < TM; t++)
+#pragma unroll
+                        for (int uu = 0; uu < TN; uu++) {
+                            const int n = tile * NW + (wn * TN + uu) * 16 + l16;
+#pragma unroll
+                            for (int r = 0; r < 4; r++) {
+                                const int m = mc * MW + (wm * TM + t) * 16 + seg * 4 + r;
+                                if (m < M && n < N) z[(size_t)m * N + n] = 0.f;
+                            }
+                        }
+                }
+            }
+        }
+        lo += b1 - b0;
     }
 }
 
@@ -682,6 +737,7 @@ int launch_reduce_slices(const float* part, int S, size_t MN, float* Y, const fl
 struct QgPlan {
     int WM, WN, TM, TN, KC, MW, NW, ntiles, mchunks, S, bps;
     bool pipe;  // qgemm_pipe_kernel (tile-major weights, batch tiles over 32 rows)
+    int skG;    // > 0: stream-K over skG workgroups (pipelined kernel only); S = the slices a tile may need
     size_t ws_bytes;
 };
 
@@ -691,6 +747,39 @@ static int g_qg_splits = 0;  // forced split count
 static int g_qg_pipe = 0;    // 1: pipelined kernel for every tiled batch over 32 rows, 2: its narrow
                              // 4-wave form, -1: never
 static int g_qg_mchunk = 0;  // batch rows per workgroup at most (0: QG_MCHUNK)
+static int g_qg_sched = 0;   // pipelined kernel: 0 automatic (the uniform split), 1 stream-K, 2 uniform split
+static int g_qg_skmin = 0;   // stream-K: quant blocks per workgroup at least (0: 16)
+
+static int qg_cu_count() {
+    static int n = 0;
+    if (!n) {
+        int d = 0;
+        hipDeviceProp_t pr;
+        if (hipGetDevice(&d) == hipSuccess && hipGetDeviceProperties(&pr, d) == hipSuccess) n = pr.multiProcessorCount;
+        if (n <= 0) n = 256;
+    }
+    return n;
+}
+
+// Stream-K for a pipelined plan (g_qg_sched == 1): `slots` workgroups
+// resident at once, each an equal share of the (tile, block) pairs (at least
+// g_qg_skmin blocks), so every CU gets the same work whatever the tile count;
+// S becomes the most segments any tile has.  Not the automatic choice: on
+// MI355X at the continuous-batch shapes (128 rows) it was slower than the
+// uniform grid (Q4 11008 x 2048: 37.6 against 33.0 us; a 128-sequence decode
+// step 6.34 against 5.96 ms), since shares of 11-21 blocks pay a pipeline
+// prologue per segment and more partial slices than the balance saves.
+static void qgemm_stream(QgPlan& p, int nb, int slots) {
+    if (g_qg_sched != 1 || g_qg_splits > 0) return;
+    const long long units = (long long)p.ntiles * p.mchunks, T = units * nb;
+    const int minb = g_qg_skmin > 0 ? g_qg_skmin : 16;
+    const int G = (int)std::max(1LL, std::min((long long)slots, T / minb));
+    int smax = 1;
+    for (long long u = 0; u < units; u++)
+        smax = std::max(smax, sk_owner(u * nb + nb - 1, T, G) - sk_owner(u * nb, T, G) + 1);
+    p.skG = G;
+    p.S = smax;
+}
 
 // Tile shape and split count for an N x K matrix times M rows.  Batch tiles
 // of more than 32 rows use 2 x WN waves of 64 weight rows each; smaller ones
@@ -731,6 +820,7 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
             while (S < 64 && tiles * S * 2 <= slots && nb >= 32 * S) S *= 2;
         p.bps = ((nb + S - 1) / S + p.KC - 1) / p.KC * p.KC;
         p.S = (nb + p.bps - 1) / p.bps;
+        qgemm_stream(p, nb, qg_cu_count() * (p.TM == 4 ? 2 : 1));
         p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
         return p;
     }
@@ -768,6 +858,7 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
         // trips and skips the blocks past the split
         p.bps = ((nb + S - 1) / S + p.KC - 1) / p.KC * p.KC;
         p.S = (nb + p.bps - 1) / p.bps;
+        qgemm_stream(p, nb, qg_cu_count());
         p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
         return p;
     }
@@ -801,6 +892,15 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
     p.S = (nb + p.bps - 1) / p.bps;  // no empty splits
     p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
     return p;
+}
+
+int set_qgemm_schedule(int mode, int min_blocks) {
+    QH_REQUIRE(mode >= 0 && mode <= 2 && min_blocks >= 0 && min_blocks <= 4096, QRAF_HIP_ERR_INVALID,
+               "qgemm schedule: mode %d, min_blocks %d", mode, min_blocks);
+    g_qg_sched = mode;
+    g_qg_skmin = min_blocks;
+    bump_tuning_generation();
+    return QRAF_HIP_OK;
 }
 
 int set_qgemm_tuning(int waves, int splits, int pipe, int mchunk) {
@@ -886,17 +986,18 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
             part = (float*)ws;
         } else {  // no (or too small a) workspace: one split
             p.S = 1;
+            p.skG = 0;
             const int unit = (p.pipe ? 1 : 2) * p.KC;
             p.bps = (nb + unit - 1) / unit * unit;
         }
     }
     QH_REQUIRE(p.mchunks <= 65535, QRAF_HIP_ERR_INVALID, "qgemm: batch %d too large", M);
-    const dim3 grid(p.ntiles, p.S, p.mchunks);
+    const dim3 grid = p.skG > 0 ? dim3(p.skG, 1, 1) : dim3(p.ntiles, p.S, p.mchunks);
     if (p.pipe) {
 #define QH_P(F, TM_, TN_, WN_, WM_)                                                                        \
     hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_>), grid, dim3(64 * WN_ * WM_), 0, s,           \
                        (const uint8_t*)W, N, nb, \
-                       xh, xl, K, M, Y, add, p.bps, part)
+                       xh, xl, K, M, Y, add, p.bps, part, p.skG, p.ntiles, p.S)
         if (dtype == DT_Q8_0) {
             if (p.WN == 4 && p.WM == 1) {
                 if (p.TM == 8) QH_P(8, 8, 2, 4, 1);
@@ -958,6 +1059,11 @@ extern "C" {
 int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int32_t rows, int32_t cols, void* stream) {
     qraf_hip::clear_error();
     return qraf_hip::launch_split_bf16(x, x_hi, x_lo, rows, cols, 0, nullptr, qraf_hip::as_stream(stream));
+}
+
+int qraf_hip_set_qgemm_schedule(int32_t mode, int32_t min_blocks) {
+    qraf_hip::clear_error();
+    return qraf_hip::set_qgemm_schedule(mode, min_blocks);
 }
 
 int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe, int batch_chunk) {

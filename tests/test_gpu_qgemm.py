@@ -150,6 +150,56 @@ def test_qgemm_pipelined_kernel(hip, dt, case, form):
     check(Y1, wq, dt, N, K, X)
 
 
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("case", [(8192, 1024, 100), (2560, 2048, 130), (300, 512, 64), (1000, 576, 33)],
+                         ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("form", [(1, 0), (2, 0), (2, 128)], ids=["wide", "narrow64", "narrow128"])
+@pytest.mark.parametrize("min_blocks", [0, 5, 7])
+def test_qgemm_stream_k(hip, dt, case, form, min_blocks):
+    """The stream-K schedule of the pipelined kernel, forced on: equal shares
+    of the (tile, block) pairs that start and end inside tiles (shares of 16,
+    5 or 7 blocks, so segments of every length and position occur, batch
+    chunks included), each tile's segments summed in order through the
+    workspace, unused slices zeroed; against the oracle, deterministic over
+    repeats, and within the tolerance of the uniform split-K grid."""
+    N, K, M = case
+    rng = np.random.default_rng(7 * N + K + M + dt)
+    wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    call = hip._lib.call
+    call("qraf_hip_set_qgemm_tuning", 0, 0, form[0], form[1])
+    try:
+        call("qraf_hip_set_qgemm_schedule", 1, min_blocks)
+        ws = hip._lib.lib.qraf_hip_qgemm_tiled_workspace_bytes(dt, N, K, M)
+        Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, repeats=2)
+        call("qraf_hip_set_qgemm_schedule", 2, 0)
+        Yu, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True)
+    finally:
+        call("qraf_hip_set_qgemm_schedule", 0, 0)
+        call("qraf_hip_set_qgemm_tuning", 0, 0, 0, 0)
+    if min_blocks:  # shares of 5 or 7 blocks, shorter than every tile here
+        assert ws > 0, "stream-K with shares shorter than a tile must use partial slices"
+    check(Y, wq, dt, N, K, X)
+    check(Yu, wq, dt, N, K, X)
+
+
+def test_qgemm_stream_k_plan(hip):
+    """The schedule knob through the workspace query (host-side plan): the
+    default keeps the uniform grid (the 128-row gate/up product in two
+    split-K slices, the LM head in whole tiles without partials); forced
+    stream-K shares the head's tiles too."""
+    lib, call = hip._lib.lib, hip._lib.call
+    q = lib.qraf_hip_qgemm_tiled_workspace_bytes
+    assert q(po.Q4_0, 22016, 2048, 128) == 2 * 128 * 22016 * 4
+    assert q(po.Q4_0, 151936, 2048, 128) == 0
+    try:
+        call("qraf_hip_set_qgemm_schedule", 1, 0)
+        forced = q(po.Q4_0, 151936, 2048, 128)
+    finally:
+        call("qraf_hip_set_qgemm_schedule", 0, 0)
+    assert forced > 0
+
+
 def test_qgemm_split_k_is_used(hip):
     lib = hip._lib.lib
     # few 128-row tiles and a long K: the split-K path must be chosen
