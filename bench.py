@@ -386,19 +386,24 @@ def bench_decode_b1(args, rt):
     from qraf_amd.engine import Engine, model_config
     cfg = model_config(*(SMOL[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq",
                                            "rope_theta", "eps")))
-    e = Engine(cfg, kv_dtype=F32, max_batch=1)
+    # 32 rows per step (the prompt as one batched step), KV pages for two sequences
+    e = Engine(cfg, kv_dtype=F32, max_batch=32, num_pages=2 * (-(-SMOL["max_seq"] // 16)))
     e.generate_weights(Q8, Q8, Q8, False, False, 1)
     e.finalize()
     e.set_graphs(not args.no_graphs)
     prompt = np.random.default_rng(1).integers(0, SMOL["vocab"], 32).tolist()
     n_gen = 128
 
-    def run():
+    def run(batched_prefill=False):
         s = e.seq_create()
         t0 = time.perf_counter()
         nx = None
-        for i, t in enumerate(prompt):
-            _, nx = e.step([s], [t], [i], want_logits=[1 if i == len(prompt) - 1 else 0])
+        if batched_prefill:  # the whole prompt in one step, logits of its last row only
+            _, nx = e.step([s] * len(prompt), prompt, list(range(len(prompt))),
+                           want_logits=[0] * (len(prompt) - 1) + [1])
+        else:  # token by token, as inference.cpp:90-99
+            for i, t in enumerate(prompt):
+                _, nx = e.step([s], [t], [i], want_logits=[1 if i == len(prompt) - 1 else 0])
         t1 = time.perf_counter()
         toks = [int(nx[0])]
         pos = len(prompt)
@@ -412,13 +417,31 @@ def bench_decode_b1(args, rt):
 
     run()  # warm-up
     pre, dec, toks = run()
+    run(True)
+    run(True)  # a step shape is captured into a graph the second time it comes
+    pre_b, dec_b, toks_b = run(True)
     steps = n_gen - 1  # the first token comes from the prefill's logits
     gbs = steps * smol_bytes_per_token(len(prompt) + steps / 2) / dec / 1e9
+    # the reference's defaults: InferenceEngine::generate_tokens with repetition penalty 1.1 (device sampler on the
+    # step's logits) and EOS 2, prompt fed token by token
+    from qraf_amd.engine import InferenceEngine, Transformer
+    ie = InferenceEngine(Transformer(e), eos_token=2)
+    ie.generate_tokens(prompt, n_gen, repetition_penalty=1.1)
+    t0 = time.perf_counter()
+    out_p = ie.generate_tokens(prompt, n_gen, repetition_penalty=1.1)
+    el_p = time.perf_counter() - t0
     e.close()
     return {"model": "SmolLM2-135M architecture, Q8_0 weights, f32 KV pages, random init", "prompt": len(prompt),
             "generated": n_gen, "decode_tok_s": round(steps / dec, 1), "ms_per_token": round(dec / steps * 1e3, 3),
-            "prefill_plus_decode_tok_s": round(n_gen / (pre + dec), 1), "decode_GB_s": round(gbs, 1),
-            "first_tokens": toks[:8]}
+            "prefill_plus_decode_tok_s": round(n_gen / (pre + dec), 1), "prefill_ms_token_by_token": round(pre * 1e3, 2),
+            "batched_prefill": {"prefill_ms": round(pre_b * 1e3, 2),
+                                "prefill_plus_decode_tok_s": round(n_gen / (pre_b + dec_b), 1),
+                                "same_tokens": toks_b == toks},
+            "decode_GB_s": round(gbs, 1), "first_tokens": toks[:8],
+            "reference_defaults": {"repetition_penalty": 1.1, "eos": 2, "generated": len(out_p),
+                                   "tok_s": round(len(out_p) / el_p, 1),
+                                   "note": "generated / (prefill + decode) as inference.cpp:150-153; one device "
+                                           "sampler call per token after its step"}}
 
 
 def cpu_decode_b1(n_tokens=8):
