@@ -281,6 +281,19 @@ int qraf_hip_qgemm_tiled_dev(const void* w_tiled, uint32_t dtype, uint32_t out_d
                              const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, float* y, const float* add,
                              void* workspace, uint64_t workspace_bytes, void* stream);
 
+/* The SwiGLU front of mlp_forward (attention.cpp:172-178) fused into the
+ * tile-major GEMM: w_tiled's rows interleave the gate and up projections (row
+ * 2i = gate_i, row 2i+1 = up_i, out_dim = 2F, even); out_hi/out_lo [batch][F]
+ * receive silu(gate) * up as the hi/lo planes the down projection's GEMM
+ * reads (qraf_hip_split_bf16_dev form; they must not overlap x_hi/x_lo).
+ * The pipelined kernel runs unsplit (128 weight rows x 64 batch rows per
+ * workgroup), so no workspace is needed and the gate/up sums never leave the
+ * registers; the sums are those of qraf_hip_qgemm_tiled_dev in the same form.
+ * No counterpart in the reference (a fusion of two of its steps). */
+int qraf_hip_qgemm_tiled_silu_dev(const void* w_tiled, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
+                                  const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, uint16_t* out_hi,
+                                  uint16_t* out_lo, void* stream);
+
 /* MFMA-ready ("mx") copy of a Q8_0/Q4_0 matrix (block size 32) for large
  * batches, where the product is bound by the matrix cores rather than by
  * weight bytes: per quant block b and 16-row tile t, 576 bytes at
@@ -488,11 +501,15 @@ int qraf_engine_get_stats(qraf_engine* engine, qraf_engine_stats* stats, int32_t
  * whatever the padding.  rows 1: off; default 32.  No reference counterpart
  * (a launch-cost measure). */
 int qraf_engine_set_row_padding(qraf_engine* engine, int32_t rows);
-/* Fusions that change how a step runs, not what it computes (results are
- * bit-identical either way): bit 0 (default on) = one-row steps apply the
- * QKV bias, RoPE and the K/V store inside the QKV matvec (its one-shot form;
- * f32 and fp16 pages) instead of a separate launch.  No reference
- * counterpart (a launch-count measure). */
+/* Fusions that change how a step runs, not what it computes: bit 0
+ * (default on) = one-row steps apply the QKV bias, RoPE and the K/V store
+ * inside the QKV matvec (its one-shot form; f32 and fp16 pages) instead of a
+ * separate launch (bit-identical either way); bit 1 (default on) = steps of
+ * more than 256 rows run the gate/up GEMM unsplit with the SiLU-gate in its
+ * epilogue (qraf_hip_qgemm_tiled_silu_dev) instead of split-K partials and
+ * a separate SiLU/split launch (the same arithmetic summed in another order,
+ * within the GEMM's error bound).  No reference counterpart (launch-count
+ * and traffic measures). */
 int qraf_engine_set_fusion(qraf_engine* engine, int32_t flags);
 /* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)
  * on the engine's default sequence, and Transformer::reset() (:641-643). */

@@ -78,6 +78,7 @@ SIGNATURES = {
     "qraf_hip_repack_tiles_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
     "qraf_hip_qgemm_tiled_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp, vp,
                                            C.c_uint64, vp]),
+    "qraf_hip_qgemm_tiled_silu_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp, vp]),
     "qraf_hip_qgemm_tiled_workspace_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32]),
     "qraf_hip_qgemm_workspace_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32]),
     "qraf_hip_qgemm_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp,

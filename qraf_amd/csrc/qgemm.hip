@@ -457,7 +457,8 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
                                                                  const uint16_t* __restrict__ xl, int K, int M,
                                                                  float* Y, const float* add, int bps,
                                                                  float* __restrict__ part, int skG, int sk_ntiles,
-                                                                 int skS) {
+                                                                 int skS, uint16_t* __restrict__ act_hi,
+                                                                 uint16_t* __restrict__ act_lo) {
     using G = PipeGeom<FMT, TM, TN, KC, WN, WMN>;
     constexpr int MW = G::MW, NW = G::NW, TB = G::TB, NWV = G::NWV;
 
@@ -630,6 +631,30 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
             acc[TM - 1][u][r] = __builtin_fmaf(dR[3][u][r], sP[u], acc[TM - 1][u][r]);
         }
 
+    if (act_hi) {
+        // SwiGLU front (mlp_forward, attention.cpp:172-178) on complete sums of
+        // interleaved rows (2i = gate_i, 2i+1 = up_i): the even lane of each
+        // pair writes silu(g) * u as the hi/lo planes [M][N/2] of the next GEMM
+        const int F2 = N >> 1;
+#pragma unroll
+        for (int t = 0; t < TM; t++) {
+#pragma unroll
+            for (int u = 0; u < TN; u++) {
+                const int n = n0 + (wn * TN + u) * 16 + l16;
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + (wm * TM + t) * 16 + seg * 4 + r;
+                    const float v = acc[t][u][r];
+                    const float up = __shfl_xor(v, 1);
+                    if (!(l16 & 1) && m < M && n < N) {
+                        const size_t e = (size_t)m * F2 + (n >> 1);
+                        split_bf16(silu_gate(v, up), &act_hi[e], &act_lo[e]);
+                    }
+                }
+            }
+        }
+        return;
+    }
     // epilogue: direct (+ residual) or a partial tile
 #pragma unroll
     for (int t = 0; t < TM; t++) {
@@ -997,7 +1022,7 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
 #define QH_P(F, TM_, TN_, WN_, WM_)                                                                        \
     hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_>), grid, dim3(64 * WN_ * WM_), 0, s,           \
                        (const uint8_t*)W, N, nb, \
-                       xh, xl, K, M, Y, add, p.bps, part, p.skG, p.ntiles, p.S)
+                       xh, xl, K, M, Y, add, p.bps, part, p.skG, p.ntiles, p.S, nullptr, nullptr)
         if (dtype == DT_Q8_0) {
             if (p.WN == 4 && p.WM == 1) {
                 if (p.TM == 8) QH_P(8, 8, 2, 4, 1);
@@ -1052,6 +1077,32 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
     return QRAF_HIP_OK;
 }
 
+// Gate/up projection of interleaved rows with the SwiGLU front in the
+// epilogue: the narrow pipelined form (4 waves x 128 weight rows, 64-row
+// batch chunks, one workgroup per (tile, chunk), no split) so that every
+// workgroup holds complete sums; act_hi/act_lo [M][N/2] must not overlap xh/xl.
+int launch_qgemm_silu(const void* Wt, uint32_t dtype, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
+                      uint16_t* act_hi, uint16_t* act_lo, hipStream_t s) {
+    QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "qgemm silu: unsupported dtype %u", dtype);
+    QH_REQUIRE(K % 32 == 0 && K > 0 && N > 0 && N % 2 == 0 && M > 0, QRAF_HIP_ERR_INVALID,
+               "qgemm silu: N=%d (even), K=%d (multiple of 32), M=%d", N, K, M);
+    QH_REQUIRE(Wt && xh && xl && act_hi && act_lo, QRAF_HIP_ERR_INVALID, "qgemm silu: null pointer");
+    QH_REQUIRE(((((uintptr_t)Wt) | ((uintptr_t)xh) | ((uintptr_t)xl)) & 15) == 0, QRAF_HIP_ERR_INVALID,
+               "qgemm silu: misaligned operands");
+    const int nb = K / 32, KC = 2;
+    const dim3 grid((N + 127) / 128, 1, (M + 63) / 64);
+    QH_REQUIRE(grid.z <= 65535, QRAF_HIP_ERR_INVALID, "qgemm silu: batch %d too large", M);
+    const int bps = (nb + KC - 1) / KC * KC;
+    if (dtype == DT_Q8_0)
+        hipLaunchKernelGGL((qgemm_pipe_kernel<8, 4, 2, 2, 4, 1>), grid, dim3(256), 0, s, (const uint8_t*)Wt, N, nb, xh, xl,
+                           K, M, nullptr, nullptr, bps, nullptr, 0, 0, 1, act_hi, act_lo);
+    else
+        hipLaunchKernelGGL((qgemm_pipe_kernel<4, 4, 2, 2, 4, 1>), grid, dim3(256), 0, s, (const uint8_t*)Wt, N, nb, xh, xl,
+                           K, M, nullptr, nullptr, bps, nullptr, 0, 0, 1, act_hi, act_lo);
+    QH_CHECK_HIP(hipGetLastError());
+    return QRAF_HIP_OK;
+}
+
 }  // namespace qraf_hip
 
 extern "C" {
@@ -1059,6 +1110,14 @@ extern "C" {
 int qraf_hip_split_bf16_dev(const float* x, uint16_t* x_hi, uint16_t* x_lo, int32_t rows, int32_t cols, void* stream) {
     qraf_hip::clear_error();
     return qraf_hip::launch_split_bf16(x, x_hi, x_lo, rows, cols, 0, nullptr, qraf_hip::as_stream(stream));
+}
+
+int qraf_hip_qgemm_tiled_silu_dev(const void* w_tiled, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
+                                  const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, uint16_t* out_hi,
+                                  uint16_t* out_lo, void* stream) {
+    qraf_hip::clear_error();
+    return qraf_hip::launch_qgemm_silu(w_tiled, dtype, (int)out_dim, (int)in_dim, x_hi, x_lo, batch, out_hi, out_lo,
+                                       qraf_hip::as_stream(stream));
 }
 
 int qraf_hip_set_qgemm_schedule(int32_t mode, int32_t min_blocks) {

@@ -231,7 +231,9 @@ class Engine:
 
     def set_fusion(self, flags: int) -> None:
         """Bit 0: one-row steps fuse the QKV bias, RoPE and K/V store into the
-        QKV matvec (default on); results are bit-identical either way."""
+        QKV matvec (default on; bit-identical either way).  Bit 1: steps of
+        more than 256 rows run the gate/up GEMM with the SiLU-gate in its
+        epilogue (default on; the same sums in another order)."""
         call("qraf_engine_set_fusion", self.h, int(flags))
 
     def set_row_padding(self, rows: int) -> None:

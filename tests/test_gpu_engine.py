@@ -344,6 +344,52 @@ def test_fused_qkv_epilogue_equals_separate_launch(hip, name, kv):
     m.close()
 
 
+@pytest.mark.parametrize("name", ["q4_gqa8_hd128", "q8_hd64_gqa3"])
+def test_swiglu_epilogue_batched_steps(hip, name):
+    """Steps over 256 rows with the SiLU-gate in the gate/up GEMM's epilogue
+    (fusion bit 1, the default) and with the split-K GEMM plus a separate
+    SiLU/split launch: 100 sequences of 3 prompt tokens in one 300-row step,
+    then two 100-row decode steps; every logit row of both runs within the
+    bar of the oracle's single-sequence decode (the two GEMM forms sum in
+    different orders, so they are not bit-identical)."""
+    from qraf_amd.engine import Engine
+    kw, seed = SMALL[name]
+    m = oracle_model(kw, seed)
+    L = po.lib()
+    prompts = [[L.or_gen_token(seed + 40 + r, i, kw["vocab"]) for i in range(3)] for r in range(100)]
+    want, fed = [], []
+    for p in prompts:  # the oracle: each sequence alone, 3 prompt tokens then two greedy tokens (fed to both)
+        m.reset()
+        lg = [m.forward(t, i) for i, t in enumerate(p)][-1]
+        rows, toks = [lg], []
+        for k in range(2):
+            toks.append(int(np.argmax(lg)))
+            lg = m.forward(toks[-1], 3 + k)
+            rows.append(lg)
+        want.append(rows)
+        fed.append(toks)
+    for flags in (3, 1):
+        e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=320)
+        for tname, dt, shape, data in m.tensors():
+            e.set_tensor(tname, dt, shape, data)
+        e.finalize()
+        e.set_fusion(flags)
+        seqs = [e.seq_create() for _ in prompts]
+        rows = [(s, t, i) for s, p in zip(seqs, prompts) for i, t in enumerate(p)]
+        lg, nx = e.step([r[0] for r in rows], [r[1] for r in rows], [r[2] for r in rows],
+                        want_logits=[r[2] == 2 for r in rows], logits=True, argmax=True)
+        got = [[lg[j]] for j in range(len(prompts))]
+        for k in range(2):
+            lg, nx = e.step(seqs, [f[k] for f in fed], [3 + k] * len(seqs), logits=True, argmax=True)
+            for j in range(len(prompts)):
+                got[j].append(lg[j])
+        e.close()
+        for j in range(len(prompts)):
+            for k in range(3):
+                check_logits(got[j][k], want[j][k].astype(np.float64), f"flags {flags} sequence {j} row {k}")
+    m.close()
+
+
 def test_attention_form_change_reaches_captured_steps(hip):
     """Changing the attention form (qraf_hip_set_attention_tuning) between
     replayed step graphs: the engine captures new graphs in the new form, so

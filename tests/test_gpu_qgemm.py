@@ -200,6 +200,48 @@ def test_qgemm_stream_k_plan(hip):
     assert forced > 0
 
 
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("case", [(2 * 1536, 576, 128), (2 * 11008, 2048, 128), (2 * 300, 1024, 70),
+                                  (2 * 11008, 2048, 200), (2 * 64, 64, 33)], ids=lambda c: "x".join(map(str, c)))
+def test_qgemm_tiled_silu_epilogue(hip, dt, case):
+    """qraf_hip_qgemm_tiled_silu_dev: rows 2i (gate) and 2i+1 (up) summed by
+    the pipelined kernel unsplit, the epilogue writing silu(g) * u as hi/lo
+    planes.  The plain tiled GEMM forced into the same form (narrow, 64-row
+    chunks, one split) gives the same sums bit for bit, which are checked
+    against the oracle; the planes must hold silu_gate of those sums to the
+    planes' own precision (2^-20 relative + 2^-25) plus a few ulp of expf."""
+    from qraf_amd.backend import DeviceBuffer
+    N, K, M = case
+    print(f"qgemm tiled silu dt={dt} N={N} K={K} M={M}", flush=True)
+    rng = np.random.default_rng(N + 5 * K + M)
+    wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    call, lib = hip._lib.call, hip._lib.lib
+    call("qraf_hip_set_qgemm_tuning", 0, 1, 2, 0)
+    try:
+        Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
+    finally:
+        call("qraf_hip_set_qgemm_tuning", 0, 0, 0, 0)
+    check(Y, wq, dt, N, K, X)
+    F = N // 2
+    dw, dx = DeviceBuffer.from_array(wq), DeviceBuffer.from_array(X)
+    dtl = DeviceBuffer(lib.qraf_hip_tiled_weight_bytes(dt, N, K))
+    call("qraf_hip_repack_tiles_dev", dw.ptr, dt, N, K, dtl.ptr, None)
+    dh, dl = DeviceBuffer(M * K * 2), DeviceBuffer(M * K * 2)
+    call("qraf_hip_split_bf16_dev", dx.ptr, dh.ptr, dl.ptr, M, K, None)
+    oh, ol = DeviceBuffer(M * F * 2), DeviceBuffer(M * F * 2)
+    call("qraf_hip_qgemm_tiled_silu_dev", dtl.ptr, dt, N, K, dh.ptr, dl.ptr, M, oh.ptr, ol.ptr, None)
+    call("qraf_hip_stream_synchronize", None)
+    hi = oh.download(np.uint16, M * F).reshape(M, F)
+    lo = ol.download(np.uint16, M * F).reshape(M, F)
+    g, u = Y[:, 0::2].astype(np.float64), Y[:, 1::2].astype(np.float64)
+    want = g / (1.0 + np.exp(-g)) * u
+    got = (hi.astype(np.uint32) << 16).view(np.float32).astype(np.float64) + lo.view(np.float16).astype(np.float64)
+    tol = 2.0 ** -20 * np.abs(want) + 2.0 ** -25 + 8 * 2.0 ** -24 * np.abs(want)
+    err = np.abs(got - want)
+    assert np.all(err <= tol), f"max err {err.max():.3e}, worst ratio {(err / tol).max():.3f}"
+
+
 def test_qgemm_split_k_is_used(hip):
     lib = hip._lib.lib
     # few 128-row tiles and a long K: the split-K path must be chosen
