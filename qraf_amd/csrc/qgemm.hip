@@ -451,7 +451,10 @@ __host__ __device__ inline int sk_owner(long long x, long long T, int G) {
     return w;
 }
 
-template <int FMT, int TM, int TN, int KC, int WN, int WMN>
+// SK: the stream-K schedule (skG workgroups), else the uniform split grid.  Two
+// instantiations, since one kernel holding both loops spills ~100-200 SGPRs
+// into VGPR lanes (a readlane per descriptor word at every DMA issue).
+template <int FMT, int TM, int TN, int KC, int WN, int WMN, bool SK>
 __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>::MINB)) void qgemm_pipe_kernel(const uint8_t* __restrict__ Wt, int N, int nb,
                                                                  const uint16_t* __restrict__ xh,
                                                                  const uint16_t* __restrict__ xl, int K, int M,
@@ -674,12 +677,12 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
     }
     };  // segment
 
-    if (skG == 0) {  // uniform split: workgroup (tile, split, batch chunk)
+    if constexpr (!SK) {  // uniform split: workgroup (tile, split, batch chunk)
         const int b_begin = blockIdx.y * bps;  // bps: a positive multiple of KC
         segment(blockIdx.x * NW, blockIdx.z * MW, b_begin, min(nb, b_begin + bps),
                 part ? part + (size_t)blockIdx.y * M * N : Y, part ? nullptr : add);
         return;
-    }
+    } else {
     // stream-K: this workgroup's equal share of the (tile, block) pairs, one
     // segment per tile it touches; segment k of a tile writes partial slice k
     // (or Y itself when no tile is shared, skS == 1), and the tile's last
@@ -718,6 +721,7 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
             }
         }
         lo += b1 - b0;
+    }
     }
 }
 
@@ -1020,9 +1024,16 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
     const dim3 grid = p.skG > 0 ? dim3(p.skG, 1, 1) : dim3(p.ntiles, p.S, p.mchunks);
     if (p.pipe) {
 #define QH_P(F, TM_, TN_, WN_, WM_)                                                                        \
-    hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_>), grid, dim3(64 * WN_ * WM_), 0, s,           \
-                       (const uint8_t*)W, N, nb, \
-                       xh, xl, K, M, Y, add, p.bps, part, p.skG, p.ntiles, p.S, nullptr, nullptr)
+    do {                                                                                                  \
+    if (p.skG > 0)                                                                                        \
+        hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_, true>), grid, dim3(64 * WN_ * WM_), 0, s, \
+                           (const uint8_t*)W, N, nb, xh, xl, K, M, Y, add, p.bps, part, p.skG, p.ntiles, p.S,     \
+                           nullptr, nullptr);                                                              \
+    else                                                                                                  \
+        hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_, false>), grid, dim3(64 * WN_ * WM_), 0, s, \
+                           (const uint8_t*)W, N, nb, xh, xl, K, M, Y, add, p.bps, part, 0, p.ntiles, p.S,        \
+                           nullptr, nullptr);                                                              \
+    } while (0)
         if (dtype == DT_Q8_0) {
             if (p.WN == 4 && p.WM == 1) {
                 if (p.TM == 8) QH_P(8, 8, 2, 4, 1);
@@ -1094,10 +1105,10 @@ int launch_qgemm_silu(const void* Wt, uint32_t dtype, int N, int K, const uint16
     QH_REQUIRE(grid.z <= 65535, QRAF_HIP_ERR_INVALID, "qgemm silu: batch %d too large", M);
     const int bps = (nb + KC - 1) / KC * KC;
     if (dtype == DT_Q8_0)
-        hipLaunchKernelGGL((qgemm_pipe_kernel<8, 4, 2, 2, 4, 1>), grid, dim3(256), 0, s, (const uint8_t*)Wt, N, nb, xh, xl,
+        hipLaunchKernelGGL((qgemm_pipe_kernel<8, 4, 2, 2, 4, 1, false>), grid, dim3(256), 0, s, (const uint8_t*)Wt, N, nb, xh, xl,
                            K, M, nullptr, nullptr, bps, nullptr, 0, 0, 1, act_hi, act_lo);
     else
-        hipLaunchKernelGGL((qgemm_pipe_kernel<4, 4, 2, 2, 4, 1>), grid, dim3(256), 0, s, (const uint8_t*)Wt, N, nb, xh, xl,
+        hipLaunchKernelGGL((qgemm_pipe_kernel<4, 4, 2, 2, 4, 1, false>), grid, dim3(256), 0, s, (const uint8_t*)Wt, N, nb, xh, xl,
                            K, M, nullptr, nullptr, bps, nullptr, 0, 0, 1, act_hi, act_lo);
     QH_CHECK_HIP(hipGetLastError());
     return QRAF_HIP_OK;
