@@ -891,7 +891,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only; --gpus {args.gpus} is not supported "
-              "(the decode path shards by sequence across GPUs, see DESIGN.md)", file=sys.stderr)
+              "(the decode path would shard by sequence across GPUs)", file=sys.stderr)
         sys.exit(2)
     only = set(args.only.split(","))
 
