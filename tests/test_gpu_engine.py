@@ -55,6 +55,8 @@ SMALL = {
                            rope_theta=1e6, eps=1e-6, wdtype=po.Q4_0, tied=True, qkv_bias=True), 14),
     "q8_hd64_gqa3": (dict(vocab=800, hidden=576, layers=2, heads=9, kv_heads=3, inter=1536, max_seq=256,
                           rope_theta=1e5, eps=1e-5, wdtype=po.Q8_0), 15),
+    "q4_hd64_gqa2": (dict(vocab=700, hidden=256, layers=2, heads=4, kv_heads=2, inter=512, max_seq=256,
+                          rope_theta=1e4, eps=1e-5, wdtype=po.Q4_0), 16),
 }
 
 
