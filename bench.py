@@ -249,6 +249,16 @@ def cpu_baseline_matvec(cases_host, budget_s):
 
 # --------------------------------------------------------------------------- batched GEMM
 
+def batch_matvec_covered(dt, k, nv):
+    """qraf_hip_matvec_q_batch_dev's coverage: K a multiple of 32 (64 for
+    Q4_0), the batch rounded up to 2/4/8/16 vectors staged in 144 KB."""
+    if k % (32 if dt == Q8 else 64):
+        return False
+    nvr = 2 if nv <= 2 else 4 if nv <= 4 else 8 if nv <= 8 else 16
+    per = (k // 32) * 36 * 4 if dt == Q8 else (k // 64) * 76 * 4
+    return nvr * per <= 144 * 1024
+
+
 def bench_gemm(args, rt):
     call, DeviceBuffer, stream, lib = rt["call"], rt["DeviceBuffer"], rt["stream"], rt["lib"]
     rng = np.random.default_rng(7)
@@ -288,10 +298,22 @@ def bench_gemm(args, rt):
                                                       dt, n, k, xh.ptr, xl.ptr, b, y.ptr, None,
                                                       wst.ptr if wst else None, wsbt, stream.h), 100)
                 by, fl = mv_bytes(dt, n, k, b), 2.0 * b * n * k
-                out.append({"case": f"{fmt} {n}x{k} B={b}", "us": round(us, 2),
-                            "GB_s": round(by / (us * 1e-6) / 1e9, 1), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 2),
-                            "mfma_frac": round(2 * fl / (us * 1e-6) / 1e12 / MFMA_BF16_TFLOPS, 4),
-                            "us_reference_layout": round(us_ref, 2)})
+                rec = {"case": f"{fmt} {n}x{k} B={b}", "us": round(us, 2),
+                       "GB_s": round(by / (us * 1e-6) / 1e9, 1), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 2),
+                       "mfma_frac": round(2 * fl / (us * 1e-6) / 1e12 / MFMA_BF16_TFLOPS, 4),
+                       "us_reference_layout": round(us_ref, 2)}
+                rec["engine_form"] = ("batch matvec" if 2 <= b <= 8 and batch_matvec_covered(dt, k, b)
+                                      and b * n * k <= 96 << 20 else "GEMM")
+                if b <= 8 and batch_matvec_covered(dt, k, b):
+                    # below the matrix cores' batch: the multi-vector matvec on the
+                    # reference layout, fp32 x as is (the engine's form for 2-8 rows)
+                    us_mv = graph_time_us(rt, lambda i: call("qraf_hip_matvec_q_batch_dev",
+                                                             pool.ptr + (i % copies) * wbytes, dt, n, k, dx.ptr, b,
+                                                             y.ptr, stream.h), 100)
+                    rec.update({"us_batch_matvec": round(us_mv, 2),
+                                "GB_s_batch_matvec": round(by / (us_mv * 1e-6) / 1e9, 1),
+                                "frac_hbm_batch_matvec": round(by / (us_mv * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+                out.append(rec)
                 for d in (dx, xh, xl, y):
                     d.free()
             pool.free()

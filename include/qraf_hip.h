@@ -117,6 +117,18 @@ int qraf_hip_matvec_q_dev(const void* w, uint32_t dtype, uint32_t block_size, ui
                           uint32_t in_dim, const float* x, float* y, void* stream);
 int qraf_hip_matvec_f32_dev(const float* W, const float* x, float* y, uint32_t out_dim,
                             uint32_t in_dim, void* stream);
+/* dispatch_matvec_q (backend.h:31-34, backend.cpp:131-199) applied to each of
+ * `batch` activation rows at once: y[b][out_dim] = W x[b] for b < batch,
+ * x [batch][in_dim] and y [batch][out_dim] on the device, stream-ordered.
+ * Every weight unit is read once for all rows, each row's sum running the
+ * batch-1 persistent kernel's arithmetic.  Q8_0 / Q4_0 with block size 32;
+ * batch 1..16; in_dim a multiple of 32 (of 64 for Q4_0) such that the
+ * batch rounded up to 2, 4, 8 or 16, times in_dim, fits the kernel's LDS
+ * staging (144 KB: 32,768 elements for Q8_0, 31,040 for Q4_0); anything
+ * else is an error (the batched GEMM takes larger batches).  The engine runs steps of 2-8 rows this way where every
+ * projection fits. */
+int qraf_hip_matvec_q_batch_dev(const void* w, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
+                                const float* x, int32_t batch, float* y, void* stream);
 /* Tuning of the batch-1 kernel (process-wide): kernel 0 = automatic,
  * 1 = one-shot, 2 = persistent streaming, 3 / 4 = ring with workgroups of
  * 8 / 4 waves (the automatic choice is 3 when K % 32 == 0, x is 16-byte
@@ -508,8 +520,14 @@ int qraf_engine_set_row_padding(qraf_engine* engine, int32_t rows);
  * more than 256 rows run the gate/up GEMM unsplit with the SiLU-gate in its
  * epilogue (qraf_hip_qgemm_tiled_silu_dev) instead of split-K partials and
  * a separate SiLU/split launch (the same arithmetic summed in another order,
- * within the GEMM's error bound).  No reference counterpart (launch-count
- * and traffic measures). */
+ * within the GEMM's error bound); bit 2 (default on) = steps of 2-8 rows
+ * run each projection that qraf_hip_matvec_q_batch_dev covers with rows x
+ * out_dim x in_dim at most 96 Mi (where it measured faster than the GEMM's
+ * split, GEMM and reduction launches) on it, with the RMSNorm / SiLU-gate
+ * formed in its staging; when the QKV and O projections qualify, the layer
+ * runs projection by projection instead of as the split-K GEMM layer (fp32
+ * products as at batch 1, summed in another order than the GEMM's).  No
+ * reference counterpart (launch-count and traffic measures). */
 int qraf_engine_set_fusion(qraf_engine* engine, int32_t flags);
 /* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)
  * on the engine's default sequence, and Transformer::reset() (:641-643). */

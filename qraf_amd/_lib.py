@@ -59,6 +59,7 @@ SIGNATURES = {
     "qraf_hip_mul": (C.c_int, [fp, fp, C.c_int]),
     "qraf_hip_scale": (C.c_int, [fp, C.c_float, C.c_int]),
     "qraf_hip_matvec_q_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, vp]),
+    "qraf_hip_matvec_q_batch_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, C.c_int32, vp, vp]),
     "qraf_hip_matvec_f32_dev": (C.c_int, [vp, vp, vp, C.c_uint32, C.c_uint32, vp]),
     "qraf_hip_set_matvec_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int]),
     "qraf_hip_quantize_dev": (C.c_int, [vp, C.c_uint64, C.c_uint32, vp, vp]),

@@ -388,6 +388,13 @@ int qraf_hip_matvec_q_dev(const void* w, uint32_t dtype, uint32_t block_size, ui
     return launch_matvec_q(w, dtype, block_size ? (int)block_size : 32, out_dim, in_dim, x, y, as_stream(stream));
 }
 
+int qraf_hip_matvec_q_batch_dev(const void* w, uint32_t dtype, uint32_t out_dim, uint32_t in_dim, const float* x,
+                                int32_t batch, float* y, void* stream) {
+    clear_error();
+    return launch_matvec_q_batch(w, dtype, out_dim, in_dim, x, (int)in_dim, (int)batch, y, (int)out_dim,
+                                 as_stream(stream));
+}
+
 int qraf_hip_matvec_f32_dev(const float* W, const float* x, float* y, uint32_t out_dim, uint32_t in_dim,
                             void* stream) {
     clear_error();

@@ -87,6 +87,22 @@ int launch_matvec_q(const void* W, uint32_t dtype, int bs, uint32_t N, uint32_t 
                     const MvRope* rope = nullptr, bool* fused = nullptr);
 int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s,
                       const float* add = nullptr);
+// nv (1..MV_BATCH_MAX) vectors at once: x rows of ldx floats (2K for the
+// SiLU-gate's interleaved source), y rows of ldy floats, add likewise; the
+// vectors are staged in LDS together (at most MV_BATCH_LDS bytes), so K is
+// bounded; matvec_batch_ok says whether a shape is covered.  Q8_0 / Q4_0,
+// block size 32.
+constexpr int MV_BATCH_MAX = 16;
+constexpr int MV_BATCH_SMALL = 8;  // the engine's steps of 2..8 rows (larger steps are padded for graph reuse)
+// rows x N x K up to which the engine prefers it to the GEMM (split, GEMM and
+// reduction launches): MI355X, Qwen2.5-3B / SmolLM2-135M projection shapes at
+// 2-8 rows, e.g. 2048 x 2048 Q4_0 at 2 / 8 rows 6.7 / 10.9 us against 12.3 /
+// 12.5; 22016 x 2048 at 2 / 3 rows 21.4 / 27.0 against 22.8 / 22.8
+constexpr long long MV_BATCH_WORK = 96LL << 20;
+constexpr int MV_BATCH_LDS = 144 * 1024;
+bool matvec_batch_ok(uint32_t dtype, uint32_t K, int nv);
+int launch_matvec_q_batch(const void* W, uint32_t dtype, uint32_t N, uint32_t K, const float* x, int ldx, int nv,
+                          float* y, int ldy, hipStream_t s, const float* add = nullptr, const MvPrep* prep = nullptr);
 int set_matvec_tuning(int kernel, int rows, int wgs_per_cu);
 // Bumped by every tuning call: captured launch sequences (the engine's step
 // graphs) record it and are rebuilt when it changes.

@@ -344,6 +344,7 @@ struct qraf_engine {
     int row_pad = 32;                 // steps of more than 8 rows are padded to a multiple of this (graphs on)
     bool fuse_rope = true;            // one-row steps: RoPE/append fused into the QKV matvec
     bool fuse_swiglu = true;          // steps over 256 rows: SiLU-gate in the gate/up GEMM's epilogue
+    bool batch_mv = true;             // steps of 2-8 rows: projections on the multi-vector matvec
     int32_t default_seq = -1;
     int last_logit_rows = 0;          // logit rows the last step left in `logits`
     qraf_engine_stats stats{};        // host-side time of qraf_engine_step
@@ -984,6 +985,11 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     const int H = (int)c.num_heads, Hkv = (int)c.num_kv_heads, hd = e->hd;
     const float scale = 1.0f / sqrtf((float)hd);  // attention.cpp:122
 
+    // 2-8 rows: the multi-vector matvec where it covers the shape and beats the GEMM
+    auto use_bmv = [&](uint32_t dt, int N, int K, int rows) {
+        return rows >= 2 && rows <= MV_BATCH_SMALL && e->batch_mv && dt != DT_F32 && matvec_batch_ok(dt, K, rows) &&
+               (long long)rows * N * K <= MV_BATCH_WORK;
+    };
     // y[n][N] = x[n][K] * W^T (+ add): matvec at batch 1, else the matrix-core GEMM
     // Wt: the tile-major copy (batched steps); K not a multiple of 32: one matvec per row
     // prep (optional): x is formed from its source first (norm or SiLU-gate):
@@ -994,6 +1000,9 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
                     const float* add, const MvPrep* prep = nullptr, const MvRope* rope = nullptr,
                     bool* fused = nullptr) -> int {
         if (fused) *fused = false;
+        if (use_bmv(dt, N, K, rows))
+            return launch_matvec_q_batch(W, dt, N, K, x, prep && prep->op == XP_SILU_GATE ? 2 * K : K, rows, y, N, s,
+                                         add, prep);
         if (prep && (dt == DT_F32 || rows != 1)) {
             if (prep->op == XP_NORM)
                 hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(256), 0, s, x, prep->w, K, prep->eps,
@@ -1028,7 +1037,16 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
         hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, 32, D, d_tok, d_src, e->amax,
                            e->h);
         QH_CHECK_HIP(hipGetLastError());
-        if (n > 1 && e->fused) {
+        // steps of 2-8 rows whose QKV and O projections go to the multi-vector
+        // matvec take the per-projection loop below (gate/up and down each
+        // take it or the GEMM)
+        bool small_mv = n >= 2 && n <= MV_BATCH_SMALL && e->batch_mv;
+        for (uint32_t l = 0; l < c.num_layers && small_mv; l++) {
+            const qraf_engine::Layer& L = e->layers[l];
+            small_mv = use_bmv(L.dt_attn, e->qkvd, D, n) && use_bmv(L.dt_attn, D, e->qd, n);
+        }
+        const bool gemm_layers = n > 1 && e->fused && !small_mv;
+        if (gemm_layers) {
             // Batched layer on the matrix cores, 9 launches (8 with the SwiGLU
             // epilogue): each projection writes split-K partials that the next
             // kernel sums (with the bias, residual, norm or SiLU-gate it applies
@@ -1070,7 +1088,7 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
                 QH_TRY(launch_residual_norm_split(P, S, (size_t)n * D, e->h, wn, D, c.rms_norm_eps, e->xh, e->xl, n, s));
             }
         }
-        for (uint32_t l = 0; l < c.num_layers && !(n > 1 && e->fused); l++) {
+        for (uint32_t l = 0; l < c.num_layers && !gemm_layers; l++) {
             qraf_engine::Layer& L = e->layers[l];
             uint8_t* kc = e->kpool + (size_t)l * e->layer_kv_bytes;
             uint8_t* vc = e->vpool + (size_t)l * e->layer_kv_bytes;
@@ -1100,7 +1118,7 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
             QH_TRY(proj(L.wo, L.wo_t, L.dt_attn, D, e->qd, e->att, n, e->h, e->h));  // + residual (transformer.cpp:593)
             const MvPrep ffn_norm{XP_NORM, L.fn, c.rms_norm_eps, e->xn};  // transformer.cpp:595
             QH_TRY(proj(L.wgu, L.wgu_t, L.dt_mlp, 2 * F, D, e->h, n, e->gu, nullptr, &ffn_norm));
-            if (n == 1 || !L.wd_t) {
+            if (n == 1 || !L.wd_t || use_bmv(L.dt_mlp, D, F, n)) {
                 const MvPrep gate{XP_SILU_GATE, nullptr, 0.f, e->act};  // attention.cpp:172-183
                 QH_TRY(proj(L.wd, L.wd_t, L.dt_mlp, D, F, e->gu, n, e->h, e->h, &gate));  // + residual (transformer.cpp:601)
             } else {
@@ -1285,10 +1303,11 @@ int qraf_engine_read_logits(qraf_engine* e, int32_t row0, int32_t rows, float* o
 
 int qraf_engine_set_fusion(qraf_engine* e, int32_t flags) {
     clear_error();
-    QH_REQUIRE(e && (flags & ~3) == 0, QRAF_HIP_ERR_INVALID, "set_fusion: flags %d", flags);
+    QH_REQUIRE(e && (flags & ~7) == 0, QRAF_HIP_ERR_INVALID, "set_fusion: flags %d", flags);
     QH_CHECK_HIP(hipStreamSynchronize(e->stream));  // no captured step still in flight
     e->fuse_rope = (flags & 1) != 0;
     e->fuse_swiglu = (flags & 2) != 0;
+    e->batch_mv = (flags & 4) != 0;
     e->drop_graphs();  // captured steps hold the other form
     return QRAF_HIP_OK;
 }

@@ -1097,6 +1097,306 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
     return QRAF_HIP_OK;
 }
 
+// ----------------------------------------------------------------------------
+// Several vectors at once (dispatch_matvec_q, backend.cpp:131-199, applied to
+// each of nv rows of x): the persistent streaming form above with NV >= nv x
+// vectors staged in LDS (each formed as the batch-1 kernels form x: as is,
+// RMSNorm or SiLU-gate), each weight unit loaded once and applied to every
+// vector.  A unit's quants are converted to floats once; each vector's sum
+// then runs the batch-1 compute's exact sequence (q8_compute / q4_compute,
+// R = 1), so a row's result is the batch-1 persistent kernel's.  For batches
+// below the matrix cores' reach: no split-K partials, no activation planes,
+// one launch.  Vectors past nv repeat the last one and are not stored.
+// ----------------------------------------------------------------------------
+// Staging of NV vectors at once (rows min(v, nv - 1) of x, ldx floats apart)
+// into sx + v * S in stage_x's layout and arithmetic, with every thread's
+// loads of up to 8 elements groups requested together (a chunk of 8 per
+// thread per round trip over all vectors), where stage_x's loop would wait
+// for each group: vector-major (v, group) indices, so the four threads of a
+// Q4 block are consecutive lanes of one vector.  The RMSNorm factors come
+// first, from norm_r_256's strided sums for all vectors in one pass.
+template <int FMT, int XP, int NV>
+__device__ __forceinline__ void stage_x_batch(float* sx, int S, const float* __restrict__ x, int ldx, int nv, int K,
+                                              int nb, const float* __restrict__ xw, float eps) {
+    __shared__ float red[NV][4];
+    __shared__ float s_r[NV];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    if (XP == XP_NORM) {
+        float ss[NV];
+#pragma unroll
+        for (int v = 0; v < NV; v++) ss[v] = 0.f;
+#pragma unroll 4
+        for (int i = tid; i < K; i += 256)
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                const float a = x[(size_t)min(v, nv - 1) * ldx + i];
+                ss[v] = __builtin_fmaf(a, a, ss[v]);
+            }
+#pragma unroll
+        for (int v = 0; v < NV; v++) {
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ss[v] += __shfl_xor(ss[v], o);
+            if (lane == 0) red[v][wave] = ss[v];
+        }
+        __syncthreads();
+        if (tid < NV) s_r[tid] = 1.0f / sqrtf(((red[tid][0] + red[tid][1]) + (red[tid][2] + red[tid][3])) / (float)K + eps);
+        __syncthreads();
+    }
+    const bool vec = (((uintptr_t)x) & 15) == 0 && (ldx & 3) == 0 && (XP != XP_NORM || (((uintptr_t)xw) & 15) == 0);
+    constexpr int CH = 8;  // element groups per thread per round trip
+    if (FMT == 8) {
+        const int n4 = nb * 8;  // float4 groups per vector (K padded to whole blocks)
+        const int total = NV * n4;
+        for (int base = 0; base < total; base += 256 * CH) {
+            f32x4 g[CH];
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const int c = min(base + tid + 256 * u, total - 1);
+                const int v = c / n4, i = 4 * (c - v * n4);
+                const float* xs = x + (size_t)min(v, nv - 1) * ldx;
+                const float r = XP == XP_NORM ? s_r[v] : 1.f;
+                if (i + 3 < K && vec) {
+                    g[u] = x_vec4<XP>(xs, i, r, xw);
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) g[u][e] = (i + e < K) ? x_elem<XP>(xs, i + e, r, xw) : 0.f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const int c = base + tid + 256 * u;
+                if (c < total) {
+                    const int v = c / n4, i = 4 * (c - v * n4);
+                    *(f32x4*)(sx + v * S + (i >> 5) * XS8 + (i & 31)) = g[u];
+                }
+            }
+        }
+    } else {
+        const int Keff = K & ~1;
+        const int ng = nb * 4;  // 8-element groups per vector
+        const int total = NV * ng;
+        for (int base = 0; base < total; base += 256 * CH) {
+            float g[CH][8];
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const int c = min(base + tid + 256 * u, total - 1);
+                const int v = c / ng, i = 8 * (c - v * ng);
+                const float* xs = x + (size_t)min(v, nv - 1) * ldx;
+                const float r = XP == XP_NORM ? s_r[v] : 1.f;
+                if (i + 7 < Keff && vec) {
+                    const f32x4 a = x_vec4<XP>(xs, i, r, xw), b = x_vec4<XP>(xs, i + 4, r, xw);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        g[u][e] = a[e];
+                        g[u][4 + e] = b[e];
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 8; e++) g[u][e] = (i + e < Keff) ? x_elem<XP>(xs, i + e, r, xw) : 0.f;
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < CH; u++) {
+                const int c = base + tid + 256 * u;  // lanes of a block: consecutive, one vector (ng % 4 == 0)
+                const float* v8 = g[u];
+                float part = ((v8[0] + v8[2]) + (v8[4] + v8[6])) + ((v8[1] + v8[3]) + (v8[5] + v8[7]));
+                part += __shfl_xor(part, 1);
+                part += __shfl_xor(part, 2);
+                if (c < total) {
+                    const int v = c / ng, t = c - v * ng, i = 8 * t;
+                    const int blk = i >> 5, gg = (i & 31) >> 3;
+                    float* dst = sx + v * S + (blk >> 1) * XS4 + (blk & 1) * 36;
+                    *(f32x4*)(dst + gg * 8) = f32x4{v8[0], v8[2], v8[4], v8[6]};
+                    *(f32x4*)(dst + gg * 8 + 4) = f32x4{v8[1], v8[3], v8[5], v8[7]};
+                    if ((t & 3) == 0) dst[32] = part;
+                }
+            }
+        }
+    }
+}
+
+template <int FMT, int NV, int XP>
+__global__ __launch_bounds__(WG) void qmv_batch_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N, int K,
+                                                       int nb, const float* __restrict__ x, int ldx, int nv,
+                                                       float* __restrict__ y, int ldy, const float* __restrict__ add,
+                                                       const float* __restrict__ xw, float eps) {
+    extern __shared__ __align__(16) float sx[];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int U = FMT == 8 ? nb : nb >> 1;
+    const int J = (U + 63) >> 6;
+    const int S = FMT == 8 ? nb * XS8 : (nb >> 1) * XS4;  // staged floats per vector
+    const int gw = blockIdx.x * 4 + wave, nw = gridDim.x * 4;
+    const int my_rows = gw < N ? (N - 1 - gw) / nw + 1 : 0;
+    const int n_it = my_rows * J;
+
+    // step it -> row gw + (it / J) * nw, unit column it % J
+    auto row_of = [&](int it) { return W + (size_t)min(gw + (it / J) * nw, N - 1) * row_bytes; };
+    auto unit_of = [&](int it) { return min(lane + 64 * (it % J), U - 1); };
+
+    Units<1> b0, b1;
+    if (n_it > 0) {
+        const uint8_t* rp[1] = {row_of(0)};
+        load_units<1>(b0, rp, unit_of(0));
+    }
+    stage_x_batch<FMT, XP, NV>(sx, S, x, ldx, nv, K, nb, xw, eps);
+    __syncthreads();
+    if (n_it == 0) return;
+
+    float acc[NV];
+#pragma unroll
+    for (int v = 0; v < NV; v++) acc[v] = 0.f;
+
+    auto compute = [&](const Units<1>& w, int it) {
+        const int u = lane + 64 * (it % J);
+        if (u < U) {
+            if (FMT == 8) {
+                float q[32];
+#pragma unroll
+                for (int j = 0; j < 8; j++)
+#pragma unroll
+                    for (int k = 0; k < 4; k++) q[4 * j + k] = (float)(int8_t)(dword(w, 0, 1 + j) >> (8 * k));
+                const float sc = __builtin_bit_cast(float, dword(w, 0, 0));
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const f32x4* xv = (const f32x4*)(sx + v * S + u * XS8);
+                    f32x4 xr[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) xr[j] = xv[j];
+                    float bs = 0.f;
+#pragma unroll
+                    for (int j = 0; j < 8; j++)
+#pragma unroll
+                        for (int k = 0; k < 4; k++) bs = __builtin_fmaf(q[4 * j + k], xr[j][k], bs);
+                    acc[v] = __builtin_fmaf(bs, sc, acc[v]);
+                }
+            } else {
+                uint32_t dw[9];
+#pragma unroll
+                for (int i = 0; i < 9; i++) dw[i] = dword(w, 0, i);
+                float el[16], eh[16], ol[16], oh[16];  // nibbles of the even and odd block, low and high
+#pragma unroll
+                for (int k = 0; k < 4; k++) {
+                    const uint32_t ne = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2);
+                    const uint32_t no = dw[5 + k];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        el[4 * k + q] = (float)((ne >> (8 * q)) & 0x0Fu);
+                        eh[4 * k + q] = (float)((ne >> (8 * q + 4)) & 0x0Fu);
+                        ol[4 * k + q] = (float)((no >> (8 * q)) & 0x0Fu);
+                        oh[4 * k + q] = (float)((no >> (8 * q + 4)) & 0x0Fu);
+                    }
+                }
+                const float se = half_bits_to_float(dw[0]), so = half_bits_to_float(dw[4] >> 16);
+#pragma unroll
+                for (int v = 0; v < NV; v++) {
+                    const float* xu = sx + v * S + u * XS4;
+                    f32x4 xe[8], xo[8];
+#pragma unroll
+                    for (int j = 0; j < 8; j++) {
+                        xe[j] = ((const f32x4*)xu)[j];
+                        xo[j] = ((const f32x4*)(xu + 36))[j];
+                    }
+                    const float se8 = 8.f * xu[32], so8 = 8.f * xu[36 + 32];
+                    float be = 0.f, bo = 0.f;
+#pragma unroll
+                    for (int k = 0; k < 4; k++)
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            be = __builtin_fmaf(el[4 * k + q], xe[2 * k][q], be);
+                            be = __builtin_fmaf(eh[4 * k + q], xe[2 * k + 1][q], be);
+                            bo = __builtin_fmaf(ol[4 * k + q], xo[2 * k][q], bo);
+                            bo = __builtin_fmaf(oh[4 * k + q], xo[2 * k + 1][q], bo);
+                        }
+                    acc[v] = __builtin_fmaf(be - se8, se, acc[v]);
+                    acc[v] = __builtin_fmaf(bo - so8, so, acc[v]);
+                }
+            }
+        }
+        if (it % J == J - 1) {  // the row's last unit column: reduce and store each vector's sum
+            const int row = gw + (it / J) * nw;
+#pragma unroll
+            for (int v = 0; v < NV; v++) {
+                float a1[1] = {acc[v]};
+                int rr;
+                const float t = wave_reduce_rows<1>(a1, lane, &rr);
+                if (lane == 0 && v < nv && row < N) {
+                    const size_t e = (size_t)v * ldy + row;
+                    y[e] = add ? t + add[e] : t;
+                }
+                acc[v] = 0.f;
+            }
+        }
+    };
+
+    for (int it = 0; it < n_it; it += 2) {
+        const uint8_t* rp1[1] = {row_of(min(it + 1, n_it - 1))};
+        load_units<1>(b1, rp1, unit_of(min(it + 1, n_it - 1)));
+        compute(b0, it);
+        if (it + 1 >= n_it) break;
+        const uint8_t* rp0[1] = {row_of(min(it + 2, n_it - 1))};
+        load_units<1>(b0, rp0, unit_of(min(it + 2, n_it - 1)));
+        compute(b1, it + 1);
+    }
+}
+
+// bytes of LDS the batch kernel stages nv vectors of K elements in (0: not coverable)
+static size_t batch_lds(uint32_t dtype, uint32_t K, int nv) {
+    if ((dtype != DT_Q8_0 && dtype != DT_Q4_0) || K == 0 || K % 32 != 0 || nv < 1 || nv > MV_BATCH_MAX) return 0;
+    const int nb = (int)(K / 32);
+    if (dtype == DT_Q4_0 && nb % 2 != 0) return 0;
+    const int NV = nv <= 2 ? 2 : nv <= 4 ? 4 : nv <= 8 ? 8 : 16;
+    const size_t per = dtype == DT_Q8_0 ? (size_t)nb * XS8 * 4 : (size_t)(nb / 2) * XS4 * 4;
+    const size_t lds = per * NV;
+    return lds <= MV_BATCH_LDS ? lds : 0;
+}
+
+bool matvec_batch_ok(uint32_t dtype, uint32_t K, int nv) { return batch_lds(dtype, K, nv) != 0; }
+
+int launch_matvec_q_batch(const void* Wv, uint32_t dtype, uint32_t N, uint32_t K, const float* x, int ldx, int nv,
+                          float* y, int ldy, hipStream_t s, const float* add, const MvPrep* prep) {
+    QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "batch matvec: unsupported dtype %u", dtype);
+    QH_REQUIRE(Wv && x && y && N > 0 && K > 0, QRAF_HIP_ERR_INVALID, "batch matvec: null pointer or empty shape");
+    QH_REQUIRE(nv >= 1 && nv <= MV_BATCH_MAX, QRAF_HIP_ERR_INVALID, "batch matvec: %d vectors (1..%d)", nv,
+               MV_BATCH_MAX);
+    const int xp = prep ? prep->op : XP_NONE;
+    QH_REQUIRE(xp == XP_NONE || xp == XP_NORM || xp == XP_SILU_GATE, QRAF_HIP_ERR_INVALID, "batch matvec: x op %d", xp);
+    QH_REQUIRE(xp != XP_NORM || prep->w, QRAF_HIP_ERR_INVALID, "batch matvec: norm weights missing");
+    const int xlen = xp == XP_SILU_GATE ? 2 * (int)K : (int)K;
+    QH_REQUIRE(ldx >= xlen && ldy >= (int)N, QRAF_HIP_ERR_INVALID, "batch matvec: row strides %d / %d too short", ldx,
+               ldy);
+    const size_t lds = batch_lds(dtype, K, nv);
+    QH_REQUIRE(lds, QRAF_HIP_ERR_INVALID,
+               "batch matvec: K=%u (a multiple of 32; of 64 for Q4_0) and %d vectors must fit %d bytes of LDS", K, nv,
+               MV_BATCH_LDS);
+    QH_REQUIRE((((uintptr_t)Wv) & 3) == 0, QRAF_HIP_ERR_INVALID, "batch matvec: weights must be 4-byte aligned");
+    const int NV = nv <= 2 ? 2 : nv <= 4 ? 4 : nv <= 8 ? 8 : 16;
+    const float* xw = xp == XP_NORM ? prep->w : nullptr;
+    const float eps = xp == XP_NORM ? prep->eps : 0.f;
+    typedef void (*fn)(const uint8_t*, uint32_t, int, int, int, const float*, int, int, float*, int, const float*,
+                       const float*, float);
+    fn k = nullptr;
+#define QH_MB(F, N_)                                                                                 \
+    if (NV == N_) k = xp == XP_NORM ? qmv_batch_kernel<F, N_, XP_NORM>                               \
+                      : xp == XP_SILU_GATE ? qmv_batch_kernel<F, N_, XP_SILU_GATE> : qmv_batch_kernel<F, N_, XP_NONE>;
+    if (dtype == DT_Q8_0) {
+        QH_MB(8, 2) QH_MB(8, 4) QH_MB(8, 8) QH_MB(8, 16)
+    } else {
+        QH_MB(4, 2) QH_MB(4, 4) QH_MB(4, 8) QH_MB(4, 16)
+    }
+#undef QH_MB
+    const int nb = (int)(K / 32);
+    const size_t rb = q_row_bytes(dtype, 32, K);
+    QH_REQUIRE(rb <= 0xFFFFFFFFu, QRAF_HIP_ERR_INVALID, "batch matvec: rows too long");
+    if (lds > 65536) QH_CHECK_HIP(hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds));
+    int fit = 0;
+    QH_CHECK_HIP(resident_wgs((const void*)k, WG, lds, &fit));
+    const int grid = max(1, min((int)((N + 3) / 4), max(1, fit) * cu_count()));
+    hipLaunchKernelGGL(k, dim3(grid), dim3(WG), lds, s, (const uint8_t*)Wv, (uint32_t)rb, (int)N, (int)K, nb, x, ldx,
+                       nv, y, ldy, add, xw, eps);
+    QH_CHECK_HIP(hipGetLastError());
+    return QRAF_HIP_OK;
+}
+
 int launch_matvec_f32(const float* W, const float* x, float* y, uint32_t N, uint32_t K, hipStream_t s,
                       const float* add) {
     QH_REQUIRE(W && x && y && N > 0 && K > 0, QRAF_HIP_ERR_INVALID, "bad f32 matvec arguments");

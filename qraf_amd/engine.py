@@ -233,7 +233,9 @@ class Engine:
         """Bit 0: one-row steps fuse the QKV bias, RoPE and K/V store into the
         QKV matvec (default on; bit-identical either way).  Bit 1: steps of
         more than 256 rows run the gate/up GEMM with the SiLU-gate in its
-        epilogue (default on; the same sums in another order)."""
+        epilogue (default on; the same sums in another order).  Bit 2: steps
+        of 2-8 rows run their projections on the multi-vector matvec where
+        it covers them (default on; batch-1 arithmetic instead of the GEMM's)."""
         call("qraf_engine_set_fusion", self.h, int(flags))
 
     def set_row_padding(self, rows: int) -> None:

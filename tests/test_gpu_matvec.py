@@ -179,3 +179,57 @@ def test_elementwise_ops_vs_oracle(hip):
         assert np.array_equal(b, x * np.float32(0.37))
         d = hip.backend.dispatch_dot_f32(x, y, n)
         assert abs(d - float(np.dot(x.astype(np.float64), y))) <= 2 * n * 2.0 ** -24 * float(np.abs(x * y).sum())
+
+
+def batch_covered(dt, k, nv):
+    """The batch matvec's own coverage rule: K a multiple of 32 (64 for Q4_0),
+    the batch rounded up to 2/4/8/16 vectors staged within 144 KB."""
+    if k % (32 if dt == po.Q8_0 else 64):
+        return False
+    nvr = 2 if nv <= 2 else 4 if nv <= 4 else 8 if nv <= 8 else 16
+    per = (k // 32) * 36 * 4 if dt == po.Q8_0 else (k // 64) * 76 * 4
+    return nvr * per <= 144 * 1024
+
+
+BATCH_SHAPES = [(576, 576), (1536, 576), (576, 1536), (2048, 2048), (256, 2048), (11008, 2048), (49152, 576),
+                (999, 4096), (33, 128), (5, 2048)]
+
+
+@pytest.mark.parametrize("nv", [1, 2, 3, 5, 8, 16])
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("shape", BATCH_SHAPES, ids=lambda s: "x".join(map(str, s)))
+def test_matvec_batch_vs_oracle(hip, shape, dt, nv):
+    """qraf_hip_matvec_q_batch_dev: every row of y = W x[b] against the
+    oracle's matvec of that row within the bound above, and each row
+    bit-identical to the same vector alone (nv = 1): the vectors' sums do not
+    depend on the batch they ride in."""
+    from qraf_amd.backend import DeviceBuffer
+    n, k = shape
+    if not batch_covered(dt, k, nv):
+        pytest.skip("not covered by the LDS staging (the error path is tested below)")
+    print(f"batch matvec dt={dt} N={n} K={k} nv={nv}", flush=True)
+    rng = np.random.default_rng(n * 17 + k * 3 + nv + dt)
+    wq = po.quantize(dt, (rng.standard_normal(n * k) * 0.02).astype(np.float32))
+    x = rng.standard_normal((nv, k)).astype(np.float32)
+    dw, dx, dy = DeviceBuffer.from_array(wq), DeviceBuffer.from_array(x), DeviceBuffer(nv * n * 4)
+    hip._lib.call("qraf_hip_matvec_q_batch_dev", dw.ptr, dt, n, k, dx.ptr, nv, dy.ptr, None)
+    hip._lib.call("qraf_hip_stream_synchronize", None)
+    y = dy.download(np.float32, nv * n).reshape(nv, n)
+    for b in range(nv):
+        check(y[b], po.matvec_q(wq, dt, n, k, x[b]), tol_rows(dt, wq, n, k, x[b]))
+    d1, dy1 = DeviceBuffer.from_array(np.ascontiguousarray(x[nv - 1])), DeviceBuffer(n * 4)
+    hip._lib.call("qraf_hip_matvec_q_batch_dev", dw.ptr, dt, n, k, d1.ptr, 1, dy1.ptr, None)
+    hip._lib.call("qraf_hip_stream_synchronize", None)
+    assert np.array_equal(dy1.download(np.float32, n).view(np.uint32), y[nv - 1].view(np.uint32))
+    for d in (dw, dx, dy, d1, dy1):
+        d.free()
+
+
+def test_matvec_batch_refuses_what_it_does_not_cover(hip):
+    from qraf_amd.backend import DeviceBuffer
+    d = DeviceBuffer(1 << 20)
+    for dt, n, k, nv in ((po.Q8_0, 64, 11008, 4), (po.Q4_0, 64, 96, 2), (po.Q8_0, 64, 100, 2), (po.Q8_0, 64, 64, 17),
+                         (po.Q8_0, 64, 64, 0), (7, 64, 64, 2)):
+        with pytest.raises(hip.HipError):
+            hip._lib.call("qraf_hip_matvec_q_batch_dev", d.ptr, dt, n, k, d.ptr, nv, d.ptr, None)
+    d.free()
