@@ -1011,7 +1011,10 @@ int launch_matvec_q(const void* Wv, uint32_t dtype, int bs, uint32_t N, uint32_t
         int kern = kern_req;
         if (kern == 0) kern = (N >= 8192 && J <= 8) ? 2 : 1;
         if ((kern == 3 || kern == 4) && ring_ok) {
-            int R = g_rows_per_wave ? min(g_rows_per_wave, 2) : (g_kernel == 0 && q4_wide && NWr == 4 ? 2 : 1);
+            // two rows per wave for short rows too (at most 32 units: most lanes
+            // would hold no unit of a single row)
+            int R = g_rows_per_wave ? min(g_rows_per_wave, 2)
+                                    : (g_kernel == 0 && ((q4_wide && NWr == 4) || U <= 32) ? 2 : 1);
             if (N % R) R = 1;  // every stored row must exist
             qmv_fn kf = dtype == DT_Q8_0 ? pick_ring<8>(R, NWr, xj, xp) : pick_ring<4>(R, NWr, xj, xp);
             QH_REQUIRE(kf, QRAF_HIP_ERR_INVALID, "no ring matvec kernel for K=%u", K);
