@@ -416,7 +416,7 @@ def bench_decode_b1(args, rt):
     prompt = np.random.default_rng(1).integers(0, SMOL["vocab"], 32).tolist()
     n_gen = 128
 
-    def run(batched_prefill=False):
+    def run(batched_prefill=False, pipeline=True):
         s = e.seq_create()
         t0 = time.perf_counter()
         nx = None
@@ -429,16 +429,30 @@ def bench_decode_b1(args, rt):
         t1 = time.perf_counter()
         toks = [int(nx[0])]
         pos = len(prompt)
-        while len(toks) < n_gen:
-            _, nx = e.step([s], [toks[-1]], [pos])
-            toks.append(int(nx[0]))
+        if pipeline:
+            # step k+1 issued before step k's token reaches the host: it takes that
+            # token from step k's argmax on the device (no EOS stop here)
+            e.step_async([s], [toks[0]], [pos])
             pos += 1
+            known = 2  # tokens collected or in flight
+            while known < n_gen:
+                e.step_async([s], [0], [pos], token_src=[0])
+                pos += 1
+                known += 1
+                toks.append(int(e.collect()[0]))
+            toks.append(int(e.collect()[0]))
+        else:  # each token read back before the next step is issued
+            while len(toks) < n_gen:
+                _, nx = e.step([s], [toks[-1]], [pos])
+                toks.append(int(nx[0]))
+                pos += 1
         t2 = time.perf_counter()
         e.seq_release(s)
         return t1 - t0, t2 - t1, toks
 
     run()  # warm-up
     pre, dec, toks = run()
+    _, dec_u, toks_u = run(pipeline=False)
     run(True)
     run(True)  # a step shape is captured into a graph the second time it comes
     pre_b, dec_b, toks_b = run(True)
@@ -455,6 +469,9 @@ def bench_decode_b1(args, rt):
     e.close()
     return {"model": "SmolLM2-135M architecture, Q8_0 weights, f32 KV pages, random init", "prompt": len(prompt),
             "generated": n_gen, "decode_tok_s": round(steps / dec, 1), "ms_per_token": round(dec / steps * 1e3, 3),
+            "pipelined": True,
+            "unpipelined": {"decode_tok_s": round(steps / dec_u, 1), "ms_per_token": round(dec_u / steps * 1e3, 3),
+                            "same_tokens": toks_u == toks},
             "prefill_plus_decode_tok_s": round(n_gen / (pre + dec), 1), "prefill_ms_token_by_token": round(pre * 1e3, 2),
             "batched_prefill": {"prefill_ms": round(pre_b * 1e3, 2),
                                 "prefill_plus_decode_tok_s": round(n_gen / (pre_b + dec_b), 1),
