@@ -161,47 +161,6 @@ __global__ void silu_gate_kernel(const float* __restrict__ gu, int F, int n, flo
     }
 }
 
-// Sampler::argmax (sampler.cpp:25-35): strict '>', lowest index wins ties
-__global__ __launch_bounds__(256) void argmax_rows_kernel(const float* __restrict__ logits, int V,
-                                                         uint32_t* __restrict__ out) {
-    __shared__ float sv[4];
-    __shared__ int si[4];
-    const float* l = logits + (size_t)blockIdx.x * V;
-    // each thread scans its strided indices in increasing order: its first
-    // value seeds the running maximum, then only strictly larger values win
-    float best = -INFINITY;
-    int bi = V;  // sentinel: no index seen yet
-    for (int i = threadIdx.x; i < V; i += 256) {
-        const float v = l[i];
-        if (bi == V || v > best) {
-            best = v;
-            bi = i;
-        }
-    }
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) {
-        const float ov = __shfl_xor(best, o);
-        const int oi = __shfl_xor(bi, o);
-        if (ov > best || (ov == best && oi < bi)) {
-            best = ov;
-            bi = oi;
-        }
-    }
-    if ((threadIdx.x & 63) == 0) {
-        sv[threadIdx.x >> 6] = best;
-        si[threadIdx.x >> 6] = bi;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        for (int w = 1; w < 4; w++)
-            if (sv[w] > best || (sv[w] == best && si[w] < bi)) {
-                best = sv[w];
-                bi = si[w];
-            }
-        out[blockIdx.x] = (uint32_t)(bi == V ? 0 : bi);
-    }
-}
-
 // Two-pass Sampler::argmax for long rows: 32 chunks per row, each scanned by
 // one workgroup with 8 loads in flight per thread (ascending index per thread,
 // so strict '>' keeps the lowest index), then a per-row pass over the chunk
@@ -277,6 +236,51 @@ __global__ void argmax_final_kernel(const float* __restrict__ pv, const int* __r
         }
     }
     out[row] = (uint32_t)(bi == INT_MAX || bi >= V ? 0 : bi);
+}
+
+// One pass of Sampler::argmax per row (sampler.cpp:25-35), a 1024-thread
+// workgroup per row: each thread scans its 16-byte groups i, i + 1024, ... in
+// ascending index order (strict '>': its lowest index of its maximum), 16
+// groups in flight per round, then the workgroup keeps the maximum, ties to
+// the lower index.  Needs V % 4 == 0 and 16-byte aligned rows.
+__global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ logits, int V,
+                                                          uint32_t* __restrict__ out) {
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    const int row = blockIdx.x, tid = threadIdx.x;
+    const float4* l4 = (const float4*)(logits + (size_t)row * V);
+    const int n4 = V >> 2;
+    float best = -INFINITY;
+    int bi = INT_MAX;
+    for (int base = tid; base < n4; base += 1024 * 16) {
+        float4 v[16];
+#pragma unroll
+        for (int u = 0; u < 16; u++) v[u] = l4[min(base + 1024 * u, n4 - 1)];
+#pragma unroll
+        for (int u = 0; u < 16; u++) {
+            const int g = base + 1024 * u;
+            if (g < n4) {
+                const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+                for (int k = 0; k < 4; k++)
+                    if (bi == INT_MAX || e[k] > best) {
+                        best = e[k];
+                        bi = 4 * g + k;
+                    }
+            }
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) argmax_take(best, bi, __shfl_xor(best, o), __shfl_xor(bi, o));
+    if ((tid & 63) == 0) {
+        sv[tid >> 6] = best;
+        si[tid >> 6] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 16; w++) argmax_take(best, bi, sv[w], si[w]);
+        out[row] = (uint32_t)(bi == INT_MAX || bi >= V ? 0 : bi);
+    }
 }
 
 __global__ void fill_kernel(float* p, float v, size_t n) {
@@ -1140,9 +1144,13 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
                                    c.rms_norm_eps, e->xhead, d_lrows);
                 QH_TRY(proj(W, e->head_t, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
             }
-            hipLaunchKernelGGL(argmax_chunk_kernel, dim3(ARGMAX_CHUNKS, n_logit_rows), dim3(256), 0, s, e->logits, V,
-                               e->am_val, e->am_idx);
-            hipLaunchKernelGGL(argmax_final_kernel, dim3(n_logit_rows), dim3(64), 0, s, e->am_val, e->am_idx, V, e->amax);
+            if (V % 4 == 0) {  // one pass per row (logits rows are 16-byte aligned then)
+                hipLaunchKernelGGL(argmax_rows_kernel, dim3(n_logit_rows), dim3(1024), 0, s, e->logits, V, e->amax);
+            } else {
+                hipLaunchKernelGGL(argmax_chunk_kernel, dim3(ARGMAX_CHUNKS, n_logit_rows), dim3(256), 0, s, e->logits, V,
+                                   e->am_val, e->am_idx);
+                hipLaunchKernelGGL(argmax_final_kernel, dim3(n_logit_rows), dim3(64), 0, s, e->am_val, e->am_idx, V, e->amax);
+            }
             QH_CHECK_HIP(hipGetLastError());
         }
         return QRAF_HIP_OK;
