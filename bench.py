@@ -483,9 +483,10 @@ def bench_decode_b1(args, rt):
                                            "sampler call per token after its step"}}
 
 
-def cpu_decode_b1(n_tokens=8):
+def cpu_decode_b1(n_prompt=32, n_tokens=128):
     """SmolLM2-135M-architecture Q8 decode with the reference's own
-    InferenceEngine (oracle/_ref) on this host: 8-token prompt + 8 tokens."""
+    InferenceEngine (oracle/_ref) on this host, the whole C1 run: a 32-token
+    prompt fed token by token, then 128 greedy tokens (about 15 s of one core)."""
     import tempfile
     from oracle import pyoracle as po
     if po.ref() is None:
@@ -495,13 +496,13 @@ def cpu_decode_b1(n_tokens=8):
     m.write_qraf(path)
     m.close()
     eng = po.RefEngine(path)
-    prompt = [po.lib().or_gen_token(1, i, SMOL["vocab"]) for i in range(8)]
+    prompt = [po.lib().or_gen_token(1, i, SMOL["vocab"]) for i in range(n_prompt)]
     toks, ms = eng.generate(prompt, n_tokens, 1.0)
     eng.close()
     os.remove(path)
     return {"value": round(len(toks) / (ms / 1e3), 3),
             "unit": "tok/s, generated / (prefill + decode) as inference.cpp:150-153 reports", "cores": 1,
-            "kind": "reference", "sample": f"8-token prompt + {len(toks)} greedy tokens via "
+            "kind": "reference", "sample": f"{n_prompt}-token prompt + {len(toks)} greedy tokens via "
                                            f"InferenceEngine::generate_tokens, {ms / 1e3:.1f} s, host CPU {host_cpu()}"}
 
 
