@@ -924,7 +924,7 @@ def main():
     ap.add_argument("--kernel", type=int, default=0,
                     help="matvec kernel: 0 auto, 1 one-shot, 2 persistent, 3 ring (8-wave groups), 4 ring (4-wave groups)")
     ap.add_argument("--wgs-per-cu", type=int, default=0)
-    ap.add_argument("--row-padding", type=int, default=32,
+    ap.add_argument("--row-padding", type=int, default=16,
                     help="batched engine steps of more than 8 rows run padded to a multiple of this (1: off)")
     ap.add_argument("--attn-form", type=int, default=0,
                     help="attention work form for every leg: 0 auto, 1 chunk grid, 2 balanced split, 3 VALU kernel")

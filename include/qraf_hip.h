@@ -510,7 +510,7 @@ int qraf_engine_get_stats(qraf_engine* engine, qraf_engine_stats* stats, int32_t
  * padded to a multiple of `rows` (at most max_batch), its logit rows too, so
  * that steps of nearby sizes replay one graph.  Pad rows use a scratch KV
  * page of their own and return nothing; results of real rows are the same
- * whatever the padding.  rows 1: off; default 32.  No reference counterpart
+ * whatever the padding.  rows 1: off; default 16.  No reference counterpart
  * (a launch-cost measure). */
 int qraf_engine_set_row_padding(qraf_engine* engine, int32_t rows);
 /* Fusions that change how a step runs, not what it computes: bit 0

@@ -345,7 +345,7 @@ struct qraf_engine {
     };
     std::vector<Seq> seqs;
     uint64_t step_stamp = 0;
-    int row_pad = 32;                 // steps of more than 8 rows are padded to a multiple of this (graphs on)
+    int row_pad = 16;                 // steps of more than 8 rows are padded to a multiple of this (graphs on)
     bool fuse_rope = true;            // one-row steps: RoPE/append fused into the QKV matvec
     bool fuse_swiglu = true;          // steps over 256 rows: SiLU-gate in the gate/up GEMM's epilogue
     bool batch_mv = true;             // steps of 2-8 rows: projections on the multi-vector matvec
