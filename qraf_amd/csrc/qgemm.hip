@@ -213,6 +213,60 @@ __device__ __forceinline__ void convert<4>(const WRaw<4>& r, bf16x8& w, f16x8& w
     wh = __builtin_bit_cast(f16x8, ph);
 }
 
+// A wave's TM x TN tiles of 16 x 16 MFMA results (lane: weight row nb + 16u +
+// l16, batch rows mb + 16t + 4seg + r) stored to dst[m][n] (+ add[m][n]).  A
+// wave whose tiles lie wholly inside M x N (the uniform case) stores without
+// per-element bounds checks and issues all its residual loads before the first
+// store; the other waves check every element.
+template <int TM, int TN>
+__device__ __forceinline__ void store_tiles(const f32x4 (&acc)[TM][TN], float* dst, const float* add, int M, int N,
+                                            int mb, int nb, int seg, int l16) {
+    if (mb + 16 * TM <= M && nb + 16 * TN <= N) {
+        const size_t o = (size_t)(mb + 4 * seg) * N + nb + l16;
+        float* d = dst + o;
+        if (add) {
+            const float* a = add + o;
+            float av[TM][TN][4];
+#pragma unroll
+            for (int t = 0; t < TM; t++)
+#pragma unroll
+                for (int u = 0; u < TN; u++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) av[t][u][r] = a[(size_t)(16 * t + r) * N + 16 * u];
+#pragma unroll
+            for (int t = 0; t < TM; t++)
+#pragma unroll
+                for (int u = 0; u < TN; u++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) d[(size_t)(16 * t + r) * N + 16 * u] = acc[t][u][r] + av[t][u][r];
+        } else {
+#pragma unroll
+            for (int t = 0; t < TM; t++)
+#pragma unroll
+                for (int u = 0; u < TN; u++)
+#pragma unroll
+                    for (int r = 0; r < 4; r++) d[(size_t)(16 * t + r) * N + 16 * u] = acc[t][u][r];
+        }
+        return;
+    }
+#pragma unroll
+    for (int t = 0; t < TM; t++) {
+#pragma unroll
+        for (int u = 0; u < TN; u++) {
+            const int n = nb + u * 16 + l16;
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const int m = mb + t * 16 + seg * 4 + r;
+                if (m < M && n < N) {
+                    float v = acc[t][u][r];
+                    if (add) v += add[(size_t)m * N + n];
+                    dst[(size_t)m * N + n] = v;
+                }
+            }
+        }
+    }
+}
+
 // WM x WN waves (batch x weight rows); TM: 16-row batch tiles per wave; TN:
 // 16-row weight tiles per wave; KC: quant blocks per stage.  A workgroup
 // owns WM*TM*16 batch rows x WN*TN*16 weight rows.
@@ -367,22 +421,7 @@ __global__ __launch_bounds__(64 * WM * WNW, 512 / (64 * WM * WNW)) void qgemm_ke
 
     // epilogue: direct (+ residual) or this split's partial tile
     float* dst = part ? part + (size_t)blockIdx.y * M * N : Y;
-#pragma unroll
-    for (int t = 0; t < TM; t++) {
-#pragma unroll
-        for (int u = 0; u < TN; u++) {
-            const int n = nbase + u * 16 + l16;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + (wm * TM + t) * 16 + seg * 4 + r;
-                if (m < M && n < N) {
-                    float v = acc[t][u][r];
-                    if (!part && add) v += add[(size_t)m * N + n];
-                    dst[(size_t)m * N + n] = v;
-                }
-            }
-        }
-    }
+    store_tiles<TM, TN>(acc, dst, part ? nullptr : add, M, N, m0 + wm * TM * 16, nbase, seg, l16);
 }
 
 // ---------------------------------------------------------------------------
@@ -659,22 +698,7 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
         return;
     }
     // epilogue: direct (+ residual) or a partial tile
-#pragma unroll
-    for (int t = 0; t < TM; t++) {
-#pragma unroll
-        for (int u = 0; u < TN; u++) {
-            const int n = n0 + (wn * TN + u) * 16 + l16;
-#pragma unroll
-            for (int r = 0; r < 4; r++) {
-                const int m = m0 + (wm * TM + t) * 16 + seg * 4 + r;
-                if (m < M && n < N) {
-                    float v = acc[t][u][r];
-                    if (addp) v += addp[(size_t)m * N + n];
-                    dst[(size_t)m * N + n] = v;
-                }
-            }
-        }
-    }
+    store_tiles<TM, TN>(acc, dst, addp, M, N, m0 + wm * TM * 16, n0 + wn * TN * 16, seg, l16);
     };  // segment
 
     if constexpr (!SK) {  // uniform split: workgroup (tile, split, batch chunk)
