@@ -675,22 +675,29 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
 
     if (act_hi) {
         // SwiGLU front (mlp_forward, attention.cpp:172-178) on complete sums of
-        // interleaved rows (2i = gate_i, 2i+1 = up_i): the even lane of each
-        // pair writes silu(g) * u as the hi/lo planes [M][N/2] of the next GEMM
+        // interleaved rows (2i = gate_i, 2i+1 = up_i), written as the hi/lo
+        // planes [M][N/2] of the next GEMM.  The two lanes of a pair exchange
+        // their 4 sums; the even lane writes batch rows r = 0, 1 of its 4 and
+        // the odd lane rows 2, 3.
         const int F2 = N >> 1;
+        const bool odd = l16 & 1;
+        const bool full = m0 + (wm + 1) * TM * 16 <= M && n0 + (wn + 1) * TN * 16 <= N;  // uniform
 #pragma unroll
         for (int t = 0; t < TM; t++) {
 #pragma unroll
             for (int u = 0; u < TN; u++) {
-                const int n = n0 + (wn * TN + u) * 16 + l16;
+                const int n2 = (n0 + (wn * TN + u) * 16 + l16) >> 1;  // the pair's output column
+                float p[4];
 #pragma unroll
-                for (int r = 0; r < 4; r++) {
-                    const int m = m0 + (wm * TM + t) * 16 + seg * 4 + r;
-                    const float v = acc[t][u][r];
-                    const float up = __shfl_xor(v, 1);
-                    if (!(l16 & 1) && m < M && n < N) {
-                        const size_t e = (size_t)m * F2 + (n >> 1);
-                        split_bf16(silu_gate(v, up), &act_hi[e], &act_lo[e]);
+                for (int r = 0; r < 4; r++) p[r] = __shfl_xor(acc[t][u][r], 1);
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const float g = odd ? p[2 + k] : acc[t][u][k];
+                    const float up = odd ? acc[t][u][2 + k] : p[k];
+                    const int m = m0 + (wm * TM + t) * 16 + seg * 4 + (odd ? 2 + k : k);
+                    if (full || (m < M && 2 * n2 < N)) {
+                        const size_t e = (size_t)m * F2 + n2;
+                        split_bf16(silu_gate(g, up), &act_hi[e], &act_lo[e]);
                     }
                 }
             }
