@@ -327,13 +327,33 @@ enum : int { KV_F16 = 0, KV_I8 = 1, KV_F32 = 2 };
 // Output tile d, register r of lane (j, s) is O[head 4s + r][dvf(j, d)].
 __device__ __forceinline__ constexpr int dvf(int j, int d) { return 4 * j + 64 * (d >> 2) + (d & 3); }
 
+// Start of the (page pg, KV head kvh) block of a K or V pool whose blocks are
+// block_bytes long.  Loads add 32-bit byte offsets inside the block (a block
+// is at most page_size * (head_dim + 4) * 4 bytes): with a wave-uniform page
+// id the base lives in scalar registers and each load needs no 64-bit
+// address arithmetic per lane.
+__device__ __forceinline__ const char* page_block(const void* pool, int pg, int Hkv, int kvh, size_t block_bytes) {
+    return (const char*)pool + ((size_t)pg * Hkv + kvh) * block_bytes;
+}
+// A page id read from the table: UPG (page_size >= 16) makes it wave-uniform.
+// Each id a lane reads is that of a 16-aligned group of 16 positions (K rows
+// pw + 16t + l16) or of 4-position runs inside one (V runs pw + 16t + 4s), each
+// clamped into the context; with pages of 16 or more positions the whole
+// group lies in one page, so every lane of the wave reads the same id.
+template <bool UPG>
+__device__ __forceinline__ int page_id(const int32_t* ptab, int idx) {
+    const int v = ptab[idx];
+    return UPG ? __builtin_amdgcn_readfirstlane(v) : v;
+}
+
 // K operands of one f32 score tile: position pc of page pg, the lane group's dims
 template <int HD>
 __device__ __forceinline__ void kload_f32(const AttnArgs& a, int pg, int kvh, int row, int seg,
                                           float4 (&kb)[HD / 16]) {
-    const float* kr = (const float*)a.kc + (((size_t)pg * a.Hkv + kvh) * a.page_size + row) * HD + 4 * seg;
+    const char* kp = page_block(a.kc, pg, a.Hkv, kvh, (size_t)a.page_size * HD * 4);
+    const uint32_t o = (uint32_t)(row * HD + 4 * seg) * 4u;
 #pragma unroll
-    for (int c = 0; c < HD / 16; c++) kb[c] = *(const float4*)(kr + 16 * c);
+    for (int c = 0; c < HD / 16; c++) kb[c] = *(const float4*)(kp + (o + 64u * c));
 }
 
 // V operands of one f32 P.V tile: 4 positions (rows r0 .. of page pg, each
@@ -341,11 +361,12 @@ __device__ __forceinline__ void kload_f32(const AttnArgs& a, int pg, int kvh, in
 template <int HD>
 __device__ __forceinline__ void vload_f32(const AttnArgs& a, int pg, int kvh, const int (&rows)[4], int l16,
                                           float4 (&vb)[4][HD / 64]) {
-    const float* vp = (const float*)a.vc + ((size_t)pg * a.Hkv + kvh) * a.page_size * HD + 4 * l16;
+    const char* vp = page_block(a.vc, pg, a.Hkv, kvh, (size_t)a.page_size * HD * 4);
 #pragma unroll
     for (int r = 0; r < 4; r++)
 #pragma unroll
-        for (int i = 0; i < HD / 64; i++) vb[r][i] = *(const float4*)(vp + (size_t)rows[r] * HD + 64 * i);
+        for (int i = 0; i < HD / 64; i++)
+            vb[r][i] = *(const float4*)(vp + (uint32_t)(rows[r] * HD + 4 * l16 + 64 * i) * 4u);
 }
 
 // one f32 score tile: sc += K . q^T over all HD dims (q from LDS, row stride HD + 4)
@@ -412,7 +433,7 @@ __device__ __forceinline__ f16x8 i8x8_to_f16x8(uint32_t w0, uint32_t w1) {
 // 4 workgroups per CU (at most 128 VGPRs): the K and V loads of one wave
 // already cover its own latency, more resident workgroups cover the
 // prologue and epilogue of the others
-template <int HD, int KV>
+template <int HD, int KV, bool UPG>
 __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
     constexpr bool I8 = KV == KV_I8, F32 = KV == KV_F32;
@@ -465,10 +486,10 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     // the context, so every read is inside the page table)
     int kpg[4], vpg[4];
 #pragma unroll
-    for (int t = 0; t < 4; t++) kpg[t] = ptab[min(pw + 16 * t + l16, ctx - 1) >> psl];
+    for (int t = 0; t < 4; t++) kpg[t] = page_id<UPG>(ptab, min(pw + 16 * t + l16, ctx - 1) >> psl);
     const int vlast = (ctx - 1) & ~3;
 #pragma unroll
-    for (int j = 0; j < 4; j++) vpg[j] = ptab[min(pw + 16 * j + 4 * seg, vlast) >> psl];
+    for (int j = 0; j < 4; j++) vpg[j] = page_id<UPG>(ptab, min(pw + 16 * j + 4 * seg, vlast) >> psl);
     // int8: lane l loads the K and V scales of position pw + l (clamped like
     // its K row, whose page is kpg[l / 16]) and stores them to LDS before the
     // staging barrier; a score's or probability's lane reads its 4-position
@@ -495,14 +516,15 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
         for (int t = 0; t < 4; t++) {
             const int pc = min(pw + 16 * t + l16, ctx - 1);
             if constexpr (I8) {
-                const int8_t* kr = (const int8_t*)a.kc + ((size_t)kpg[t] * a.Hkv + kvh) * blk +
-                                   (size_t)(pc & psm) * HD + 8 * KK * seg;
+                const char* kb = page_block(a.kc, kpg[t], a.Hkv, kvh, blk);
+                const uint32_t o = (uint32_t)((pc & psm) * HD + 8 * KK * seg);
 #pragma unroll
-                for (int i = 0; i < KK / 2; i++) kreg[t][i] = *(const uint4*)(kr + 16 * i);
+                for (int i = 0; i < KK / 2; i++) kreg[t][i] = *(const uint4*)(kb + (o + 16u * i));
             } else {
-                const _Float16* kr = kc + (((size_t)kpg[t] * a.Hkv + kvh) * ps + (pc & psm)) * HD + 8 * seg;
+                const char* kb = page_block(kc, kpg[t], a.Hkv, kvh, (size_t)ps * HD * 2);
+                const uint32_t o = (uint32_t)((pc & psm) * HD + 8 * seg) * 2u;
 #pragma unroll
-                for (int kk = 0; kk < KK; kk++) kreg[t][kk] = *(const f16x8*)(kr + 32 * kk);
+                for (int kk = 0; kk < KK; kk++) kreg[t][kk] = *(const f16x8*)(kb + (o + 64u * kk));
             }
         }
     };
@@ -520,22 +542,22 @@ __global__ __launch_bounds__(ACH, 4) void attn_mfma_kernel(AttnArgs a, int G) {
     auto vload = [&](int b, VRun (&ra)[DT], VRun (&rb)[DT]) {
         const int pac = min(pw + 32 * b + 4 * seg, vlast), pbc = min(pw + 32 * b + 16 + 4 * seg, vlast);
         if constexpr (I8) {
-            const int8_t* va = (const int8_t*)a.vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * blk + (pac & psm);
-            const int8_t* vb = (const int8_t*)a.vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * blk + (pbc & psm);
+            const char* va = page_block(a.vc, vpg[2 * b], a.Hkv, kvh, blk);
+            const char* vb = page_block(a.vc, vpg[2 * b + 1], a.Hkv, kvh, blk);
 #pragma unroll
             for (int d = 0; d < DT; d++) {
                 const int dim = 16 * d + l16;
-                ra[d] = *(const uint32_t*)(va + (size_t)dim * ps);
-                rb[d] = *(const uint32_t*)(vb + (size_t)dim * ps);
+                ra[d] = *(const uint32_t*)(va + (uint32_t)((pac & psm) + dim * ps));
+                rb[d] = *(const uint32_t*)(vb + (uint32_t)((pbc & psm) + dim * ps));
             }
         } else {
-            const _Float16* va = vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * HD * ps + (pac & psm);
-            const _Float16* vb = vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * HD * ps + (pbc & psm);
+            const char* va = page_block(vc, vpg[2 * b], a.Hkv, kvh, (size_t)HD * ps * 2);
+            const char* vb = page_block(vc, vpg[2 * b + 1], a.Hkv, kvh, (size_t)HD * ps * 2);
 #pragma unroll
             for (int d = 0; d < DT; d++) {
                 const int dim = 16 * d + l16;
-                ra[d] = *(const uint2*)(va + (size_t)dim * ps);
-                rb[d] = *(const uint2*)(vb + (size_t)dim * ps);
+                ra[d] = *(const uint2*)(va + (uint32_t)((pac & psm) + dim * ps) * 2u);
+                rb[d] = *(const uint2*)(vb + (uint32_t)((pbc & psm) + dim * ps) * 2u);
             }
         }
     };
@@ -813,7 +835,7 @@ constexpr int SPLIT_MAXN = 1024;   // sequences per launch (the batch bound)
 // 128, whose 148-168 registers per lane leave room for 3)
 constexpr int split_slots(int hd) { return 256 * (hd == 128 ? 3 : 4); }
 
-template <int HD, int KV>
+template <int HD, int KV, bool UPG>
 __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(AttnArgs a, int G) {
     static_assert(HD == 64 || HD == 128, "head_dim 64 or 128");
     constexpr bool I8 = KV == KV_I8, F32 = KV == KV_F32;
@@ -914,9 +936,9 @@ __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(Attn
         auto ids_to = [&](int j, int (&kp)[4], int (&vp)[4]) {
             const int pw = 64 * j;
 #pragma unroll
-            for (int t = 0; t < 4; t++) kp[t] = ptab[min(pw + 16 * t + l16, ctx - 1) >> psl];
+            for (int t = 0; t < 4; t++) kp[t] = page_id<UPG>(ptab, min(pw + 16 * t + l16, ctx - 1) >> psl);
 #pragma unroll
-            for (int t = 0; t < 4; t++) vp[t] = ptab[min(pw + 16 * t + 4 * seg, vlast) >> psl];
+            for (int t = 0; t < 4; t++) vp[t] = page_id<UPG>(ptab, min(pw + 16 * t + 4 * seg, vlast) >> psl);
         };
         auto ids = [&](int j) { ids_to(j, kpg, vpg); };
         KRow kreg[4];
@@ -926,14 +948,15 @@ __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(Attn
             for (int t = 0; t < 4; t++) {
                 const int pc = min(pw + 16 * t + l16, ctx - 1);
                 if constexpr (I8) {
-                    const int8_t* kr = (const int8_t*)a.kc + ((size_t)kpg[t] * a.Hkv + kvh) * blk +
-                                       ((pc & psm) * HD + 8 * KK * seg);
+                    const char* kb = page_block(a.kc, kpg[t], a.Hkv, kvh, blk);
+                    const uint32_t o = (uint32_t)((pc & psm) * HD + 8 * KK * seg);
 #pragma unroll
-                    for (int i = 0; i < KK / 2; i++) kreg[t][i] = *(const uint4*)(kr + 16 * i);
+                    for (int i = 0; i < KK / 2; i++) kreg[t][i] = *(const uint4*)(kb + (o + 16u * i));
                 } else {
-                    const _Float16* kr = kc + ((size_t)kpg[t] * a.Hkv + kvh) * ps * HD + ((pc & psm) * HD + 8 * seg);
+                    const char* kb = page_block(kc, kpg[t], a.Hkv, kvh, (size_t)ps * HD * 2);
+                    const uint32_t o = (uint32_t)((pc & psm) * HD + 8 * seg) * 2u;
 #pragma unroll
-                    for (int kk = 0; kk < KK; kk++) kreg[t][kk] = *(const f16x8*)(kr + 32 * kk);
+                    for (int kk = 0; kk < KK; kk++) kreg[t][kk] = *(const f16x8*)(kb + (o + 64u * kk));
                 }
             }
         };
@@ -942,22 +965,22 @@ __global__ __launch_bounds__(ACH, HD == 128 ? 3 : 4) void attn_split_kernel(Attn
             const int pw = 64 * j;
             const int pac = min(pw + 32 * b + 4 * seg, vlast), pbc = min(pw + 32 * b + 16 + 4 * seg, vlast);
             if constexpr (I8) {
-                const int8_t* va = (const int8_t*)a.vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * blk + (pac & psm);
-                const int8_t* vb = (const int8_t*)a.vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * blk + (pbc & psm);
-#pragma unroll
-                for (int d = 0; d < DT; d++) {
-                    const int off = (16 * d + l16) * ps;  // in-block offsets stay 32-bit
-                    ra[d] = *(const uint32_t*)(va + off);
-                    rb[d] = *(const uint32_t*)(vb + off);
-                }
-            } else {
-                const _Float16* va = vc + ((size_t)vpg[2 * b] * a.Hkv + kvh) * HD * ps + (pac & psm);
-                const _Float16* vb = vc + ((size_t)vpg[2 * b + 1] * a.Hkv + kvh) * HD * ps + (pbc & psm);
+                const char* va = page_block(a.vc, vpg[2 * b], a.Hkv, kvh, blk);
+                const char* vb = page_block(a.vc, vpg[2 * b + 1], a.Hkv, kvh, blk);
 #pragma unroll
                 for (int d = 0; d < DT; d++) {
                     const int off = (16 * d + l16) * ps;
-                    ra[d] = *(const uint2*)(va + off);
-                    rb[d] = *(const uint2*)(vb + off);
+                    ra[d] = *(const uint32_t*)(va + (uint32_t)((pac & psm) + off));
+                    rb[d] = *(const uint32_t*)(vb + (uint32_t)((pbc & psm) + off));
+                }
+            } else {
+                const char* va = page_block(vc, vpg[2 * b], a.Hkv, kvh, (size_t)HD * ps * 2);
+                const char* vb = page_block(vc, vpg[2 * b + 1], a.Hkv, kvh, (size_t)HD * ps * 2);
+#pragma unroll
+                for (int d = 0; d < DT; d++) {
+                    const int off = (16 * d + l16) * ps;
+                    ra[d] = *(const uint2*)(va + (uint32_t)((pac & psm) + off) * 2u);
+                    rb[d] = *(const uint2*)(vb + (uint32_t)((pbc & psm) + off) * 2u);
                 }
             }
         };
@@ -1459,8 +1482,12 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
         const int kind = kv_dtype == DT_I8 ? KV_I8 : kv_dtype == DT_F32 ? KV_F32 : KV_F16;
         const dim3 grid(split ? a.gx : items, Hkv);
         const size_t lds = 4 * G * hd * sizeof(float);
-#define QH_ATTN_MFMA(K, HDv, KINDv)                                                     \
-    if (kind == KINDv && hd == HDv) hipLaunchKernelGGL((K<HDv, KINDv>), grid, dim3(ACH), lds, st, a, G);
+        const bool upg = page_size >= 16;  // page ids uniform per wave (page_id)
+#define QH_ATTN_MFMA(K, HDv, KINDv)                                                                    \
+    if (kind == KINDv && hd == HDv) {                                                                  \
+        if (upg) hipLaunchKernelGGL((K<HDv, KINDv, true>), grid, dim3(ACH), lds, st, a, G);            \
+        else hipLaunchKernelGGL((K<HDv, KINDv, false>), grid, dim3(ACH), lds, st, a, G);               \
+    }
         if (split) {
             QH_ATTN_MFMA(attn_split_kernel, 128, KV_F16) QH_ATTN_MFMA(attn_split_kernel, 64, KV_F16)
             QH_ATTN_MFMA(attn_split_kernel, 128, KV_I8) QH_ATTN_MFMA(attn_split_kernel, 64, KV_I8)
