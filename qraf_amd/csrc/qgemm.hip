@@ -70,6 +70,44 @@ __global__ void split_bf16_kernel(const float* __restrict__ x, uint16_t* __restr
     }
 }
 
+// op 1 with four outputs per thread: outputs k..k+3 of row m read the 8
+// interleaved gate/up floats 2k..2k+7 of each slice as two 16-byte loads (all
+// slices' loads issued before the first add, sums in slice order as in
+// split_bf16_kernel, so the planes are the same bit for bit) and write 8-byte
+// hi and lo stores.  K % 4 == 0, 16-byte aligned x and slice, 8-byte aligned
+// planes, M * K < 2^31.
+template <int S>
+__global__ __launch_bounds__(256) void silu_split4_kernel(const float* __restrict__ x, uint16_t* __restrict__ hi,
+                                                          uint16_t* __restrict__ lo, int M, int K, size_t slice) {
+    const int n4 = M * (K >> 2);
+    for (int i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+        const int m = i / (K >> 2), k = (i - m * (K >> 2)) << 2;
+        const float* p = x + (size_t)m * 2 * K + 2 * k;
+        f32x4 a[S], b[S];
+#pragma unroll
+        for (int u = 0; u < S; u++) {
+            a[u] = *(const f32x4*)(p + (size_t)u * slice);
+            b[u] = *(const f32x4*)(p + (size_t)u * slice + 4);
+        }
+        f32x4 ga = a[0], gb = b[0];
+#pragma unroll
+        for (int u = 1; u < S; u++) {
+            ga += a[u];
+            gb += b[u];
+        }
+        const float v0 = silu_gate(ga[0], ga[1]), v1 = silu_gate(ga[2], ga[3]);
+        const float v2 = silu_gate(gb[0], gb[1]), v3 = silu_gate(gb[2], gb[3]);
+        uint16_t h[4], l[4];
+        split_bf16(v0, &h[0], &l[0]);
+        split_bf16(v1, &h[1], &l[1]);
+        split_bf16(v2, &h[2], &l[2]);
+        split_bf16(v3, &h[3], &l[3]);
+        const size_t e = (size_t)m * K + k;
+        *(uint2*)(hi + e) = make_uint2(h[0] | ((uint32_t)h[1] << 16), h[2] | ((uint32_t)h[3] << 16));
+        *(uint2*)(lo + e) = make_uint2(l[0] | ((uint32_t)l[1] << 16), l[2] | ((uint32_t)l[3] << 16));
+    }
+}
+
 // Raw weight fragment of one lane for one (16-row tile, block): the block
 // scale and the 8 quants k = 8*seg..8*seg+7 of the lane's row.
 template <int FMT>
@@ -991,6 +1029,18 @@ int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, 
                       int S, size_t slice) {
     QH_REQUIRE(x && hi && lo && M > 0 && K > 0 && S >= 1, QRAF_HIP_ERR_INVALID, "split: bad arguments");
     const size_t n = (size_t)M * K;
+    if (op == 1 && !xout && S <= 4 && K % 4 == 0 && n < ((size_t)1 << 31) && (((uintptr_t)x) & 15) == 0 &&
+        (S == 1 || slice % 4 == 0) && (((uintptr_t)hi) & 7) == 0 && (((uintptr_t)lo) & 7) == 0) {
+        const int grid4 = (int)min((n / 4 + 255) / 256, (size_t)4096);
+#define QH_S4(Sv) hipLaunchKernelGGL(silu_split4_kernel<Sv>, dim3(grid4), dim3(256), 0, s, x, hi, lo, M, K, slice)
+        if (S == 1) QH_S4(1);
+        else if (S == 2) QH_S4(2);
+        else if (S == 3) QH_S4(3);
+        else QH_S4(4);
+#undef QH_S4
+        QH_CHECK_HIP(hipGetLastError());
+        return QRAF_HIP_OK;
+    }
     const int grid = (int)min((n + 255) / 256, (size_t)4096);
     hipLaunchKernelGGL(split_bf16_kernel, dim3(grid), dim3(256), 0, s, x, hi, lo, M, K, op, xout, S, slice);
     QH_CHECK_HIP(hipGetLastError());
