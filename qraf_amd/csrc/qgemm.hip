@@ -926,32 +926,55 @@ static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
         // pipelined kernel, 3-stage LDS ring, 1 workgroup per CU, 256 weight rows:
         // up to 64 batch rows 2 x 4 waves of 16*TM x 64 rows; beyond, 8 waves
         // side by side of all 128 batch rows x 32 weight rows (each converted
-        // weight fragment then feeds 8 batch tiles instead of 4)
+        // weight fragment then feeds 8 batch tiles instead of 4), or for Q4_0
+        // x 48 weight rows (384 per workgroup; Q8_0's stages would not fit
+        // the LDS) when that grid fills more CUs in one round
         p.pipe = true;
         p.KC = 2;
-        p.NW = 256;
+        const int nb = K / 32;
+        const int unit = 3 * p.KC;  // blocks per trip of the 3-stage loop
+        auto fill = [&](int tn, int& S) {  // workgroups of the tn form, S its split count
+            const size_t tiles = (size_t)((N + 16 * tn * 8 - 1) / (16 * tn * 8)) * ((M + 127) / 128);
+            S = 1;
+            if (g_qg_splits > 0) S = g_qg_splits;
+            else if (tn == 3)  // at most one round of workgroups (one per CU)
+                while (S < 64 && tiles * S * 2 <= (size_t)qg_cu_count() && nb >= 2 * S * unit) S *= 2;
+            else  // about one round of workgroups (one per CU): a second, partial round costs a full stage loop
+                while (S < 64 && tiles * S * 2 <= 200 && nb >= 2 * S * unit) S *= 2;
+            return tiles * S;
+        };
+        int S = 1;
         if (Mc > 64) {
             p.WM = 1;
             p.WN = 8;
             p.TM = 8;
-            p.TN = 2;
             p.MW = 128;
+            // the form with the smaller rounds of workgroups x work per
+            // workgroup, (weight tiles) x (blocks per split + 10: the pipeline's
+            // fill and drain and the partial tile, in blocks); MI355X, Q4_0 at 128
+            // rows: 22016 x 2048 232 workgroups of 384 rows against 172 of 256
+            // (the 128-row decode step 5.67 -> 5.56 ms); 11008 x 2048 172 of 256
+            // rows in 4 splits (30.7 us) against 232 of 384 rows in 8 (32.5 us)
+            int S3 = 1;
+            const size_t cu = (size_t)qg_cu_count(), g2 = fill(2, S), g3 = fill(3, S3);
+            const double t2 = (double)((g2 + cu - 1) / cu) * 2 * ((double)nb / S + 10),
+                         t3 = (double)((g3 + cu - 1) / cu) * 3 * ((double)nb / S3 + 10);
+            p.TN = row_bytes == (size_t)nb * 18 && t3 < t2 ? 3 : 2;
+            if (p.TN == 3) S = S3;
         } else {
             p.WM = 2;
             p.WN = 4;
             p.TM = 2;  // 33..64 rows
             p.TN = 4;
             p.MW = 32 * p.TM;
+            const size_t tiles = (size_t)((N + 255) / 256) * ((M + p.MW - 1) / p.MW);
+            if (g_qg_splits > 0) S = g_qg_splits;
+            else
+                while (S < 64 && tiles * S * 2 <= 200 && nb >= 2 * S * unit) S *= 2;
         }
+        p.NW = 16 * p.TN * p.WN;
         p.ntiles = (N + p.NW - 1) / p.NW;
         p.mchunks = (M + p.MW - 1) / p.MW;
-        const int nb = K / 32;
-        const size_t tiles = (size_t)p.ntiles * p.mchunks;
-        const int unit = 3 * p.KC;  // blocks per trip of the 3-stage loop
-        int S = 1;
-        if (g_qg_splits > 0) S = g_qg_splits;
-        else  // about one round of workgroups (one per CU): a second, partial round costs a full stage loop
-            while (S < 64 && tiles * S * 2 <= 200 && nb >= 2 * S * unit) S *= 2;
         // whole stages per split; the kernel rounds its stage loop up to whole
         // trips and skips the blocks past the split
         p.bps = ((nb + S - 1) / S + p.KC - 1) / p.KC * p.KC;
@@ -1125,8 +1148,10 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
             if (p.WN == 4 && p.WM == 1) {
                 if (p.TM == 8) QH_P(4, 8, 2, 4, 1);
                 else QH_P(4, 4, 2, 4, 1);
-            } else if (p.WM == 1) QH_P(4, 8, 2, 8, 1);
-            else QH_P(4, 2, 4, 4, 2);
+            } else if (p.WM == 1) {
+                if (p.TN == 3) QH_P(4, 8, 3, 8, 1);
+                else QH_P(4, 8, 2, 8, 1);
+            } else QH_P(4, 2, 4, 4, 2);
         }
 #undef QH_P
     } else {

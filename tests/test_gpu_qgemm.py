@@ -150,6 +150,23 @@ def test_qgemm_pipelined_kernel(hip, dt, case, form):
     check(Y1, wq, dt, N, K, X)
 
 
+@pytest.mark.parametrize("case", [(16384, 2048, 128), (16384, 2048, 200)], ids=lambda c: "x".join(map(str, c)))
+def test_qgemm_pipelined_384_row_tiles(hip, case):
+    """Q4_0 wide products where the plan takes the 384-weight-row form of the
+    pipelined kernel (8 waves of 128 batch rows x 48 weight rows; it fills more
+    CUs than 256-row tiles at these shapes: four split-K slices at 128 rows,
+    two at 200, the second batch chunk partial), against the oracle."""
+    N, K, M = case
+    lib = hip._lib.lib
+    assert lib.qraf_hip_qgemm_tiled_workspace_bytes(po.Q4_0, N, K, M) == (4 if M == 128 else 2) * M * N * 4
+    rng = np.random.default_rng(N + 7 * K + M)
+    wq = po.quantize(po.Q4_0, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    print(f"qgemm 384-row tiles N={N} K={K} M={M}", flush=True)
+    Y, _, _ = run_gemm(hip, wq, po.Q4_0, N, K, X, tiled=True, repeats=2)
+    check(Y, wq, po.Q4_0, N, K, X)
+
+
 @pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
 @pytest.mark.parametrize("case", [(8192, 1024, 100), (2560, 2048, 130), (300, 512, 64), (1000, 576, 33)],
                          ids=lambda c: "x".join(map(str, c)))
@@ -185,12 +202,14 @@ def test_qgemm_stream_k(hip, dt, case, form, min_blocks):
 
 def test_qgemm_stream_k_plan(hip):
     """The schedule knob through the workspace query (host-side plan): the
-    default keeps the uniform grid (the 128-row gate/up product in two
-    split-K slices, the LM head in whole tiles without partials); forced
-    stream-K shares the head's tiles too."""
+    default keeps the uniform grid (the 128-row gate/up product in four
+    split-K slices of 384-row tiles, 11008 rows in four slices of 256-row
+    tiles, the LM head in whole tiles without partials); forced stream-K
+    shares the head's tiles too."""
     lib, call = hip._lib.lib, hip._lib.call
     q = lib.qraf_hip_qgemm_tiled_workspace_bytes
-    assert q(po.Q4_0, 22016, 2048, 128) == 2 * 128 * 22016 * 4
+    assert q(po.Q4_0, 22016, 2048, 128) == 4 * 128 * 22016 * 4
+    assert q(po.Q4_0, 11008, 2048, 128) == 4 * 128 * 11008 * 4
     assert q(po.Q4_0, 151936, 2048, 128) == 0
     try:
         call("qraf_hip_set_qgemm_schedule", 1, 0)
