@@ -165,6 +165,12 @@ def test_qgemm_pipelined_384_row_tiles(hip, case):
     print(f"qgemm 384-row tiles N={N} K={K} M={M}", flush=True)
     Y, _, _ = run_gemm(hip, wq, po.Q4_0, N, K, X, tiled=True, repeats=2)
     check(Y, wq, po.Q4_0, N, K, X)
+    try:  # the same form under the stream-K schedule
+        hip._lib.call("qraf_hip_set_qgemm_schedule", 1, 0)
+        Ys, _, _ = run_gemm(hip, wq, po.Q4_0, N, K, X, tiled=True)
+    finally:
+        hip._lib.call("qraf_hip_set_qgemm_schedule", 0, 0)
+    check(Ys, wq, po.Q4_0, N, K, X)
 
 
 @pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
