@@ -137,9 +137,72 @@ __global__ __launch_bounds__(1024) void residual_norm_split_kernel(const float* 
     }
 }
 
+// The same with elements 2t, 2t+1 per thread (8-byte loads of each slice and
+// of h, half the load instructions); D even, D <= 2048, 8-byte aligned rows.
+template <int S>
+__global__ __launch_bounds__(1024) void residual_norm_split_v2_kernel(const float* __restrict__ part, size_t slice,
+                                                                     float* __restrict__ h, const float* __restrict__ w,
+                                                                     int D, float eps, uint16_t* __restrict__ xh,
+                                                                     uint16_t* __restrict__ xl) {
+    __shared__ float red[16];
+    const int m = blockIdx.x, tid = threadIdx.x, i = 2 * tid;
+    float2* hr = (float2*)(h + (size_t)m * D);
+    float2 v = make_float2(0.f, 0.f);
+    if (i < D) {
+        v = hr[tid];
+        if (S > 0) {
+            float2 t[S > 0 ? S : 1];
+#pragma unroll
+            for (int u = 0; u < S; u++) t[u] = *(const float2*)(part + (size_t)u * slice + (size_t)m * D + i);
+            float a = t[0].x, b = t[0].y;
+#pragma unroll
+            for (int u = 1; u < S; u++) {
+                a += t[u].x;
+                b += t[u].y;
+            }
+            v = make_float2(a + v.x, b + v.y);
+            hr[tid] = v;
+        }
+    }
+    float ss = __builtin_fmaf(v.y, v.y, v.x * v.x);
+    if (!w) return;
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; k++) ss += red[k];
+    const float r = 1.0f / sqrtf(ss / (float)D + eps);
+    if (i < D) {
+        const size_t e = (size_t)m * D + i;
+        split_bf16(__fmul_rn(__fmul_rn(v.x, r), w[i]), &xh[e], &xl[e]);
+        split_bf16(__fmul_rn(__fmul_rn(v.y, r), w[i + 1]), &xh[e + 1], &xl[e + 1]);
+    }
+}
+
 static int launch_residual_norm_split(const float* part, int S, size_t slice, float* h, const float* w, int D, float eps,
                                       uint16_t* xh, uint16_t* xl, int rows, hipStream_t s) {
     QH_REQUIRE(D <= 8192, QRAF_HIP_ERR_INVALID, "residual/norm: hidden size %d > 8192", D);
+    if (D % 2 == 0 && D <= 2048 && S <= 8 && (S == 0 || slice % 2 == 0) && (((uintptr_t)h) & 7) == 0 &&
+        (((uintptr_t)part) & 7) == 0) {
+#define QH_RN2(Sv) hipLaunchKernelGGL(residual_norm_split_v2_kernel<Sv>, dim3(rows), dim3(1024), 0, s, part, slice, h, w, \
+                                      D, eps, xh, xl)
+        switch (S) {
+            case 0: QH_RN2(0); break;
+            case 1: QH_RN2(1); break;
+            case 2: QH_RN2(2); break;
+            case 3: QH_RN2(3); break;
+            case 4: QH_RN2(4); break;
+            case 5: QH_RN2(5); break;
+            case 6: QH_RN2(6); break;
+            case 7: QH_RN2(7); break;
+            default: QH_RN2(8); break;
+        }
+#undef QH_RN2
+        QH_CHECK_HIP(hipGetLastError());
+        return QRAF_HIP_OK;
+    }
 #define QH_RNS(Jv) hipLaunchKernelGGL(residual_norm_split_kernel<Jv>, dim3(rows), dim3(1024), 0, s, part, S, slice, h, w, \
                                       D, eps, xh, xl)
     if (D <= 1024) QH_RNS(1);
