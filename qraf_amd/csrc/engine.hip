@@ -138,7 +138,8 @@ __global__ __launch_bounds__(1024) void residual_norm_split_kernel(const float* 
 }
 
 // The same with elements 2t, 2t+1 per thread (8-byte loads of each slice and
-// of h, half the load instructions); D even, D <= 2048, 8-byte aligned rows.
+// of h, half the load instructions, every slice's load issued before the
+// first add); D even, D <= 2048, 8-byte aligned rows, S <= 8 or 16.
 template <int S>
 __global__ __launch_bounds__(1024) void residual_norm_split_v2_kernel(const float* __restrict__ part, size_t slice,
                                                                      float* __restrict__ h, const float* __restrict__ w,
@@ -184,7 +185,7 @@ __global__ __launch_bounds__(1024) void residual_norm_split_v2_kernel(const floa
 static int launch_residual_norm_split(const float* part, int S, size_t slice, float* h, const float* w, int D, float eps,
                                       uint16_t* xh, uint16_t* xl, int rows, hipStream_t s) {
     QH_REQUIRE(D <= 8192, QRAF_HIP_ERR_INVALID, "residual/norm: hidden size %d > 8192", D);
-    if (D % 2 == 0 && D <= 2048 && S <= 8 && (S == 0 || slice % 2 == 0) && (((uintptr_t)h) & 7) == 0 &&
+    if (D % 2 == 0 && D <= 2048 && (S <= 8 || S == 16) && (S == 0 || slice % 2 == 0) && (((uintptr_t)h) & 7) == 0 &&
         (((uintptr_t)part) & 7) == 0) {
 #define QH_RN2(Sv) hipLaunchKernelGGL(residual_norm_split_v2_kernel<Sv>, dim3(rows), dim3(1024), 0, s, part, slice, h, w, \
                                       D, eps, xh, xl)
@@ -197,7 +198,8 @@ static int launch_residual_norm_split(const float* part, int S, size_t slice, fl
             case 5: QH_RN2(5); break;
             case 6: QH_RN2(6); break;
             case 7: QH_RN2(7); break;
-            default: QH_RN2(8); break;
+            case 8: QH_RN2(8); break;
+            default: QH_RN2(16); break;
         }
 #undef QH_RN2
         QH_CHECK_HIP(hipGetLastError());
