@@ -259,6 +259,15 @@ int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe, int batch_chunk);
  * workspace queries too.  No counterpart in the reference (a performance
  * knob). */
 int qraf_hip_set_qgemm_schedule(int32_t mode, int32_t min_blocks);
+/* Wave-split form of the tile-major GEMM (each workgroup's 4 waves take its
+ * quant blocks in turn and meet once in LDS at the end): mode 1 selects it
+ * for every tiled batch over 16 rows, -1 never, 0 (the default) for batches
+ * of 17-32 rows and of 33-64 rows below 16384 output rows, unless
+ * qraf_hip_set_qgemm_tuning forces another form;
+ * tiles_per_workgroup 2, 3 or 4 fixes its 16-row weight tiles per workgroup
+ * (0: automatic).  Affects the workspace queries and the SwiGLU-epilogue
+ * entry point too.  No counterpart in the reference (a performance knob). */
+int qraf_hip_set_qgemm_kw(int32_t mode, int32_t tiles_per_workgroup);
 /* Workspace (bytes) that lets qraf_hip_qgemm_dev split the in_dim range of an
  * out_dim x in_dim product at this batch across workgroups; 0 when it does
  * not split. */

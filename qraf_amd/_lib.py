@@ -75,6 +75,7 @@ SIGNATURES = {
     "qraf_hip_split_bf16_dev": (C.c_int, [vp, vp, vp, C.c_int32, C.c_int32, vp]),
     "qraf_hip_set_qgemm_tuning": (C.c_int, [C.c_int, C.c_int, C.c_int, C.c_int]),
     "qraf_hip_set_qgemm_schedule": (C.c_int, [C.c_int32, C.c_int32]),
+    "qraf_hip_set_qgemm_kw": (C.c_int, [C.c_int32, C.c_int32]),
     "qraf_hip_tiled_weight_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32, C.c_uint32]),
     "qraf_hip_repack_tiles_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
     "qraf_hip_qgemm_tiled_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp, vp,

@@ -99,6 +99,7 @@ int qraf_hip_init(int device) {
     QH_REQUIRE(device >= 0 && device < n, QRAF_HIP_ERR_INVALID, "device %d out of range (%d devices)", device, n);
     QH_CHECK_HIP(hipSetDevice(device));
     QH_TRY(ensure_init());
+    QH_TRY(qgemm_kw_init());
     return attn_scratch_init(device);
 }
 

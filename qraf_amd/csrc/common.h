@@ -189,6 +189,8 @@ int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, 
 int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
                  float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled = false,
                  int* slices = nullptr);
+// sets the dynamic-LDS attribute of every wave-split GEMM instantiation (qraf_hip_init)
+int qgemm_kw_init();
 int launch_qgemm_silu(const void* Wt, uint32_t dtype, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
                       uint16_t* act_hi, uint16_t* act_lo, hipStream_t s);
 size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M, bool tiled = false);

@@ -794,6 +794,219 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
     }
 }
 
+// ---------------------------------------------------------------------------
+// Wave-split GEMM for tile-major weights (qgemm_kw_kernel): batches of up to
+// 128 rows per workgroup.
+//
+// A workgroup owns R weight tiles (16R rows) x 16T batch rows over a range of
+// quant blocks; its 4 waves take the range's blocks in turn (wave w: blocks
+// b0 + w, b0 + w + 4, ...) and every wave computes the whole 16R x 16T tile
+// for its blocks.  Weight fragments and X fragments are loaded by each wave
+// straight into registers (weights three blocks ahead in a register ring, X
+// fragments reloaded for the next block right after their MFMAs), so the
+// main loop holds no LDS access and no barrier: a wave
+// waits only on its own loads.  Each converted weight fragment feeds T batch
+// tiles; each X fragment feeds R weight tiles.  The scale FMAs of a batch
+// tile issue after the next tile's MFMAs, when its results are complete.
+// At the end the four waves' sums meet in LDS and are added in wave order
+// ((w0 + w1) + w2) + w3, a fixed order: a result does not depend on
+// scheduling.  The epilogue stores coalesced rows of the tile: Y (+ add),
+// a partial slice, or the SwiGLU front of interleaved gate/up rows written as
+// the next GEMM's hi/lo planes.
+// ---------------------------------------------------------------------------
+constexpr int KW_WAVES = 4;
+
+template <int FMT, int R, int T>
+struct KwGeom {
+    static constexpr int TB = tile_block_bytes(FMT);
+    static constexpr int SB = FMT == 8 ? 4 : 2, QB = FMT == 8 ? 32 : 16;
+    // result tiles per wave per reduction pass: the largest divisor of T with
+    // R * TC <= 32 (at most 128 KB of LDS)
+    static constexpr int TC = (R * T <= 32) ? T : (R * (T / 2) <= 32) ? T / 2 : (R * (T / 4) <= 32) ? T / 4 : 1;
+    static_assert(T % TC == 0 && R * TC <= 32, "reduction pass");
+    static constexpr size_t LDS = (size_t)KW_WAVES * R * TC * 64 * 16;
+    // two workgroups per CU where the registers (<= 256 per lane) and the LDS allow
+    static constexpr int MINB = (R * T <= 16 && 2 * LDS <= 160 * 1024) ? 2 : 1;
+};
+
+// mode 0: Y[m][n] (+ add[m][n]) of the split's sums, Y offset by blockIdx.y * slice
+// (slice = M*N for split-K partials, 0 for a single split); mode 1: SwiGLU front
+// of interleaved gate/up rows (2i = gate_i, 2i+1 = up_i) written as the hi/lo planes
+// act_hi/act_lo [M][N/2] (one split only).  Dynamic LDS: KwGeom::LDS bytes.
+template <int FMT, int R, int T>
+__global__ __launch_bounds__(256, (KwGeom<FMT, R, T>::MINB)) void qgemm_kw_kernel(
+    const uint8_t* __restrict__ Wt, int N, int nb, const uint16_t* __restrict__ xh, const uint16_t* __restrict__ xl,
+    int K, int M, int bps, float* Y, const float* add, size_t slice, int mode, uint16_t* __restrict__ act_hi,
+    uint16_t* __restrict__ act_lo) {
+    using G = KwGeom<FMT, R, T>;
+    constexpr int TB = G::TB;
+    extern __shared__ __align__(16) f32x4 kw_red[];
+    static_assert(T % 2 == 0, "the result ring alternates between two batch tiles");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int seg = lane >> 4, l16 = lane & 15;
+    const int ntile16 = (N + 15) / 16;
+    const int n0 = blockIdx.x * 16 * R, m0 = blockIdx.z * 16 * T;
+    const int b0 = blockIdx.y * bps, b1 = min(nb, b0 + bps);
+    const int nblk = b1 - b0 > wave ? (b1 - b0 - wave + KW_WAVES - 1) / KW_WAVES : 0;  // this wave's blocks
+
+    const rsrc_t wrs = make_rsrc(Wt, (uint32_t)min((size_t)ntile16 * nb * TB, (size_t)0xFFFFFFFFu));
+    const uint32_t xbytes = (uint32_t)((size_t)M * K * 2);
+    const rsrc_t xrh = make_rsrc(xh, xbytes), xrl = make_rsrc(xl, xbytes);
+    // lane offsets: the scale and 8 quants of row l16 within a tile-block; X row
+    // m0 + 16t + l16 (clamped), elements 8*seg.. of a block
+    const uint32_t wsc = (uint32_t)(G::SB * l16), wqo = (uint32_t)(16 * G::SB + G::QB * l16 + (G::QB / 4) * seg);
+    const uint32_t xo0 = (uint32_t)((size_t)min(m0 + l16, M - 1) * K * 2) + 16u * seg;
+    auto xoff = [&](int t) {  // X row offset of batch tile t (rows past M read row M - 1)
+        return t == 0 ? xo0 : (uint32_t)((size_t)min(m0 + 16 * t + l16, M - 1) * K * 2) + 16u * seg;
+    };
+    uint32_t tbase[R];  // uniform: byte offset of each weight tile's first tile-block
+#pragma unroll
+    for (int u = 0; u < R; u++) tbase[u] = (uint32_t)((size_t)min((int)blockIdx.x * R + u, ntile16 - 1) * nb * TB);
+
+    // block of this wave's i-th step (clamped for the loads past the end)
+    auto blk = [&](int i) { return b0 + wave + KW_WAVES * min(i, max(nblk - 1, 0)); };
+    auto load_w = [&](WRaw<FMT>(&wr)[R], int i) {
+        const uint32_t k = (uint32_t)blk(i);
+#pragma unroll
+        for (int u = 0; u < R; u++) load_tiled<FMT>(wrs, wsc, wqo, tbase[u] + k * TB, wr[u]);
+    };
+    u32x4 xa[T], xb[T];  // X fragments of the current block; tile t reloads for the next block after its MFMAs
+    auto load_xt = [&](int t, int i) {
+        const uint32_t koff = (uint32_t)blk(i) * 64u, o = xoff(t);
+        xa[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrh, o, koff, 0));
+        xb[t] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xrl, o, koff, 0));
+    };
+
+    f32x4 acc[T][R];
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int u = 0; u < R; u++) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 dR[2][R];  // MFMA results of the previous and current batch tile
+    float sP[R];     // scales of the previous block (its last tile is pending when a block starts)
+#pragma unroll
+    for (int u = 0; u < R; u++) {
+        dR[0][u] = dR[1][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        sP[u] = 0.f;
+    }
+
+    // Weight ring: the raw fragments of steps i .. i+3 (the loads of step i + 3
+    // are requested when step i begins), rotated by register moves.
+    WRaw<FMT> w0[R], w1[R], w2[R];
+    load_w(w0, 0);
+    load_w(w1, 1);
+    load_w(w2, 2);
+#pragma unroll
+    for (int t = 0; t < T; t++) load_xt(t, 0);
+    for (int i = 0; i < nblk; i++) {
+        WRaw<FMT> w3[R];
+        load_w(w3, i + 3);
+        __builtin_amdgcn_sched_barrier(0);
+        // convert the weights of step i; per batch tile t the MFMAs, the reload
+        // of its X fragment with block i + 1, the scale FMAs of tile t - 1 (of
+        // the previous block for t = 0)
+        bf16x8 wf[R];
+        f16x8 wh[R];
+        float sc[R];
+#pragma unroll
+        for (int u = 0; u < R; u++) convert<FMT>(w0[u], wf[u], wh[u], sc[u]);
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+            const bf16x8 ah = __builtin_bit_cast(bf16x8, xa[t]);
+            const f16x8 al = __builtin_bit_cast(f16x8, xb[t]);
+            const int q = t & 1, pq = q ^ 1;
+            const int pt = t > 0 ? t - 1 : T - 1;
+#pragma unroll
+            for (int u = 0; u < R; u++) {
+                const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[u], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                dR[q][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, wh[u], d, 0, 0, 0);
+            }
+            load_xt(t, i + 1);
+#pragma unroll
+            for (int u = 0; u < R; u++) {
+                const float ps = t > 0 ? sc[u] : sP[u];
+#pragma unroll
+                for (int r = 0; r < 4; r++) acc[pt][u][r] = __builtin_fmaf(dR[pq][u][r], ps, acc[pt][u][r]);
+            }
+            // keep each tile's reload behind its MFMAs (hoisted reloads would
+            // hold a second block of X fragments in registers)
+            __builtin_amdgcn_sched_barrier(0);
+        }
+#pragma unroll
+        for (int u = 0; u < R; u++) {
+            sP[u] = sc[u];
+            w0[u] = w1[u];
+            w1[u] = w2[u];
+            w2[u] = w3[u];
+        }
+    }
+    // the last block's last tile (a wave without blocks adds zeros)
+#pragma unroll
+    for (int u = 0; u < R; u++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[T - 1][u][r] = __builtin_fmaf(dR[(T - 1) & 1][u][r], sP[u], acc[T - 1][u][r]);
+
+    // ---- reduction over the waves and epilogue, TC batch tiles per pass
+    constexpr int TC = G::TC;
+    float* dst = mode == 0 ? Y + (size_t)blockIdx.y * slice : nullptr;
+    const int F2 = N >> 1;
+#pragma unroll
+    for (int t0 = 0; t0 < T; t0 += TC) {
+        if (t0) __syncthreads();  // the previous pass's reads are done
+#pragma unroll
+        for (int tt = 0; tt < TC; tt++)
+#pragma unroll
+            for (int u = 0; u < R; u++) kw_red[((wave * TC + tt) * R + u) * 64 + lane] = acc[t0 + tt][u];
+        __syncthreads();
+        if (mode == 0) {
+            // unit j: (tile tt, segment sg, weight tile u, row c16): 4 batch rows of one column
+            for (int j = tid; j < TC * 4 * R * 16; j += 256) {
+                const int c16 = j & 15, u = (j >> 4) % R, sg = (j / (16 * R)) & 3, tt = j / (64 * R);
+                const int e = (tt * R + u) * 64 + sg * 16 + c16;
+                f32x4 v = kw_red[e];
+#pragma unroll
+                for (int w = 1; w < KW_WAVES; w++) v += kw_red[w * TC * R * 64 + e];
+                const int n = n0 + 16 * u + c16;
+                if (n < N) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int m = m0 + 16 * (t0 + tt) + 4 * sg + r;
+                        if (m < M) {
+                            const size_t o = (size_t)m * N + n;
+                            dst[o] = add ? v[r] + add[o] : v[r];
+                        }
+                    }
+                }
+            }
+        } else {
+            // unit j: (tile tt, segment sg, weight tile u, pair p): the gate row
+            // 16u + 2p and the up row 16u + 2p + 1 of 4 batch rows
+            for (int j = tid; j < TC * 4 * R * 8; j += 256) {
+                const int p = j & 7, u = (j >> 3) % R, sg = (j / (8 * R)) & 3, tt = j / (32 * R);
+                const int e = (tt * R + u) * 64 + sg * 16 + 2 * p;
+                f32x4 g = kw_red[e], up = kw_red[e + 1];
+#pragma unroll
+                for (int w = 1; w < KW_WAVES; w++) {
+                    g += kw_red[w * TC * R * 64 + e];
+                    up += kw_red[w * TC * R * 64 + e + 1];
+                }
+                const int c = (n0 + 16 * u) / 2 + p;
+                if (2 * c < N) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const int m = m0 + 16 * (t0 + tt) + 4 * sg + r;
+                        if (m < M) {
+                            const size_t o = (size_t)m * F2 + c;
+                            split_bf16(silu_gate(g[r], up[r]), &act_hi[o], &act_lo[o]);
+                        }
+                    }
+                }
+            }
+        }
+    }
+}
+
 // Y = sum_{s < S} part[s] (+ add), in split order.
 __global__ __launch_bounds__(256) void qgemm_reduce_kernel(const float* __restrict__ part, int S, size_t MN, float* Y,
                                                            const float* add) {
@@ -835,6 +1048,7 @@ int launch_reduce_slices(const float* part, int S, size_t MN, float* Y, const fl
 struct QgPlan {
     int WM, WN, TM, TN, KC, MW, NW, ntiles, mchunks, S, bps;
     bool pipe;  // qgemm_pipe_kernel (tile-major weights, batch tiles over 32 rows)
+    int kwR, kwT;  // kwR > 0: qgemm_kw_kernel<FMT, kwR, kwT> (tile-major weights)
     int skG;    // > 0: stream-K over skG workgroups (pipelined kernel only); S = the slices a tile may need
     size_t ws_bytes;
 };
@@ -847,6 +1061,8 @@ static int g_qg_pipe = 0;    // 1: pipelined kernel for every tiled batch over 3
 static int g_qg_mchunk = 0;  // batch rows per workgroup at most (0: QG_MCHUNK)
 static int g_qg_sched = 0;   // pipelined kernel: 0 automatic (the uniform split), 1 stream-K, 2 uniform split
 static int g_qg_skmin = 0;   // stream-K: quant blocks per workgroup at least (0: 16)
+static int g_qg_kw = 0;      // wave-split kernel: 0 automatic, 1 for every tiled batch over 16 rows, -1 never
+static int g_qg_kwR = 0;     // wave-split kernel: weight tiles per workgroup (0: automatic, else 2, 3 or 4)
 
 static int qg_cu_count() {
     static int n = 0;
@@ -879,6 +1095,61 @@ static void qgemm_stream(QgPlan& p, int nb, int slots) {
     p.S = smax;
 }
 
+// The wave-split kernel for a tiled N x K product of M rows.  Automatic
+// choice (MI355X, Q4_0 and Q8_0 at the Qwen2.5-3B shapes, GEMM + partial sums,
+// graph-timed): batches of 17-32 rows on every shape (Q4 11008 x 2048 14.8 us
+// against 20.8 for the 32-row-chunk kernel, 2048 x 2048 8.3 against 12.2) and
+// of 33-64 rows below 16384 weight rows (11008 x 2048 23.0 against 25.7, 2048 x
+// 11008 22.7 against 28.9); from 65 rows, and for the 22016-row gate/up
+// product at 33-64 rows (42.1 against 37.4), the LDS-shared pipelined kernels,
+// whose X fragments each feed 8 waves (here each wave reads its own: 5x the X
+// bytes per MFMA at 128 rows, 40-83 us against 29-49).
+static bool kw_wanted(int N, int M) {
+    if (g_qg_kw < 0 || (g_qg_pipe != 0 && g_qg_kw == 0)) return false;  // an older form forced
+    if (g_qg_kw > 0) return M > 16;
+    return M > 16 && (M <= 32 || (M <= 64 && N < 16384));
+}
+
+// Wave-split plan: batch tiles T = 2, 4 or 8 (chunks of up to 128 rows),
+// R = 2, 3 or 4 weight tiles per workgroup and S splits of the quant blocks,
+// chosen for the fewest rounds of workgroups (one per CU) x the time of one,
+// modelled as (steps per wave) x (R + 2) + 3R: a step costs its R tiles'
+// MFMAs plus a fixed part (X loads, FMAs), the reduction and stores about 3
+// steps per weight tile (fitted to the measured best R on the Qwen2.5-3B
+// shapes at 32 and 64 rows).  Splits (not with the SwiGLU epilogue, which
+// needs whole sums) fill the CUs when the weight tiles alone do not, keeping
+// at least 8 blocks (2 per wave) per split.
+static void kw_plan(QgPlan& p, int N, int nb, int M, bool whole) {
+    const int ntile16 = (N + 15) / 16, cu = qg_cu_count();
+    p.kwT = M > 64 ? 8 : M > 32 ? 4 : 2;
+    if (g_qg_mchunk) p.kwT = std::max(2, std::min(p.kwT, g_qg_mchunk / 16));
+    p.mchunks = (M + 16 * p.kwT - 1) / (16 * p.kwT);
+    double best = 1e30;
+    for (int R = 2; R <= 4; R++) {  // ties go to the smaller R (fewer registers, two workgroups per CU)
+        if (g_qg_kwR && R != g_qg_kwR) continue;
+        const long long base = (long long)((ntile16 + R - 1) / R) * p.mchunks;
+        int S = 1;
+        if (!whole) {
+            if (g_qg_splits > 0) S = g_qg_splits;
+            else S = (int)std::max(1LL, std::min((long long)cu / base, (long long)nb / 8));
+        }
+        int bps = (nb + S - 1) / S;
+        S = (nb + bps - 1) / bps;
+        const long long rounds = (base * S + cu - 1) / cu;
+        const double cost = (double)rounds * ((double)((bps + KW_WAVES - 1) / KW_WAVES) * (R + 2) + 3 * R);
+        if (cost < best) {
+            best = cost;
+            p.kwR = R;
+            p.S = S;
+            p.bps = bps;
+            p.ntiles = (ntile16 + R - 1) / R;
+        }
+    }
+    p.NW = 16 * p.kwR;
+    p.MW = 16 * p.kwT;
+    p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
+}
+
 // Tile shape and split count for an N x K matrix times M rows.  Batch tiles
 // of more than 32 rows use 2 x WN waves of 64 weight rows each; smaller ones
 // 4 waves of 32 weight rows.  Splits are added (powers of two, at most 64)
@@ -886,6 +1157,10 @@ static void qgemm_stream(QgPlan& p, int nb, int slots) {
 // split keeps at least one ping-pong pair of stages.
 static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
     QgPlan p{};
+    if (tiled && kw_wanted(N, M)) {
+        kw_plan(p, N, K / 32, M, false);
+        return p;
+    }
     int Mc = min(M, g_qg_mchunk ? g_qg_mchunk : QG_MCHUNK);
     const bool pipe = g_qg_pipe == 1 || (g_qg_pipe == 0 && N >= 8192);
     // the narrow form is the default for narrow products at > 64 rows except
@@ -1024,6 +1299,15 @@ int set_qgemm_schedule(int mode, int min_blocks) {
     return QRAF_HIP_OK;
 }
 
+int set_qgemm_kw(int mode, int tiles) {
+    QH_REQUIRE(mode >= -1 && mode <= 1 && (tiles == 0 || (tiles >= 2 && tiles <= 4)), QRAF_HIP_ERR_INVALID,
+               "qgemm kw: mode %d, tiles %d", mode, tiles);
+    g_qg_kw = mode;
+    g_qg_kwR = tiles;
+    bump_tuning_generation();
+    return QRAF_HIP_OK;
+}
+
 int set_qgemm_tuning(int waves, int splits, int pipe, int mchunk) {
     QH_REQUIRE(waves == 0 || waves == 4 || waves == 8, QRAF_HIP_ERR_INVALID, "qgemm tuning: waves %d", waves);
     QH_REQUIRE(mchunk == 0 || mchunk == 16 || mchunk == 32 || mchunk == 64 || mchunk == 128, QRAF_HIP_ERR_INVALID,
@@ -1092,6 +1376,74 @@ int launch_repack_tiles(const void* W, uint32_t dtype, int N, int K, void* dst, 
     return QRAF_HIP_OK;
 }
 
+// One launch of qgemm_kw_kernel<F, R, T>; dynamic LDS beyond 64 KB is opted
+// into once per instantiation.
+template <int F, int R, int T>
+static int kw_attr() {
+    static bool done = false;
+    if (!done) {
+        QH_CHECK_HIP(hipFuncSetAttribute((const void*)qgemm_kw_kernel<F, R, T>,
+                                         hipFuncAttributeMaxDynamicSharedMemorySize, (int)KwGeom<F, R, T>::LDS));
+        done = true;
+    }
+    return QRAF_HIP_OK;
+}
+
+template <int F, int R>
+static int kw_attr_t() {
+    QH_TRY((kw_attr<F, R, 2>()));
+    QH_TRY((kw_attr<F, R, 4>()));
+    return kw_attr<F, R, 8>();
+}
+
+// Called by qraf_hip_init (the first launch of each form also does it), so
+// that no attribute call happens while a caller captures a graph.
+int qgemm_kw_init() {
+    QH_TRY((kw_attr_t<4, 2>()));
+    QH_TRY((kw_attr_t<4, 3>()));
+    QH_TRY((kw_attr_t<4, 4>()));
+    QH_TRY((kw_attr_t<8, 2>()));
+    QH_TRY((kw_attr_t<8, 3>()));
+    return kw_attr_t<8, 4>();
+}
+
+template <int F, int R, int T>
+static int kw_go(dim3 grid, const uint8_t* W, int N, int nb, const uint16_t* xh, const uint16_t* xl, int K, int M,
+                 int bps, float* Y, const float* add, size_t slice, int mode, uint16_t* act_hi, uint16_t* act_lo,
+                 hipStream_t s) {
+    constexpr size_t lds = KwGeom<F, R, T>::LDS;
+    QH_TRY((kw_attr<F, R, T>()));
+    hipLaunchKernelGGL((qgemm_kw_kernel<F, R, T>), grid, dim3(64 * KW_WAVES), lds, s, W, N, nb, xh, xl, K, M, bps, Y,
+                       add, slice, mode, act_hi, act_lo);
+    return QRAF_HIP_OK;
+}
+
+// qgemm_kw_kernel<FMT, p.kwR, p.kwT> (mode 0: Y / partial slices, 1: SwiGLU planes).
+static int launch_kw(uint32_t dtype, const QgPlan& p, dim3 grid, const uint8_t* W, int N, int nb, const uint16_t* xh,
+                     const uint16_t* xl, int K, int M, float* Y, const float* add, size_t slice, int mode,
+                     uint16_t* act_hi, uint16_t* act_lo, hipStream_t s) {
+#define QH_KW(F, R_, T_) \
+    QH_TRY((kw_go<F, R_, T_>(grid, W, N, nb, xh, xl, K, M, p.bps, Y, add, slice, mode, act_hi, act_lo, s)))
+#define QH_KWT(F, R_)                       \
+    if (p.kwT == 2) { QH_KW(F, R_, 2); }      \
+    else if (p.kwT == 4) { QH_KW(F, R_, 4); } \
+    else { QH_KW(F, R_, 8); }
+#define QH_KWR(F)                   \
+    if (p.kwR == 2) { QH_KWT(F, 2) }      \
+    else if (p.kwR == 3) { QH_KWT(F, 3) } \
+    else { QH_KWT(F, 4) }
+    if (dtype == DT_Q8_0) {
+        QH_KWR(8)
+    } else {
+        QH_KWR(4)
+    }
+#undef QH_KWR
+#undef QH_KWT
+#undef QH_KW
+    QH_CHECK_HIP(hipGetLastError());
+    return QRAF_HIP_OK;
+}
+
 int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
                  float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled, int* slices) {
     QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "qgemm: unsupported dtype %u", dtype);
@@ -1120,13 +1472,18 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
         } else {  // no (or too small a) workspace: one split
             p.S = 1;
             p.skG = 0;
-            const int unit = (p.pipe ? 1 : 2) * p.KC;
+            const int unit = p.kwR ? 1 : (p.pipe ? 1 : 2) * p.KC;
             p.bps = (nb + unit - 1) / unit * unit;
         }
     }
     QH_REQUIRE(p.mchunks <= 65535, QRAF_HIP_ERR_INVALID, "qgemm: batch %d too large", M);
     const dim3 grid = p.skG > 0 ? dim3(p.skG, 1, 1) : dim3(p.ntiles, p.S, p.mchunks);
-    if (p.pipe) {
+    if (p.kwR) {
+        float* yk = part ? part : Y;
+        const size_t slice = part ? (size_t)M * N : 0;
+        QH_TRY(launch_kw(dtype, p, grid, (const uint8_t*)W, N, nb, xh, xl, K, M, yk, part ? nullptr : add, slice, 0,
+                         nullptr, nullptr, s));
+    } else if (p.pipe) {
 #define QH_P(F, TM_, TN_, WN_, WM_)                                                                        \
     do {                                                                                                  \
     if (p.skG > 0)                                                                                        \
@@ -1207,6 +1564,13 @@ int launch_qgemm_silu(const void* Wt, uint32_t dtype, int N, int K, const uint16
     QH_REQUIRE(((((uintptr_t)Wt) | ((uintptr_t)xh) | ((uintptr_t)xl)) & 15) == 0, QRAF_HIP_ERR_INVALID,
                "qgemm silu: misaligned operands");
     const int nb = K / 32, KC = 2;
+    if (kw_wanted(N, M)) {
+        QgPlan p{};
+        kw_plan(p, N, nb, M, true);
+        QH_REQUIRE(p.mchunks <= 65535, QRAF_HIP_ERR_INVALID, "qgemm silu: batch %d too large", M);
+        return launch_kw(dtype, p, dim3(p.ntiles, 1, p.mchunks), (const uint8_t*)Wt, N, nb, xh, xl, K, M, nullptr,
+                         nullptr, 0, 1, act_hi, act_lo, s);
+    }
     const dim3 grid((N + 127) / 128, 1, (M + 63) / 64);
     QH_REQUIRE(grid.z <= 65535, QRAF_HIP_ERR_INVALID, "qgemm silu: batch %d too large", M);
     const int bps = (nb + KC - 1) / KC * KC;
@@ -1245,6 +1609,11 @@ int qraf_hip_set_qgemm_schedule(int32_t mode, int32_t min_blocks) {
 int qraf_hip_set_qgemm_tuning(int waves, int splits, int pipe, int batch_chunk) {
     qraf_hip::clear_error();
     return qraf_hip::set_qgemm_tuning(waves, splits, pipe, batch_chunk);
+}
+
+int qraf_hip_set_qgemm_kw(int32_t mode, int32_t tiles_per_workgroup) {
+    qraf_hip::clear_error();
+    return qraf_hip::set_qgemm_kw(mode, tiles_per_workgroup);
 }
 
 uint64_t qraf_hip_qgemm_workspace_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim, int32_t batch) {

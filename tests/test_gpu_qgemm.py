@@ -89,14 +89,85 @@ def test_qgemm_vs_oracle(hip, dt, case):
     check(Y, wq, dt, N, K, X)
     Y1, _, _ = run_gemm(hip, wq, dt, N, K, X, split=False)  # one split, no workspace
     check(Y1, wq, dt, N, K, X)
-    # tile-major weights: up to 32 rows the same kernel and split, bit for bit;
-    # larger batches run the pipelined kernel (own tiling and split)
+    # tile-major weights: up to 16 rows the same kernel and split, bit for bit;
+    # larger batches run the wave-split or the pipelined kernel (own tiling and split)
     Yt, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, repeats=2)
     check(Yt, wq, dt, N, K, X)
-    if M <= 32:
+    if M <= 16:
         assert np.array_equal(Yt.view(np.uint32), Y.view(np.uint32))
     Yt1, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
     check(Yt1, wq, dt, N, K, X)
+
+
+C3_SHAPES = [(2048, 2048), (256, 2048), (11008, 2048), (2048, 11008)]
+
+
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("shape", C3_SHAPES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("M", [8, 32, 64, 128])
+def test_qgemm_c3_grid(hip, dt, shape, M):
+    """The whole batched-GEMM grid of the benchmark: Qwen2.5-3B projection
+    shapes at 8, 32, 64 and 128 activation rows, Q8_0 and Q4_0, through the
+    tile-major path the engine uses (its automatic kernel and split choice,
+    with the split-K workspace), against the oracle; repeated calls
+    bit-identical."""
+    N, K = shape
+    print(f"qgemm C3 dt={dt} N={N} K={K} M={M}", flush=True)
+    rng = np.random.default_rng(11 * N + K + M + dt)
+    wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, repeats=2)
+    check(Y, wq, dt, N, K, X)
+
+
+KW_CASES = [
+    # (N, K, batch): ragged tile groups, batch tiles and wave shares of the blocks
+    (2048, 2048, 128), (11008, 2048, 32), (2048, 11008, 64), (2560, 2048, 17), (300, 512, 64), (1000, 576, 100),
+    (513, 1024, 200), (100, 96, 33), (22016, 2048, 48),
+]
+
+
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("case", KW_CASES, ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("tiles", [0, 2, 3, 4])
+def test_qgemm_wave_split_kernel(hip, dt, case, tiles):
+    """The wave-split tiled kernel (qraf_hip_set_qgemm_kw) forced on for every
+    shape with 2, 3 or 4 weight tiles per workgroup or its automatic choice:
+    the 4 waves' shares of the quant blocks (3 to 86 blocks a wave, shares
+    that differ by one, waves without blocks when a split holds fewer than 4),
+    batch tiles past the rows and weight tiles past the matrix, with split-K
+    partials and without, against the oracle and bit-identical over repeats."""
+    N, K, M = case
+    rng = np.random.default_rng(3 * N + K + 7 * M + dt)
+    wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    call = hip._lib.call
+    call("qraf_hip_set_qgemm_kw", 1, tiles)
+    try:
+        Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, repeats=2)
+        Y1, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
+    finally:
+        call("qraf_hip_set_qgemm_kw", 0, 0)
+    check(Y, wq, dt, N, K, X)
+    check(Y1, wq, dt, N, K, X)
+
+
+@pytest.mark.parametrize("in_place", [True, False])
+@pytest.mark.parametrize("split", [True, False])
+def test_qgemm_wave_split_residual(hip, split, in_place):
+    """The wave-split kernel's residual epilogue (y = W x + add, add == y in
+    place) in the single-split form and through the split-K reduction."""
+    rng = np.random.default_rng(9)
+    N, K, M = 2048, 2048, 40
+    wq = po.quantize(po.Q4_0, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    add = rng.standard_normal((M, N)).astype(np.float32)
+    hip._lib.call("qraf_hip_set_qgemm_kw", 1, 0)
+    try:
+        Y, _, _ = run_gemm(hip, wq, po.Q4_0, N, K, X, add, split=split, in_place=in_place, tiled=True)
+    finally:
+        hip._lib.call("qraf_hip_set_qgemm_kw", 0, 0)
+    check(Y, wq, po.Q4_0, N, K, X, add)
 
 
 def tile_major_reference(wq, dt, N, K):
@@ -227,27 +298,24 @@ def test_qgemm_stream_k_plan(hip):
 
 @pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
 @pytest.mark.parametrize("case", [(2 * 1536, 576, 128), (2 * 11008, 2048, 128), (2 * 300, 1024, 70),
-                                  (2 * 11008, 2048, 200), (2 * 64, 64, 33)], ids=lambda c: "x".join(map(str, c)))
-def test_qgemm_tiled_silu_epilogue(hip, dt, case):
-    """qraf_hip_qgemm_tiled_silu_dev: rows 2i (gate) and 2i+1 (up) summed by
-    the pipelined kernel unsplit, the epilogue writing silu(g) * u as hi/lo
-    planes.  The plain tiled GEMM forced into the same form (narrow, 64-row
-    chunks, one split) gives the same sums bit for bit, which are checked
-    against the oracle; the planes must hold silu_gate of those sums to the
-    planes' own precision (2^-20 relative + 2^-25) plus a few ulp of expf."""
+                                  (2 * 11008, 2048, 200), (2 * 64, 64, 33), (2 * 11008, 2048, 32)],
+                         ids=lambda c: "x".join(map(str, c)))
+@pytest.mark.parametrize("form", ["pipelined", "wave_split"])
+def test_qgemm_tiled_silu_epilogue(hip, dt, case, form):
+    """qraf_hip_qgemm_tiled_silu_dev: rows 2i (gate) and 2i+1 (up) summed
+    unsplit by the pipelined kernel (narrow form, 64-row chunks) or the
+    wave-split kernel, the epilogue writing silu(g) * u as hi/lo planes.  The
+    plain tiled GEMM forced into the same form with one split gives the same
+    sums bit for bit, which are checked against the oracle; the planes must
+    hold silu_gate of those sums to the planes' own precision (2^-20 relative
+    + 2^-25) plus a few ulp of expf."""
     from qraf_amd.backend import DeviceBuffer
     N, K, M = case
-    print(f"qgemm tiled silu dt={dt} N={N} K={K} M={M}", flush=True)
+    print(f"qgemm tiled silu dt={dt} N={N} K={K} M={M} {form}", flush=True)
     rng = np.random.default_rng(N + 5 * K + M)
     wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
     X = rng.standard_normal((M, K)).astype(np.float32)
     call, lib = hip._lib.call, hip._lib.lib
-    call("qraf_hip_set_qgemm_tuning", 0, 1, 2, 0)
-    try:
-        Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
-    finally:
-        call("qraf_hip_set_qgemm_tuning", 0, 0, 0, 0)
-    check(Y, wq, dt, N, K, X)
     F = N // 2
     dw, dx = DeviceBuffer.from_array(wq), DeviceBuffer.from_array(X)
     dtl = DeviceBuffer(lib.qraf_hip_tiled_weight_bytes(dt, N, K))
@@ -255,8 +323,22 @@ def test_qgemm_tiled_silu_epilogue(hip, dt, case):
     dh, dl = DeviceBuffer(M * K * 2), DeviceBuffer(M * K * 2)
     call("qraf_hip_split_bf16_dev", dx.ptr, dh.ptr, dl.ptr, M, K, None)
     oh, ol = DeviceBuffer(M * F * 2), DeviceBuffer(M * F * 2)
-    call("qraf_hip_qgemm_tiled_silu_dev", dtl.ptr, dt, N, K, dh.ptr, dl.ptr, M, oh.ptr, ol.ptr, None)
-    call("qraf_hip_stream_synchronize", None)
+    if form == "pipelined":
+        call("qraf_hip_set_qgemm_tuning", 0, 1, 2, 0)
+    else:
+        call("qraf_hip_set_qgemm_tuning", 0, 1, 0, 0)
+        call("qraf_hip_set_qgemm_kw", 1, 0)
+    try:
+        Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
+        if form == "pipelined":  # the epilogue entry's own automatic choice is this form at these shapes
+            call("qraf_hip_set_qgemm_tuning", 0, 0, 0, 0)
+            call("qraf_hip_set_qgemm_kw", -1, 0)
+        call("qraf_hip_qgemm_tiled_silu_dev", dtl.ptr, dt, N, K, dh.ptr, dl.ptr, M, oh.ptr, ol.ptr, None)
+        call("qraf_hip_stream_synchronize", None)
+    finally:
+        call("qraf_hip_set_qgemm_tuning", 0, 0, 0, 0)
+        call("qraf_hip_set_qgemm_kw", 0, 0)
+    check(Y, wq, dt, N, K, X)
     hi = oh.download(np.uint16, M * F).reshape(M, F)
     lo = ol.download(np.uint16, M * F).reshape(M, F)
     g, u = Y[:, 0::2].astype(np.float64), Y[:, 1::2].astype(np.float64)
