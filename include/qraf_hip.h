@@ -315,38 +315,6 @@ int qraf_hip_qgemm_tiled_silu_dev(const void* w_tiled, uint32_t dtype, uint32_t 
                                   const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, uint16_t* out_hi,
                                   uint16_t* out_lo, void* stream);
 
-/* MFMA-ready ("mx") copy of a Q8_0/Q4_0 matrix (block size 32) for large
- * batches, where the product is bound by the matrix cores rather than by
- * weight bytes: per quant block b and 16-row tile t, 576 bytes at
- * (b * ceil(out_dim / 16) + t) * 576 holding the 16 block scales
- * as fp32, then 8 bytes per (k segment s, row r) at 64 + (16 s + r) * 8 holding
- * elements k = 8 s .. 8 s + 7 of row r: the int8 quants (Q8_0) or the fp8
- * e4m3 codes of nibble - 8 (Q4_0; integers -8..7 are exact).  Twice the bytes
- * of Q4_0, the same as Q8_0; rows past out_dim are zero.  No counterpart in
- * the reference (a layout of the same values). */
-uint64_t qraf_hip_mx_weight_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim);
-int qraf_hip_repack_mx_dev(const void* w, uint32_t dtype, uint32_t out_dim, uint32_t in_dim, void* dst, void* stream);
-/* qraf_hip_qgemm_dev (dispatch_matvec_q, backend.cpp:131-199, for `batch`
- * rows) on an mx copy (16-byte aligned), same arithmetic and error bound;
- * workspace of qraf_hip_qgemm_mx_workspace_bytes bytes (16-byte aligned)
- * enables split-K, NULL runs one split. */
-uint64_t qraf_hip_qgemm_mx_workspace_bytes(uint32_t dtype, uint32_t out_dim, uint32_t in_dim, int32_t batch);
-int qraf_hip_qgemm_mx_dev(const void* w_mx, uint32_t dtype, uint32_t out_dim, uint32_t in_dim, const uint16_t* x_hi,
-                          const uint16_t* x_lo, int32_t batch, float* y, const float* add, void* workspace,
-                          uint64_t workspace_bytes, void* stream);
-/* The SwiGLU front of mlp_forward (attention.cpp:172-178) for a weight whose
- * rows interleave the gate and up projections (row 2i = gate_i, row 2i+1 =
- * up_i, out_dim = 2F): act[m][i] = silu(gate) * up, written as the hi/lo
- * planes out_hi/out_lo [batch][F] that the down projection's GEMM reads
- * (qraf_hip_split_bf16_dev form).  One split; no workspace. */
-int qraf_hip_qgemm_mx_silu_dev(const void* w_mx, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
-                               const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, uint16_t* out_hi,
-                               uint16_t* out_lo, void* stream);
-/* Tuning of the mx GEMM (process-wide): shape -1 automatic, 0..3 forces the
- * workgroup tile (128x256, 64x256, 128x192, 64x192 batch x weight rows);
- * splits > 0 forces the split count.  No counterpart in the reference. */
-int qraf_hip_set_mx_tuning(int32_t shape, int32_t splits);
-
 /* ------------------------------------------------------------- engine */
 
 /* The model hyper-parameters the reference reads from the QRAF config block

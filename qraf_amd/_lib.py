@@ -85,13 +85,6 @@ SIGNATURES = {
     "qraf_hip_qgemm_workspace_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32]),
     "qraf_hip_qgemm_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp,
                                      vp, C.c_uint64, vp]),
-    "qraf_hip_mx_weight_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32, C.c_uint32]),
-    "qraf_hip_repack_mx_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
-    "qraf_hip_qgemm_mx_workspace_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32]),
-    "qraf_hip_qgemm_mx_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp, vp,
-                                        C.c_uint64, vp]),
-    "qraf_hip_qgemm_mx_silu_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp, vp]),
-    "qraf_hip_set_mx_tuning": (C.c_int, [C.c_int32, C.c_int32]),
     "qraf_hip_rope_table_host": (C.c_int, [C.c_int32, C.c_int32, C.c_float, fp]),
     "qraf_hip_rope_append_dev": (C.c_int, [vp, vp] + [C.c_int32] * 4 + [vp, vp, vp, vp, vp, C.c_uint32, vp,
                                                                        C.c_int32, C.c_int32, vp]),

@@ -47,11 +47,6 @@ def build(verbose: bool = True) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{r.stderr[-6000:]}")
     os.replace(tmp, OUT)
-    for src in sorted(glob.glob(os.path.join(PKG, "probes", "*.hip"))):  # standalone measurement programs
-        exe = src[:-4]
-        r = subprocess.run([HIPCC, *[f for f in FLAGS if f != "-fPIC"], "-o", exe, src], capture_output=True, text=True)
-        if r.returncode != 0:
-            raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr[-6000:]}")
     if verbose:
         print(f"built {OUT} from {len(srcs)} sources")
     return OUT

@@ -201,14 +201,6 @@ size_t tiled_weight_bytes(uint32_t dtype, int N, int K);
 int launch_repack_tiles(const void* W, uint32_t dtype, int N, int K, void* dst, hipStream_t s);
 // Y = sum of S slices [S][MN] (+ add), in slice order
 int launch_reduce_slices(const float* part, int S, size_t MN, float* Y, const float* add, hipStream_t s);
-// MFMA-ready ("mx") weight copy and the large-batch GEMM on it (qgemm_mx.hip)
-size_t mx_weight_bytes(uint32_t dtype, int N, int K);
-int launch_repack_mx(const void* W, uint32_t dtype, int N, int K, void* dst, hipStream_t s);
-size_t qgemm_mx_partials_bytes(uint32_t dtype, int N, int K, int M);
-int launch_qgemm_mx(const void* W, uint32_t dtype, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
-                    float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, int* slices,
-                    uint16_t* silu_hi, uint16_t* silu_lo);
-int set_mx_tuning(int shape, int splits);
 size_t attn_workspace_bytes(int n, int H, int Hkv, int hd, int max_ctx);
 // resolves the device address of the no-allocation attention workspace on
 // `device` (current); called once per device by qraf_hip_init
