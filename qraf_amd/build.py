@@ -2,8 +2,10 @@
 
     python qraf_amd/build.py          # or __graft_entry__.build()
 
-Every csrc/*.hip file is compiled to an object in parallel and the objects
-are linked into qraf_amd/libqraf_hip.so.  Packed-FP32 instruction selection
+Every csrc/*.hip file is compiled to an object by hipcc and every csrc/*.cpp
+file (host-only code: the .qraf parser, status text) by the host C++
+compiler, in parallel, and the objects are linked into
+qraf_amd/libqraf_hip.so.  Packed-FP32 instruction selection
 is disabled for all device code (-target-feature -packed-fp32-ops), and no
 multiply-add is contracted into an FMA unless the source asks for one
 (-ffp-contract=off): unfused products round like the reference's scalar code.
@@ -28,9 +30,16 @@ FLAGS = ["-O3", "-std=c++17", "-fPIC", "-ffp-contract=off", f"--offload-arch={AR
          "-Xclang", "-packed-fp32-ops", "-Wno-unused-command-line-argument", "-I", os.path.join(ROOT, "include")]
 
 
+CXX = os.environ.get("CXX", "g++")
+CXXFLAGS = ["-O3", "-std=c++17", "-fPIC", "-Wall", "-I", os.path.join(ROOT, "include")]
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(OBJ, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    if src.endswith(".cpp"):  # host-only sources (no HIP): the plain C++ compiler
+        cmd = [CXX, *CXXFLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stderr[-6000:]}")
@@ -39,7 +48,7 @@ def _compile(src: str) -> str:
 
 def build(verbose: bool = True) -> str:
     os.makedirs(OBJ, exist_ok=True)
-    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")))
+    srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.cpp")))
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(_compile, srcs))
     tmp = OUT + ".tmp"

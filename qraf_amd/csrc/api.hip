@@ -13,17 +13,6 @@
 
 namespace qraf_hip {
 
-static thread_local char g_err[512] = "";
-
-int set_error(int code, const char* fmt, ...) {
-    va_list ap;
-    va_start(ap, fmt);
-    vsnprintf(g_err, sizeof(g_err), fmt, ap);
-    va_end(ap);
-    return code;
-}
-void clear_error() { g_err[0] = 0; }
-
 // Per-process device state.  One default stream per device the library was
 // initialised on; op-level calls serialise on g_mu (the reference's dispatch
 // layer is single-threaded as well, backend.cpp:16).
@@ -87,7 +76,6 @@ using namespace qraf_hip;
 
 extern "C" {
 
-const char* qraf_hip_last_error(void) { return g_err; }
 
 const char* qraf_hip_version(void) { return "gfx950 " __VERSION__; }
 

@@ -8,15 +8,13 @@
 #include <string>
 
 #include "../../include/qraf_hip.h"
+#include "status.h"
 
 namespace qraf_hip {
 
 // QRAF dtype codes (reference include/core/types.h:27-39).
 constexpr uint32_t DT_F32 = 0, DT_F16 = 1, DT_Q8_0 = 10, DT_Q4_0 = 20, DT_I8 = 102;  // types.h:27-38
 
-// Sets the calling thread's last-error string and returns `code`.
-int set_error(int code, const char* fmt, ...);
-void clear_error();
 
 #define QH_CHECK_HIP(expr)                                                              \
     do {                                                                                \
@@ -26,17 +24,6 @@ void clear_error();
                                          hipGetErrorString(e_), __FILE__, __LINE__);     \
     } while (0)
 
-#define QH_REQUIRE(cond, code, ...)                                  \
-    do {                                                             \
-        if (!(cond)) return ::qraf_hip::set_error(code, __VA_ARGS__); \
-    } while (0)
-
-// Propagates a failed status (the error text is already set).
-#define QH_TRY(expr)                        \
-    do {                                    \
-        int rc_ = (expr);                   \
-        if (rc_ != QRAF_HIP_OK) return rc_; \
-    } while (0)
 
 // Bytes of one quantized block (reference quantize.cpp:107, :146).
 __host__ __device__ inline size_t q_block_bytes(uint32_t dtype, int bs) {
