@@ -404,6 +404,13 @@ def smol_bytes_per_token(ctx):
     return L * layer + V * row_bytes(Q8, D) + int(ctx * L * 2 * kvd * 4)
 
 
+def c1_prompt():
+    """The batch-1 workload's prompt: 32 tokens uniform over the vocabulary,
+    numpy's default generator seeded with 1; the GPU legs and the reference's
+    CPU leg decode this same prompt."""
+    return np.random.default_rng(1).integers(0, SMOL["vocab"], 32).tolist()
+
+
 def bench_decode_b1(args, rt):
     from qraf_amd.engine import Engine, model_config
     cfg = model_config(*(SMOL[k] for k in ("vocab", "hidden", "layers", "heads", "kv_heads", "inter", "max_seq",
@@ -413,7 +420,7 @@ def bench_decode_b1(args, rt):
     e.generate_weights(Q8, Q8, Q8, False, False, 1)
     e.finalize()
     e.set_graphs(not args.no_graphs)
-    prompt = np.random.default_rng(1).integers(0, SMOL["vocab"], 32).tolist()
+    prompt = c1_prompt()
     n_gen = 128
 
     def run(batched_prefill=False, pipeline=True):
@@ -467,6 +474,7 @@ def bench_decode_b1(args, rt):
     out_p = ie.generate_tokens(prompt, n_gen, repetition_penalty=1.1)
     el_p = time.perf_counter() - t0
     e.close()
+    rt["c1_tokens"] = toks
     return {"model": "SmolLM2-135M architecture, Q8_0 weights, f32 KV pages, random init", "prompt": len(prompt),
             "generated": n_gen, "decode_tok_s": round(steps / dec, 1), "ms_per_token": round(dec / steps * 1e3, 3),
             "pipelined": True,
@@ -483,10 +491,14 @@ def bench_decode_b1(args, rt):
                                            "sampler call per token after its step"}}
 
 
-def cpu_decode_b1(n_prompt=32, n_tokens=128):
+def cpu_decode_b1(gpu_tokens=None, n_tokens=128):
     """SmolLM2-135M-architecture Q8 decode with the reference's own
-    InferenceEngine (oracle/_ref) on this host, the whole C1 run: a 32-token
-    prompt fed token by token, then 128 greedy tokens (about 15 s of one core)."""
+    InferenceEngine (oracle/_ref) on this host, the whole C1 run: the GPU
+    legs' 32-token prompt fed token by token, then 128 greedy tokens (about
+    15 s of one core), on the same weights (seed 1).  With the GPU leg's
+    stream: whether it equals the reference's, the first position where they
+    differ and the reference's own top-2 logit gap there (its forward replayed
+    along its own stream)."""
     import tempfile
     from oracle import pyoracle as po
     if po.ref() is None:
@@ -496,14 +508,31 @@ def cpu_decode_b1(n_prompt=32, n_tokens=128):
     m.write_qraf(path)
     m.close()
     eng = po.RefEngine(path)
-    prompt = [po.lib().or_gen_token(1, i, SMOL["vocab"]) for i in range(n_prompt)]
+    prompt = c1_prompt()
     toks, ms = eng.generate(prompt, n_tokens, 1.0)
     eng.close()
+    out = {"value": round(len(toks) / (ms / 1e3), 3),
+           "unit": "tok/s, generated / (prefill + decode) as inference.cpp:150-153 reports", "cores": 1,
+           "kind": "reference", "sample": f"{len(prompt)}-token prompt + {len(toks)} greedy tokens via "
+                                          f"InferenceEngine::generate_tokens, {ms / 1e3:.1f} s, host CPU {host_cpu()}"}
+    if gpu_tokens is not None:
+        same = list(gpu_tokens) == list(toks)
+        cmp = {"same_tokens_as_reference": same, "tokens_compared": len(toks),
+               "same_first_32": list(gpu_tokens[:32]) == list(toks[:32])}
+        if not same:
+            d = next((i for i in range(min(len(toks), len(gpu_tokens))) if toks[i] != gpu_tokens[i]),
+                     min(len(toks), len(gpu_tokens)))
+            rm = po.RefModel(path, SMOL["vocab"])
+            lg = None
+            for i, t in enumerate(prompt + toks[:d]):
+                lg = rm.forward(t, i)
+            rm.close()
+            s2 = np.sort(lg)
+            cmp.update({"first_divergence": d, "reference_top2_gap_there": float(s2[-1] - s2[-2]),
+                        "reference_top_logit_there": float(s2[-1])})
+        out["stream_check"] = cmp
     os.remove(path)
-    return {"value": round(len(toks) / (ms / 1e3), 3),
-            "unit": "tok/s, generated / (prefill + decode) as inference.cpp:150-153 reports", "cores": 1,
-            "kind": "reference", "sample": f"{n_prompt}-token prompt + {len(toks)} greedy tokens via "
-                                           f"InferenceEngine::generate_tokens, {ms / 1e3:.1f} s, host CPU {host_cpu()}"}
+    return out
 
 
 # --------------------------------------------------------------------------- decode, batch 128
@@ -969,7 +998,10 @@ def main():
     if not args.no_cpu:
         cpu = cpu_baseline_matvec(hosts, args.cpu_seconds)
         if "decode_b1" in only:
-            extra["cpu_decode_b1"] = cpu_decode_b1()
+            extra["cpu_decode_b1"] = cpu_decode_b1(rt.get("c1_tokens"))
+            chk = (extra["cpu_decode_b1"] or {}).get("stream_check")
+            if chk and "decode_b1" in extra:
+                extra["decode_b1"]["same_tokens_as_reference"] = chk["same_tokens_as_reference"]
         if "sampler" in only:
             extra["cpu_sampler"] = cpu_sampler()
         if "decode_b128" in only:
