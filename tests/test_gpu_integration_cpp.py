@@ -19,6 +19,7 @@ pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("reference")]
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "tests", "cpp", "integration_test")
+BATCH_BIN = os.path.join(ROOT, "tests", "cpp", "batch_integration_test")
 
 
 @pytest.mark.parametrize("name,tokens", [("q8_llama", 24), ("q4_qwen2_tied_bias", 24), ("q8_hd64_gqa3", 12)])
@@ -33,6 +34,32 @@ def test_reference_bindings_compiled_against_reference_headers(hip, tmp_path, na
     m.close()
     print(f"integration_test {name} tokens={tokens}", flush=True)
     r = subprocess.run([BIN, path, str(tokens)], capture_output=True, text=True, timeout=120)
+    print(r.stdout)
+    assert r.returncode == 0, f"exit {r.returncode}\n{r.stdout}\n{r.stderr[-2000:]}"
+    assert r.stdout.strip().endswith("PASS")
+
+
+@pytest.mark.parametrize("name,requests,seed", [("q4_qwen2_tied_bias", 24, 5), ("q8_hd64_gqa3", 24, 6),
+                                                ("q4_gqa8_hd128", 16, 7)])
+def test_batch_scheduler_binding_against_reference(hip, tmp_path, name, requests, seed):
+    """tests/cpp/batch_integration_test: HipBatchScheduler (the reference
+    BatchScheduler's interface over qraf_engine_step_async / _step_collect,
+    compiled against runtime/batch_scheduler.h) runs ragged requests with
+    admission into 6 slots and a 32-row budget; every stream equals the
+    reference Transformer's decode of that request alone, pipelined and with
+    every logit row read back, the logits of the first 32 tokens within
+    1e-3/1e-4.  The same binary checks the elementwise Backend::HIP branches
+    against the reference's dispatch_* functions."""
+    from tests.test_gpu_engine import SMALL
+    if not os.path.exists(BATCH_BIN):
+        pytest.fail(f"{BATCH_BIN} is missing; build it with `make -C tests/cpp` (needs the reference checkout)")
+    kw, mseed = SMALL[name]
+    m = po.Model(po.make_config(**kw), mseed)
+    path = str(tmp_path / "m.qraf")
+    m.write_qraf(path)
+    m.close()
+    print(f"batch_integration_test {name} requests={requests} seed={seed}", flush=True)
+    r = subprocess.run([BATCH_BIN, path, str(requests), str(seed)], capture_output=True, text=True, timeout=150)
     print(r.stdout)
     assert r.returncode == 0, f"exit {r.returncode}\n{r.stdout}\n{r.stderr[-2000:]}"
     assert r.stdout.strip().endswith("PASS")
