@@ -795,6 +795,226 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
 }
 
 // ---------------------------------------------------------------------------
+// Row-split GEMM with LDS-shared activations (qgemm_kx_kernel): tile-major
+// weights, 128-row batch chunks.
+//
+// A workgroup (4 waves) owns 4R weight tiles (64R rows) x 16T batch rows over
+// a range of quant blocks; wave w computes tiles 4R.. of its own R tiles for
+// all 16T batch rows, so each X fragment it reads feeds R weight tiles and
+// each converted weight fragment T batch tiles.  X and the weights come
+// through a 3-stage LDS ring filled by direct-to-LDS loads, KC quant blocks a
+// stage: X fragment-major (one 1 KB load instruction = one 16x32 fragment of
+// one plane, lane l's 16 bytes at lane offset 16 l, so the MFMA operand reads
+// are conflict-free without a swizzle), the 4R tile-blocks of each block in
+// the tile-major order.  One barrier per stage, after the wave's own loads of
+// the stage have landed; stages c+1 and c+2 stay in flight while c computes.
+// Epilogue as the other tiled kernels: Y (+ add), a partial slice, or the
+// SwiGLU front of interleaved gate/up rows.
+// ---------------------------------------------------------------------------
+template <int FMT, int R, int T, int KC>
+struct KxGeom {
+    static constexpr int TB = tile_block_bytes(FMT);
+    static constexpr int SB = FMT == 8 ? 4 : 2, QB = FMT == 8 ? 32 : 16;
+    static constexpr int XI = KC * 2 * T;               // X load instructions per stage (1 KB each)
+    static constexpr int XW = XI / 4;                   // ... per wave
+    static constexpr int WBYTES = KC * 4 * R * TB;      // weight bytes per stage
+    static constexpr int WI = (WBYTES + 1023) / 1024;   // weight load instructions per stage
+    static constexpr int WL = WI / 4, WEXTRA = WI % 4;  // waves < WEXTRA issue WL + 1
+    static constexpr int XBYTES = XI * 1024;
+    static constexpr int STAGE = XBYTES + WI * 1024;
+    static_assert(XI % 4 == 0, "X stage must split evenly over the 4 waves");
+};
+constexpr int KX_STAGE_MAX = 24576;  // Q8_0, R = 3, T = 8, KC = 1: 16 KB of X + 7 KB of weights
+__shared__ __align__(16) uint8_t kx_s0[KX_STAGE_MAX];
+__shared__ __align__(16) uint8_t kx_s1[KX_STAGE_MAX];
+__shared__ __align__(16) uint8_t kx_s2[KX_STAGE_MAX];
+template <int B>
+__device__ __forceinline__ uint8_t* kx_stage() {
+    return B == 0 ? kx_s0 : B == 1 ? kx_s1 : kx_s2;
+}
+
+// part != nullptr: split-K partial slice blockIdx.y of [S][M][N]; act_hi: SwiGLU planes (one split)
+template <int FMT, int R, int T, int KC>
+__global__ __launch_bounds__(256, 2) void qgemm_kx_kernel(const uint8_t* __restrict__ Wt, int N, int nb,
+                                                          const uint16_t* __restrict__ xh,
+                                                          const uint16_t* __restrict__ xl, int K, int M, float* Y,
+                                                          const float* add, int bps, float* __restrict__ part,
+                                                          uint16_t* __restrict__ act_hi,
+                                                          uint16_t* __restrict__ act_lo) {
+    using G = KxGeom<FMT, R, T, KC>;
+    static_assert(G::STAGE <= KX_STAGE_MAX, "stage buffer too small");
+    static_assert(T % 2 == 0, "the result ring alternates between two batch tiles");
+    constexpr int TB = G::TB;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int seg = lane >> 4, l16 = lane & 15;
+    const int ntile16 = (N + 15) / 16;
+    const int n0 = blockIdx.x * 64 * R, m0 = blockIdx.z * 16 * T;
+    const int b_begin = blockIdx.y * bps, b_end = min(nb, b_begin + bps);
+    const bool wextra = wave < G::WEXTRA;
+    const uint32_t xbytes = (uint32_t)((size_t)M * K * 2);
+    const v4i xrs[2] = {make_rsrc_words(xh, xbytes), make_rsrc_words(xl, xbytes)};
+    const v4i wrs = make_rsrc_words(Wt, (uint32_t)min((size_t)ntile16 * nb * TB, (size_t)0xFFFFFFFFu));
+
+    // per-lane source offsets of this wave's load instructions (a stage's first
+    // block adds cb * 64 (X) or cb * TB (weights))
+    uint32_t xo[G::XW];
+#pragma unroll
+    for (int i = 0; i < G::XW; i++) {
+        const int q = wave + 4 * i;  // ((kc * 2 + plane) * T + t)
+        const int t = q % T, kc = q / (2 * T);
+        const int row = min(m0 + 16 * t + l16, M - 1);
+        xo[i] = (uint32_t)((size_t)row * K * 2) + 64u * kc + 16u * seg;
+    }
+    uint32_t wo[G::WL + 1];
+#pragma unroll
+    for (int i = 0; i <= G::WL; i++) {
+        const int f = min((wave + 4 * i) * 1024 + 16 * lane, G::WBYTES - 16);  // bytes past the stage re-read the last piece
+        const int kc = f / (4 * R * TB), rem = f % (4 * R * TB);
+        const int j = rem / TB, off = rem % TB;
+        const int tile = min((int)blockIdx.x * 4 * R + j, ntile16 - 1);
+        wo[i] = (uint32_t)((size_t)tile * nb * TB) + (uint32_t)(kc * TB + off);
+    }
+    auto issue = [&](auto bsel, int c) {
+        uint8_t* buf = kx_stage<decltype(bsel)::value>();
+        const int cb = min(b_begin + c * KC, b_end - 1);  // stages past the range re-read a valid block
+#pragma unroll
+        for (int i = 0; i < G::XW; i++) {
+            const int q = wave + 4 * i;
+            const int plane = (q / T) & 1;  // wave-uniform
+            dma16(xrs[plane], xo[i] + (uint32_t)cb * 64u, buf + q * 1024);
+        }
+#pragma unroll
+        for (int i = 0; i < G::WL; i++) dma16(wrs, wo[i] + (uint32_t)cb * TB, buf + G::XBYTES + (wave + 4 * i) * 1024);
+        if (G::WEXTRA && wextra)
+            dma16(wrs, wo[G::WL] + (uint32_t)cb * TB, buf + G::XBYTES + (wave + 4 * G::WL) * 1024);
+    };
+    // this wave's loads of the oldest stage in flight have landed (one stage may remain outstanding)
+    auto wait_stage = [&]() {
+        if (wextra) wait_vm_lgkm0<G::XW + G::WL + 1>();
+        else wait_vm_lgkm0<G::XW + G::WL>();
+    };
+
+    f32x4 acc[T][R];
+#pragma unroll
+    for (int t = 0; t < T; t++)
+#pragma unroll
+        for (int u = 0; u < R; u++) acc[t][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 dR[2][R];  // MFMA results of the previous and current batch tile
+    float sP[R];     // scales of the previous block (its last tile is pending when a block starts)
+#pragma unroll
+    for (int u = 0; u < R; u++) {
+        dR[0][u] = dR[1][u] = f32x4{0.f, 0.f, 0.f, 0.f};
+        sP[u] = 0.f;
+    }
+    auto compute = [&](auto bsel, int c) {
+        const uint8_t* buf = kx_stage<decltype(bsel)::value>();
+        const int cb = b_begin + c * KC;
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) {
+            if (cb + kc >= b_end) break;  // uniform: past the split's range (stage padding)
+            bf16x8 wf[R];
+            f16x8 wh[R];
+            float sc[R];
+#pragma unroll
+            for (int u = 0; u < R; u++) {
+                const uint8_t* tb = buf + G::XBYTES + (kc * 4 * R + wave * R + u) * TB;
+                WRaw<FMT> r;
+                if (FMT == 8) {
+                    r.scale = *(const uint32_t*)(tb + 4 * l16);
+                    const uint2 q = *(const uint2*)(tb + 64 + 32 * l16 + 8 * seg);
+                    reinterpret_cast<uint32_t*>(&r)[1] = q.x;
+                    reinterpret_cast<uint32_t*>(&r)[2] = q.y;
+                } else {
+                    r.scale = *(const uint16_t*)(tb + 2 * l16);
+                    reinterpret_cast<uint32_t*>(&r)[1] = *(const uint32_t*)(tb + 32 + 16 * l16 + 4 * seg);
+                }
+                convert<FMT>(r, wf[u], wh[u], sc[u]);
+            }
+            const uint8_t* xa = buf + (kc * 2 * T) * 1024 + 16 * lane;
+#pragma unroll
+            for (int t = 0; t < T; t++) {
+                const bf16x8 ah = *(const bf16x8*)(xa + t * 1024);
+                const f16x8 al = *(const f16x8*)(xa + (T + t) * 1024);
+                const int q = t & 1, pq = q ^ 1;
+                const int pt = t > 0 ? t - 1 : T - 1;
+#pragma unroll
+                for (int u = 0; u < R; u++) {
+                    const f32x4 d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, wf[u], f32x4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
+                    dR[q][u] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, wh[u], d, 0, 0, 0);
+                }
+#pragma unroll
+                for (int u = 0; u < R; u++) {
+                    const float ps = t > 0 ? sc[u] : sP[u];
+#pragma unroll
+                    for (int r = 0; r < 4; r++) acc[pt][u][r] = __builtin_fmaf(dR[pq][u][r], ps, acc[pt][u][r]);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < R; u++) sP[u] = sc[u];
+        }
+    };
+
+    const int nstages = ((b_end - b_begin + KC - 1) / KC + 2) / 3 * 3;  // whole trips of the 3-stage loop
+    using B0 = std::integral_constant<int, 0>;
+    using B1 = std::integral_constant<int, 1>;
+    using B2 = std::integral_constant<int, 2>;
+    issue(B0{}, 0);
+    issue(B1{}, 1);
+    for (int c = 0; c < nstages; c += 3) {
+        wait_stage();
+        lds_barrier();
+        issue(B2{}, c + 2);
+        compute(B0{}, c);
+        wait_stage();
+        lds_barrier();
+        issue(B0{}, c + 3);
+        compute(B1{}, c + 1);
+        wait_stage();
+        lds_barrier();
+        issue(B1{}, c + 4);
+        compute(B2{}, c + 2);
+    }
+    wait_vm_lgkm0<0>();  // drain the past-the-end stages before any other memory access
+#pragma unroll
+    for (int u = 0; u < R; u++)  // the last block's last tile
+#pragma unroll
+        for (int r = 0; r < 4; r++) acc[T - 1][u][r] = __builtin_fmaf(dR[(T - 1) & 1][u][r], sP[u], acc[T - 1][u][r]);
+
+    const int nw = n0 + wave * R * 16;  // this wave's first weight row
+    if (act_hi) {
+        // SwiGLU front (mlp_forward, attention.cpp:172-178) on interleaved rows
+        // (2i = gate_i, 2i+1 = up_i): the two lanes of a pair exchange their 4
+        // sums; the even lane writes batch rows 0, 1 of its 4, the odd lane 2, 3
+        const int F2 = N >> 1;
+        const bool odd = l16 & 1;
+#pragma unroll
+        for (int t = 0; t < T; t++) {
+#pragma unroll
+            for (int u = 0; u < R; u++) {
+                const int n2 = (nw + u * 16 + l16) >> 1;
+                float pv[4];
+#pragma unroll
+                for (int r = 0; r < 4; r++) pv[r] = __shfl_xor(acc[t][u][r], 1);
+#pragma unroll
+                for (int k = 0; k < 2; k++) {
+                    const float g = odd ? pv[2 + k] : acc[t][u][k];
+                    const float up = odd ? acc[t][u][2 + k] : pv[k];
+                    const int m = m0 + t * 16 + seg * 4 + (odd ? 2 + k : k);
+                    if (m < M && 2 * n2 < N) {
+                        const size_t e = (size_t)m * F2 + n2;
+                        split_bf16(silu_gate(g, up), &act_hi[e], &act_lo[e]);
+                    }
+                }
+            }
+        }
+        return;
+    }
+    float* dst = part ? part + (size_t)blockIdx.y * M * N : Y;
+    store_tiles<T, R>(acc, dst, part ? nullptr : add, M, N, m0, nw, seg, l16);
+}
+
+// ---------------------------------------------------------------------------
 // Wave-split GEMM for tile-major weights (qgemm_kw_kernel): batches of up to
 // 128 rows per workgroup.
 //
@@ -1049,6 +1269,7 @@ struct QgPlan {
     int WM, WN, TM, TN, KC, MW, NW, ntiles, mchunks, S, bps;
     bool pipe;  // qgemm_pipe_kernel (tile-major weights, batch tiles over 32 rows)
     int kwR, kwT;  // kwR > 0: qgemm_kw_kernel<FMT, kwR, kwT> (tile-major weights)
+    int kxT;       // > 0: qgemm_kx_kernel<FMT, 3, kxT, 1> (tile-major weights)
     int skG;    // > 0: stream-K over skG workgroups (pipelined kernel only); S = the slices a tile may need
     size_t ws_bytes;
 };
@@ -1155,8 +1376,47 @@ static void kw_plan(QgPlan& p, int N, int nb, int M, bool whole) {
 // 4 waves of 32 weight rows.  Splits are added (powers of two, at most 64)
 // while the grid has fewer workgroups than the chip has slots for and every
 // split keeps at least one ping-pong pair of stages.
-static QgPlan qgemm_plan(int N, int K, int M, size_t row_bytes, bool tiled) {
+// Row-split LDS-shared plan (qgemm_kx_kernel, 3 weight tiles per wave):
+// batch chunks of 128 (64) rows, S splits of the quant blocks so that the
+// grid holds at least one workgroup per CU, at least 8 blocks per split.
+static void kx_plan(QgPlan& p, int N, int nb, int M, bool whole) {
+    const int ntile16 = (N + 15) / 16, cu = qg_cu_count();
+    p.kxT = M > 64 ? 8 : 4;
+    p.MW = 16 * p.kxT;
+    p.NW = 64 * 3;
+    p.mchunks = (M + p.MW - 1) / p.MW;
+    p.ntiles = (ntile16 + 11) / 12;
+    const long long base = (long long)p.ntiles * p.mchunks;
+    int S = 1;
+    if (!whole) {
+        if (g_qg_splits > 0) S = g_qg_splits;
+        else S = (int)std::max(1LL, std::min((cu + base - 1) / base, (long long)nb / 8));
+    }
+    p.bps = (nb + S - 1) / S;
+    p.S = (nb + p.bps - 1) / p.bps;
+    p.ws_bytes = p.S > 1 ? (size_t)p.S * M * N * 4 : 0;
+}
+
+// The row-split LDS-shared kernel where it measured faster than the other
+// forms (MI355X, tiled, GEMM + partial sums, graph-timed): 33-64 rows on
+// products of 16384 rows and more (Q4 22016 x 2048 at 64 rows 29.9 us against
+// 38.3 for the pipelined kernel and 42.1 for the wave-split one), and Q8_0
+// products with a long in_dim from 65 rows (2048 x 11008 at 128 / 256 rows
+// 34.1 / 54.9 against 41.8 / 65.2); the SwiGLU-epilogue entry from 256 rows
+// (22016 x 2048 at 256 rows: Q4 78.7 against 84.7, Q8 81.1 against 122.7).
+// At 128 rows on the Q4 shapes it ties or trails the pipelined kernel.
+static bool kx_wanted(uint32_t dtype, int N, int K, int M) {
+    if (g_qg_pipe == 3) return M > 16;
+    if (g_qg_pipe != 0 || g_qg_kw != 0) return false;
+    return (M > 32 && M <= 64 && N >= 16384) || (M > 64 && dtype == DT_Q8_0 && K >= 8192);
+}
+
+static QgPlan qgemm_plan(uint32_t dtype, int N, int K, int M, size_t row_bytes, bool tiled) {
     QgPlan p{};
+    if (tiled && kx_wanted(dtype, N, K, M)) {
+        kx_plan(p, N, K / 32, M, false);
+        return p;
+    }
     if (tiled && kw_wanted(N, M)) {
         kw_plan(p, N, K / 32, M, false);
         return p;
@@ -1313,7 +1573,7 @@ int set_qgemm_tuning(int waves, int splits, int pipe, int mchunk) {
     QH_REQUIRE(mchunk == 0 || mchunk == 16 || mchunk == 32 || mchunk == 64 || mchunk == 128, QRAF_HIP_ERR_INVALID,
                "qgemm tuning: batch chunk %d", mchunk);
     QH_REQUIRE(splits >= 0 && splits <= 256, QRAF_HIP_ERR_INVALID, "qgemm tuning: splits %d", splits);
-    QH_REQUIRE(pipe >= -1 && pipe <= 2, QRAF_HIP_ERR_INVALID, "qgemm tuning: pipe %d", pipe);
+    QH_REQUIRE(pipe >= -1 && pipe <= 3, QRAF_HIP_ERR_INVALID, "qgemm tuning: pipe %d", pipe);
     g_qg_waves = waves;
     g_qg_splits = splits;
     g_qg_pipe = pipe;
@@ -1324,12 +1584,12 @@ int set_qgemm_tuning(int waves, int splits, int pipe, int mchunk) {
 
 size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M, bool tiled) {
     if ((dtype != DT_Q8_0 && dtype != DT_Q4_0) || N <= 0 || K <= 0 || K % 32 || M <= 0) return 0;
-    return qgemm_plan(N, K, M, q_row_bytes(dtype, 32, K), tiled).ws_bytes;
+    return qgemm_plan(dtype, N, K, M, q_row_bytes(dtype, 32, K), tiled).ws_bytes;
 }
 
 size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M, bool tiled) {
     if ((dtype != DT_Q8_0 && dtype != DT_Q4_0) || N <= 0 || K <= 0 || K % 32 || M <= 0) return 0;
-    return (size_t)qgemm_plan(N, K, M, q_row_bytes(dtype, 32, K), tiled).S * M * N * 4;
+    return (size_t)qgemm_plan(dtype, N, K, M, q_row_bytes(dtype, 32, K), tiled).S * M * N * 4;
 }
 
 int launch_split_bf16(const float* x, uint16_t* hi, uint16_t* lo, int M, int K, int op, float* xout, hipStream_t s,
@@ -1458,7 +1718,7 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
                QRAF_HIP_ERR_INVALID, "qgemm: misaligned operands");
     const size_t rb = q_row_bytes(dtype, bs, K);
     const int nb = K / 32;
-    QgPlan p = qgemm_plan(N, K, M, rb, tiled);
+    QgPlan p = qgemm_plan(dtype, N, K, M, rb, tiled);
     float* part = nullptr;
     if (slices) {  // partials mode: S slices [S][M][N] in ws, summed by the caller's next kernel
         QH_REQUIRE(ws && ws_bytes >= (size_t)p.S * M * N * 4 && (((uintptr_t)ws) & 15) == 0 && !add,
@@ -1472,13 +1732,25 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
         } else {  // no (or too small a) workspace: one split
             p.S = 1;
             p.skG = 0;
-            const int unit = p.kwR ? 1 : (p.pipe ? 1 : 2) * p.KC;
+            const int unit = (p.kwR || p.kxT) ? 1 : (p.pipe ? 1 : 2) * p.KC;
             p.bps = (nb + unit - 1) / unit * unit;
         }
     }
     QH_REQUIRE(p.mchunks <= 65535, QRAF_HIP_ERR_INVALID, "qgemm: batch %d too large", M);
     const dim3 grid = p.skG > 0 ? dim3(p.skG, 1, 1) : dim3(p.ntiles, p.S, p.mchunks);
-    if (p.kwR) {
+    if (p.kxT) {
+#define QH_KX(F, T_)                                                                                          \
+    hipLaunchKernelGGL((qgemm_kx_kernel<F, 3, T_, 1>), grid, dim3(256), 0, s, (const uint8_t*)W, N, nb, xh, xl, K, M, \
+                       Y, add, p.bps, part, nullptr, nullptr)
+        if (dtype == DT_Q8_0) {
+            if (p.kxT == 8) QH_KX(8, 8);
+            else QH_KX(8, 4);
+        } else {
+            if (p.kxT == 8) QH_KX(4, 8);
+            else QH_KX(4, 4);
+        }
+#undef QH_KX
+    } else if (p.kwR) {
         float* yk = part ? part : Y;
         const size_t slice = part ? (size_t)M * N : 0;
         QH_TRY(launch_kw(dtype, p, grid, (const uint8_t*)W, N, nb, xh, xl, K, M, yk, part ? nullptr : add, slice, 0,
@@ -1564,6 +1836,25 @@ int launch_qgemm_silu(const void* Wt, uint32_t dtype, int N, int K, const uint16
     QH_REQUIRE(((((uintptr_t)Wt) | ((uintptr_t)xh) | ((uintptr_t)xl)) & 15) == 0, QRAF_HIP_ERR_INVALID,
                "qgemm silu: misaligned operands");
     const int nb = K / 32, KC = 2;
+    if (g_qg_pipe == 3 ? M > 16 : (g_qg_pipe == 0 && g_qg_kw == 0 && M >= 256)) {
+        QgPlan p{};
+        kx_plan(p, N, nb, M, true);
+        QH_REQUIRE(p.mchunks <= 65535, QRAF_HIP_ERR_INVALID, "qgemm silu: batch %d too large", M);
+        const dim3 g(p.ntiles, 1, p.mchunks);
+#define QH_KXS(F, T_)                                                                                            \
+    hipLaunchKernelGGL((qgemm_kx_kernel<F, 3, T_, 1>), g, dim3(256), 0, s, (const uint8_t*)Wt, N, nb, xh, xl, K, M, \
+                       nullptr, nullptr, nb, nullptr, act_hi, act_lo)
+        if (dtype == DT_Q8_0) {
+            if (p.kxT == 8) QH_KXS(8, 8);
+            else QH_KXS(8, 4);
+        } else {
+            if (p.kxT == 8) QH_KXS(4, 8);
+            else QH_KXS(4, 4);
+        }
+#undef QH_KXS
+        QH_CHECK_HIP(hipGetLastError());
+        return QRAF_HIP_OK;
+    }
     if (kw_wanted(N, M)) {
         QgPlan p{};
         kw_plan(p, N, nb, M, true);

@@ -152,6 +152,31 @@ def test_qgemm_wave_split_kernel(hip, dt, case, tiles):
     check(Y1, wq, dt, N, K, X)
 
 
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("case", KW_CASES + [(15000, 512, 128), (2048, 11008, 256)],
+                         ids=lambda c: "x".join(map(str, c)))
+def test_qgemm_row_split_kernel(hip, dt, case):
+    """The row-split tiled kernel with LDS-shared activations (forced on
+    through qraf_hip_set_qgemm_tuning's pipe = 3): 192 weight rows per
+    workgroup in 4 waves of 48, 64- or 128-row batch chunks, a 3-stage ring
+    of direct-to-LDS loads (workgroups past the weight tiles, batch tiles past
+    the rows, the last stage trip padded), with split-K partials and without,
+    against the oracle and bit-identical over repeats."""
+    N, K, M = case
+    rng = np.random.default_rng(5 * N + K + 3 * M + dt)
+    wq = po.quantize(dt, (rng.standard_normal(N * K) * 0.02).astype(np.float32))
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    call = hip._lib.call
+    call("qraf_hip_set_qgemm_tuning", 0, 0, 3, 0)
+    try:
+        Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, repeats=2)
+        Y1, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
+    finally:
+        call("qraf_hip_set_qgemm_tuning", 0, 0, 0, 0)
+    check(Y, wq, dt, N, K, X)
+    check(Y1, wq, dt, N, K, X)
+
+
 @pytest.mark.parametrize("in_place", [True, False])
 @pytest.mark.parametrize("split", [True, False])
 def test_qgemm_wave_split_residual(hip, split, in_place):
@@ -300,13 +325,13 @@ def test_qgemm_stream_k_plan(hip):
 @pytest.mark.parametrize("case", [(2 * 1536, 576, 128), (2 * 11008, 2048, 128), (2 * 300, 1024, 70),
                                   (2 * 11008, 2048, 200), (2 * 64, 64, 33), (2 * 11008, 2048, 32)],
                          ids=lambda c: "x".join(map(str, c)))
-@pytest.mark.parametrize("form", ["pipelined", "wave_split"])
+@pytest.mark.parametrize("form", ["pipelined", "wave_split", "row_split"])
 def test_qgemm_tiled_silu_epilogue(hip, dt, case, form):
     """qraf_hip_qgemm_tiled_silu_dev: rows 2i (gate) and 2i+1 (up) summed
     unsplit by the pipelined kernel (narrow form, 64-row chunks) or the
     wave-split kernel, the epilogue writing silu(g) * u as hi/lo planes.  The
     plain tiled GEMM forced into the same form with one split gives the same
-    sums bit for bit, which are checked against the oracle; the planes must
+    sums bit for bit (the row-split kernel, pipe = 3, as a third form), which are checked against the oracle; the planes must
     hold silu_gate of those sums to the planes' own precision (2^-20 relative
     + 2^-25) plus a few ulp of expf."""
     from qraf_amd.backend import DeviceBuffer
@@ -325,6 +350,8 @@ def test_qgemm_tiled_silu_epilogue(hip, dt, case, form):
     oh, ol = DeviceBuffer(M * F * 2), DeviceBuffer(M * F * 2)
     if form == "pipelined":
         call("qraf_hip_set_qgemm_tuning", 0, 1, 2, 0)
+    elif form == "row_split":
+        call("qraf_hip_set_qgemm_tuning", 0, 1, 3, 0)
     else:
         call("qraf_hip_set_qgemm_tuning", 0, 1, 0, 0)
         call("qraf_hip_set_qgemm_kw", 1, 0)
