@@ -955,6 +955,8 @@ def main():
     ap.add_argument("--wgs-per-cu", type=int, default=0)
     ap.add_argument("--row-padding", type=int, default=16,
                     help="batched engine steps of more than 8 rows run padded to a multiple of this (1: off)")
+    ap.add_argument("--gemm-form", default="auto", choices=["auto", "pipelined", "wave_split", "row_split"],
+                    help="tiled batched-GEMM form for every leg (auto: the library's per-shape choice)")
     ap.add_argument("--attn-form", type=int, default=0,
                     help="attention work form for every leg: 0 auto, 1 chunk grid, 2 balanced split, 3 VALU kernel")
     args = ap.parse_args()
@@ -971,6 +973,12 @@ def main():
     qraf_amd.backend.backend_init(0)
     call("qraf_hip_set_matvec_tuning", args.kernel, args.rows_per_wave, args.wgs_per_cu)
     call("qraf_hip_set_attention_tuning", args.attn_form)
+    if args.gemm_form == "pipelined":  # the LDS-ring kernels everywhere over 32 rows
+        call("qraf_hip_set_qgemm_kw", -1, 0)
+    elif args.gemm_form == "wave_split":
+        call("qraf_hip_set_qgemm_kw", 1, 0)
+    elif args.gemm_form == "row_split":
+        call("qraf_hip_set_qgemm_tuning", 0, 0, 3, 0)
     rt = dict(call=call, DeviceBuffer=DeviceBuffer, Event=Event, Graph=Graph, stream=Stream(), lib=qraf_amd.lib,
               eager=args.no_graphs, attn_form=args.attn_form)
 
@@ -993,7 +1001,11 @@ def main():
                 if traffic else None,
                 "kernel": kname,
                 "case": dom["case"], "alg_bytes_per_launch": dom["alg_bytes"],
-                "plain_read_GB_s": dom.get("plain_read_GB_s"), "frac_of_plain_read": dom.get("frac_of_plain_read")}
+                "plain_read_GB_s": dom.get("plain_read_GB_s"), "frac_of_plain_read": dom.get("frac_of_plain_read"),
+                # every case of the step in brief: [case, us per launch, GB/s, fraction of HBM peak,
+                # fraction of the same-size plain read]
+                "per_case": [[p["case"], p["us_per_launch"], p["GB_s"], p["frac_hbm_peak"], p.get("frac_of_plain_read")]
+                             for p in per_case]}
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline_matvec(hosts, args.cpu_seconds)

@@ -949,6 +949,16 @@ __global__ __launch_bounds__(256, 2) void qgemm_kx_kernel(const uint8_t* __restr
 #pragma unroll
                     for (int r = 0; r < 4; r++) acc[pt][u][r] = __builtin_fmaf(dR[pq][u][r], ps, acc[pt][u][r]);
                 }
+                // issue order of the tile: its X fragment reads, then each of its
+                // 2R MFMAs followed by two of the pending tile's 4R scale FMAs, so
+                // the wave's VALU work runs in the shadow of its own MFMAs
+                __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+#pragma unroll
+                for (int i = 0; i < 2 * R; i++) {
+                    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+                    __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);
+                }
+                __builtin_amdgcn_sched_barrier(0);
             }
 #pragma unroll
             for (int u = 0; u < R; u++) sP[u] = sc[u];
