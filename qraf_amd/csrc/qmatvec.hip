@@ -12,12 +12,13 @@
 // and loads each unit with two dwordx4 loads + one dword (4-byte aligned),
 // so a wave reads 2304 contiguous bytes per row step.  The activation vector
 // is staged once per workgroup in LDS, padded to 36 floats per 32-element
-// block (16-byte aligned, free of bank conflicts for ds_read_b128), and for
-// Q4 permuted inside each 8-element group to match the even/odd nibble split.
+// block (16-byte aligned, free of bank conflicts for ds_read_b128), for Q4
+// with every odd element pre-scaled by 1/16 (see q4_compute).
 // Dequantisation happens in registers: v_cvt_f32_i32 with an SDWA byte select
-// for Q8, v_cvt_f32_ubyteN of a 0x0F0F0F0F-masked dword for Q4 (the -8 offset
-// is applied once per block through the staged block sum).  Accumulation is
-// fp32; each wave reduces its R rows with a transposing butterfly.
+// for Q8; for Q4 one mask per two nibbles and v_fma_mix_f32, which reads the
+// masked nibble as an fp16 subnormal (the -8 offset is applied once per block
+// through the staged block sum).  Accumulation is fp32; each wave reduces its
+// R rows with a transposing butterfly.
 #include "common.h"
 
 #include <atomic>
@@ -35,12 +36,17 @@ __device__ __forceinline__ float half_bits_to_float(uint32_t h) {
     return (float)__builtin_bit_cast(_Float16, (uint16_t)(h & 0xFFFFu));
 }
 
-// Q4 staging position of element e (0..31) of a block: inside each group of 8,
-// even elements first, then odd ones.
-__device__ __forceinline__ int q4_slot(int e) {
-    int g = e >> 3, o = e & 7;
-    return g * 8 + ((o & 1) ? 4 + (o >> 1) : (o >> 1));
+// Q4 staging of x: elements in order, odd ones times 1/16 (exact: a power of
+// two).  q4_compute reads nibble pairs as fp16 subnormals: masking a dword of
+// 8 nibbles with 0x000F000F leaves elements 0 and 4 as n * 2^-24 in its two
+// halves, with 0x00F000F0 elements 1 and 5 as 16n * 2^-24, and the same masks
+// of the dword shifted right by 8 give elements 2/6 and 3/7.  With the odd
+// elements' x staged as x / 16 every product is n * x * 2^-24 exactly.
+__device__ __forceinline__ f32x4 q4_stage4(float a, float b, float c, float d) {
+    return f32x4{a, b * 0.0625f, c, d * 0.0625f};
 }
+__device__ __forceinline__ float half_lo(uint32_t t) { return (float)__builtin_bit_cast(_Float16, (uint16_t)t); }
+__device__ __forceinline__ float half_hi(uint32_t t) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(t >> 16)); }
 
 // Sum over the 64 lanes for each of R accumulators.  On return lanes with
 // (lane & (64/R - 1)) == 0 hold the total of row `*row` in acc[0].
@@ -117,6 +123,23 @@ __device__ __forceinline__ void q8_compute(const Units<R>& w, const float* xs, f
     }
 }
 
+// The nibbles of one dword (elements 8k..8k+7 of a block) as the four masked
+// dwords q4_compute multiplies: halves (e0, e4), (16 e1, 16 e5), (e2, e6),
+// (16 e3, 16 e7), each an fp16 subnormal of value half * 2^-24.
+__device__ __forceinline__ void q4_split(uint32_t d, uint32_t (&t)[4]) {
+    const uint32_t u = d >> 8;
+    t[0] = d & 0x000F000Fu;
+    t[1] = d & 0x00F000F0u;
+    t[2] = u & 0x000F000Fu;
+    t[3] = u & 0x00F000F0u;
+}
+
+// Block sums of the unit's two blocks: every product is n * x * 2^-24 (exact
+// inside the fma), so be and bo are the sums of n * x scaled by 2^-24 -- the
+// same roundings, as binary scaling commutes with them while values stay
+// normal -- and the -8 offset and the block scale are applied at that scale
+// (8 * sum * 2^-24 = sum * 2^-21; scale * 2^24), so acc gets the unscaled
+// arithmetic's value.
 template <int R>
 __device__ __forceinline__ void q4_compute(const Units<R>& w, const float* xu, float (&acc)[R]) {
     f32x4 xe[8], xo[8];
@@ -125,7 +148,7 @@ __device__ __forceinline__ void q4_compute(const Units<R>& w, const float* xu, f
         xe[j] = ((const f32x4*)xu)[j];
         xo[j] = ((const f32x4*)(xu + 36))[j];
     }
-    const float se8 = 8.f * xu[32], so8 = 8.f * xu[36 + 32];
+    const float se8 = 0x1p-21f * xu[32], so8 = 0x1p-21f * xu[36 + 32];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         // unit dwords: s = 0, a = 1..4, b = 5..8
@@ -135,20 +158,21 @@ __device__ __forceinline__ void q4_compute(const Units<R>& w, const float* xu, f
         float be = 0.f, bo = 0.f;
 #pragma unroll
         for (int k = 0; k < 4; k++) {
-            uint32_t ne = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2);  // even block, nibble bytes 4k..4k+3
-            uint32_t no = dw[5 + k];                                         // odd block, nibble bytes 4k..4k+3
-            uint32_t elo = ne & 0x0F0F0F0Fu, ehi = (ne >> 4) & 0x0F0F0F0Fu;
-            uint32_t olo = no & 0x0F0F0F0Fu, ohi = (no >> 4) & 0x0F0F0F0Fu;
-            asm volatile("" : "+v"(elo), "+v"(ehi), "+v"(olo), "+v"(ohi));  // keep v_cvt_f32_ubyteN selection
+            uint32_t te[4], to[4];
+            q4_split(__builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2), te);  // even block, nibble bytes 4k..4k+3
+            q4_split(dw[5 + k], to);                                         // odd block, nibble bytes 4k..4k+3
 #pragma unroll
             for (int q = 0; q < 4; q++) {
-                be = __builtin_fmaf((float)((elo >> (8 * q)) & 0xFFu), xe[2 * k][q], be);
-                be = __builtin_fmaf((float)((ehi >> (8 * q)) & 0xFFu), xe[2 * k + 1][q], be);
-                bo = __builtin_fmaf((float)((olo >> (8 * q)) & 0xFFu), xo[2 * k][q], bo);
-                bo = __builtin_fmaf((float)((ohi >> (8 * q)) & 0xFFu), xo[2 * k + 1][q], bo);
+                be = __builtin_fmaf(half_lo(te[q]), xe[2 * k][q], be);
+                bo = __builtin_fmaf(half_lo(to[q]), xo[2 * k][q], bo);
+            }
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                be = __builtin_fmaf(half_hi(te[q]), xe[2 * k + 1][q], be);
+                bo = __builtin_fmaf(half_hi(to[q]), xo[2 * k + 1][q], bo);
             }
         }
-        const float se = half_bits_to_float(dw[0]), so = half_bits_to_float(dw[4] >> 16);
+        const float se = half_bits_to_float(dw[0]) * 0x1p24f, so = half_bits_to_float(dw[4] >> 16) * 0x1p24f;
         acc[r] = __builtin_fmaf(be - se8, se, acc[r]);
         acc[r] = __builtin_fmaf(bo - so8, so, acc[r]);
     }
@@ -209,8 +233,8 @@ __device__ __forceinline__ void stage_x(float* sx, const float* __restrict__ x, 
             *(f32x4*)(sx + (i >> 5) * XS8 + (i & 31)) = v;
         }
     } else {
-        // thread t stages elements 8t..8t+7 (even ones then odd ones) and the
-        // four threads of a block reduce its sum.  Keff drops the odd tail
+        // thread t stages elements 8t..8t+7 (odd ones scaled, q4_stage4) and
+        // the four threads of a block reduce its sum.  Keff drops the odd tail
         // element the reference never reads (quantize.cpp:227).
         const int Keff = K & ~1;
         const int nthr = nb * 4;  // 8 elements per thread
@@ -232,8 +256,8 @@ __device__ __forceinline__ void stage_x(float* sx, const float* __restrict__ x, 
             if (t < nthr) {
                 const int blk = i >> 5, g = (i & 31) >> 3;
                 float* dst = sx + (blk >> 1) * XS4 + (blk & 1) * 36;
-                *(f32x4*)(dst + g * 8) = f32x4{v[0], v[2], v[4], v[6]};
-                *(f32x4*)(dst + g * 8 + 4) = f32x4{v[1], v[3], v[5], v[7]};
+                *(f32x4*)(dst + g * 8) = q4_stage4(v[0], v[1], v[2], v[3]);
+                *(f32x4*)(dst + g * 8 + 4) = q4_stage4(v[4], v[5], v[6], v[7]);
                 if ((t & 3) == 0) dst[32] = part;
             }
         }
@@ -637,8 +661,8 @@ __global__ __launch_bounds__(64 * NW) void qmv_ring_kernel(const uint8_t* __rest
 #pragma unroll
         for (int k = 0; k < XL; k++) xr[k] = raw[k];
     }
-    // 2. x into LDS (Q8: 36-float blocks; Q4: block pairs, even/odd elements
-    //    permuted, plus block sums), the layout stage_x builds.
+    // 2. x into LDS (Q8: 36-float blocks; Q4: block pairs, odd elements
+    //    scaled, plus block sums), the layout stage_x builds.
     if (FMT == 8) {
         const int spare = nb * XS8;
 #pragma unroll
@@ -659,8 +683,8 @@ __global__ __launch_bounds__(64 * NW) void qmv_ring_kernel(const uint8_t* __rest
             const int blk = g >> 2, gg = g & 3;
             const bool ok = g < (n4 >> 1);
             const int base = ok ? (blk >> 1) * XS4 + (blk & 1) * 36 : spare;
-            *(f32x4*)(sx + base + (ok ? gg * 8 : 0)) = f32x4{a[0], a[2], b[0], b[2]};
-            *(f32x4*)(sx + base + (ok ? gg * 8 + 4 : 4)) = f32x4{a[1], a[3], b[1], b[3]};
+            *(f32x4*)(sx + base + (ok ? gg * 8 : 0)) = q4_stage4(a[0], a[1], a[2], a[3]);
+            *(f32x4*)(sx + base + (ok ? gg * 8 + 4 : 4)) = q4_stage4(b[0], b[1], b[2], b[3]);
             if (gg == 0) sx[base + (ok ? 32 : 8)] = part;
         }
     }
@@ -1209,8 +1233,8 @@ __device__ __forceinline__ void stage_x_batch(float* sx, int S, const float* __r
                     const int v = c / ng, t = c - v * ng, i = 8 * t;
                     const int blk = i >> 5, gg = (i & 31) >> 3;
                     float* dst = sx + v * S + (blk >> 1) * XS4 + (blk & 1) * 36;
-                    *(f32x4*)(dst + gg * 8) = f32x4{v8[0], v8[2], v8[4], v8[6]};
-                    *(f32x4*)(dst + gg * 8 + 4) = f32x4{v8[1], v8[3], v8[5], v8[7]};
+                    *(f32x4*)(dst + gg * 8) = q4_stage4(v8[0], v8[1], v8[2], v8[3]);
+                    *(f32x4*)(dst + gg * 8 + 4) = q4_stage4(v8[4], v8[5], v8[6], v8[7]);
                     if ((t & 3) == 0) dst[32] = part;
                 }
             }
@@ -1276,20 +1300,23 @@ __global__ __launch_bounds__(WG) void qmv_batch_kernel(const uint8_t* __restrict
                 uint32_t dw[9];
 #pragma unroll
                 for (int i = 0; i < 9; i++) dw[i] = dword(w, 0, i);
-                float el[16], eh[16], ol[16], oh[16];  // nibbles of the even and odd block, low and high
+                // the even and odd block's nibbles in element order, as the values
+                // q4_compute multiplies (n * 2^-24, odd elements 16n * 2^-24)
+                float we[32], wo[32];
 #pragma unroll
                 for (int k = 0; k < 4; k++) {
-                    const uint32_t ne = __builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2);
-                    const uint32_t no = dw[5 + k];
+                    uint32_t te[4], to[4];
+                    q4_split(__builtin_amdgcn_alignbyte(dw[k + 1], dw[k], 2), te);
+                    q4_split(dw[5 + k], to);
 #pragma unroll
                     for (int q = 0; q < 4; q++) {
-                        el[4 * k + q] = (float)((ne >> (8 * q)) & 0x0Fu);
-                        eh[4 * k + q] = (float)((ne >> (8 * q + 4)) & 0x0Fu);
-                        ol[4 * k + q] = (float)((no >> (8 * q)) & 0x0Fu);
-                        oh[4 * k + q] = (float)((no >> (8 * q + 4)) & 0x0Fu);
+                        we[8 * k + q] = half_lo(te[q]);
+                        we[8 * k + 4 + q] = half_hi(te[q]);
+                        wo[8 * k + q] = half_lo(to[q]);
+                        wo[8 * k + 4 + q] = half_hi(to[q]);
                     }
                 }
-                const float se = half_bits_to_float(dw[0]), so = half_bits_to_float(dw[4] >> 16);
+                const float se = half_bits_to_float(dw[0]) * 0x1p24f, so = half_bits_to_float(dw[4] >> 16) * 0x1p24f;
 #pragma unroll
                 for (int v = 0; v < NV; v++) {
                     const float* xu = sx + v * S + u * XS4;
@@ -1299,16 +1326,14 @@ __global__ __launch_bounds__(WG) void qmv_batch_kernel(const uint8_t* __restrict
                         xe[j] = ((const f32x4*)xu)[j];
                         xo[j] = ((const f32x4*)(xu + 36))[j];
                     }
-                    const float se8 = 8.f * xu[32], so8 = 8.f * xu[36 + 32];
+                    const float se8 = 0x1p-21f * xu[32], so8 = 0x1p-21f * xu[36 + 32];
                     float be = 0.f, bo = 0.f;
 #pragma unroll
-                    for (int k = 0; k < 4; k++)
+                    for (int j = 0; j < 8; j++)
 #pragma unroll
                         for (int q = 0; q < 4; q++) {
-                            be = __builtin_fmaf(el[4 * k + q], xe[2 * k][q], be);
-                            be = __builtin_fmaf(eh[4 * k + q], xe[2 * k + 1][q], be);
-                            bo = __builtin_fmaf(ol[4 * k + q], xo[2 * k][q], bo);
-                            bo = __builtin_fmaf(oh[4 * k + q], xo[2 * k + 1][q], bo);
+                            be = __builtin_fmaf(we[4 * j + q], xe[j][q], be);
+                            bo = __builtin_fmaf(wo[4 * j + q], xo[j][q], bo);
                         }
                     acc[v] = __builtin_fmaf(be - se8, se, acc[v]);
                     acc[v] = __builtin_fmaf(bo - so8, so, acc[v]);
