@@ -6,11 +6,12 @@ fp32 x ~ N(0,1) of length 4096 and weights N(0, 0.02) quantized to Q8_0 and
 Q4_0, shapes 4096x4096 and 11008x4096, batch 1.  One step = one matvec of
 each of the four (format, shape) cases.  Each case cycles through a pool of
 distinct weight copies larger than the 256 MB Infinity Cache, so every launch
-streams its weights from HBM.  The K timed steps run case by case, each
-case's K launches captured in one HIP graph and bracketed by HIP events on
-the stream they run on; `value` is the total algorithmic bytes of all K steps
-over the total timed time.  Algorithmic bytes per launch = weight bytes +
-4*K (x) + 4*N (y).
+streams its weights from HBM.  The K timed steps are captured in one HIP
+graph (step by step, each step the four launches in order) and bracketed by
+HIP events on the stream they run on; `value` is the total algorithmic bytes
+of all K steps over the timed time.  Per-case figures come from a second
+timing, each case's K launches in a graph of their own between events.
+Algorithmic bytes per launch = weight bytes + 4*K (x) + 4*N (y).
 
 The same JSON line also reports the other configurations of the metric:
   decode_b1    SmolLM2-135M architecture, Q8_0, batch 1: seeded 32-token
@@ -22,6 +23,8 @@ The same JSON line also reports the other configurations of the metric:
                reported beside it with their streams' agreement with the f32
                run
   gemm         batched Q-GEMM, B in {8,32,64,128}, Qwen2.5-3B projection shapes
+  gemm_library (not in the default run) hipBLASLt's bf16 GEMM (torch.mm) at the
+               same shapes: one bf16 product, no dequantisation, a yardstick
   attention    ragged paged decode attention: 128 sequences, context U[128,4096],
                16 q / 2 kv heads, head_dim 128, fp16 K/V
   sampler      the device sampler on 128 rows x 151936 logits (penalty,
@@ -171,6 +174,33 @@ def bench_matvec(args, rt):
         for g in graphs:  # one untimed replay: graph upload stays out of the timed region
             g.launch()
         stream.synchronize()
+    # the K timed steps: one graph of K steps, each step the four matvecs in order
+    step_graph = None
+    if not rt.get("eager"):
+        step_graph = Graph(stream)
+        with step_graph:
+            for i in range(args.steps):
+                for c in cases:
+                    launch(c, args.warmup + i)
+        step_graph.launch()  # untimed: graph upload stays out of the timed region
+        stream.synchronize()
+    e0, e1 = Event(), Event()
+    call("qraf_hip_device_synchronize")
+    e0.record(stream)
+    if step_graph:
+        step_graph.launch()
+    else:
+        for i in range(args.steps):
+            for c in cases:
+                launch(c, args.warmup + i)
+    e1.record(stream)
+    stream.synchronize()
+    call("qraf_hip_device_synchronize")
+    total_ms = e0.elapsed_ms(e1)
+    total_bytes = sum(mv_bytes(c["dt"], c["n"], c["k"]) for c in cases) * args.steps
+    if step_graph:
+        step_graph.destroy()
+    # per case: each case's K launches in a graph of their own, between events
     ev = [Event() for _ in range(len(cases) + 1)]
     call("qraf_hip_device_synchronize")
     ev[0].record(stream)
@@ -183,7 +213,7 @@ def bench_matvec(args, rt):
         ev[i + 1].record(stream)
     stream.synchronize()
     call("qraf_hip_device_synchronize")
-    per_case, total_ms, total_bytes = [], 0.0, 0
+    per_case = []
     for i, c in enumerate(cases):
         ms = ev[i].elapsed_ms(ev[i + 1])
         b = mv_bytes(c["dt"], c["n"], c["k"])
@@ -191,8 +221,6 @@ def bench_matvec(args, rt):
         per_case.append({"case": f"{c['name']} {c['n']}x{c['k']}", "us_per_launch": round(us, 3), "alg_bytes": b,
                          "GB_s": round(b / (us * 1e-6) / 1e9, 1),
                          "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "pool_copies": c["copies"]})
-        total_ms += ms
-        total_bytes += b * args.steps
     for g in graphs:
         g.destroy()
     # plain-read ceiling: a streaming read of the same bytes from the same rotated pool copies
@@ -319,6 +347,63 @@ def bench_gemm(args, rt):
             pool.free()
             tpool.free()
     return out
+
+
+def bench_gemm_library(args, rt):
+    """Yardstick for the tiled Q-GEMM: the platform's tuned bf16 GEMM
+    (torch.mm, which runs hipBLASLt) at the same shapes, y[B,N] = x[B,K] W^T
+    with bf16 W[N,K] in the weights' row-major layout: ONE bf16 product per
+    output (the Q-GEMM issues two, hi and lo planes), no dequantisation, 2 bytes
+    per weight (Q4_0: 0.5625).  Weights rotate through >320 MB so they stream
+    from HBM; 20 calls captured in one torch CUDA graph, one replay timed with
+    events (the results are not read).  Not in the default run.  Measured in a
+    child process: torch's own HIP runtime does not find the device in a
+    process where this library's runtime already holds it."""
+    import subprocess
+    r = subprocess.run([sys.executable, os.path.abspath(__file__), "--gemm-library-child"], capture_output=True,
+                       text=True, timeout=600)
+    if r.returncode != 0:
+        raise RuntimeError(f"gemm_library child failed ({r.returncode}):\n{r.stderr[-3000:]}")
+    return json.loads(r.stdout.strip().split("\n")[-1])
+
+
+def gemm_library_child():
+    import torch
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(7)
+    shapes = [(n, k, b) for (n, k) in GEMM_SHAPES for b in (8, 32, 64, 128)]
+    shapes += [(22016, 2048, 128), (2560, 2048, 128), (151936, 2048, 128)]  # gate/up, QKV, tied head at 128 rows
+    out, iters = [], 20
+    for (n, k, b) in shapes:
+        copies = max(2, math.ceil(POOL_BYTES / (n * k * 2)))
+        pool = torch.empty((copies, n, k), dtype=torch.bfloat16, device=dev).normal_(0.0, 0.02, generator=gen)
+        x = torch.empty((b, k), dtype=torch.bfloat16, device=dev).normal_(generator=gen)
+        y = torch.empty((b, n), dtype=torch.bfloat16, device=dev)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for i in range(3):
+                torch.mm(x, pool[i % copies].t(), out=y)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(iters):
+                torch.mm(x, pool[i % copies].t(), out=y)
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = e0.elapsed_time(e1) * 1e3 / iters
+        fl = 2.0 * b * n * k
+        out.append({"case": f"bf16 {n}x{k} B={b}", "us": round(us, 2), "TFLOPs": round(fl / (us * 1e-6) / 1e12, 1),
+                    "frac_bf16_peak": round(fl / (us * 1e-6) / 1e12 / MFMA_BF16_TFLOPS, 4)})
+        del graph, pool, x, y
+        torch.cuda.empty_cache()
+    print(json.dumps(out), flush=True)
 
 
 # --------------------------------------------------------------------------- attention
@@ -618,21 +703,25 @@ def bench_decode_b128(args, rt):
 
     pipe = not args.no_pipeline
 
-    def run(max_rows, chunk, pipeline=pipe):
-        return run_schedule(e, work, max_rows, chunk, pipeline)
+    keep = args.keep_logits
+
+    def run(max_rows, chunk, pipeline=pipe, keep_logits=keep):
+        return run_schedule(e, work, max_rows, chunk, pipeline, keep_logits)
 
     e.stats(reset=True)
     chunked, streams_c = run(rows, args.prefill_chunk)
     unpiped, streams_u = run(rows, args.prefill_chunk, False)
     tbt, streams_t = run(128, 1)
-    steady = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, F32, pipe)
+    other, streams_o = run(rows, args.prefill_chunk, pipe, not keep)  # the other head form, same schedule
+    other["streams_equal"] = streams_o == streams_c
+    steady = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, F32, pipe, keep)
     e.close()
     extras = {}
     for kv in (F16, I8):  # narrower pages: not the reference's values; agreement with the f32 streams beside them
         ek = qwen_engine(args, rows, kv)
-        res, streams_k = run_schedule(ek, work, rows, args.prefill_chunk, pipe)
+        res, streams_k = run_schedule(ek, work, rows, args.prefill_chunk, pipe, keep)
         res["stream_agreement_with_f32_pages"] = stream_agreement(streams_c, streams_k)
-        res["steady_decode"] = steady_decode_b128(ek, np.random.default_rng(3), args.decode_steps, kv, pipe)
+        res["steady_decode"] = steady_decode_b128(ek, np.random.default_rng(3), args.decode_steps, kv, pipe, keep)
         ek.close()
         extras[f"{KV_NAMES[kv]}_pages"] = res
     out = {"model": "Qwen2.5-3B architecture, Q4_0 weights, tied head, QKV bias, f32 KV pages, random init",
@@ -644,22 +733,25 @@ def bench_decode_b128(args, rt):
                         "request's last token, then prompt chunks within the row budget; f32 KV pages hold the "
                         "reference's KVCache values; pipelined: step N+1 is issued before step N's tokens reach "
                         "the host, its decode rows taking them from step N's argmax on the device",
-                "unpipelined": unpiped,
+                "unpipelined": unpiped, ("logits_kept" if not keep else "greedy_only_head"): other,
                 "token_by_token": tbt, "stream_agreement": stream_agreement(streams_c, streams_t),
                 "steady_decode": steady})
     out.update(extras)
     return out
 
 
-def run_schedule(e, work, max_rows, chunk, pipeline=False):
+def run_schedule(e, work, max_rows, chunk, pipeline=False, keep_logits=False):
     """One continuous-batching run of `work` [(prompt, max tokens)] through 128
     slots; aggregate generated tok/s, and the host's share of the wall time:
     the scheduler's own Python work plus the engine's host-side preparation of
     each step (unpipelined, the device idles meanwhile, as every step ends in a
     synchronisation; pipelined, that work overlaps the previous step's run and
-    device_wait_ms_per_step is the time the host waited for the device)."""
+    device_wait_ms_per_step is the time the host waited for the device).
+    keep_logits False: the greedy requests keep no logits (the engine's
+    greedy-only head, its argmax in the head GEMM's epilogue)."""
     from qraf_amd.engine import BatchScheduler
-    sched = BatchScheduler(e, max_batch=128, max_rows=max_rows, prefill_chunk=chunk, pipeline=pipeline)
+    sched = BatchScheduler(e, max_batch=128, max_rows=max_rows, prefill_chunk=chunk, pipeline=pipeline,
+                           keep_logits=keep_logits)
     for p, o in work:
         sched.submit(p, o)
     e.stats(reset=True)
@@ -678,7 +770,7 @@ def run_schedule(e, work, max_rows, chunk, pipeline=False):
             "device_wait_ms_per_step": round(st["wait_us"] * 1e-3 / sched.steps, 3),
             "step_launches": {"eager": st["eager_steps"], "graph_captures": st["graph_captures"],
                               "graph_launches": st["graph_launches"]},
-            "pad_rows": st["pad_rows"]}, \
+            "pad_rows": st["pad_rows"], "logits_kept": keep_logits}, \
         [r.generated for r in sorted(done, key=lambda r: r.id)]
 
 
@@ -859,7 +951,8 @@ def bench_steady_b128(args, rt):
     """The steady 128-sequence decode alone (every GEMM at 128 rows), for profiling."""
     kv = {"f32": F32, "fp16": F16, "int8": I8}[args.kv]
     e = qwen_engine(args, 128, kv)
-    out = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, kv, not args.no_pipeline)
+    out = steady_decode_b128(e, np.random.default_rng(3), args.decode_steps, kv, not args.no_pipeline,
+                             args.keep_logits)
     e.close()
     return out
 
@@ -879,11 +972,12 @@ QWEN_LAYER_WEIGHT_BYTES = 1560674304  # 36 layers of Q4_0 q/k/v/o/gate/up/down
 QWEN_HEAD_BYTES = 175030272           # the tied Q4_0 embedding read as the head
 
 
-def steady_decode_b128(e, rng, steps, kv, pipeline=False):
+def steady_decode_b128(e, rng, steps, kv, pipeline=False, keep_logits=False):
     """128 concurrent sequences at ragged contexts (prompt U[16,512] plus U[0,255] generated, the run above's
     distribution), prefilled in 128-row steps; then `steps` decode steps of 128 rows, every row generating
     (greedy, device argmax).  Timed: the decode steps only.  Pipelined: each step is issued before the previous
-    one's tokens are collected, its rows taking them from the previous step's argmax on the device."""
+    one's tokens are collected, its rows taking them from the previous step's argmax on the device.
+    keep_logits False: the decode steps keep no logits (the greedy-only head)."""
     n, V = 128, QWEN["vocab"]
     seqs = [e.seq_create() for _ in range(n)]
     ctx = rng.integers(16, 513, n) + rng.integers(0, 256, n)
@@ -894,6 +988,7 @@ def steady_decode_b128(e, rng, steps, kv, pipeline=False):
                want_logits=np.zeros(len(ch), np.uint8), logits=False, argmax=False)
     toks = rng.integers(0, V, n).tolist()
     pos = ctx.astype(np.int64).copy()
+    e.set_keep_logits(keep_logits)
     for _ in range(3):  # warm-up decode steps
         _, nx = e.step(seqs, toks, pos.tolist())
         toks, pos = nx.tolist(), pos + 1
@@ -912,6 +1007,7 @@ def steady_decode_b128(e, rng, steps, kv, pipeline=False):
             _, nx = e.step(seqs, toks, pos.tolist())
             toks, pos = nx.tolist(), pos + 1
     el = time.perf_counter() - t0
+    e.set_keep_logits(True)
     for s in seqs:
         e.seq_release(s)
     # HBM bytes per step: every layer weight, the head, and every cached K/V position read once
@@ -920,7 +1016,8 @@ def steady_decode_b128(e, rng, steps, kv, pipeline=False):
     ms = el / steps * 1e3
     return {"kv_pages": KV_NAMES[kv], "sequences": n, "context_mean_at_start": round(float(ctx.mean()) + 3, 1),
             "context_max_at_end": int(pos.max()), "decode_steps": steps, "ms_per_step": round(ms, 3),
-            "decode_tok_s": round(n * steps / el, 1), "pipelined": pipeline, "alg_bytes_per_step": int(by),
+            "decode_tok_s": round(n * steps / el, 1), "pipelined": pipeline, "logits_kept": keep_logits,
+            "alg_bytes_per_step": int(by),
             "GB_s": round(by / (ms * 1e-3) / 1e9, 1), "frac_hbm_peak": round(by / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
 
 
@@ -938,6 +1035,9 @@ def main():
     ap.add_argument("--decode-steps", type=int, default=64, help="timed steps of the steady 128-sequence decode")
     ap.add_argument("--rows", type=int, default=512, help="row budget per step of the continuous-batch run")
     ap.add_argument("--prefill-chunk", type=int, default=512, help="prompt tokens of one request per step at most")
+    ap.add_argument("--keep-logits", action="store_true",
+                    help="batch-128 legs: greedy steps keep their logits in HBM (default: the greedy-only head, "
+                         "argmax in the head GEMM's epilogue; the other form is reported beside it)")
     ap.add_argument("--cases", default="",
                     help="restrict the matvec leg to these cases, e.g. 'q8_0 11008x4096' (comma-separated; "
                          "a profile of one case then has one shape per kernel)")
@@ -985,7 +1085,8 @@ def main():
     value, total_ms, per_case, cache_res, hosts = bench_matvec(args, rt)
     print(f"# matvec done: {value:.1f} GB/s", file=sys.stderr, flush=True)
     extra = {}
-    for part, fn in (("gemm", bench_gemm), ("attention", bench_attention), ("decode_b1", bench_decode_b1),
+    for part, fn in (("gemm", bench_gemm), ("gemm_library", bench_gemm_library), ("attention", bench_attention),
+                     ("decode_b1", bench_decode_b1),
                      ("decode_b128", bench_decode_b128), ("steady_b128", bench_steady_b128), ("load", bench_load),
                      ("sampler", bench_sampler)):
         if part in only:
@@ -1033,4 +1134,7 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    if "--gemm-library-child" in sys.argv:  # the gemm_library leg's measuring process (torch only)
+        gemm_library_child()
+    else:
+        main()

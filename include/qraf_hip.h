@@ -301,6 +301,21 @@ uint64_t qraf_hip_qgemm_tiled_workspace_bytes(uint32_t dtype, uint32_t out_dim, 
 int qraf_hip_qgemm_tiled_dev(const void* w_tiled, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
                              const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, float* y, const float* add,
                              void* workspace, uint64_t workspace_bytes, void* stream);
+/* Greedy LM head without logits: tokens[b] = Sampler::argmax
+ * (sampler.cpp:25-35: the first of the largest values) of row b of
+ * qraf_hip_qgemm_tiled_dev's product (out_dim = vocabulary rows), the product
+ * never written.  Where the tiled plan for this shape is the pipelined kernel
+ * it runs unsplit, each workgroup writing its best (value, index) per row to
+ * keys (8-byte aligned, at least qraf_hip_qgemm_tiled_argmax_keys_bytes), and
+ * a second launch reduces them: *fused = 1.  Otherwise nothing is launched
+ * and *fused = 0 (the caller then takes the argmax of the written product).
+ * A row holding NaN takes the largest of its numbers (the reference keeps a
+ * NaN at position 0).  No counterpart in the reference (a fusion of the
+ * logits projection and Sampler::argmax). */
+uint64_t qraf_hip_qgemm_tiled_argmax_keys_bytes(uint32_t out_dim, int32_t batch);
+int qraf_hip_qgemm_tiled_argmax_dev(const void* w_tiled, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
+                                    const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, void* keys,
+                                    uint64_t keys_bytes, uint32_t* tokens, int32_t* fused, void* stream);
 
 /* The SwiGLU front of mlp_forward (attention.cpp:172-178) fused into the
  * tile-major GEMM: w_tiled's rows interleave the gate and up projections (row
@@ -453,6 +468,16 @@ int qraf_engine_step_collect(qraf_engine* engine, uint32_t* next_tokens, int32_t
  * (on = 1, the default); on = 0 launches every step's kernels eagerly.  No
  * reference counterpart: an execution detail of qraf_engine_step. */
 int qraf_engine_set_graphs(qraf_engine* engine, int32_t on);
+/* keep = 0: a step that wants only greedy tokens (qraf_engine_step with
+ * logits NULL and next_tokens set, qraf_engine_step_async) writes no logits:
+ * where its head runs as the pipelined tile-major GEMM (more than 64 logit
+ * rows at the usual vocabulary sizes) Sampler::argmax (sampler.cpp:25-35) is
+ * taken in that GEMM's epilogue (qraf_hip_qgemm_tiled_argmax_dev), the same
+ * tokens without the [rows][vocab] write and re-read; qraf_engine_sample and
+ * qraf_engine_read_logits return QRAF_HIP_ERR_STATE after such a step.
+ * keep = 1 (the default): every step leaves its logits in HBM.  No reference
+ * counterpart: the reference's forward always returns the logits. */
+int qraf_engine_set_keep_logits(qraf_engine* engine, int32_t keep);
 /* Sampling of the last step's logit rows where they lie in HBM (the rows
  * that step returned logits or argmax for, in order; row0 .. row0+rows-1 of
  * them): repetition penalty with each row's recent tokens (host arrays

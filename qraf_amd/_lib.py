@@ -80,6 +80,9 @@ SIGNATURES = {
     "qraf_hip_repack_tiles_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp]),
     "qraf_hip_qgemm_tiled_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp, vp,
                                            C.c_uint64, vp]),
+    "qraf_hip_qgemm_tiled_argmax_keys_bytes": (C.c_uint64, [C.c_uint32, C.c_int32]),
+    "qraf_hip_qgemm_tiled_argmax_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp,
+                                                  C.c_uint64, vp, vp, vp]),
     "qraf_hip_qgemm_tiled_silu_dev": (C.c_int, [vp, C.c_uint32, C.c_uint32, C.c_uint32, vp, vp, C.c_int32, vp, vp, vp]),
     "qraf_hip_qgemm_tiled_workspace_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32]),
     "qraf_hip_qgemm_workspace_bytes": (C.c_uint64, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_int32]),
@@ -135,6 +138,7 @@ SIGNATURES.update({
     "qraf_engine_step_async": (C.c_int, [vp, C.c_int32, i32p, u32p, i32p, i32p, C.POINTER(C.c_uint8)]),
     "qraf_engine_step_collect": (C.c_int, [vp, u32p, i32p]),
     "qraf_engine_set_graphs": (C.c_int, [vp, C.c_int32]),
+    "qraf_engine_set_keep_logits": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_set_row_padding": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_set_fusion": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_forward": (C.c_int, [vp, C.c_uint32, C.c_int32, fp]),

@@ -180,6 +180,12 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
 int qgemm_kw_init();
 int launch_qgemm_silu(const void* Wt, uint32_t dtype, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
                       uint16_t* act_hi, uint16_t* act_lo, hipStream_t s);
+// greedy head: argmax of each row of X W^T without writing it (tile-major W);
+// *done = false (nothing launched) where the tiled plan is not the pipelined form
+size_t qgemm_argmax_keys_bytes(int N, int M);
+bool qgemm_argmax_fits(uint32_t dtype, int N, int K, int M, size_t keys_bytes);
+int launch_qgemm_argmax(const void* Wt, uint32_t dtype, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
+                        uint64_t* keys, size_t keys_bytes, uint32_t* out, hipStream_t s, bool* done);
 size_t qgemm_workspace_bytes(uint32_t dtype, int N, int K, int M, bool tiled = false);
 // bytes of the [S][M][N] partial slices launch_qgemm(..., slices) writes
 size_t qgemm_partials_bytes(uint32_t dtype, int N, int K, int M, bool tiled = false);

@@ -416,6 +416,8 @@ struct qraf_engine {
     bool batch_mv = true;             // steps of 2-8 rows: projections on the multi-vector matvec
     int32_t default_seq = -1;
     int last_logit_rows = 0;          // logit rows the last step left in `logits`
+    bool keep_logits = true;          // false: greedy-only steps take the head's argmax without writing logits
+    bool last_logits_kept = true;     // the last step's logits are in `logits` (not a greedy-only step)
     qraf_engine_stats stats{};        // host-side time of qraf_engine_step
     uint8_t* samp = nullptr;          // sampling staging: recent tokens, counts, uniforms, tokens
     size_t samp_cap = 0;
@@ -447,6 +449,8 @@ struct qraf_engine {
     size_t gemm_ws_bytes = 0;
     float* am_val = nullptr;  // argmax chunk winners [max_batch][32]
     int* am_idx = nullptr;
+    uint64_t* am_keys = nullptr;  // the fused head's per-workgroup argmax keys
+    size_t am_keys_bytes = 0;
     void* part_ws = nullptr;  // [S][rows][N] partials the fused batched layer sums downstream
     size_t part_ws_bytes = 0;
     bool fused = false;  // every layer has tile-major copies: batched steps run the fused pipeline
@@ -460,7 +464,7 @@ struct qraf_engine {
     // decode step.
     struct StepGraph {
         int n = 0, n_logit_rows = 0, ctx = 0;
-        bool head = false;
+        int head = 0;  // 0: no head, 1: logits (and argmax), 2: argmax only
         uint32_t gen = 0;
         hipGraphExec_t exec = nullptr;
         uint64_t used = 0;
@@ -609,6 +613,8 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     A(e->amax, (size_t)B * 4);
     A(e->am_val, (size_t)B * ARGMAX_CHUNKS * 4);
     A(e->am_idx, (size_t)B * ARGMAX_CHUNKS * 4);
+    e->am_keys_bytes = qgemm_argmax_keys_bytes((int)V, (int)B);
+    A(e->am_keys, e->am_keys_bytes);
     e->in_words = (size_t)B * (5 + e->max_pages);
     A(e->d_in, e->in_words * 4);
     e->attn_ws_bytes = attn_workspace_bytes(B, (int)c.num_heads, (int)kvh, hd, e->capacity);
@@ -1043,6 +1049,9 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     hipStream_t s = e->stream;
     const size_t words = (size_t)n * (5 + MP);
     const bool head = n_logit_rows > 0 && (logits || tok_out);
+    // greedy-only step (no logits wanted, none kept): the head's argmax fused into its GEMM where it runs one
+    const bool argmax_only = head && !logits && tok_out && !e->keep_logits;
+    const int head_mode = head ? (argmax_only ? 2 : 1) : 0;
     const int32_t* d_tok = e->d_in;
     const int32_t* d_pos = d_tok + n;
     const int32_t* d_ctx = d_pos + n;
@@ -1207,6 +1216,16 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
             } else {
                 hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n_logit_rows), dim3(256), 0, s, e->h, e->onorm, D,
                                    c.rms_norm_eps, e->xhead, d_lrows);
+                if (argmax_only && dt != DT_F32 && e->head_t && !use_bmv(dt, V, D, n_logit_rows) &&
+                    qgemm_argmax_fits(dt, V, D, n_logit_rows, e->am_keys_bytes)) {
+                    // the GEMM proj would run, with Sampler::argmax in its epilogue
+                    QH_TRY(launch_split_bf16(e->xhead, e->xh, e->xl, n_logit_rows, D, 0, nullptr, s));
+                    bool done = false;
+                    QH_TRY(launch_qgemm_argmax(e->head_t, dt, V, D, e->xh, e->xl, n_logit_rows, e->am_keys,
+                                               e->am_keys_bytes, e->amax, s, &done));
+                    QH_REQUIRE(done, QRAF_HIP_ERR_STATE, "engine: fused head not launched");
+                    return QRAF_HIP_OK;
+                }
                 QH_TRY(proj(W, e->head_t, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
             }
             if (V % 4 == 0) {  // one pass per row (logits rows are 16-byte aligned then)
@@ -1233,12 +1252,12 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
         const uint32_t gen = tuning_generation();
         qraf_engine::StepGraph* g = nullptr;
         for (auto& sg : e->graphs)
-            if (sg.n == n && sg.n_logit_rows == n_logit_rows && sg.ctx == ctx_grid && sg.head == head && sg.gen == gen)
+            if (sg.n == n && sg.n_logit_rows == n_logit_rows && sg.ctx == ctx_grid && sg.head == head_mode && sg.gen == gen)
                 g = &sg;
         bool second = false;
         if (!g) {
             for (auto it = e->seen.begin(); it != e->seen.end(); ++it)
-                if (it->n == n && it->n_logit_rows == n_logit_rows && it->ctx == ctx_grid && it->head == head &&
+                if (it->n == n && it->n_logit_rows == n_logit_rows && it->ctx == ctx_grid && it->head == head_mode &&
                     it->gen == gen) {
                     second = true;
                     e->seen.erase(it);
@@ -1249,7 +1268,7 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
                 sg.n = n;
                 sg.n_logit_rows = n_logit_rows;
                 sg.ctx = ctx_grid;
-                sg.head = head;
+                sg.head = head_mode;
                 sg.gen = gen;
                 if (e->seen.size() >= 4 * MAX_STEP_GRAPHS) e->seen.erase(e->seen.begin());
                 e->seen.push_back(sg);
@@ -1285,7 +1304,7 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
             sg.n = n;
             sg.n_logit_rows = n_logit_rows;
             sg.ctx = ctx_grid;
-            sg.head = head;
+            sg.head = head_mode;
             sg.gen = gen;
             sg.exec = exec;
             e->graphs.push_back(sg);
@@ -1301,6 +1320,7 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
         e->stats.eager_steps += 1;
     }
     e->last_logit_rows = head ? n_logit_real : 0;
+    e->last_logits_kept = !argmax_only;
     if (head && logits)
         QH_CHECK_HIP(hipMemcpyAsync(logits, e->logits, (size_t)n_logit_real * V * 4, hipMemcpyDeviceToHost, s));
     // tokens come back through pinned staging: an async copy into pageable
@@ -1367,6 +1387,8 @@ int qraf_engine_read_logits(qraf_engine* e, int32_t row0, int32_t rows, float* o
     QH_REQUIRE(e && out && rows > 0 && row0 >= 0, QRAF_HIP_ERR_INVALID, "read_logits: bad arguments");
     QH_REQUIRE(row0 + rows <= e->last_logit_rows, QRAF_HIP_ERR_STATE,
                "read_logits: rows %d..%d, the last step left %d logit rows", row0, row0 + rows - 1, e->last_logit_rows);
+    QH_REQUIRE(e->last_logits_kept, QRAF_HIP_ERR_STATE,
+               "read_logits: the last step was greedy-only and kept no logits (qraf_engine_set_keep_logits)");
     const size_t V = e->c.vocab_size;
     QH_CHECK_HIP(hipMemcpyAsync(out, e->logits + (size_t)row0 * V, (size_t)rows * V * 4, hipMemcpyDeviceToHost,
                                 e->stream));
@@ -1409,6 +1431,8 @@ int qraf_engine_sample(qraf_engine* e, int32_t row0, int32_t rows, const qraf_sa
     QH_REQUIRE(e && p && tokens && rows > 0 && row0 >= 0, QRAF_HIP_ERR_INVALID, "sample: bad arguments");
     QH_REQUIRE(row0 + rows <= e->last_logit_rows, QRAF_HIP_ERR_STATE,
                "sample: rows %d..%d, the last step left %d logit rows", row0, row0 + rows - 1, e->last_logit_rows);
+    QH_REQUIRE(e->last_logits_kept, QRAF_HIP_ERR_STATE,
+               "sample: the last step was greedy-only and kept no logits (qraf_engine_set_keep_logits)");
     const bool greedy = !(p->temperature > 0.f);
     const bool pen = p->repetition_penalty != 1.0f && recent;
     QH_REQUIRE(!pen || (counts && stride > 0), QRAF_HIP_ERR_INVALID, "sample: recent tokens need counts");
@@ -1441,6 +1465,14 @@ int qraf_engine_sample(qraf_engine* e, int32_t row0, int32_t rows, const qraf_sa
                          e->sort_ws, e->sort_cap, s));
     QH_CHECK_HIP(hipMemcpyAsync(tokens, d_tok, (size_t)rows * 4, hipMemcpyDeviceToHost, s));
     QH_CHECK_HIP(hipStreamSynchronize(s));
+    return QRAF_HIP_OK;
+}
+
+// Greedy-only steps without logits (keep = 0) or with them (1, the default).
+int qraf_engine_set_keep_logits(qraf_engine* e, int32_t keep) {
+    clear_error();
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "set_keep_logits: null engine");
+    e->keep_logits = keep != 0;
     return QRAF_HIP_OK;
 }
 

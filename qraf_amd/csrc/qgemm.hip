@@ -520,6 +520,37 @@ struct PipeGeom {
     static constexpr int MINB = SMALL ? 2 : 1;
 };
 
+// Sampler::argmax's order (sampler.cpp:25-35: the first of the largest
+// values) as one unsigned 64-bit key: the value's bits made monotonic in the
+// high word (-0 counted as +0, as the reference's > comparison counts them
+// equal), 0xFFFFFFFF - index in the low word, so a larger key is a larger
+// value or, for equal values, a smaller index.  A NaN's high word is 0, below
+// every number's: a NaN is chosen only in a row of NaNs (then the first, as
+// the reference); the reference would also keep a NaN at position 0.
+__device__ __forceinline__ uint64_t argmax_key(float v, uint32_t idx) {
+    const uint32_t b = __float_as_uint(v + 0.0f);
+    const uint32_t o = v != v ? 0u : (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+    return ((uint64_t)o << 32) | (0xFFFFFFFFu - idx);
+}
+
+// One step of a prefix max over the 16 lanes of each DPP row, for every key
+// of a lane: key = max(key, the key of the lane CTRL's row_shr names), lanes
+// shifted in from outside the row reading 0 (the keys' identity).
+template <int CTRL>
+__device__ __forceinline__ void key_row_max(uint64_t (&k)[4]) {
+    uint32_t lo[4], hi[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        lo[r] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)k[r], CTRL, 0xF, 0xF, false);
+        hi[r] = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(k[r] >> 32), CTRL, 0xF, 0xF, false);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint64_t o = ((uint64_t)hi[r] << 32) | lo[r];
+        k[r] = o > k[r] ? o : k[r];
+    }
+}
+
 // Stream-K schedule: workgroup w of G owns blocks [w T / G, (w+1) T / G) of the T = units x nb
 // (tile, quant block) pairs, units in tile-major order; the workgroup that owns pair x:
 __host__ __device__ inline int sk_owner(long long x, long long T, int G) {
@@ -531,14 +562,17 @@ __host__ __device__ inline int sk_owner(long long x, long long T, int G) {
 // SK: the stream-K schedule (skG workgroups), else the uniform split grid.  Two
 // instantiations, since one kernel holding both loops spills ~100-200 SGPRs
 // into VGPR lanes (a readlane per descriptor word at every DMA issue).
-template <int FMT, int TM, int TN, int KC, int WN, int WMN, bool SK>
+// AMAX: the greedy head's argmax epilogue (amax), an instantiation of its own
+// so that its registers do not raise the other forms' allocation.
+template <int FMT, int TM, int TN, int KC, int WN, int WMN, bool SK, bool AMAX = false>
 __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>::MINB)) void qgemm_pipe_kernel(const uint8_t* __restrict__ Wt, int N, int nb,
                                                                  const uint16_t* __restrict__ xh,
                                                                  const uint16_t* __restrict__ xl, int K, int M,
                                                                  float* Y, const float* add, int bps,
                                                                  float* __restrict__ part, int skG, int sk_ntiles,
                                                                  int skS, uint16_t* __restrict__ act_hi,
-                                                                 uint16_t* __restrict__ act_lo) {
+                                                                 uint16_t* __restrict__ act_lo,
+                                                                 uint64_t* __restrict__ amax) {
     using G = PipeGeom<FMT, TM, TN, KC, WN, WMN>;
     constexpr int MW = G::MW, NW = G::NW, TB = G::TB, NWV = G::NWV;
 
@@ -739,6 +773,52 @@ __global__ __launch_bounds__(64 * WMN * WN, (PipeGeom<FMT, TM, TN, KC, WN, WMN>:
                     }
                 }
             }
+        }
+        return;
+    }
+    if constexpr (AMAX) {
+        // greedy head (Sampler::argmax, sampler.cpp:25-35) on complete sums:
+        // per batch row, the workgroup's largest logit as an argmax_key, written
+        // to amax[tile][m] (no split, no stream-K: the launcher guarantees it).
+        // Each lane takes the best of its TN columns; a prefix max over the
+        // 16 lanes of a DPP row (the lanes that share the row's batch rows,
+        // row_shr 1, 2, 4, 8, all 4*TM keys interleaved) leaves the 16
+        // columns' best in lane 15; the WN waves then meet in stage buffer 0,
+        // free once every wave has drained its loads and passed the barrier.
+        uint64_t* keys = (uint64_t*)qg_stage<0, G::SMALL>();
+        static_assert(WN * MW * 8 <= QG_STAGE_SMALL, "argmax keys must fit a stage buffer");
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < TM; t++) {
+            uint64_t best[4];
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                best[r] = 0;
+#pragma unroll
+                for (int u = 0; u < TN; u++) {
+                    const int n = n0 + (wn * TN + u) * 16 + l16;
+                    const uint64_t k = n < N ? argmax_key(acc[t][u][r], (uint32_t)n) : 0;
+                    best[r] = k > best[r] ? k : best[r];
+                }
+            }
+            key_row_max<0x111>(best);
+            key_row_max<0x112>(best);
+            key_row_max<0x114>(best);
+            key_row_max<0x118>(best);
+            if (l16 == 15)
+#pragma unroll
+                for (int r = 0; r < 4; r++) keys[wn * MW + (wm * TM + t) * 16 + seg * 4 + r] = best[r];
+        }
+        __syncthreads();
+        for (int i = tid; i < MW; i += 64 * NWV) {
+            if (m0 + i >= M) break;
+            uint64_t b = 0;
+#pragma unroll
+            for (int w = 0; w < WN; w++) {
+                const uint64_t k = keys[w * MW + i];
+                b = k > b ? k : b;
+            }
+            amax[(size_t)blockIdx.x * M + m0 + i] = b;
         }
         return;
     }
@@ -1714,6 +1794,44 @@ static int launch_kw(uint32_t dtype, const QgPlan& p, dim3 grid, const uint8_t* 
     return QRAF_HIP_OK;
 }
 
+// qgemm_pipe_kernel at plan p's geometry; amax: the greedy-head epilogue
+// (uniform split grid, one split, no Y).
+static void launch_pipe(uint32_t dtype, const QgPlan& p, dim3 grid, const void* W, int N, int nb, const uint16_t* xh,
+                        const uint16_t* xl, int K, int M, float* Y, const float* add, float* part, uint64_t* amax,
+                        hipStream_t s) {
+#define QH_P(F, TM_, TN_, WN_, WM_)                                                                            \
+    do {                                                                                                      \
+        if (amax)                                                                                             \
+            hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_, false, true>), grid,               \
+                               dim3(64 * WN_ * WM_), 0, s, (const uint8_t*)W, N, nb, xh, xl, K, M, nullptr,     \
+                               nullptr, p.bps, nullptr, 0, p.ntiles, 1, nullptr, nullptr, amax);              \
+        else if (p.skG > 0)                                                                                   \
+            hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_, true>), grid, dim3(64 * WN_ * WM_), 0, \
+                               s, (const uint8_t*)W, N, nb, xh, xl, K, M, Y, add, p.bps, part, p.skG, p.ntiles,  \
+                               p.S, nullptr, nullptr, nullptr);                                               \
+        else                                                                                                  \
+            hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_, false>), grid, dim3(64 * WN_ * WM_),  \
+                               0, s, (const uint8_t*)W, N, nb, xh, xl, K, M, Y, add, p.bps, part, 0, p.ntiles,  \
+                               p.S, nullptr, nullptr, nullptr);                                               \
+    } while (0)
+    if (dtype == DT_Q8_0) {
+        if (p.WN == 4 && p.WM == 1) {
+            if (p.TM == 8) QH_P(8, 8, 2, 4, 1);
+            else QH_P(8, 4, 2, 4, 1);
+        } else if (p.WM == 1) QH_P(8, 8, 2, 8, 1);
+        else QH_P(8, 2, 4, 4, 2);
+    } else {
+        if (p.WN == 4 && p.WM == 1) {
+            if (p.TM == 8) QH_P(4, 8, 2, 4, 1);
+            else QH_P(4, 4, 2, 4, 1);
+        } else if (p.WM == 1) {
+            if (p.TN == 3) QH_P(4, 8, 3, 8, 1);
+            else QH_P(4, 8, 2, 8, 1);
+        } else QH_P(4, 2, 4, 4, 2);
+    }
+#undef QH_P
+}
+
 int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
                  float* Y, const float* add, void* ws, size_t ws_bytes, hipStream_t s, bool tiled, int* slices) {
     QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "qgemm: unsupported dtype %u", dtype);
@@ -1766,33 +1884,7 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
         QH_TRY(launch_kw(dtype, p, grid, (const uint8_t*)W, N, nb, xh, xl, K, M, yk, part ? nullptr : add, slice, 0,
                          nullptr, nullptr, s));
     } else if (p.pipe) {
-#define QH_P(F, TM_, TN_, WN_, WM_)                                                                        \
-    do {                                                                                                  \
-    if (p.skG > 0)                                                                                        \
-        hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_, true>), grid, dim3(64 * WN_ * WM_), 0, s, \
-                           (const uint8_t*)W, N, nb, xh, xl, K, M, Y, add, p.bps, part, p.skG, p.ntiles, p.S,     \
-                           nullptr, nullptr);                                                              \
-    else                                                                                                  \
-        hipLaunchKernelGGL((qgemm_pipe_kernel<F, TM_, TN_, 2, WN_, WM_, false>), grid, dim3(64 * WN_ * WM_), 0, s, \
-                           (const uint8_t*)W, N, nb, xh, xl, K, M, Y, add, p.bps, part, 0, p.ntiles, p.S,        \
-                           nullptr, nullptr);                                                              \
-    } while (0)
-        if (dtype == DT_Q8_0) {
-            if (p.WN == 4 && p.WM == 1) {
-                if (p.TM == 8) QH_P(8, 8, 2, 4, 1);
-                else QH_P(8, 4, 2, 4, 1);
-            } else if (p.WM == 1) QH_P(8, 8, 2, 8, 1);
-            else QH_P(8, 2, 4, 4, 2);
-        } else {
-            if (p.WN == 4 && p.WM == 1) {
-                if (p.TM == 8) QH_P(4, 8, 2, 4, 1);
-                else QH_P(4, 4, 2, 4, 1);
-            } else if (p.WM == 1) {
-                if (p.TN == 3) QH_P(4, 8, 3, 8, 1);
-                else QH_P(4, 8, 2, 8, 1);
-            } else QH_P(4, 2, 4, 4, 2);
-        }
-#undef QH_P
+        launch_pipe(dtype, p, grid, W, N, nb, xh, xl, K, M, Y, add, part, nullptr, s);
     } else {
 #define QH_G(F, WM_, WN_, TM_, TN_, KC_)                                                                           \
     if (tiled)                                                                                                     \
@@ -1830,6 +1922,80 @@ int launch_qgemm(const void* W, uint32_t dtype, int bs, int N, int K, const uint
         hipLaunchKernelGGL(qgemm_reduce_kernel, dim3(rgrid), dim3(256), 0, s, part, p.S, MN, Y, add);
         QH_CHECK_HIP(hipGetLastError());
     }
+    return QRAF_HIP_OK;
+}
+
+// Row m's token: the largest of the per-workgroup keys [tiles][M] of
+// qgemm_pipe_kernel's argmax epilogue (0 for a key past the N rows, as
+// argmax_rows_kernel clamps).
+__global__ __launch_bounds__(256) void argmax_keys_kernel(const uint64_t* __restrict__ keys, int tiles, int M, int N,
+                                                          uint32_t* __restrict__ out) {
+    __shared__ uint64_t wb[4];
+    const int m = blockIdx.x, tid = threadIdx.x;
+    uint64_t best = 0;
+    for (int t = tid; t < tiles; t += 256) {
+        const uint64_t k = keys[(size_t)t * M + m];
+        best = k > best ? k : best;
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const uint64_t k = __shfl_xor(best, o);
+        best = k > best ? k : best;
+    }
+    if ((tid & 63) == 0) wb[tid >> 6] = best;
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < 4; w++) best = wb[w] > best ? wb[w] : best;
+        const uint32_t idx = 0xFFFFFFFFu - (uint32_t)best;
+        out[m] = best != 0 && idx < (uint32_t)N ? idx : 0u;
+    }
+}
+
+size_t qgemm_argmax_keys_bytes(int N, int M) {
+    // pipelined tiles hold at least 128 weight rows
+    return (size_t)((N + 127) / 128) * (size_t)M * 8;
+}
+
+// Greedy head: the argmax (Sampler::argmax) of each of the M rows of
+// X W^T over the N weight rows, with no product written: where the tiled plan
+// is the pipelined form, qgemm_pipe_kernel in one split writes each
+// workgroup's best key per row to keys [tiles][M] and argmax_keys_kernel
+// reduces them to out [M]; *done = false and nothing launched otherwise (the
+// caller then writes the products and takes their argmax).
+// the pipelined plan of the fused head, unsplit (false: not the pipelined form,
+// or the keys do not fit)
+static bool argmax_plan(uint32_t dtype, int N, int K, int M, size_t keys_bytes, QgPlan& p) {
+    if ((dtype != DT_Q8_0 && dtype != DT_Q4_0) || K <= 0 || K % 32 || N <= 0 || M <= 0) return false;
+    p = qgemm_plan(dtype, N, K, M, q_row_bytes(dtype, 32, K), true);
+    if (!p.pipe || p.kwR || p.kxT) return false;
+    p.S = 1;  // complete sums in every workgroup
+    p.skG = 0;
+    p.bps = K / 32;
+    return p.mchunks <= 65535 && keys_bytes >= (size_t)p.ntiles * M * 8;
+}
+
+bool qgemm_argmax_fits(uint32_t dtype, int N, int K, int M, size_t keys_bytes) {
+    QgPlan p;
+    return argmax_plan(dtype, N, K, M, keys_bytes, p);
+}
+
+int launch_qgemm_argmax(const void* Wt, uint32_t dtype, int N, int K, const uint16_t* xh, const uint16_t* xl, int M,
+                        uint64_t* keys, size_t keys_bytes, uint32_t* out, hipStream_t s, bool* done) {
+    *done = false;
+    QH_REQUIRE(dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE, "qgemm argmax: unsupported dtype %u", dtype);
+    QH_REQUIRE(K % 32 == 0 && K > 0 && N > 0 && M > 0, QRAF_HIP_ERR_INVALID, "qgemm argmax: N=%d K=%d M=%d", N, K, M);
+    QH_REQUIRE(Wt && xh && xl && keys && out, QRAF_HIP_ERR_INVALID, "qgemm argmax: null pointer");
+    QH_REQUIRE((((uintptr_t)Wt) & 15) == 0 && (((uintptr_t)xh) & 15) == 0 && (((uintptr_t)xl) & 15) == 0 &&
+                   (((uintptr_t)keys) & 7) == 0,
+               QRAF_HIP_ERR_INVALID, "qgemm argmax: misaligned operands");
+    QgPlan p;
+    if (!argmax_plan(dtype, N, K, M, keys_bytes, p)) return QRAF_HIP_OK;
+    launch_pipe(dtype, p, dim3(p.ntiles, 1, p.mchunks), Wt, N, K / 32, xh, xl, K, M, nullptr, nullptr, nullptr, keys,
+                s);
+    QH_CHECK_HIP(hipGetLastError());
+    hipLaunchKernelGGL(argmax_keys_kernel, dim3(M), dim3(256), 0, s, keys, p.ntiles, M, N, out);
+    QH_CHECK_HIP(hipGetLastError());
+    *done = true;
     return QRAF_HIP_OK;
 }
 
@@ -1877,10 +2043,10 @@ int launch_qgemm_silu(const void* Wt, uint32_t dtype, int N, int K, const uint16
     const int bps = (nb + KC - 1) / KC * KC;
     if (dtype == DT_Q8_0)
         hipLaunchKernelGGL((qgemm_pipe_kernel<8, 4, 2, 2, 4, 1, false>), grid, dim3(256), 0, s, (const uint8_t*)Wt, N, nb, xh, xl,
-                           K, M, nullptr, nullptr, bps, nullptr, 0, 0, 1, act_hi, act_lo);
+                           K, M, nullptr, nullptr, bps, nullptr, 0, 0, 1, act_hi, act_lo, nullptr);
     else
         hipLaunchKernelGGL((qgemm_pipe_kernel<4, 4, 2, 2, 4, 1, false>), grid, dim3(256), 0, s, (const uint8_t*)Wt, N, nb, xh, xl,
-                           K, M, nullptr, nullptr, bps, nullptr, 0, 0, 1, act_hi, act_lo);
+                           K, M, nullptr, nullptr, bps, nullptr, 0, 0, 1, act_hi, act_lo, nullptr);
     QH_CHECK_HIP(hipGetLastError());
     return QRAF_HIP_OK;
 }
@@ -1949,6 +2115,22 @@ int qraf_hip_qgemm_tiled_dev(const void* w_tiled, uint32_t dtype, uint32_t out_d
     qraf_hip::clear_error();
     return qraf_hip::launch_qgemm(w_tiled, dtype, 32, (int)out_dim, (int)in_dim, x_hi, x_lo, batch, y, add, workspace,
                                   workspace_bytes, qraf_hip::as_stream(stream), true);
+}
+
+uint64_t qraf_hip_qgemm_tiled_argmax_keys_bytes(uint32_t out_dim, int32_t batch) {
+    return batch > 0 ? qraf_hip::qgemm_argmax_keys_bytes((int)out_dim, batch) : 0;
+}
+
+int qraf_hip_qgemm_tiled_argmax_dev(const void* w_tiled, uint32_t dtype, uint32_t out_dim, uint32_t in_dim,
+                                    const uint16_t* x_hi, const uint16_t* x_lo, int32_t batch, void* keys,
+                                    uint64_t keys_bytes, uint32_t* tokens, int32_t* fused, void* stream) {
+    qraf_hip::clear_error();
+    bool done = false;
+    const int rc = qraf_hip::launch_qgemm_argmax(w_tiled, dtype, (int)out_dim, (int)in_dim, x_hi, x_lo, batch,
+                                                 (uint64_t*)keys, keys_bytes, tokens, qraf_hip::as_stream(stream),
+                                                 &done);
+    if (fused) *fused = done ? 1 : 0;
+    return rc;
 }
 
 }  // extern "C"

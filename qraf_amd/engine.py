@@ -155,6 +155,13 @@ class Engine:
         """Replay captured step graphs (default) or launch every step eagerly."""
         call("qraf_engine_set_graphs", self.h, int(bool(on)))
 
+    def set_keep_logits(self, keep: bool):
+        """False: steps that want only greedy tokens (step(..., logits=False),
+        step_async) take the head's argmax inside its GEMM and write no logits
+        (sample() and read_logits() then fail for such a step); True (default):
+        every step leaves its logits in HBM."""
+        call("qraf_engine_set_keep_logits", self.h, int(bool(keep)))
+
     def seq_create(self) -> int:
         i = C.c_int32()
         call("qraf_engine_seq_create", self.h, C.byref(i))
@@ -422,8 +429,11 @@ class BatchScheduler:
     sees tokens only (the logits in HBM already belong to the next step)."""
 
     def __init__(self, engine: Engine, max_batch: int | None = None, max_rows: int | None = None,
-                 prefill_chunk: int = 1, pipeline: bool = False):
+                 prefill_chunk: int = 1, pipeline: bool = False, keep_logits: bool = True):
         self.engine = engine
+        # False: a run whose requests are all greedy without penalty keeps no
+        # logits (the engine's greedy-only head); the observer then sees tokens only
+        self.keep_logits = keep_logits
         self.max_batch = max_batch or engine.max_batch
         self.max_rows = min(max_rows or self.max_batch, engine.max_batch)
         if self.max_rows < self.max_batch:
@@ -530,10 +540,18 @@ class BatchScheduler:
         return True
 
     def run(self):
-        if self.pipeline and all(r.penalty == 1.0 for r in list(self.pending) + self.active):
-            self._run_pipelined()
-        while self.step():
-            pass
+        no_penalty = all(r.penalty == 1.0 for r in list(self.pending) + self.active)
+        greedy_only = not self.keep_logits and no_penalty
+        if greedy_only:
+            self.engine.set_keep_logits(False)
+        try:
+            if self.pipeline and no_penalty:
+                self._run_pipelined()
+            while self.step():
+                pass
+        finally:
+            if greedy_only:
+                self.engine.set_keep_logits(True)
         return self.done
 
     def _run_pipelined(self):

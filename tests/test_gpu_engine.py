@@ -664,3 +664,52 @@ def test_smollm2_135m_c1_workload(hip):
             lg = m.forward(t, i)
         assert d >= 32 and gap(lg) <= 1e-3 * float(np.abs(lg).max()), f"streams differ at {d}, gap {gap(lg):.3e}"
     tf.engine.close()
+
+
+def test_greedy_only_head_same_streams(hip):
+    """keep_logits off (qraf_engine_set_keep_logits): greedy-only steps take
+    the head's argmax in its GEMM's epilogue and write no logits.  With 96
+    requests decoding together the head runs at 96-112 logit rows on a 16385-row
+    vocabulary (the pipelined form, fused), at fewer rows as requests finish
+    (not fused); every stream equals the run that keeps its logits, pipelined
+    and not, and a greedy-only step refuses sample / read_logits."""
+    from qraf_amd._lib import F32, HipError, Q4_0
+    from qraf_amd.engine import BatchScheduler, Engine, SamplingParams, model_config
+    cfg = model_config(16385, 256, 2, 4, 2, 512, 256, 1e6, 1e-6)
+    e = Engine(cfg, kv_dtype=F32, max_batch=128)
+    try:
+        e.generate_weights(Q4_0, Q4_0, Q4_0, True, True, 77)
+        e.finalize()
+        rng = np.random.default_rng(5)
+        work = [([int(t) for t in rng.integers(0, 16385, 4 + r % 5)], 6 + r % 7) for r in range(96)]
+        runs = {}
+        for keep in (True, False):
+            for pipeline in (False, True):
+                sched = BatchScheduler(e, max_batch=96, max_rows=128, prefill_chunk=8, pipeline=pipeline,
+                                       keep_logits=keep)
+                ids = [sched.submit(p, o) for p, o in work]
+                done = {r.id: r for r in sched.run()}
+                runs[keep, pipeline] = [done[i].generated for i in ids]
+        want = runs[True, False]
+        assert all(len(g) == o for g, (_, o) in zip(want, work))
+        for k, v in runs.items():
+            assert v == want, f"keep_logits={k[0]} pipeline={k[1]}: streams differ"
+        # a greedy-only step (80 logit rows) keeps no logits
+        seqs = [e.seq_create() for _ in range(80)]
+        e.set_keep_logits(False)
+        _, nx = e.step(seqs, [3] * 80, [0] * 80, logits=False, argmax=True)
+        with pytest.raises(HipError):
+            e.read_logits(0)
+        with pytest.raises(HipError):
+            e.sample(SamplingParams(0.0, 0, 1.0, 1.0), row0=0, rows=1)
+        # the same step with logits kept: the same tokens, and its logits readable
+        e.set_keep_logits(True)
+        seqs2 = [e.seq_create() for _ in range(80)]
+        lg, nx2 = e.step(seqs2, [3] * 80, [0] * 80, logits=True, argmax=True)
+        assert np.array_equal(nx, nx2)
+        assert np.array_equal(nx2, np.argmax(lg, axis=1).astype(np.uint32))
+        e.read_logits(0)
+        for s in seqs + seqs2:
+            e.seq_release(s)
+    finally:
+        e.close()

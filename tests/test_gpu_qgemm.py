@@ -9,6 +9,8 @@ The split itself is pinned bit-exactly (numpy's correctly rounded bf16 and
 fp16 conversions), and single-product GEMMs pin that the matrix cores add
 the two planes exactly, fp16 subnormals included.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -443,3 +445,65 @@ def test_planes_added_exactly(hip, N, M, tiled):
     assert np.array_equal(Y.view(np.uint32), want.view(np.uint32))
     ax = np.abs(X.astype(np.float64))[:, np.arange(N) % K]
     assert np.all(np.abs(Y - X[:, np.arange(N) % K].astype(np.float64)) <= 2.0 ** -20 * ax + 2.0 ** -25)
+
+ARGMAX_CASES = [
+    # (distinct weight rows R, K, batch): the matrix holds them twice, [W; W], plus one more row
+    (4100, 256, 100), (8192, 512, 65), (10000, 1024, 128), (16000, 2048, 200),  # wide pipelined form
+    (2500, 2048, 130),                                                           # narrow pipelined form
+    (150, 512, 64), (8192, 2048, 40),                                            # other forms: nothing fused
+]
+
+
+@pytest.mark.parametrize("dt", [po.Q8_0, po.Q4_0])
+@pytest.mark.parametrize("case", ARGMAX_CASES, ids=lambda c: "x".join(map(str, c)))
+def test_qgemm_tiled_argmax(hip, dt, case):
+    """The greedy head's fused argmax (qraf_hip_qgemm_tiled_argmax_dev) equals
+    Sampler::argmax (sampler.cpp:25-35, the first of the largest values:
+    numpy's argmax) of the unsplit tiled GEMM's own product, where the plan
+    is the pipelined form (fused = 1); elsewhere it launches nothing
+    (fused = 0, the tokens untouched).  The weights hold every row twice, at
+    i and R + i, so every logit ties with one 2R rows / many workgroups away
+    and only the smaller index wins; a last extra row makes the row count
+    ragged.  A keys buffer one entry short also launches nothing."""
+    from qraf_amd.backend import DeviceBuffer
+    call, lib = hip._lib.call, hip._lib.lib
+    R, K, M = case
+    N = 2 * R + 1
+    rng = np.random.default_rng(R + 5 * K + M + dt)
+    half = po.quantize(dt, (rng.standard_normal(R * K) * 0.02).astype(np.float32))
+    extra = po.quantize(dt, (rng.standard_normal(K) * 0.02).astype(np.float32))
+    wq = np.concatenate([half, half, extra])
+    X = rng.standard_normal((M, K)).astype(np.float32)
+    Y, _, _ = run_gemm(hip, wq, dt, N, K, X, tiled=True, split=False)
+    assert np.array_equal(Y[:, :R].view(np.uint32), Y[:, R:2 * R].view(np.uint32)), "repeated rows differ"
+    want = np.argmax(Y, axis=1)
+    assert np.all(want < R) or np.any(want == 2 * R)
+    dw, dx = DeviceBuffer.from_array(wq), DeviceBuffer.from_array(X)
+    dtl = DeviceBuffer(lib.qraf_hip_tiled_weight_bytes(dt, N, K))
+    call("qraf_hip_repack_tiles_dev", dw.ptr, dt, N, K, dtl.ptr, None)
+    dh, dl = DeviceBuffer(M * K * 2), DeviceBuffer(M * K * 2)
+    call("qraf_hip_split_bf16_dev", dx.ptr, dh.ptr, dl.ptr, M, K, None)
+    kb = lib.qraf_hip_qgemm_tiled_argmax_keys_bytes(N, M)
+    assert kb == -(-N // 128) * M * 8
+    keys = DeviceBuffer(kb)
+    sentinel = np.full(M, 0xFFFFFFFF, np.uint32)
+    dtok = DeviceBuffer.from_array(sentinel)
+    fused = C.c_int32(-1)
+    print(f"qgemm argmax N={N} K={K} M={M} dt={dt}", flush=True)
+    call("qraf_hip_qgemm_tiled_argmax_dev", dtl.ptr, dt, N, K, dh.ptr, dl.ptr, M, keys.ptr, kb, dtok.ptr,
+         C.byref(fused), None)
+    call("qraf_hip_stream_synchronize", None)
+    got = dtok.download(np.uint32, M)
+    pipelined = R != 150 and M > 64
+    assert fused.value == (1 if pipelined else 0)
+    if pipelined:
+        assert np.array_equal(got, want.astype(np.uint32)), f"first mismatch at row {np.argmax(got != want)}"
+        # a keys buffer too small for the plan's workgroups: nothing launched
+        dtok.upload(sentinel)
+        call("qraf_hip_qgemm_tiled_argmax_dev", dtl.ptr, dt, N, K, dh.ptr, dl.ptr, M, keys.ptr, 8, dtok.ptr,
+             C.byref(fused), None)
+        call("qraf_hip_stream_synchronize", None)
+        assert fused.value == 0
+    assert np.array_equal(dtok.download(np.uint32, M), sentinel)  # not fused: tokens untouched
+    for d in (dw, dx, dtl, dh, dl, keys, dtok):
+        d.free()
