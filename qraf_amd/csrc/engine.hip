@@ -32,6 +32,7 @@
 #include <vector>
 
 #include "common.h"
+#include "kv_pages.h"
 
 namespace qraf_hip {
 
@@ -399,17 +400,8 @@ struct qraf_engine {
     uint8_t* kpool = nullptr;
     uint8_t* vpool = nullptr;
     size_t layer_kv_bytes = 0;
-    std::vector<int32_t> free_pages;
+    KvPages pages;                    // sequences, their pages, the free list (host only)
     int32_t scratch_page = 0;         // one page past the pool's num_pages: written and read by pad rows only
-    struct Seq {
-        bool live = false;
-        int len = 0;
-        std::vector<int32_t> pages;
-        uint64_t stamp = 0;           // the step that last validated this sequence
-        int step_len = 0, step_pages = 0;
-    };
-    std::vector<Seq> seqs;
-    uint64_t step_stamp = 0;
     int row_pad = 16;                 // steps of more than 8 rows are padded to a multiple of this (graphs on)
     bool fuse_rope = true;            // one-row steps: RoPE/append fused into the QKV matvec
     bool fuse_swiglu = true;          // steps over 256 rows: SiLU-gate in the gate/up GEMM's epilogue
@@ -652,8 +644,10 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
         if (hipMemcpy(e->rope, tab.data(), tab.size() * 4, hipMemcpyHostToDevice) != hipSuccess)
             return fail(set_error(QRAF_HIP_ERR_HIP, "engine: rope table upload failed"));
     }
-    e->free_pages.resize(o.num_pages);
-    for (uint32_t i = 0; i < o.num_pages; i++) e->free_pages[i] = (int32_t)(o.num_pages - 1 - i);
+    {
+        const int rc = e->pages.init((int)o.num_pages, (int)o.page_size, e->capacity);
+        if (rc != QRAF_HIP_OK) return fail(rc);
+    }
     *out = e;
     return QRAF_HIP_OK;
 }
@@ -907,42 +901,24 @@ int qraf_engine_finalize(qraf_engine* e) {
 
 int qraf_engine_seq_create(qraf_engine* e, int32_t* id) {
     clear_error();
-    QH_REQUIRE(e && id, QRAF_HIP_ERR_INVALID, "seq_create: null argument");
-    for (size_t i = 0; i < e->seqs.size(); i++)
-        if (!e->seqs[i].live) {
-            e->seqs[i].live = true;
-            e->seqs[i].len = 0;
-            *id = (int32_t)i;
-            return QRAF_HIP_OK;
-        }
-    e->seqs.push_back({});
-    e->seqs.back().live = true;
-    *id = (int32_t)e->seqs.size() - 1;
-    return QRAF_HIP_OK;
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "seq_create: null engine");
+    return e->pages.seq_create(id);
 }
 
 int qraf_engine_seq_release(qraf_engine* e, int32_t id) {
     clear_error();
-    QH_REQUIRE(e && id >= 0 && id < (int32_t)e->seqs.size() && e->seqs[id].live, QRAF_HIP_ERR_INVALID,
-               "seq_release: unknown sequence %d", id);
-    qraf_engine::Seq& sq = e->seqs[id];
-    for (int32_t p : sq.pages) e->free_pages.push_back(p);
-    sq.pages.clear();
-    sq.len = 0;
-    sq.live = false;
-    return QRAF_HIP_OK;
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "seq_release: null engine");
+    return e->pages.seq_release(id);
 }
 
 int qraf_engine_seq_length(qraf_engine* e, int32_t id, int32_t* len) {
-    QH_REQUIRE(e && len && id >= 0 && id < (int32_t)e->seqs.size() && e->seqs[id].live, QRAF_HIP_ERR_INVALID,
-               "seq_length: unknown sequence %d", id);
-    *len = e->seqs[id].len;
-    return QRAF_HIP_OK;
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "seq_length: null engine");
+    return e->pages.seq_length(id, len);
 }
 
 int qraf_engine_free_pages(qraf_engine* e, int32_t* n) {
     QH_REQUIRE(e && n, QRAF_HIP_ERR_INVALID, "free_pages: null argument");
-    *n = (int32_t)e->free_pages.size();
+    *n = (int32_t)e->pages.free_pages();
     return QRAF_HIP_OK;
 }
 
@@ -964,40 +940,15 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     QH_REQUIRE(n > 0 && n <= (int32_t)e->o.max_batch, QRAF_HIP_ERR_INVALID, "step: %d rows (max_batch %u)", n,
                e->o.max_batch);
     const qraf_model_config& c = e->c;
-    const int ps = (int)e->o.page_size, MP = e->max_pages;
-    // validate, and count the pages each sequence needs (before allocating
-    // any): per sequence, the length and page count so far in this step
-    const uint64_t stamp = ++e->step_stamp;
-    int need_pages = 0;
+    const int MP = e->max_pages;
     for (int i = 0; i < n; i++) {
-        const int32_t id = seq_ids[i], p = positions[i];
-        QH_REQUIRE(id >= 0 && id < (int32_t)e->seqs.size() && e->seqs[id].live, QRAF_HIP_ERR_INVALID,
-                   "step: unknown sequence %d", id);
         const int32_t from = token_src ? token_src[i] : -1;
         QH_REQUIRE(from < e->last_logit_rows, QRAF_HIP_ERR_INVALID,
                    "step: row %d takes the token of logit row %d of the previous step, which left %d", i, from,
                    e->last_logit_rows);
         QH_REQUIRE(from >= 0 || tokens[i] < c.vocab_size, QRAF_HIP_ERR_INVALID, "Token %u >= vocab %u", tokens[i],
                    c.vocab_size);
-        QH_REQUIRE(p >= 0 && p < e->capacity, QRAF_HIP_ERR_INVALID, "step: position %d outside the cache (%d)", p,
-                   e->capacity);
-        qraf_engine::Seq& sq = e->seqs[id];
-        if (sq.stamp != stamp) {
-            sq.stamp = stamp;
-            sq.step_len = sq.len;
-            sq.step_pages = (int)sq.pages.size();
-        }
-        // rows of one sequence add positions without gaps (earlier rows count)
-        QH_REQUIRE(p <= sq.step_len, QRAF_HIP_ERR_INVALID, "step: sequence %d position %d skips past its length %d",
-                   id, p, sq.step_len);
-        sq.step_len = std::max(sq.step_len, p + 1);
-        const int pages = std::max(sq.step_pages, p / ps + 1);
-        need_pages += pages - sq.step_pages;
-        sq.step_pages = pages;
     }
-    QH_REQUIRE(need_pages <= (int)e->free_pages.size(), QRAF_HIP_ERR_NOMEM,
-               "step: KV page pool exhausted (%d pages needed, %zu free)", need_pages, e->free_pages.size());
-    e->last_logit_rows = 0;  // set again once this step's launches are issued
     // With step graphs, a step of more than 8 rows runs padded to a multiple
     // of row_pad rows (at most max_batch), and its logit rows likewise, so
     // that steps of nearby sizes share one graph: a pad row is token 0 at
@@ -1016,21 +967,19 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     int32_t* lrows = ctx + n_pad;
     int32_t* src = lrows + n_pad;
     int32_t* ptab = src + n_pad;
-    int step_ctx = 1;  // longest context of this step: sizes the attention grid (and skips the merge)
+    // the rows' sequences and positions checked, their new pages taken from
+    // the pool and their page-table rows written (nothing changes on failure);
+    // step_ctx, the longest context of this step, sizes the attention grid
+    // (and skips the merge)
+    int step_ctx = 1;
+    QH_TRY(e->pages.plan_step(n, seq_ids, positions, ptab, &step_ctx));
+    e->last_logit_rows = 0;  // set again once this step's launches are issued
     for (int i = 0; i < n; i++) {
-        qraf_engine::Seq& sq = e->seqs[seq_ids[i]];
-        while ((int)sq.pages.size() < positions[i] / ps + 1) {
-            sq.pages.push_back(e->free_pages.back());
-            e->free_pages.pop_back();
-        }
-        sq.len = std::max(sq.len, positions[i] + 1);
         src[i] = token_src ? token_src[i] : -1;
         tok[i] = src[i] >= 0 ? 0 : (int32_t)tokens[i];
         pos[i] = positions[i];
         ctx[i] = positions[i] + 1;
-        step_ctx = std::max(step_ctx, ctx[i]);
         if (!want_logits || want_logits[i]) lrows[n_logit_rows++] = i;
-        for (int j = 0; j < MP; j++) ptab[(size_t)i * MP + j] = j < (int)sq.pages.size() ? sq.pages[j] : 0;
     }
     for (int i = n; i < n_pad; i++) {
         tok[i] = 0;
