@@ -9,8 +9,9 @@ distinct weight copies larger than the 256 MB Infinity Cache, so every launch
 streams its weights from HBM.  The K timed steps are captured in one HIP
 graph (step by step, each step the four launches in order) and bracketed by
 HIP events on the stream they run on; `value` is the total algorithmic bytes
-of all K steps over the timed time.  Per-case figures come from a second
-timing, each case's K launches in a graph of their own between events.
+of all K steps over the timed time.  Per-case figures (and the roofline's
+kernel time) come from a second timing, each case's max(K, 200) launches in
+a graph of their own between events.
 Algorithmic bytes per launch = weight bytes + 4*K (x) + 4*N (y).
 
 The same JSON line also reports the other configurations of the metric:
@@ -163,12 +164,15 @@ def bench_matvec(args, rt):
         for c in cases:
             launch(c, i)
     stream.synchronize()
+    # per-case launches: at least 200, so that one graph launch's fixed cost
+    # (10-13 us of GPU time) stays within about 1% of a launch's figure
+    kc = max(args.steps, 200)
     graphs = []
     if not rt.get("eager"):
         for c in cases:
             g = Graph(stream)
             with g:
-                for i in range(args.steps):
+                for i in range(kc):
                     launch(c, args.warmup + i)
             graphs.append(g)
         for g in graphs:  # one untimed replay: graph upload stays out of the timed region
@@ -200,7 +204,7 @@ def bench_matvec(args, rt):
     total_bytes = sum(mv_bytes(c["dt"], c["n"], c["k"]) for c in cases) * args.steps
     if step_graph:
         step_graph.destroy()
-    # per case: each case's K launches in a graph of their own, between events
+    # per case: each case's kc launches in a graph of their own, between events
     ev = [Event() for _ in range(len(cases) + 1)]
     call("qraf_hip_device_synchronize")
     ev[0].record(stream)
@@ -208,7 +212,7 @@ def bench_matvec(args, rt):
         if graphs:
             graphs[i].launch()
         else:
-            for j in range(args.steps):
+            for j in range(kc):
                 launch(c, args.warmup + j)
         ev[i + 1].record(stream)
     stream.synchronize()
@@ -217,7 +221,7 @@ def bench_matvec(args, rt):
     for i, c in enumerate(cases):
         ms = ev[i].elapsed_ms(ev[i + 1])
         b = mv_bytes(c["dt"], c["n"], c["k"])
-        us = ms * 1e3 / args.steps
+        us = ms * 1e3 / kc
         per_case.append({"case": f"{c['name']} {c['n']}x{c['k']}", "us_per_launch": round(us, 3), "alg_bytes": b,
                          "GB_s": round(b / (us * 1e-6) / 1e9, 1),
                          "frac_hbm_peak": round(b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4), "pool_copies": c["copies"]})
@@ -228,7 +232,7 @@ def bench_matvec(args, rt):
     for c, p in zip(cases, per_case):
         b = mv_bytes(c["dt"], c["n"], c["k"])
         us = graph_time_us(rt, lambda i: call("qraf_hip_read_probe_dev", c["pool"].ptr + (i % c["copies"]) * c["wbytes"],
-                                              c["wbytes"], rp_out.ptr, stream.h), args.steps)
+                                              c["wbytes"], rp_out.ptr, stream.h), kc)
         p["plain_read_us"] = round(us, 3)
         p["plain_read_GB_s"] = round(c["wbytes"] / (us * 1e-6) / 1e9, 1)
         p["frac_of_plain_read"] = round(us / p["us_per_launch"], 4)  # plain-read time / matvec time
