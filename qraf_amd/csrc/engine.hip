@@ -409,6 +409,7 @@ struct qraf_engine {
     int32_t default_seq = -1;
     int last_logit_rows = 0;          // logit rows the last step left in `logits`
     bool keep_logits = true;          // false: greedy-only steps take the head's argmax without writing logits
+    int qbs = 0;                      // quant block size of every quantized tensor (0: none bound yet, then 32)
     bool last_logits_kept = true;     // the last step's logits are in `logits` (not a greedy-only step)
     qraf_engine_stats stats{};        // host-side time of qraf_engine_step
     uint8_t* samp = nullptr;          // sampling staging: recent tokens, counts, uniforms, tokens
@@ -486,10 +487,10 @@ static int ealloc(qraf_engine* e, void** p, size_t bytes) {
     return QRAF_HIP_OK;
 }
 
-static size_t dt_row_bytes(uint32_t dt, uint32_t cols) {
+static size_t dt_row_bytes(uint32_t dt, uint32_t cols, int bs) {
     if (dt == DT_F32) return (size_t)cols * 4;
     if (dt == DT_F16) return (size_t)cols * 2;
-    return q_row_bytes(dt, 32, cols);
+    return q_row_bytes(dt, bs, cols);
 }
 
 enum {
@@ -675,17 +676,30 @@ int qraf_engine_set_tensor(qraf_engine* e, const char* name, uint32_t dtype, uin
     QH_REQUIRE(!e->finalized, QRAF_HIP_ERR_STATE, "set_tensor: engine already finalized");
     QH_REQUIRE(dtype == DT_F32 || dtype == DT_F16 || dtype == DT_Q8_0 || dtype == DT_Q4_0, QRAF_HIP_ERR_DTYPE,
                "set_tensor %s: unsupported dtype %u", name, dtype);
-    QH_REQUIRE(dtype == DT_F32 || dtype == DT_F16 || block_size == 0 || block_size == 32, QRAF_HIP_ERR_DTYPE,
-               "set_tensor %s: quant block size %u (32 supported)", name, block_size);
     const qraf_model_config& c = e->c;
     const uint32_t D = c.hidden_size, F = c.intermediate_size;
+    // One quant block size per model (the reference's QrafModel keeps one
+    // scheme per dtype, quant.h): 32, or 4 / 8 / 16 dividing every matrix
+    // width, so that a row holds whole blocks; the model's first quantized
+    // tensor binds it.  Block sizes other than 32 run every projection on the
+    // matvec (the batched GEMM's tiles are 32 wide).
+    const int bs = block_size ? (int)block_size : 32;
+    if (dtype == DT_Q8_0 || dtype == DT_Q4_0) {
+        QH_REQUIRE(bs == 4 || bs == 8 || bs == 16 || bs == 32, QRAF_HIP_ERR_DTYPE,
+                   "set_tensor %s: quant block size %d (4, 8, 16 or 32 supported)", name, bs);
+        QH_REQUIRE(D % bs == 0 && F % bs == 0 && e->qd % bs == 0, QRAF_HIP_ERR_DTYPE,
+                   "set_tensor %s: quant block size %d does not divide the model's widths", name, bs);
+        QH_REQUIRE(!e->qbs || e->qbs == bs, QRAF_HIP_ERR_DTYPE,
+                   "set_tensor %s: quant block size %d differs from the model's %d", name, bs, e->qbs);
+        e->qbs = bs;
+    }
     const uint32_t rows = shape[0], cols = ndim > 1 ? shape[1] : 1;
     auto need = [&](uint32_t r, uint32_t cc) -> int {
         QH_REQUIRE(rows == r && (ndim == 1 ? cc == 1 : cols == cc), QRAF_HIP_ERR_INVALID,
                    "set_tensor %s: shape [%u, %u], expected [%u, %u]", name, rows, cols, r, cc);
-        QH_REQUIRE(bytes >= (uint64_t)r * dt_row_bytes(dtype, cc), QRAF_HIP_ERR_INVALID,
+        QH_REQUIRE(bytes >= (uint64_t)r * dt_row_bytes(dtype, cc, bs), QRAF_HIP_ERR_INVALID,
                    "set_tensor %s: %llu bytes, expected %zu", name, (unsigned long long)bytes,
-                   (size_t)r * dt_row_bytes(dtype, cc));
+                   (size_t)r * dt_row_bytes(dtype, cc, bs));
         return QRAF_HIP_OK;
     };
     auto upload = [&](void* dst, const void* src, size_t n) -> int {
@@ -699,7 +713,7 @@ int qraf_engine_set_tensor(qraf_engine* e, const char* name, uint32_t dtype, uin
 
     if (!strcmp(name, "model.embed_tokens.weight")) {
         QH_TRY(need(c.vocab_size, D));
-        const size_t n = (size_t)c.vocab_size * dt_row_bytes(dtype, D);
+        const size_t n = (size_t)c.vocab_size * dt_row_bytes(dtype, D, bs);
         QH_REQUIRE(!e->embed || e->dt_embed == dtype, QRAF_HIP_ERR_STATE, "embedding dtype changed");
         QH_TRY(ensure(&e->embed, n));
         e->dt_embed = dtype;
@@ -707,7 +721,7 @@ int qraf_engine_set_tensor(qraf_engine* e, const char* name, uint32_t dtype, uin
     }
     if (!strcmp(name, "lm_head.weight")) {
         QH_TRY(need(c.vocab_size, D));
-        const size_t n = (size_t)c.vocab_size * dt_row_bytes(dtype, D);
+        const size_t n = (size_t)c.vocab_size * dt_row_bytes(dtype, D, bs);
         QH_REQUIRE(!e->head || e->dt_head == dtype, QRAF_HIP_ERR_STATE, "lm_head dtype changed");
         QH_TRY(ensure(&e->head, n));
         e->dt_head = dtype;
@@ -767,7 +781,7 @@ int qraf_engine_set_tensor(qraf_engine* e, const char* name, uint32_t dtype, uin
         uint32_t& gdt = t.group == 0 ? L.dt_attn : L.dt_mlp;
         QH_REQUIRE(gdt == 0xFFFFFFFFu || gdt == dtype, QRAF_HIP_ERR_DTYPE,
                    "set_tensor %s: dtype %u differs from the other matrices of its group (%u)", name, dtype, gdt);
-        const size_t rb = dt_row_bytes(dtype, t.cc);
+        const size_t rb = dt_row_bytes(dtype, t.cc, bs);
         const size_t n = (size_t)t.r * rb;
         if (t.bit == T_Q || t.bit == T_K || t.bit == T_V) {
             if (L.wqkv && gdt != dtype) return set_error(QRAF_HIP_ERR_STATE, "dtype changed");
@@ -818,10 +832,13 @@ int qraf_engine_generate_weights(qraf_engine* e, uint32_t wdtype, uint32_t embed
         QH_CHECK_HIP(hipGetLastError());
         return QRAF_HIP_OK;
     };
+    QH_REQUIRE(!e->qbs || e->qbs == 32, QRAF_HIP_ERR_DTYPE, "generate_weights: tensors of block size %d bound", e->qbs);
+    e->qbs = 32;  // the device generator quantizes in blocks of 32
     e->dt_embed = embed_dtype;
-    QH_TRY(ealloc(e, (void**)&e->embed, (size_t)c.vocab_size * dt_row_bytes(embed_dtype, D)));
+    QH_TRY(ealloc(e, (void**)&e->embed, (size_t)c.vocab_size * dt_row_bytes(embed_dtype, D, 32)));
     QH_TRY(gen("model.embed_tokens.weight", e->embed, embed_dtype, (size_t)c.vocab_size * D));
-    const size_t rbD = dt_row_bytes(wdtype, D), rbF = dt_row_bytes(wdtype, F), rbQ = dt_row_bytes(wdtype, e->qd);
+    const size_t rbD = dt_row_bytes(wdtype, D, 32), rbF = dt_row_bytes(wdtype, F, 32),
+                 rbQ = dt_row_bytes(wdtype, e->qd, 32);
     uint8_t* tmp = nullptr;
     QH_TRY(ealloc(e, (void**)&tmp, std::max((size_t)F * rbD, (size_t)e->qd * 4)));
     for (uint32_t l = 0; l < c.num_layers; l++) {
@@ -859,7 +876,7 @@ int qraf_engine_generate_weights(qraf_engine* e, uint32_t wdtype, uint32_t embed
     QH_TRY(fill1(e->onorm, D));
     if (!tied) {
         e->dt_head = head_dtype;
-        QH_TRY(ealloc(e, (void**)&e->head, (size_t)c.vocab_size * dt_row_bytes(head_dtype, D)));
+        QH_TRY(ealloc(e, (void**)&e->head, (size_t)c.vocab_size * dt_row_bytes(head_dtype, D, 32)));
         QH_TRY(gen("lm_head.weight", e->head, head_dtype, (size_t)c.vocab_size * D));
     }
     QH_CHECK_HIP(hipStreamSynchronize(s));
@@ -880,7 +897,7 @@ int qraf_engine_finalize(qraf_engine* e) {
         const qraf_model_config& c = e->c;
         const int D = (int)c.hidden_size, F = (int)c.intermediate_size;
         auto tile = [&](const uint8_t* w, uint32_t dt, int N, int K, uint8_t** out) -> int {
-            if ((dt != DT_Q8_0 && dt != DT_Q4_0) || K % 32) return QRAF_HIP_OK;
+            if ((dt != DT_Q8_0 && dt != DT_Q4_0) || K % 32 || (e->qbs && e->qbs != 32)) return QRAF_HIP_OK;
             QH_TRY(ealloc(e, (void**)out, tiled_weight_bytes(dt, N, K)));
             return launch_repack_tiles(w, dt, N, K, *out, e->stream);
         };
@@ -940,7 +957,7 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     QH_REQUIRE(n > 0 && n <= (int32_t)e->o.max_batch, QRAF_HIP_ERR_INVALID, "step: %d rows (max_batch %u)", n,
                e->o.max_batch);
     const qraf_model_config& c = e->c;
-    const int MP = e->max_pages;
+    const int ps = (int)e->o.page_size, MP = e->max_pages;
     for (int i = 0; i < n; i++) {
         const int32_t from = token_src ? token_src[i] : -1;
         QH_REQUIRE(from < e->last_logit_rows, QRAF_HIP_ERR_INVALID,
@@ -1013,8 +1030,10 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     const float scale = 1.0f / sqrtf((float)hd);  // attention.cpp:122
 
     // 2-8 rows: the multi-vector matvec where it covers the shape and beats the GEMM
+    const int qbs = e->qbs ? e->qbs : 32;  // the model's quant block size
     auto use_bmv = [&](uint32_t dt, int N, int K, int rows) {
-        return rows >= 2 && rows <= MV_BATCH_SMALL && e->batch_mv && dt != DT_F32 && matvec_batch_ok(dt, K, rows) &&
+        return rows >= 2 && rows <= MV_BATCH_SMALL && e->batch_mv && dt != DT_F32 && qbs == 32 &&
+               matvec_batch_ok(dt, K, rows) &&
                (long long)rows * N * K <= MV_BATCH_WORK;
     };
     // y[n][N] = x[n][K] * W^T (+ add): matvec at batch 1, else the matrix-core GEMM
@@ -1047,10 +1066,10 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
                                          add ? add + (size_t)r * N : nullptr));
             return QRAF_HIP_OK;
         }
-        if (rows == 1 && rope) return launch_matvec_q(W, dt, 32, N, K, x, y, s, add, prep, rope, fused);
+        if (rows == 1 && rope) return launch_matvec_q(W, dt, qbs, N, K, x, y, s, add, prep, rope, fused);
         if (rows == 1 || !Wt) {
             for (int r = 0; r < rows; r++)
-                QH_TRY(launch_matvec_q(W, dt, 32, N, K, x + (size_t)r * K, y + (size_t)r * N, s,
+                QH_TRY(launch_matvec_q(W, dt, qbs, N, K, x + (size_t)r * K, y + (size_t)r * N, s,
                                        add ? add + (size_t)r * N : nullptr, prep));
             return QRAF_HIP_OK;
         }
@@ -1061,7 +1080,7 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     // The step's launches, stream-ordered: embedding, layers, head and argmax.
     // ctx_grid >= every row's context sizes the attention grid.
     auto enqueue = [&](int ctx_grid) -> int {
-        hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, 32, D, d_tok, d_src, e->amax,
+        hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, qbs, D, d_tok, d_src, e->amax,
                            e->h);
         QH_CHECK_HIP(hipGetLastError());
         // steps of 2-8 rows whose QKV and O projections go to the multi-vector

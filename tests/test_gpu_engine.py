@@ -713,3 +713,48 @@ def test_greedy_only_head_same_streams(hip):
             e.seq_release(s)
     finally:
         e.close()
+
+
+@pytest.mark.parametrize("bs,dt", [(8, po.Q8_0), (16, po.Q4_0), (4, po.Q4_0)])
+def test_quant_block_sizes(hip, bs, dt):
+    """Models quantized in blocks of 4, 8 or 16 (the reference reads the block
+    size from the file's quant scheme, backend.cpp:135 and quantize.cpp:105-183):
+    every projection on the matvec (the batched GEMM's tiles are 32 wide), the
+    embedding dequantized at that size.  One sequence decoded position by
+    position: logits within the bar of the oracle's model of the same block
+    size; three requests through the scheduler (steps of several rows, one
+    matvec per row): each stream equal to its independent greedy decode; a
+    tensor of another block size, or a size the engine does not take, refused."""
+    from qraf_amd._lib import HipError
+    from qraf_amd.engine import BatchScheduler, Engine
+    kw = dict(vocab=300, hidden=128, layers=2, heads=4, kv_heads=2, inter=192, max_seq=64, rope_theta=1e5, eps=1e-5,
+              wdtype=dt, tied=(dt == po.Q4_0))
+    m = po.Model(po.make_config(**kw, block_size=bs), 40 + bs)
+    e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=8)
+    try:
+        tensors = m.tensors()
+        for name, tdt, shape, data in tensors:
+            e.set_tensor(name, tdt, shape, data, block_size=bs)
+        # another block size, or one the engine does not take: refused
+        name, tdt, shape, data = next(t for t in tensors if t[0].endswith("mlp.down_proj.weight"))
+        for bad in (32 if bs != 32 else 8, 12):
+            with pytest.raises(HipError) as x:
+                e.set_tensor(name, tdt, shape, data, block_size=bad)
+            assert x.value.code == -2  # QRAF_HIP_ERR_DTYPE
+        e.finalize()
+        s = e.seq_create()
+        prompt = [5, 299, 0, 42, 42, 7]
+        for pos, tok in enumerate(prompt):
+            lg, _ = e.step([s], [tok], [pos], logits=True, argmax=False)
+            check_logits(lg[0], m.forward(tok, pos).astype(np.float64), f"block size {bs}, position {pos}")
+        e.seq_release(s)
+        L = po.lib()
+        prompts = [[L.or_gen_token(700 + r, i, kw["vocab"]) for i in range(3 + 2 * r)] for r in range(3)]
+        sched = BatchScheduler(e, max_batch=3, max_rows=8, prefill_chunk=4)
+        ids = [sched.submit(p, 6) for p in prompts]
+        done = {r.id: r for r in sched.run()}
+        for i, p in zip(ids, prompts):
+            assert done[i].generated == m.generate(p, 6, 1.0, eos=-1), f"block size {bs}"
+    finally:
+        e.close()
+        m.close()

@@ -281,3 +281,22 @@ def test_oracle_vs_reference_model_gqa8():
         assert same_bits(m.forward(tok, pos), rm.forward(tok, pos))
     rm.close()
     m.close()
+
+
+@needs_ref
+@pytest.mark.parametrize("bs,dt", [(8, po.Q8_0), (16, po.Q4_0), (4, po.Q4_0)])
+def test_oracle_vs_reference_model_block_sizes(bs, dt):
+    """The oracle's model at quant block sizes other than 32 (its weights
+    written to a .qraf file whose quant scheme carries the block size, read
+    back by the compiled reference's own loader): forward logits bit-identical
+    at every position."""
+    cfg = po.make_config(vocab=300, hidden=128, layers=2, heads=4, kv_heads=2, inter=192, max_seq=64,
+                         rope_theta=1e5, eps=1e-5, wdtype=dt, tied=(dt == po.Q4_0), block_size=bs)
+    m = po.Model(cfg, 40 + bs)
+    path = os.path.join(tempfile.mkdtemp(), "m.qraf")
+    m.write_qraf(path)
+    rm = po.RefModel(path, 300)
+    for pos, tok in enumerate([5, 299, 0, 42, 42, 7]):
+        assert same_bits(m.forward(tok, pos), rm.forward(tok, pos)), f"position {pos}"
+    rm.close()
+    m.close()
