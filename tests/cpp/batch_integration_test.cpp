@@ -172,6 +172,9 @@ private:
                 }
                 bool pipelined = !on_logits;
                 for (auto& r : active_) pipelined = pipelined && r->greedy();
+                // greedy-only steps need no logits: the head's argmax runs in
+                // its GEMM where it can; the sampling path keeps them
+                hip_check(qraf_engine_set_keep_logits(e_, pipelined ? 0 : 1));
                 if (pipelined) step_pipelined();
                 else step_sync();
                 retire();

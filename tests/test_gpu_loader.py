@@ -66,3 +66,28 @@ def test_malformed_file_is_refused_before_any_allocation(hip, tmp_path):
         Engine.from_file(path)
     assert e.value.code == ERR_FORMAT
     m.close()
+
+
+@pytest.mark.parametrize("bs,dt", [(8, po.Q8_0), (16, po.Q4_0)])
+def test_file_load_block_sizes(hip, tmp_path, bs, dt):
+    """A file whose quant scheme carries block size 8 or 16 (QrafWriter writes
+    the model's block size into the scheme record): qraf_engine_create_from_file
+    binds every tensor at that size, and its logits are within the engine bar of
+    the oracle's model of the same block size, which the reference's own loader
+    reproduces bit for bit."""
+    from qraf_amd.engine import Transformer
+    kw = dict(vocab=300, hidden=128, layers=2, heads=4, kv_heads=2, inter=192, max_seq=64, rope_theta=1e5, eps=1e-5,
+              wdtype=dt, tied=(dt == po.Q4_0), qkv_bias=(dt == po.Q4_0))
+    m = po.Model(po.make_config(**kw, block_size=bs), 60 + bs)
+    path = str(tmp_path / f"bs{bs}.qraf")
+    m.write_qraf(path)
+    tf = Transformer.from_file(path)
+    ref = po.RefModel(path, kw["vocab"])
+    m.reset()
+    for pos, t in enumerate([5, 299, 0, 42, 42, 7, 100, 3]):
+        got, want = tf.forward(t, pos), m.forward(t, pos)
+        check_logits(got, want, f"block size {bs} pos {pos}")
+        assert np.array_equal(ref.forward(t, pos), want), f"block size {bs} pos {pos}: reference loader vs oracle"
+    ref.close()
+    tf.engine.close()
+    m.close()
