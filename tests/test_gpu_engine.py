@@ -147,54 +147,6 @@ def test_greedy_streams_32_tokens(hip, kv):
     tf.engine.close()
 
 
-def c1_prompt(vocab=49152):
-    """The benchmark's batch-1 workload prompt: 32 tokens uniform over the
-    vocabulary from numpy's default generator seeded with 1 (bench.py draws
-    the same)."""
-    return np.random.default_rng(1).integers(0, vocab, 32).tolist()
-
-
-def test_smollm2_135m_c1_workload(hip):
-    """The batch-1 benchmark workload exactly: SmolLM2-135M architecture, Q8_0
-    weights of seed 1, the benchmark's 32-token prompt fed token by token, then
-    128 greedy tokens.  Every logit vector of the prompt and of the first 32
-    generated tokens within 1e-3 relative / 1e-4 absolute of the oracle's,
-    those 32 tokens identical; the whole 128-token stream equal to the
-    oracle's, or (were float ordering ever to flip a near-tie) first differing
-    past token 32 at a position where the oracle's own top-2 gap is under
-    1e-3 of its top logit."""
-    from qraf_amd.engine import InferenceEngine
-    kw = dict(vocab=49152, hidden=576, layers=30, heads=9, kv_heads=3, inter=1536, max_seq=2048, rope_theta=1e5,
-              eps=1e-5, wdtype=po.Q8_0)
-    m = oracle_model(kw, 1)
-    tf = upload(m, kw)
-    prompt = c1_prompt(kw["vocab"])
-    print("C1 workload: 32-token prompt, 128 greedy tokens", flush=True)
-    m.reset()
-    tf.reset()
-    toks = []
-    ref = None
-    for i, t in enumerate(prompt):
-        ref = m.forward(t, i)
-        check_logits(tf.forward(t, i), ref, f"prompt pos {i}")
-    for j in range(32):  # the first 32 generated tokens, each from logits checked against the oracle's
-        nxt = int(np.argmax(ref))
-        toks.append(nxt)
-        ref = m.forward(nxt, len(prompt) + j)
-        check_logits(tf.forward(nxt, len(prompt) + j), ref, f"generated token {j}")
-    want = m.generate(prompt, 128, 1.0, eos=-1)
-    assert want[:32] == toks
-    got = InferenceEngine(tf, eos_token=None).generate_tokens(prompt, 128, repetition_penalty=1.0)
-    assert len(got) == 128 and got[:32] == want[:32]
-    if got != want:
-        d = next(i for i in range(128) if got[i] != want[i])
-        m.reset()
-        for i, t in enumerate(prompt + want[:d]):
-            lg = m.forward(t, i)
-        assert d >= 32 and gap(lg) <= 1e-3 * float(np.abs(lg).max()), f"streams differ at {d}, gap {gap(lg):.3e}"
-    tf.engine.close()
-
-
 @pytest.mark.parametrize("pipeline", [False, True])
 def test_batched_step_equals_single_sequence_decode(hip, pipeline):
     """Several sequences of different lengths advanced together (GEMM path,
@@ -758,3 +710,4 @@ def test_quant_block_sizes(hip, bs, dt):
     finally:
         e.close()
         m.close()
+
