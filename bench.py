@@ -546,6 +546,11 @@ def bench_decode_b1(args, rt):
         e.seq_release(s)
         return t1 - t0, t2 - t1, toks
 
+    # the per-launch floor: empty kernels back to back in one graph, as a step's
+    # 150 layer kernels run (1 workgroup, and 256 as the decode matvecs launch)
+    floor = {f"{w}_wg": round(graph_time_us(rt, lambda i, w=w: rt["call"]("qraf_hip_launch_floor_dev", w,
+                                                                          rt["stream"].h), 150), 3)
+             for w in (1, 256)}
     run()  # warm-up
     pre, dec, toks = run()
     _, dec_u, toks_u = run(pipeline=False)
@@ -574,6 +579,7 @@ def bench_decode_b1(args, rt):
                                 "prefill_plus_decode_tok_s": round(n_gen / (pre_b + dec_b), 1),
                                 "same_tokens": toks_b == toks},
             "decode_GB_s": round(gbs, 1), "first_tokens": toks[:8],
+            "launch_floor_us": floor, "launches_per_token": 5 * SMOL["layers"] + 3,
             "reference_defaults": {"repetition_penalty": 1.1, "eos": 2, "generated": len(out_p),
                                    "tok_s": round(len(out_p) / el_p, 1),
                                    "note": "generated / (prefill + decode) as inference.cpp:150-153; one device "

@@ -68,6 +68,11 @@ int qraf_hip_memset(void* dev_ptr, int value, uint64_t bytes);
  * the reference (a measurement aid). */
 int qraf_hip_read_probe_dev(const void* dev_ptr, uint64_t bytes, float* out, void* stream);
 uint64_t qraf_hip_read_probe_out_bytes(void);
+/* One launch of an empty kernel over `workgroups` (1..65536) 64-thread
+ * workgroups on `stream`: the fixed cost every launch pays, measured the way
+ * a step's kernels run (back to back in a graph).  No counterpart in the
+ * reference: a measurement entry point. */
+int qraf_hip_launch_floor_dev(int32_t workgroups, void* stream);
 int qraf_hip_stream_create(void** stream);
 int qraf_hip_stream_destroy(void* stream);
 int qraf_hip_stream_synchronize(void* stream);

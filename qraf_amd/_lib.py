@@ -34,6 +34,7 @@ SIGNATURES = {
     "qraf_hip_memcpy_d2d": (C.c_int, [vp, vp, C.c_uint64, vp]),
     "qraf_hip_read_probe_dev": (C.c_int, [vp, C.c_uint64, vp, vp]),
     "qraf_hip_read_probe_out_bytes": (C.c_uint64, []),
+    "qraf_hip_launch_floor_dev": (C.c_int, [C.c_int32, vp]),
     "qraf_hip_memset": (C.c_int, [vp, C.c_int, C.c_uint64]),
     "qraf_hip_stream_create": (C.c_int, [C.POINTER(vp)]),
     "qraf_hip_stream_destroy": (C.c_int, [vp]),

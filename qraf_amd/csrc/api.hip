@@ -131,6 +131,9 @@ int qraf_hip_read_probe_dev(const void* p, uint64_t bytes, float* out, void* str
     return qraf_hip::launch_read_probe(p, bytes, out, as_stream(stream));
 }
 uint64_t qraf_hip_read_probe_out_bytes(void) { return qraf_hip::read_probe_out_floats() * sizeof(float); }
+int qraf_hip_launch_floor_dev(int32_t workgroups, void* stream) {
+    return qraf_hip::launch_empty(workgroups, as_stream(stream));
+}
 int qraf_hip_memset(void* p, int v, uint64_t n) {
     if (n) QH_CHECK_HIP(hipMemset(p, v, n));
     return QRAF_HIP_OK;

@@ -102,6 +102,7 @@ int launch_dot(const float* a, const float* b, int n, float* out, hipStream_t s)
 int launch_ew(int op, float* x, const float* y, float sc, int n, hipStream_t s);
 // streaming read of `bytes` (the plain-read ceiling); out: read_probe_out_floats() floats
 int launch_read_probe(const void* p, size_t bytes, float* out, hipStream_t s);
+int launch_empty(int wgs, hipStream_t s);
 size_t read_probe_out_floats();
 
 __device__ __forceinline__ uint32_t f32_to_bf16_rne(float f) {

@@ -146,6 +146,17 @@ __global__ __launch_bounds__(RP_WG) void read_probe_kernel(const f32x4* __restri
 
 size_t read_probe_out_floats() { return (size_t)RP_WGS * (RP_WG / 64); }
 
+// An empty kernel: the fixed cost of one launch of `wgs` 64-thread
+// workgroups, the floor under every kernel of a latency-bound step.
+__global__ __launch_bounds__(64) void empty_kernel() {}
+
+int launch_empty(int wgs, hipStream_t s) {
+    QH_REQUIRE(wgs > 0 && wgs <= 65536, QRAF_HIP_ERR_INVALID, "empty launch: %d workgroups", wgs);
+    hipLaunchKernelGGL(empty_kernel, dim3(wgs), dim3(64), 0, s);
+    QH_CHECK_HIP(hipGetLastError());
+    return QRAF_HIP_OK;
+}
+
 int launch_read_probe(const void* p, size_t bytes, float* out, hipStream_t s) {
     QH_REQUIRE(p && out && bytes > 0 && bytes % 16 == 0 && ((uintptr_t)p & 15) == 0, QRAF_HIP_ERR_INVALID,
                "read probe: null or misaligned pointer, or bytes not a positive multiple of 16");
