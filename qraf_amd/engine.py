@@ -411,7 +411,7 @@ class BatchScheduler:
     tokens and frees its KV pages for the next admission.  Every request's
     token stream equals an independent greedy decode of its prompt (the
     reference's scheduler runs requests one at a time over one shared cache,
-    F3 in the survey, so it offers no batched numerics to mirror).  With the
+    batch_scheduler.h:187-228, so it offers no batched numerics to mirror).  With the
     defaults (prefill_chunk 1, max_rows = max_batch) every active request
     feeds exactly one token per step.
 
