@@ -15,7 +15,9 @@ namespace qraf_hip {
 
 // Per-process device state.  One default stream per device the library was
 // initialised on; op-level calls serialise on g_mu (the reference's dispatch
-// layer is single-threaded as well, backend.cpp:16).
+// layer is single-threaded as well, backend.cpp:16).  g_dev itself is guarded
+// by g_dev_mu, since device-level calls with a NULL stream look up their
+// device's default stream without taking g_mu.
 struct DeviceState {
     hipStream_t stream = nullptr;
     // op-level staging buffers, grown on demand
@@ -23,6 +25,7 @@ struct DeviceState {
     size_t cap[3] = {0, 0, 0};
 };
 static std::mutex g_mu;
+static std::mutex g_dev_mu;
 static std::map<int, DeviceState> g_dev;
 struct Registered {
     void* dev;
@@ -30,34 +33,39 @@ struct Registered {
 };
 static std::map<const void*, Registered> g_weights;  // host ptr -> HBM copy
 
-static int ensure_init() {
-    int d = 0;
-    QH_CHECK_HIP(hipGetDevice(&d));
-    auto it = g_dev.find(d);
-    if (it == g_dev.end() || !it->second.stream) {
-        hipStream_t s;
-        QH_CHECK_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
-        g_dev[d].stream = s;
-    }
-    return QRAF_HIP_OK;
-}
-
-hipStream_t default_stream() {
-    int d = 0;
-    if (hipGetDevice(&d) != hipSuccess) return nullptr;
-    auto it = g_dev.find(d);
-    if (it == g_dev.end() || !it->second.stream) {
-        if (ensure_init() != QRAF_HIP_OK) return nullptr;
-        it = g_dev.find(d);
-    }
-    return it->second.stream;
-}
-
-// Staging buffer `i` of at least `bytes` on the current device.
-static int staging(int i, size_t bytes, void** out) {
+// The current device's default stream, created on first use (g_dev_mu held).
+static int stream_of_current(hipStream_t* out) {
     int d = 0;
     QH_CHECK_HIP(hipGetDevice(&d));
     DeviceState& st = g_dev[d];
+    if (!st.stream) QH_CHECK_HIP(hipStreamCreateWithFlags(&st.stream, hipStreamNonBlocking));
+    *out = st.stream;
+    return QRAF_HIP_OK;
+}
+
+static int ensure_init() {
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    hipStream_t s;
+    return stream_of_current(&s);
+}
+
+hipStream_t default_stream() {
+    std::lock_guard<std::mutex> lk(g_dev_mu);
+    hipStream_t s = nullptr;
+    return stream_of_current(&s) == QRAF_HIP_OK ? s : nullptr;
+}
+
+// Staging buffer `i` of at least `bytes` on the current device (callers hold
+// g_mu, which serialises the buffers' use; g_dev_mu covers the lookup).
+static int staging(int i, size_t bytes, void** out) {
+    int d = 0;
+    QH_CHECK_HIP(hipGetDevice(&d));
+    DeviceState* stp;
+    {
+        std::lock_guard<std::mutex> lk(g_dev_mu);
+        stp = &g_dev[d];  // std::map nodes stay where they are when others are inserted
+    }
+    DeviceState& st = *stp;
     if (st.cap[i] < bytes) {
         if (st.buf[i]) QH_CHECK_HIP(hipFree(st.buf[i]));
         st.buf[i] = nullptr;
@@ -173,6 +181,7 @@ int qraf_hip_event_record(void* e, void* s) {
     return QRAF_HIP_OK;
 }
 int qraf_hip_event_elapsed_ms(void* a, void* b, float* ms) {
+    QH_REQUIRE(a && b && ms, QRAF_HIP_ERR_INVALID, "null event or out pointer");
     QH_CHECK_HIP(hipEventSynchronize((hipEvent_t)b));
     QH_CHECK_HIP(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
     return QRAF_HIP_OK;
