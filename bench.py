@@ -509,6 +509,8 @@ def bench_decode_b1(args, rt):
     e.generate_weights(Q8, Q8, Q8, False, False, 1)
     e.finalize()
     e.set_graphs(not args.no_graphs)
+    if args.fusion >= 0:
+        e.set_fusion(args.fusion)
     prompt = c1_prompt()
     n_gen = 128
 
@@ -1067,6 +1069,8 @@ def main():
                     help="batched engine steps of more than 8 rows run padded to a multiple of this (1: off)")
     ap.add_argument("--gemm-form", default="auto", choices=["auto", "pipelined", "wave_split", "row_split"],
                     help="tiled batched-GEMM form for every leg (auto: the library's per-shape choice)")
+    ap.add_argument("--fusion", type=int, default=-1,
+                    help="engine fusion flags of the batch-1 decode leg (qraf_engine_set_fusion; -1: the defaults)")
     ap.add_argument("--attn-form", type=int, default=0,
                     help="attention work form for every leg: 0 auto, 1 chunk grid, 2 balanced split, 3 VALU kernel")
     args = ap.parse_args()
