@@ -62,3 +62,11 @@ def test_noalloc_attention_refuses_shapes_beyond_its_scratch():
                                                   0.1, max_ctx, None, None)
     assert rc == ERR_INVALID
     assert b"scratch holds" in lib.qraf_hip_last_error()
+
+
+def test_integration_guide_names_every_declared_symbol():
+    """INTEGRATION.md, the guide a reference maintainer binds from, names every
+    entry point the header declares."""
+    guide = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    missing = [s for s in sorted(declared_symbols()) if not re.search(r"\b" + s + r"\b", guide)]
+    assert not missing, missing
