@@ -711,3 +711,35 @@ def test_quant_block_sizes(hip, bs, dt):
         e.close()
         m.close()
 
+
+
+@pytest.mark.parametrize("graphs", [True, False])
+def test_long_context_batch1_decode(hip, graphs):
+    """One sequence decoded token by token to 1,100 positions (f32 pages,
+    Q8 weights, head_dim 64, 2 KV heads): one-row steps whose attention
+    leaves the single-chunk kernel at 256 positions for the chunked form and
+    its merge, with step graphs captured at each context bound (256, 512,
+    1,024, 2,048) or every step eager.  Logits at every position within the
+    1e-3 / 1e-4 bar of the oracle's forward on the same tokens."""
+    from qraf_amd.engine import Engine
+    kw = dict(vocab=500, hidden=256, layers=2, heads=4, kv_heads=2, inter=512, max_seq=2048, rope_theta=1e4,
+              eps=1e-5, wdtype=po.Q8_0)
+    m = oracle_model(kw, 61)
+    e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=1)
+    try:
+        for name, dt, shape, data in m.tensors():
+            e.set_tensor(name, dt, shape, data)
+        e.finalize()
+        e.set_graphs(graphs)
+        L = po.lib()
+        s = e.seq_create()
+        m.reset()
+        print(f"long context decode, graphs {graphs}", flush=True)
+        for pos in range(1100):
+            tok = L.or_gen_token(61, pos, kw["vocab"])
+            lg, _ = e.step([s], [tok], [pos], logits=True, argmax=False)
+            check_logits(lg[0], m.forward(tok, pos), f"pos {pos}")
+        assert e.seq_length(s) == 1100
+    finally:
+        e.close()
+        m.close()
