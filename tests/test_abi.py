@@ -70,3 +70,12 @@ def test_integration_guide_names_every_declared_symbol():
     guide = open(os.path.join(ROOT, "INTEGRATION.md")).read()
     missing = [s for s in sorted(declared_symbols()) if not re.search(r"\b" + s + r"\b", guide)]
     assert not missing, missing
+
+
+def test_launch_floor_refuses_workgroup_counts_outside_its_range():
+    """qraf_hip_launch_floor_dev takes 1..65536 workgroups; other counts are
+    refused before anything is launched (no GPU needed)."""
+    from qraf_amd._lib import ERR_INVALID, lib
+    for w in (0, -1, 65537):
+        assert lib.qraf_hip_launch_floor_dev(w, None) == ERR_INVALID
+        assert b"workgroups" in lib.qraf_hip_last_error()

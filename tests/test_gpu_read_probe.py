@@ -29,3 +29,25 @@ def test_read_probe_refusals(hip):
     for bad in (0, 20):
         with pytest.raises(HipError):
             call("qraf_hip_read_probe_dev", d.ptr, bad, out.ptr, None)
+
+
+@pytest.mark.parametrize("wgs", [1, 256, 65536])
+def test_launch_floor_runs_in_a_graph(hip, wgs):
+    """The per-launch floor's empty kernel, as bench.py times it: launched
+    eagerly and replayed in a captured graph on a stream of its own, every
+    launch completing."""
+    from qraf_amd.backend import Graph, Stream
+    call = hip._lib.call
+    s = Stream()
+    call("qraf_hip_launch_floor_dev", wgs, s.h)
+    call("qraf_hip_stream_synchronize", s.h)
+    with Graph(s) as g:
+        for _ in range(8):
+            call("qraf_hip_launch_floor_dev", wgs, s.h)
+    try:
+        for _ in range(3):
+            g.launch()
+        call("qraf_hip_stream_synchronize", s.h)
+    finally:
+        g.destroy()
+        s.destroy()
