@@ -743,3 +743,43 @@ def test_long_context_batch1_decode(hip, graphs):
     finally:
         e.close()
         m.close()
+
+
+def test_two_engines_in_two_threads(hip):
+    """Two engines (different models, each with its own stream, pages and
+    step graphs) decoding at the same time from two host threads (ctypes
+    releases the interpreter lock in every library call): each thread's
+    greedy stream and final logits equal the same engine's run alone."""
+    import threading
+    from qraf_amd.engine import InferenceEngine
+    names = ["q8_hd64_gqa3", "q4_gqa8_hd128"]
+    models = {n: oracle_model(*SMALL[n]) for n in names}
+    prompts = {n: [po.lib().or_gen_token(SMALL[n][1] + 3, i, SMALL[n][0]["vocab"]) for i in range(10)] for n in names}
+
+    def run(n, out):
+        tf = upload(models[n], SMALL[n][0])
+        try:
+            toks = InferenceEngine(tf, eos_token=None).generate_tokens(prompts[n], 48, repetition_penalty=1.0)
+            tf.reset()
+            lg = None
+            for i, t in enumerate(prompts[n] + toks[:16]):
+                lg = tf.forward(t, i)
+            out[n] = (toks, lg.copy())
+        finally:
+            tf.engine.close()
+
+    alone = {}
+    for n in names:
+        run(n, alone)
+    together = {}
+    threads = [threading.Thread(target=run, args=(n, together)) for n in names]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    for n in names:
+        assert n in together, f"{n}: thread did not finish"
+        assert together[n][0] == alone[n][0], n
+        assert np.array_equal(together[n][1].view(np.uint32), alone[n][1].view(np.uint32)), n
+    for m in models.values():
+        m.close()
