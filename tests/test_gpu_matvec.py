@@ -141,6 +141,46 @@ def test_matvec_device_level_matches_op_level(hip):
         assert np.array_equal(dy.download(np.float32, n).view(np.uint32), y.view(np.uint32))
 
 
+def test_matvec_from_several_host_threads(hip):
+    """Four host threads at once, each alternating the op-level matvec (host
+    pointers, serialised inside the library) with the device-level one on the
+    library's default stream (NULL stream) into buffers of its own: every
+    result equals the single-threaded one bit for bit."""
+    import threading
+    from qraf_amd.backend import DeviceBuffer
+    n, k = 1024, 2048
+    rng = np.random.default_rng(21)
+    wq = po.quantize(po.Q8_0, (rng.standard_normal(n * k) * 0.02).astype(np.float32))
+    xs = [rng.standard_normal(k).astype(np.float32) for _ in range(4)]
+    want = []
+    for x in xs:
+        y = np.zeros(n, np.float32)
+        hip.backend.dispatch_matvec_q(wq, 0, po.Q8_0, 32, n, k, x, y)
+        want.append(y)
+    dw = DeviceBuffer.from_array(wq)
+    bad = []
+
+    def work(i):
+        dx, dy = DeviceBuffer.from_array(xs[i]), DeviceBuffer(n * 4)
+        for it in range(20):
+            y = np.zeros(n, np.float32)
+            hip.backend.dispatch_matvec_q(wq, 0, po.Q8_0, 32, n, k, xs[i], y)
+            hip._lib.call("qraf_hip_matvec_q_dev", dw.ptr, po.Q8_0, 32, n, k, dx.ptr, dy.ptr, None)
+            hip._lib.call("qraf_hip_stream_synchronize", None)
+            got = dy.download(np.float32, n)
+            if not (np.array_equal(y.view(np.uint32), want[i].view(np.uint32)) and
+                    np.array_equal(got.view(np.uint32), want[i].view(np.uint32))):
+                bad.append((i, it))
+
+    threads = [threading.Thread(target=work, args=(i,)) for i in range(4)]
+    for th in threads:
+        th.start()
+    for th in threads:
+        th.join(timeout=120)
+    assert not any(th.is_alive() for th in threads)
+    assert not bad, bad
+
+
 def test_matvec_error_codes(hip):
     x = np.ones(64, np.float32)
     y = np.zeros(4, np.float32)
