@@ -76,6 +76,8 @@ CASES = [
     (2048, 2048, 128), (256, 2048, 64), (11008, 2048, 32), (2048, 11008, 8), (2048, 11008, 128),
     (2560, 2048, 17), (100, 64, 1), (65, 96, 3), (1000, 576, 100), (576, 1536, 16), (300, 2048, 80),
     (700, 4096, 48), (130, 128, 2), (2048, 2048, 200), (513, 1024, 257),
+    # the largest steps the engine takes (max_batch up to 1024 rows)
+    (2560, 2048, 512), (576, 1536, 1024),
 ]
 
 
