@@ -783,3 +783,50 @@ def test_two_engines_in_two_threads(hip):
         assert np.array_equal(together[n][1].view(np.uint32), alone[n][1].view(np.uint32)), n
     for m in models.values():
         m.close()
+
+
+def test_1024_row_prefill_step(hip):
+    """The engine's largest step: four 256-token prompts as one 1,024-row step
+    (the gate/up GEMM with the SiLU-gate epilogue, every projection at 1,024
+    rows), then eight 4-row decode steps.  Each sequence's last prompt row's
+    logits within the 1e-3 / 1e-4 bar of the oracle's forward of that prompt
+    alone, and its nine greedy tokens equal to the oracle's decode of it."""
+    from qraf_amd.engine import Engine
+    kw, seed = SMALL["q4_gqa8_hd128"]
+    kw = dict(kw, max_seq=512)
+    m = oracle_model(kw, seed)
+    e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=1024)
+    try:
+        for name, dt, shape, data in m.tensors():
+            e.set_tensor(name, dt, shape, data)
+        e.finalize()
+        L = po.lib()
+        prompts = [[L.or_gen_token(seed + 50 + r, i, kw["vocab"]) for i in range(256)] for r in range(4)]
+        sids = [e.seq_create() for _ in range(4)]
+        rows_s, rows_t, rows_p, want = [], [], [], []
+        for s, p in zip(sids, prompts):
+            rows_s += [s] * 256
+            rows_t += p
+            rows_p += list(range(256))
+            want += [0] * 255 + [1]
+        lg, nx = e.step(rows_s, rows_t, rows_p, want_logits=want, logits=True, argmax=True)
+        refs = []
+        for r, p in enumerate(prompts):
+            m.reset()
+            for i, t in enumerate(p):
+                ref = m.forward(t, i)
+            check_logits(lg[r], ref, f"sequence {r} prompt end")
+            assert int(nx[r]) == int(np.argmax(ref)), f"sequence {r} first token"
+            refs.append(m.generate(p, 9, 1.0, eos=-1))
+        toks = [int(t) for t in nx]
+        streams = [[t] for t in toks]
+        for k in range(8):
+            lg, nx = e.step(sids, toks, [256 + k] * 4, logits=True, argmax=True)
+            toks = [int(t) for t in nx]
+            for r in range(4):
+                streams[r].append(toks[r])
+        for r in range(4):
+            assert streams[r] == refs[r], f"sequence {r}"
+    finally:
+        e.close()
+        m.close()
