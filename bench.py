@@ -584,8 +584,8 @@ def bench_decode_b1(args, rt):
             "launch_floor_us": floor, "launches_per_token": 5 * SMOL["layers"] + 3,
             "reference_defaults": {"repetition_penalty": 1.1, "eos": 2, "generated": len(out_p),
                                    "tok_s": round(len(out_p) / el_p, 1),
-                                   "note": "generated / (prefill + decode) as inference.cpp:150-153; one device "
-                                           "sampler call per token after its step"}}
+                                   "note": "generated / (prefill + decode) as inference.cpp:150-153; the penalty "
+                                           "applied on the device from counts of the fed tokens, decode pipelined"}}
 
 
 def cpu_decode_b1(gpu_tokens=None, n_tokens=128):

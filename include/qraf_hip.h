@@ -536,6 +536,23 @@ int qraf_engine_set_row_padding(qraf_engine* engine, int32_t rows);
  * products as at batch 1, summed in another order than the GEMM's).  No
  * reference counterpart (launch-count and traffic measures). */
 int qraf_engine_set_fusion(qraf_engine* engine, int32_t flags);
+/* Repetition penalty on the device for one sequence, set before its first
+ * step (QRAF_HIP_ERR_STATE after): from then on every token the sequence is
+ * fed (prompt rows, decode rows, tokens taken on the device from a previous
+ * step's argmax) is counted on the device, and the greedy token of each of
+ * its logit rows (next_tokens of qraf_engine_step, the tokens of
+ * qraf_engine_step_async / _step_collect) is Sampler::argmax after
+ * Sampler::apply_repetition_penalty (sampler.cpp:25-49) with the prompt and
+ * every fed token as the recent list, as InferenceEngine::generate_tokens
+ * builds it (inference.cpp:104-125): the same token as qraf_engine_sample with
+ * that list, without the list crossing PCIe, so penalised greedy decoding
+ * can run pipelined.  The logits the step leaves or returns stay
+ * unpenalised.  penalty 1 turns it off.  At most max_batch penalised
+ * sequences at a time (QRAF_HIP_ERR_NOMEM beyond); vocabularies that are a
+ * multiple of 4 only (QRAF_HIP_ERR_INVALID otherwise).  The first call
+ * allocates max_batch * vocab * 4 bytes of counts and drops the captured
+ * step graphs.  No reference counterpart as an entry point. */
+int qraf_engine_set_repetition_penalty(qraf_engine* engine, int32_t seq_id, float penalty);
 /* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)
  * on the engine's default sequence, and Transformer::reset() (:641-643). */
 int qraf_engine_forward(qraf_engine* engine, uint32_t token, int32_t pos, float* logits);

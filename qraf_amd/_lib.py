@@ -142,6 +142,7 @@ SIGNATURES.update({
     "qraf_engine_set_keep_logits": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_set_row_padding": (C.c_int, [vp, C.c_int32]),
     "qraf_engine_set_fusion": (C.c_int, [vp, C.c_int32]),
+    "qraf_engine_set_repetition_penalty": (C.c_int, [vp, C.c_int32, C.c_float]),
     "qraf_engine_forward": (C.c_int, [vp, C.c_uint32, C.c_int32, fp]),
     "qraf_engine_read_logits": (C.c_int, [vp, C.c_int32, C.c_int32, fp]),
     "qraf_engine_get_stats": (C.c_int, [vp, vp, C.c_int32]),

@@ -24,6 +24,8 @@
 // streaming matvec, larger batches on the matrix-core GEMM.
 #include <limits.h>
 #include <math.h>
+
+#include <cmath>
 #include <string.h>
 
 #include <algorithm>
@@ -42,12 +44,17 @@ namespace qraf_hip {
 // transformer.cpp:34-39, :577): dequantised values (f32)q * scale.  The token
 // is tok[s], or, where src[s] >= 0, the previous step's greedy token of its
 // logit row src[s] (prev, still in HBM: the token never visits the host).
+// Rows of a sequence with a repetition penalty on the device (pslot[s] >= 0)
+// also count their token in that sequence's occurrence counts, the
+// reference's recent_for_penalty list (inference.cpp:104-108, :125) as counts.
 __global__ void embed_kernel(const uint8_t* __restrict__ emb, uint32_t dtype, int bs, int D,
                              const int32_t* __restrict__ tok, const int32_t* __restrict__ src,
-                             const uint32_t* __restrict__ prev, float* __restrict__ h) {
+                             const uint32_t* __restrict__ prev, float* __restrict__ h,
+                             const int32_t* __restrict__ pslot, uint32_t* __restrict__ pcounts, int V) {
     const int s = blockIdx.x;
     const int32_t from = src[s];
     const size_t row = from >= 0 ? (size_t)prev[from] : (size_t)tok[s];
+    if (pcounts && threadIdx.x == 0 && pslot[s] >= 0) atomicAdd(&pcounts[(size_t)pslot[s] * V + row], 1u);
     for (int i = threadIdx.x; i < D; i += blockDim.x) {
         const size_t e = row * D + i;
         float v;
@@ -308,20 +315,46 @@ __global__ void argmax_final_kernel(const float* __restrict__ pv, const int* __r
 // workgroup per row: each thread scans its 16-byte groups i, i + 1024, ... in
 // ascending index order (strict '>': its lowest index of its maximum), 16
 // groups in flight per round, then the workgroup keeps the maximum, ties to
-// the lower index.  Needs V % 4 == 0 and 16-byte aligned rows.
+// the lower index.  Needs V % 4 == 0 and 16-byte aligned rows.  A row whose
+// sequence has a repetition penalty on the device (pslot of its step row
+// lrows[row] >= 0) takes each logit through
+// Sampler::apply_repetition_penalty (sampler.cpp:37-49) first: k times
+// v > 0 ? v / penalty : v * penalty for a token fed k times (the reference
+// applies it once per list entry; a value keeps its sign, so the entries of
+// one token are these k steps, and distinct tokens are independent).  The
+// logits in HBM stay as they are.
 __global__ __launch_bounds__(1024) void argmax_rows_kernel(const float* __restrict__ logits, int V,
-                                                          uint32_t* __restrict__ out) {
+                                                          uint32_t* __restrict__ out,
+                                                          const int32_t* __restrict__ lrows,
+                                                          const int32_t* __restrict__ pslot,
+                                                          const float* __restrict__ ppen,
+                                                          const uint32_t* __restrict__ pcounts) {
     __shared__ float sv[16];
     __shared__ int si[16];
     const int row = blockIdx.x, tid = threadIdx.x;
     const float4* l4 = (const float4*)(logits + (size_t)row * V);
     const int n4 = V >> 2;
+    const int srow = pcounts ? lrows[row] : 0;
+    const int slot = pcounts ? pslot[srow] : -1;
+    const float pen = slot >= 0 ? ppen[srow] : 1.f;
+    const uint4* c4 = (const uint4*)(pcounts + (size_t)(slot >= 0 ? slot : 0) * V);
     float best = -INFINITY;
     int bi = INT_MAX;
     for (int base = tid; base < n4; base += 1024 * 16) {
         float4 v[16];
 #pragma unroll
         for (int u = 0; u < 16; u++) v[u] = l4[min(base + 1024 * u, n4 - 1)];
+        if (slot >= 0) {  // uniform per workgroup
+#pragma unroll
+            for (int u = 0; u < 16; u++) {
+                const uint4 k = c4[min(base + 1024 * u, n4 - 1)];
+                const uint32_t kk[4] = {k.x, k.y, k.z, k.w};
+                float* e = (float*)&v[u];
+#pragma unroll
+                for (int j = 0; j < 4; j++)
+                    for (uint32_t r = 0; r < kk[j]; r++) e[j] = e[j] > 0.f ? e[j] / pen : e[j] * pen;
+            }
+        }
 #pragma unroll
         for (int u = 0; u < 16; u++) {
             const int g = base + 1024 * u;
@@ -412,6 +445,14 @@ struct qraf_engine {
     int qbs = 0;                      // quant block size of every quantized tensor (0: none bound yet, then 32)
     bool last_logits_kept = true;     // the last step's logits are in `logits` (not a greedy-only step)
     qraf_engine_stats stats{};        // host-side time of qraf_engine_step
+    // Repetition penalty on the device (qraf_engine_set_repetition_penalty):
+    // a slot of V occurrence counts per penalised sequence, bumped by the
+    // embedding for every token the sequence is fed, read by the argmax
+    uint32_t* pen_counts = nullptr;   // [max_batch slots][V], allocated on first use
+    std::vector<int32_t> pen_slot;    // sequence id -> slot, -1 for none
+    std::vector<float> pen_value;     // sequence id -> penalty
+    std::vector<int32_t> pen_free;    // free slots
+    int pen_live = 0;                 // sequences with a slot
     uint8_t* samp = nullptr;          // sampling staging: recent tokens, counts, uniforms, tokens
     size_t samp_cap = 0;
     void* sort_ws = nullptr;          // sampling sort storage (large top_k, flat whole-vocabulary rows)
@@ -423,7 +464,8 @@ struct qraf_engine {
     uint16_t *xh = nullptr, *xl = nullptr;
     uint16_t *ah = nullptr, *al = nullptr;  // SwiGLU activation planes [max_batch][F] (fused gate/up epilogue)
     uint32_t* amax = nullptr;
-    int32_t* d_in = nullptr;  // tokens | positions | ctx | logit rows | token sources | page table rows
+    int32_t* d_in = nullptr;  // tokens | positions | ctx | logit rows | token sources | penalty slots | penalties |
+                              // page table rows
     // Pinned staging, one slot per step in flight: a step's inputs are written
     // into slot `slot` while the previous step (the other slot) may still be
     // queued; its tokens come back into h_amax of the same slot.
@@ -608,7 +650,7 @@ int qraf_engine_create(const qraf_model_config* cfg, const qraf_engine_options* 
     A(e->am_idx, (size_t)B * ARGMAX_CHUNKS * 4);
     e->am_keys_bytes = qgemm_argmax_keys_bytes((int)V, (int)B);
     A(e->am_keys, e->am_keys_bytes);
-    e->in_words = (size_t)B * (5 + e->max_pages);
+    e->in_words = (size_t)B * (7 + e->max_pages);
     A(e->d_in, e->in_words * 4);
     e->attn_ws_bytes = attn_workspace_bytes(B, (int)c.num_heads, (int)kvh, hd, e->capacity);
     A(e->attn_ws, e->attn_ws_bytes);
@@ -925,7 +967,64 @@ int qraf_engine_seq_create(qraf_engine* e, int32_t* id) {
 int qraf_engine_seq_release(qraf_engine* e, int32_t id) {
     clear_error();
     QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "seq_release: null engine");
-    return e->pages.seq_release(id);
+    QH_TRY(e->pages.seq_release(id));
+    if (id < (int32_t)e->pen_slot.size() && e->pen_slot[id] >= 0) {  // its penalty slot back to the free list
+        e->pen_free.push_back(e->pen_slot[id]);
+        e->pen_slot[id] = -1;
+        e->pen_live -= 1;
+    }
+    return QRAF_HIP_OK;
+}
+
+int qraf_engine_set_repetition_penalty(qraf_engine* e, int32_t id, float penalty) {
+    clear_error();
+    QH_REQUIRE(e, QRAF_HIP_ERR_INVALID, "set_repetition_penalty: null engine");
+    QH_REQUIRE(e->pages.live(id), QRAF_HIP_ERR_INVALID, "set_repetition_penalty: unknown sequence %d", id);
+    QH_REQUIRE(std::isfinite(penalty) && penalty > 0.f, QRAF_HIP_ERR_INVALID, "set_repetition_penalty: penalty %g",
+               (double)penalty);
+    QH_REQUIRE(e->c.vocab_size % 4 == 0, QRAF_HIP_ERR_INVALID,
+               "set_repetition_penalty: the device argmax needs a vocabulary that is a multiple of 4 (%u)",
+               e->c.vocab_size);
+    int32_t len = 0;
+    QH_TRY(e->pages.seq_length(id, &len));
+    QH_REQUIRE(len == 0, QRAF_HIP_ERR_STATE,
+               "set_repetition_penalty: sequence %d already holds %d positions (set it before its first step)", id, len);
+    QH_REQUIRE(e->n_pending == 0, QRAF_HIP_ERR_STATE, "set_repetition_penalty: steps in flight");
+    if ((int32_t)e->pen_slot.size() <= id) {
+        e->pen_slot.resize((size_t)id + 1, -1);
+        e->pen_value.resize((size_t)id + 1, 1.f);
+    }
+    if (penalty == 1.0f) {  // sampler.cpp:39: no penalty; the slot, if any, goes back
+        if (e->pen_slot[id] >= 0) {
+            e->pen_free.push_back(e->pen_slot[id]);
+            e->pen_slot[id] = -1;
+            e->pen_live -= 1;
+        }
+        return QRAF_HIP_OK;
+    }
+    if (!e->pen_counts) {  // first use: max_batch slots of V counts; captured steps hold the old (absent) counts
+        const size_t bytes = (size_t)e->o.max_batch * e->c.vocab_size * 4;
+        void* p = nullptr;
+        const hipError_t err = hipMalloc(&p, bytes);
+        QH_REQUIRE(err == hipSuccess, QRAF_HIP_ERR_NOMEM, "set_repetition_penalty: %zu bytes of counts", bytes);
+        e->allocs.push_back(p);
+        e->pen_counts = (uint32_t*)p;
+        for (int k = (int)e->o.max_batch - 1; k >= 0; k--) e->pen_free.push_back(k);
+        QH_CHECK_HIP(hipStreamSynchronize(e->stream));
+        e->drop_graphs();
+    }
+    if (e->pen_slot[id] < 0) {
+        QH_REQUIRE(!e->pen_free.empty(), QRAF_HIP_ERR_NOMEM,
+                   "set_repetition_penalty: all %u penalty slots in use", e->o.max_batch);
+        e->pen_slot[id] = e->pen_free.back();
+        e->pen_free.pop_back();
+        e->pen_live += 1;
+        // stream-ordered after every step issued so far, before the next
+        QH_CHECK_HIP(hipMemsetAsync(e->pen_counts + (size_t)e->pen_slot[id] * e->c.vocab_size, 0,
+                                    (size_t)e->c.vocab_size * 4, e->stream));
+    }
+    e->pen_value[id] = penalty;
+    return QRAF_HIP_OK;
 }
 
 int qraf_engine_seq_length(qraf_engine* e, int32_t id, int32_t* len) {
@@ -983,7 +1082,9 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     int32_t* ctx = pos + n_pad;
     int32_t* lrows = ctx + n_pad;
     int32_t* src = lrows + n_pad;
-    int32_t* ptab = src + n_pad;
+    int32_t* pslot = src + n_pad;
+    float* ppen = (float*)(pslot + n_pad);
+    int32_t* ptab = (int32_t*)(ppen + n_pad);
     // the rows' sequences and positions checked, their new pages taken from
     // the pool and their page-table rows written (nothing changes on failure);
     // step_ctx, the longest context of this step, sizes the attention grid
@@ -996,6 +1097,10 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
         tok[i] = src[i] >= 0 ? 0 : (int32_t)tokens[i];
         pos[i] = positions[i];
         ctx[i] = positions[i] + 1;
+        const int32_t sq = seq_ids[i];
+        const bool pen = sq < (int32_t)e->pen_slot.size() && e->pen_slot[sq] >= 0;
+        pslot[i] = pen ? e->pen_slot[sq] : -1;
+        ppen[i] = pen ? e->pen_value[sq] : 1.f;
         if (!want_logits || want_logits[i]) lrows[n_logit_rows++] = i;
     }
     for (int i = n; i < n_pad; i++) {
@@ -1003,6 +1108,8 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
         pos[i] = 0;
         ctx[i] = 1;
         src[i] = -1;
+        pslot[i] = -1;
+        ppen[i] = 1.f;
         for (int j = 0; j < MP; j++) ptab[(size_t)i * MP + j] = j == 0 ? e->scratch_page : 0;
     }
     const int n_logit_real = n_logit_rows;
@@ -1013,17 +1120,19 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     }
     n = n_pad;
     hipStream_t s = e->stream;
-    const size_t words = (size_t)n * (5 + MP);
+    const size_t words = (size_t)n * (7 + MP);
     const bool head = n_logit_rows > 0 && (logits || tok_out);
     // greedy-only step (no logits wanted, none kept): the head's argmax fused into its GEMM where it runs one
-    const bool argmax_only = head && !logits && tok_out && !e->keep_logits;
+    const bool argmax_only = head && !logits && tok_out && !e->keep_logits && e->pen_live == 0;
     const int head_mode = head ? (argmax_only ? 2 : 1) : 0;
     const int32_t* d_tok = e->d_in;
     const int32_t* d_pos = d_tok + n;
     const int32_t* d_ctx = d_pos + n;
     const int32_t* d_lrows = d_ctx + n;
     const int32_t* d_src = d_lrows + n;
-    const int32_t* d_ptab = d_src + n;
+    const int32_t* d_pslot = d_src + n;
+    const float* d_ppen = (const float*)(d_pslot + n);
+    const int32_t* d_ptab = (const int32_t*)(d_ppen + n);
 
     const int D = (int)c.hidden_size, F = (int)c.intermediate_size, V = (int)c.vocab_size;
     const int H = (int)c.num_heads, Hkv = (int)c.num_kv_heads, hd = e->hd;
@@ -1081,7 +1190,7 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
     // ctx_grid >= every row's context sizes the attention grid.
     auto enqueue = [&](int ctx_grid) -> int {
         hipLaunchKernelGGL(embed_kernel, dim3(n), dim3(256), 0, s, e->embed, e->dt_embed, qbs, D, d_tok, d_src, e->amax,
-                           e->h);
+                           e->h, d_pslot, e->pen_counts, V);
         QH_CHECK_HIP(hipGetLastError());
         // steps of 2-8 rows whose QKV and O projections go to the multi-vector
         // matvec take the per-projection loop below (gate/up and down each
@@ -1197,7 +1306,8 @@ static int step_issue(qraf_engine* e, int32_t n, const int32_t* seq_ids, const u
                 QH_TRY(proj(W, e->head_t, dt, V, D, e->xhead, n_logit_rows, e->logits, nullptr));
             }
             if (V % 4 == 0) {  // one pass per row (logits rows are 16-byte aligned then)
-                hipLaunchKernelGGL(argmax_rows_kernel, dim3(n_logit_rows), dim3(1024), 0, s, e->logits, V, e->amax);
+                hipLaunchKernelGGL(argmax_rows_kernel, dim3(n_logit_rows), dim3(1024), 0, s, e->logits, V, e->amax,
+                                   d_lrows, d_pslot, d_ppen, e->pen_counts);
             } else {
                 hipLaunchKernelGGL(argmax_chunk_kernel, dim3(ARGMAX_CHUNKS, n_logit_rows), dim3(256), 0, s, e->logits, V,
                                    e->am_val, e->am_idx);

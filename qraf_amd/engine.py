@@ -170,6 +170,12 @@ class Engine:
     def seq_release(self, seq_id: int):
         call("qraf_engine_seq_release", self.h, seq_id)
 
+    def set_repetition_penalty(self, seq_id: int, penalty: float):
+        """Greedy tokens of this sequence (set before its first step) taken
+        after Sampler::apply_repetition_penalty with every token it was fed,
+        counted on the device (qraf_engine_set_repetition_penalty)."""
+        call("qraf_engine_set_repetition_penalty", self.h, seq_id, C.c_float(penalty))
+
     def seq_length(self, seq_id: int) -> int:
         i = C.c_int32()
         call("qraf_engine_seq_length", self.h, seq_id, C.byref(i))
@@ -340,12 +346,17 @@ class InferenceEngine:
         self.eos = eos_token  # tokenizer.h:62 default when the file has no tokenizer
 
     def generate_tokens(self, prompt_tokens, max_tokens=256, repetition_penalty=1.1, stop_tokens=(),
-                        sampling: SamplingConfig | None = None):
+                        sampling: SamplingConfig | None = None, pipeline: bool = True):
         """Greedy with `repetition_penalty` unless a SamplingConfig is given.
         The prompt is fed token by token (inference.cpp:90-99); then every
         token is the device sampler's pick from the last logits, penalised
         with the prompt and every generated token so far (inference.cpp:104-
-        116), and is fed back until a stop token or max_tokens."""
+        116), and is fed back until a stop token or max_tokens.  Greedy with
+        a penalty (and pipeline, vocabularies a multiple of 4) runs
+        pipelined: the penalty is applied on the device from counts of the
+        tokens fed (qraf_engine_set_repetition_penalty) and each step takes
+        its token from the previous step's argmax on the device, a stop token
+        being seen one step late; the same tokens."""
         if len(prompt_tokens) == 0:
             raise ValueError("empty prompt")
         if sampling is None:
@@ -357,6 +368,12 @@ class InferenceEngine:
         stops = set(stop_tokens) | ({self.eos} if self.eos is not None else set())
         self.transformer.reset()  # frees the default sequence's pages
         seq = e.seq_create()
+        if pipeline and sampler is None and params.repetition_penalty != 1.0 and e.vocab % 4 == 0:
+            try:
+                return self._penalised_greedy_pipelined(e, seq, list(prompt_tokens), max_tokens, stops,
+                                                        params.repetition_penalty)
+            finally:
+                e.seq_release(seq)
         try:
             last = len(prompt_tokens) - 1
             for i, t in enumerate(prompt_tokens):
@@ -375,6 +392,29 @@ class InferenceEngine:
                 pos += 1
         finally:
             e.seq_release(seq)
+        return out
+
+    @staticmethod
+    def _penalised_greedy_pipelined(e, seq, prompt, max_tokens, stops, penalty):
+        e.set_repetition_penalty(seq, penalty)
+        for i, t in enumerate(prompt[:-1]):
+            e.step([seq], [t], [i], want_logits=[0], logits=False, argmax=False)
+        e.step_async([seq], [prompt[-1]], [len(prompt) - 1])  # its argmax is the first token
+        pending, out = 1, []
+        try:
+            while len(out) < max_tokens:
+                if len(out) + 1 < max_tokens:  # the next step feeds this step's token, taken on the device
+                    e.step_async([seq], [0], [len(prompt) + len(out)], token_src=[0])
+                    pending += 1
+                tok = int(e.collect()[0])
+                pending -= 1
+                if tok in stops:
+                    break
+                out.append(tok)
+        finally:
+            while pending:  # a step issued past a stop token or the last token: its token is not used
+                e.collect()
+                pending -= 1
         return out
 
 

@@ -830,3 +830,77 @@ def test_1024_row_prefill_step(hip):
     finally:
         e.close()
         m.close()
+
+
+@pytest.mark.parametrize("name,penalty", [("q8_hd64_gqa3", 1.1), ("q4_gqa8_hd128", 1.3), ("q4_hd64_gqa2", 0.9),
+                                          ("q4_qwen2_tied_bias", 1.1)])
+def test_penalised_greedy_on_device(hip, name, penalty):
+    """Greedy decoding with a repetition penalty, pipelined with the penalty
+    applied on the device from counts of the fed tokens
+    (qraf_engine_set_repetition_penalty), against the unpipelined loop that
+    penalises on the host-built recent list (qraf_engine_sample) and against
+    the oracle's generate: the same tokens, for prompts that repeat tokens
+    (counts above 1), with a stop token met and without; the engine's
+    penalty slots all returned."""
+    from qraf_amd.engine import InferenceEngine
+    kw, seed = SMALL[name]
+    m = oracle_model(kw, seed)
+    tf = upload(m, kw)
+    try:
+        L = po.lib()
+        base = [L.or_gen_token(seed + 17, i, kw["vocab"]) for i in range(9)]
+        prompts = [base, base[:3] * 4, [base[0]] * 6 + base]
+        for p in prompts:
+            want = m.generate(p, 40, penalty, eos=-1)
+            got = InferenceEngine(tf, eos_token=None).generate_tokens(p, 40, repetition_penalty=penalty)
+            host = InferenceEngine(tf, eos_token=None).generate_tokens(p, 40, repetition_penalty=penalty,
+                                                                      pipeline=False)
+            assert got == host == want, name
+            # a stop token met part-way: the stream up to it, the same either way
+            stop = want[len(want) // 2]
+            got_s = InferenceEngine(tf, eos_token=stop).generate_tokens(p, 40, repetition_penalty=penalty)
+            host_s = InferenceEngine(tf, eos_token=stop).generate_tokens(p, 40, repetition_penalty=penalty,
+                                                                        pipeline=False)
+            assert got_s == host_s == want[:want.index(stop)], name
+    finally:
+        tf.engine.close()
+        m.close()
+
+
+def test_device_penalty_refusals(hip):
+    """qraf_engine_set_repetition_penalty: refused for a sequence that already
+    holds positions, an unknown sequence, a penalty that is not positive and
+    finite; more penalised sequences than max_batch run out of slots, and a
+    released sequence's slot is reused."""
+    from qraf_amd._lib import HipError
+    from qraf_amd.engine import Engine
+    kw, seed = SMALL["q8_llama"]
+    m = oracle_model(kw, seed)
+    e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=2)
+    try:
+        for tname, dt, shape, data in m.tensors():
+            e.set_tensor(tname, dt, shape, data)
+        e.finalize()
+        a, b, c = e.seq_create(), e.seq_create(), e.seq_create()
+        e.step([a], [5], [0])
+        with pytest.raises(HipError) as x:
+            e.set_repetition_penalty(a, 1.1)
+        assert x.value.code == -5  # QRAF_HIP_ERR_STATE
+        for bad in (0.0, -1.0, float("inf"), float("nan")):
+            with pytest.raises(HipError):
+                e.set_repetition_penalty(b, bad)
+        with pytest.raises(HipError):
+            e.set_repetition_penalty(999, 1.1)
+        e.set_repetition_penalty(b, 1.1)
+        e.set_repetition_penalty(c, 1.2)
+        d = e.seq_create()
+        with pytest.raises(HipError) as x:
+            e.set_repetition_penalty(d, 1.1)
+        assert x.value.code == -4  # QRAF_HIP_ERR_NOMEM: both slots in use
+        e.seq_release(b)
+        e.set_repetition_penalty(d, 1.1)  # b's slot
+        e.set_repetition_penalty(c, 1.0)  # off: its slot back
+        e.set_repetition_penalty(e.seq_create(), 1.5)
+    finally:
+        e.close()
+        m.close()
