@@ -547,10 +547,10 @@ int qraf_engine_set_fusion(qraf_engine* engine, int32_t flags);
  * builds it (inference.cpp:104-125): the same token as qraf_engine_sample with
  * that list, without the list crossing PCIe, so penalised greedy decoding
  * can run pipelined.  The logits the step leaves or returns stay
- * unpenalised.  penalty 1 turns it off.  At most max_batch penalised
+ * unpenalised.  penalty 1 turns it off.  At most 2 * max_batch penalised
  * sequences at a time (QRAF_HIP_ERR_NOMEM beyond); vocabularies that are a
  * multiple of 4 only (QRAF_HIP_ERR_INVALID otherwise).  The first call
- * allocates max_batch * vocab * 4 bytes of counts and drops the captured
+ * allocates 2 * max_batch * vocab * 4 bytes of counts and drops the captured
  * step graphs.  No reference counterpart as an entry point. */
 int qraf_engine_set_repetition_penalty(qraf_engine* engine, int32_t seq_id, float penalty);
 /* Transformer::forward(token, pos) -> logits [vocab] (transformer.cpp:622-639)

@@ -448,7 +448,8 @@ struct qraf_engine {
     // Repetition penalty on the device (qraf_engine_set_repetition_penalty):
     // a slot of V occurrence counts per penalised sequence, bumped by the
     // embedding for every token the sequence is fed, read by the argmax
-    uint32_t* pen_counts = nullptr;   // [max_batch slots][V], allocated on first use
+    uint32_t* pen_counts = nullptr;   // [2 max_batch slots][V], allocated on first use (a pipelined scheduler
+                                      // admits a request while one whose last token is in flight still holds its slot)
     std::vector<int32_t> pen_slot;    // sequence id -> slot, -1 for none
     std::vector<float> pen_value;     // sequence id -> penalty
     std::vector<int32_t> pen_free;    // free slots
@@ -989,7 +990,6 @@ int qraf_engine_set_repetition_penalty(qraf_engine* e, int32_t id, float penalty
     QH_TRY(e->pages.seq_length(id, &len));
     QH_REQUIRE(len == 0, QRAF_HIP_ERR_STATE,
                "set_repetition_penalty: sequence %d already holds %d positions (set it before its first step)", id, len);
-    QH_REQUIRE(e->n_pending == 0, QRAF_HIP_ERR_STATE, "set_repetition_penalty: steps in flight");
     if ((int32_t)e->pen_slot.size() <= id) {
         e->pen_slot.resize((size_t)id + 1, -1);
         e->pen_value.resize((size_t)id + 1, 1.f);
@@ -1002,20 +1002,20 @@ int qraf_engine_set_repetition_penalty(qraf_engine* e, int32_t id, float penalty
         }
         return QRAF_HIP_OK;
     }
-    if (!e->pen_counts) {  // first use: max_batch slots of V counts; captured steps hold the old (absent) counts
-        const size_t bytes = (size_t)e->o.max_batch * e->c.vocab_size * 4;
+    if (!e->pen_counts) {  // first use: 2 max_batch slots of V counts; captured steps hold the old (absent) counts
+        const size_t bytes = (size_t)2 * e->o.max_batch * e->c.vocab_size * 4;
         void* p = nullptr;
         const hipError_t err = hipMalloc(&p, bytes);
         QH_REQUIRE(err == hipSuccess, QRAF_HIP_ERR_NOMEM, "set_repetition_penalty: %zu bytes of counts", bytes);
         e->allocs.push_back(p);
         e->pen_counts = (uint32_t*)p;
-        for (int k = (int)e->o.max_batch - 1; k >= 0; k--) e->pen_free.push_back(k);
-        QH_CHECK_HIP(hipStreamSynchronize(e->stream));
+        for (int k = 2 * (int)e->o.max_batch - 1; k >= 0; k--) e->pen_free.push_back(k);
+        QH_CHECK_HIP(hipStreamSynchronize(e->stream));  // steps in flight finish before their graphs go
         e->drop_graphs();
     }
     if (e->pen_slot[id] < 0) {
         QH_REQUIRE(!e->pen_free.empty(), QRAF_HIP_ERR_NOMEM,
-                   "set_repetition_penalty: all %u penalty slots in use", e->o.max_batch);
+                   "set_repetition_penalty: all %u penalty slots in use", 2 * e->o.max_batch);
         e->pen_slot[id] = e->pen_free.back();
         e->pen_free.pop_back();
         e->pen_live += 1;

@@ -455,7 +455,14 @@ class BatchScheduler:
     defaults (prefill_chunk 1, max_rows = max_batch) every active request
     feeds exactly one token per step.
 
-    pipeline=True (when no request has a repetition penalty): run() issues
+    Requests with a repetition penalty take it on the device (device_penalty,
+    vocabularies a multiple of 4: qraf_engine_set_repetition_penalty at
+    admission, counts of every token fed), so their greedy tokens come from
+    the step's own argmax like the others'; otherwise each step re-samples
+    their logit rows with the penalty on the host-built recent lists
+    (qraf_engine_sample).
+
+    pipeline=True (unless some request's penalty is taken on the host): run() issues
     step N+1 before it collects step N's tokens (Engine.step_async), each
     decode row taking its token from step N's argmax on the device, so the
     host builds the next step while the device runs this one.  A request
@@ -469,8 +476,10 @@ class BatchScheduler:
     sees tokens only (the logits in HBM already belong to the next step)."""
 
     def __init__(self, engine: Engine, max_batch: int | None = None, max_rows: int | None = None,
-                 prefill_chunk: int = 1, pipeline: bool = False, keep_logits: bool = True):
+                 prefill_chunk: int = 1, pipeline: bool = False, keep_logits: bool = True,
+                 device_penalty: bool = True):
         self.engine = engine
+        self.device_penalty = device_penalty and getattr(engine, "vocab", 1) % 4 == 0
         # False: a run whose requests are all greedy without penalty keeps no
         # logits (the engine's greedy-only head); the observer then sees tokens only
         self.keep_logits = keep_logits
@@ -501,10 +510,18 @@ class BatchScheduler:
         self.pending.append(r)
         return r.id
 
+    def _new_seq(self, r):
+        r.seq = self.engine.seq_create()
+        if self.device_penalty and r.penalty != 1.0:
+            self.engine.set_repetition_penalty(r.seq, r.penalty)
+
+    def _host_penalty(self, r) -> bool:
+        return r.penalty != 1.0 and not self.device_penalty
+
     def _admit(self):
         while self.pending and len(self.active) < self.max_batch:
             r = self.pending.popleft()
-            r.seq = self.engine.seq_create()
+            self._new_seq(r)
             r.state = "PREFILLING"
             r.admit_step = self.steps
             self.active.append(r)
@@ -545,7 +562,7 @@ class BatchScheduler:
             j = i + 1
             while j < len(lrows) and lrows[j].penalty == lrows[i].penalty:
                 j += 1
-            if lrows[i].penalty != 1.0:
+            if self._host_penalty(lrows[i]):
                 gp = SamplingParams(0.0, 0, 1.0, lrows[i].penalty)
                 nx[i:j] = self.engine.sample(gp, [r.prompt + r.generated for r in lrows[i:j]], row0=i)
             i = j
@@ -580,7 +597,7 @@ class BatchScheduler:
         return True
 
     def run(self):
-        no_penalty = all(r.penalty == 1.0 for r in list(self.pending) + self.active)
+        no_penalty = not any(self._host_penalty(r) for r in list(self.pending) + self.active)
         greedy_only = not self.keep_logits and no_penalty
         if greedy_only:
             self.engine.set_keep_logits(False)
@@ -617,7 +634,7 @@ class BatchScheduler:
                    if r.state != "DECODING" or len(r.generated) + r.inflight < r.max_tokens)
         while self.pending and held < self.max_batch:
             r = self.pending.popleft()
-            r.seq = self.engine.seq_create()
+            self._new_seq(r)
             r.state = "PREFILLING"
             r.admit_step = self.steps
             self.active.append(r)

@@ -870,13 +870,13 @@ def test_penalised_greedy_on_device(hip, name, penalty):
 def test_device_penalty_refusals(hip):
     """qraf_engine_set_repetition_penalty: refused for a sequence that already
     holds positions, an unknown sequence, a penalty that is not positive and
-    finite; more penalised sequences than max_batch run out of slots, and a
-    released sequence's slot is reused."""
+    finite; more penalised sequences than 2 * max_batch run out of slots, and
+    a released sequence's slot is reused."""
     from qraf_amd._lib import HipError
     from qraf_amd.engine import Engine
     kw, seed = SMALL["q8_llama"]
     m = oracle_model(kw, seed)
-    e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=2)
+    e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=1)
     try:
         for tname, dt, shape, data in m.tensors():
             e.set_tensor(tname, dt, shape, data)
@@ -896,11 +896,46 @@ def test_device_penalty_refusals(hip):
         d = e.seq_create()
         with pytest.raises(HipError) as x:
             e.set_repetition_penalty(d, 1.1)
-        assert x.value.code == -4  # QRAF_HIP_ERR_NOMEM: both slots in use
+        assert x.value.code == -4  # QRAF_HIP_ERR_NOMEM: both slots (2 * max_batch) in use
         e.seq_release(b)
         e.set_repetition_penalty(d, 1.1)  # b's slot
         e.set_repetition_penalty(c, 1.0)  # off: its slot back
         e.set_repetition_penalty(e.seq_create(), 1.5)
+    finally:
+        e.close()
+        m.close()
+
+
+def test_scheduler_penalties_on_device(hip):
+    """Requests with repetition penalties 1.0, 1.1 and 1.3 side by side through
+    the scheduler, with chunked prefill and admission as others finish: with
+    the penalty on the device (pipelined and not) and on the host-built recent
+    lists (unpipelined), every request's stream equals the oracle's decode of
+    it alone with its penalty, with an EOS token and without."""
+    from qraf_amd.engine import BatchScheduler, Engine
+    kw, seed = SMALL["q4_gqa8_hd128"]
+    m = oracle_model(kw, seed)
+    L = po.lib()
+    prompts = [[L.or_gen_token(300 + r, i, kw["vocab"]) for i in range(3 + 4 * r)] * (1 + r % 2) for r in range(7)]
+    pens = [1.0, 1.1, 1.3, 1.1, 1.0, 1.3, 1.1]
+    want = {None: [m.generate(p, 20, pen, eos=-1) for p, pen in zip(prompts, pens)]}
+    eos = want[None][1][5]
+    want[eos] = [m.generate(p, 20, pen, eos=eos) for p, pen in zip(prompts, pens)]
+    e = Engine(engine_config(kw), kv_dtype=po.F32, max_batch=16)
+    try:
+        for name, dt, shape, data in m.tensors():
+            e.set_tensor(name, dt, shape, data)
+        e.finalize()
+        pool = e.free_pages()
+        for stop in (None, eos):
+            for device_penalty, pipeline in ((True, True), (True, False), (False, False)):
+                sched = BatchScheduler(e, max_batch=4, max_rows=16, prefill_chunk=5, pipeline=pipeline,
+                                       device_penalty=device_penalty)
+                ids = [sched.submit(p, 20, repetition_penalty=pen, eos=stop) for p, pen in zip(prompts, pens)]
+                done = {r.id: r for r in sched.run()}
+                got = [done[i].generated for i in ids]
+                assert got == want[stop], (stop, device_penalty, pipeline)
+                assert e.free_pages() == pool
     finally:
         e.close()
         m.close()
