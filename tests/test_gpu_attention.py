@@ -118,8 +118,8 @@ def test_attention_ragged_batch_config(hip, form, kv_dtype):
     check(got[0], oracle_attention(q, table, K, V, ctxs, H, Hkv, hd, ps))
 
 
-@pytest.mark.parametrize("H,Hkv,hd", [(9, 3, 64), (16, 16, 64), (4, 1, 128), (32, 4, 128), (12, 2, 64), (16, 1, 128),
-                                     (4, 1, 16), (8, 2, 32)])
+@pytest.mark.parametrize("H,Hkv,hd", [(9, 3, 64), (16, 16, 64), (8, 4, 64), (16, 4, 64), (4, 1, 128), (32, 4, 128),
+                                     (12, 2, 64), (16, 1, 128), (4, 1, 16), (8, 2, 32)])
 @pytest.mark.parametrize("kv_dtype", [po.F16, po.F32])
 def test_attention_edge_lengths(hip, form, H, Hkv, hd, kv_dtype):
     # head_dim 16 and 32 take the VALU kernel for fp16 pages too
