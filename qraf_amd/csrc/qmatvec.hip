@@ -264,6 +264,80 @@ __device__ __forceinline__ void stage_x(float* sx, const float* __restrict__ x, 
     }
 }
 
+// Q8 staging of x in two phases, for K == nb * 32 <= 2048 * JX and 16-byte
+// aligned x (and xw): issue() requests every load the staging needs (the
+// norm's strided elements, the float4s to stage), each index clamped into x
+// so that no load sits in a branch; finish() forms and stores them.  A caller
+// that requests its weights between the two waits for x with the weights
+// still in flight (the wait counter is in order).  The values are those of
+// stage_x<8, XP>: the same strided fma order and reduction for the norm, the
+// same products per element.
+template <int XP, int JX>
+struct XStage8 {
+    static constexpr int NI = 2 * JX;                      // float4 steps of 1024 elements
+    static constexpr int NN = XP == XP_NORM ? 8 * JX : 1;  // strided norm elements per thread
+    f32x4 a[NI], b[XP == XP_NONE ? 1 : NI];                // x, and the SiLU-gate's second float4 or xw
+    float n[NN];
+    __device__ __forceinline__ void issue(const float* __restrict__ x, const float* __restrict__ xw, int K) {
+        const int t = threadIdx.x;
+        if (XP == XP_NORM) {
+#pragma unroll
+            for (int k = 0; k < NN; k++) n[k] = x[min(t + 256 * k, K - 1)];
+        }
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int i = min(4 * t + 1024 * k, K - 4);
+            if (XP == XP_SILU_GATE) {
+                a[k] = *(const f32x4*)(x + 2 * i);
+                b[k] = *(const f32x4*)(x + 2 * i + 4);
+            } else {
+                a[k] = *(const f32x4*)(x + i);
+                if (XP == XP_NORM) b[k] = *(const f32x4*)(xw + i);
+            }
+        }
+    }
+    __device__ __forceinline__ void finish(float* sx, int K, float eps) {
+        const int t = threadIdx.x;
+        float r = 1.f;
+        if (XP == XP_NORM) {  // norm_r_256's sums in its order
+            __shared__ float red[4];
+            float ss = 0.f;
+#pragma unroll
+            for (int k = 0; k < NN; k++) ss = t + 256 * k < K ? __builtin_fmaf(n[k], n[k], ss) : ss;
+#pragma unroll
+            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+            if ((t & 63) == 0) red[t >> 6] = ss;
+            __syncthreads();
+            ss = (red[0] + red[1]) + (red[2] + red[3]);
+            r = 1.0f / sqrtf(ss / (float)K + eps);
+        }
+#pragma unroll
+        for (int k = 0; k < NI; k++) {
+            const int i = 4 * t + 1024 * k;
+            f32x4 v;
+            if (XP == XP_SILU_GATE) {
+                v = f32x4{silu_gate(a[k][0], a[k][1]), silu_gate(a[k][2], a[k][3]), silu_gate(b[k][0], b[k][1]),
+                          silu_gate(b[k][2], b[k][3])};
+            } else if (XP == XP_NORM) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = __fmul_rn(__fmul_rn(a[k][e], r), b[k][e]);
+            } else {
+                v = a[k];
+            }
+            if (i < K) *(f32x4*)(sx + (i >> 5) * XS8 + (i & 31)) = v;
+        }
+    }
+};
+
+// The row of its group that lane `lane` holds after wave_reduce_rows<R>.
+template <int R>
+__device__ __forceinline__ int reduced_row_of_lane(int lane) {
+    int r = 0;
+#pragma unroll
+    for (int m = 32, c = R; c > 1; c >>= 1, m >>= 1) r = r * 2 + ((lane & m) != 0 ? 1 : 0);
+    return r;
+}
+
 // FMT 8: unit = one Q8_0 block; FMT 4: unit = a pair of Q4_0 blocks.
 template <int FMT, int R>
 __global__ __launch_bounds__(WG) void qmv_stream_kernel(const uint8_t* __restrict__ W, uint32_t row_bytes, int N,
@@ -316,22 +390,32 @@ __global__ __launch_bounds__(WG) void qmv_stream_kernel(const uint8_t* __restric
 // the HBM latency several times.
 // ----------------------------------------------------------------------------
 // The rows of one wave: returns row row0 + *rr's sum on the lanes with
-// (lane & (64/R - 1)) == 0 (sx: the workgroup's x staging).
-template <int FMT, int R, int J, int XP>
+// (lane & (64/R - 1)) == 0 (sx: the workgroup's x staging).  Q8 with whole
+// blocks and aligned x requests x first, then the weights, then whatever
+// tail() requests (the epilogue's operands), so the wait for x leaves the
+// weights in flight and the epilogue finds its operands arrived.
+template <int FMT, int R, int J, int XP, typename Tail>
 __device__ __forceinline__ float oneshot_rows(const uint8_t* __restrict__ W, uint32_t row_bytes, int N, int K, int nb,
                                               const float* __restrict__ x, const float* __restrict__ xw, float eps,
-                                              float* sx, int row0, int lane, int* rr) {
+                                              float* sx, int row0, int lane, int* rr, Tail&& tail) {
     const int U = FMT == 8 ? nb : nb >> 1;
+    const bool two_phase = FMT == 8 && K == nb * 32 && (((uintptr_t)x) & 15) == 0 &&
+                           (XP != XP_NORM || (((uintptr_t)xw) & 15) == 0);  // uniform
 
     const uint8_t* rowp[R];
 #pragma unroll
     for (int r = 0; r < R; r++) rowp[r] = W + (size_t)min(row0 + r, N - 1) * row_bytes;
 
+    XStage8<XP, J> xs;
+    if (two_phase) xs.issue(x, xw, K);
     Units<R> w[J];
 #pragma unroll
     for (int j = 0; j < J; j++) load_units<R>(w[j], rowp, min(lane + 64 * j, U - 1));
+    __builtin_amdgcn_sched_barrier(0);  // tail's loads (and any wait they need) behind the weights
+    tail();
 
-    stage_x<FMT, XP>(sx, x, K, nb, xw, eps);
+    if (two_phase) xs.finish(sx, K, eps);
+    else stage_x<FMT, XP>(sx, x, K, nb, xw, eps);
     __syncthreads();
 
     float acc[R];
@@ -356,9 +440,14 @@ __global__ __launch_bounds__(WG) void qmv_oneshot_kernel(const uint8_t* __restri
     extern __shared__ __align__(16) float sx[];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * R;
+    // the residual of the row this lane stores, requested behind the weights
+    // (without a residual the load reads x[0] and is not used)
+    const float* ap = add ? add + min(row0 + reduced_row_of_lane<R>(lane), N - 1) : x;
+    float addv = 0.f;
     int rr;
-    const float v = oneshot_rows<FMT, R, J, XP>(W, row_bytes, N, K, nb, x, xw, eps, sx, row0, lane, &rr);
-    if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = add ? v + add[row0 + rr] : v;
+    const float v = oneshot_rows<FMT, R, J, XP>(W, row_bytes, N, K, nb, x, xw, eps, sx, row0, lane, &rr,
+                                                [&]() { addv = *ap; });
+    if ((lane & (64 / R - 1)) == 0 && row0 + rr < N) y[row0 + rr] = add ? v + addv : v;
 }
 
 // The one-shot kernel with the QKV epilogue (MvRope): a workgroup's 4R rows
@@ -373,24 +462,36 @@ __global__ __launch_bounds__(WG) void qmv_oneshot_rope_kernel(const uint8_t* __r
     __shared__ float s_y[4 * R];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int row0 = (blockIdx.x * 4 + wave) * R;
+    const int t = threadIdx.x, r = blockIdx.x * 4 * R + 2 * t;
+    const int hd = rp.hd, qd = rp.H * hd, kvd = rp.Hkv * hd, ps = rp.page_size;
+    // the epilogue's operands, requested behind the weights: the position,
+    // its page, the pair's bias and rotation (at a pair index clamped into
+    // the rows; without a bias those loads read x and are not used)
+    const int rc = min(r, N - 2);
+    int p = 0, page = 0;
+    float ba = 0.f, bb = 0.f, c = 0.f, sn = 0.f;
     int rr;
-    const float v = oneshot_rows<FMT, R, J, XP>(W, row_bytes, N, K, nb, x, xw, eps, sx, row0, lane, &rr);
+    const float v = oneshot_rows<FMT, R, J, XP>(W, row_bytes, N, K, nb, x, xw, eps, sx, row0, lane, &rr, [&]() {
+        p = *rp.pos;
+        page = rp.page_table[p / ps];
+        const float* bp = rp.bias ? rp.bias + rc : x;
+        ba = bp[0];
+        bb = bp[1];
+        const float* cs = rp.rope + (size_t)p * hd + rc % hd;
+        c = cs[0];
+        sn = cs[1];
+    });
     if ((lane & (64 / R - 1)) == 0) s_y[wave * R + rr] = v;
     __syncthreads();
-    const int t = threadIdx.x, r = blockIdx.x * 4 * R + 2 * t;
     if (t >= 2 * R || r >= N) return;
     float a = s_y[2 * t], b = s_y[2 * t + 1];
     if (rp.bias) {
-        a = __fadd_rn(a, rp.bias[r]);
-        b = __fadd_rn(b, rp.bias[r + 1]);
+        a = __fadd_rn(a, ba);
+        b = __fadd_rn(b, bb);
     }
-    const int hd = rp.hd, qd = rp.H * hd, kvd = rp.Hkv * hd, ps = rp.page_size;
-    const int p = *rp.pos;
-    const int page = rp.page_table[p / ps], off = p % ps;
+    const int off = p % ps;
     if (r < qd + kvd) {
         const int i = r % hd;  // even index inside the head
-        const float* cs = rp.rope + (size_t)p * hd;
-        const float c = cs[i], sn = cs[i + 1];
         const float ra = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn));
         const float rb = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, c));
         if (r < qd) {
