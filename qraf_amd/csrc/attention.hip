@@ -122,7 +122,9 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     constexpr int PVU = 16;                      // V loads in flight per thread in the PV phase
     constexpr int PADP = PVU * NG;               // past-the-end slots its unrolled loop may touch
     static_assert(PADP <= ACH, "padding is written by the first PADP threads");
-    __shared__ float s_q[G][HD];
+    constexpr int QPT = (G * HD + ACH - 1) / ACH;  // q elements per thread
+    __shared__ __align__(16) float s_qf[QPT * ACH];  // q of the G heads, [G][HD], padded to whole rounds
+    float (*s_q)[HD] = (float (*)[HD])s_qf;
     __shared__ float s_p[G][ACH + PADP];         // probabilities (zero past the end); then PV partials
     __shared__ uint32_t s_voff[ACH + PADP];      // element offset of each position's V row in the layer pages
     __shared__ float s_red[G][4];
@@ -140,15 +142,27 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
     const int s = item / per, chunk = item - s * per;
     const int t0 = chunk * ACH;
     const int t = t0 + tid;
+    // (q's loads are in flight with the page id's: the K row is requested
+    // after one round trip.)
     const int ctx_raw = a.ctx[s];
-    for (int i = tid; i < G * HD; i += ACH) s_q[i / HD][i % HD] = a.q[((size_t)s * a.H + kvh * G) * HD + i];
     const int page_t = a.page_table[(size_t)s * a.max_pages + min(t, a.max_ctx - 1) / a.page_size];
+    float qv[QPT];
+#pragma unroll
+    for (int k = 0; k < QPT; k++) qv[k] = a.q[((size_t)s * a.H + kvh * G) * HD + min(tid + ACH * k, G * HD - 1)];
     const int ctx = min(ctx_raw, a.max_ctx);
     const int nchunks = (ctx + ACH - 1) / ACH;
-    if (chunk >= nchunks) return;  // the whole workgroup
 
     const KT* kc = (const KT*)a.kc;
     const KT* vc = (const KT*)a.vc;
+    // every thread's V row offset from its page id (positions past the
+    // context are given position t0's below), so the page id is waited for
+    // once, before the branch, in parallel with the context length
+    {
+        const uint32_t row = ((uint32_t)page_t * a.Hkv + kvh) * a.page_size;
+        s_voff[tid] = sizeof(KT) == 4 ? (row + t % a.page_size) * HD : row * HD + t % a.page_size;
+    }
+#pragma unroll
+    for (int k = 0; k < QPT; k++) s_qf[tid + ACH * k] = qv[k];  // unconditional: the loads stay ahead of the branch
     float kv[HD];
     if (t < ctx) {
         const KT* kr = kc + (((size_t)page_t * a.Hkv + kvh) * a.page_size + t % a.page_size) * HD;
@@ -159,10 +173,9 @@ __global__ __launch_bounds__(ACH) void attn_decode_kernel(AttnArgs a) {
 #pragma unroll
             for (int i = 0; i < 8; i++) kv[d + i] = k8[i];
         }
-        const uint32_t row = ((uint32_t)page_t * a.Hkv + kvh) * a.page_size;
-        s_voff[tid] = sizeof(KT) == 4 ? (row + t % a.page_size) * HD : row * HD + t % a.page_size;
     }
     __syncthreads();
+    if (chunk >= nchunks) return;  // the whole workgroup (no position of its chunk was loaded)
     // V row offsets of positions past the end (and of the padding the PV
     // loop may touch): position t0's row, which exists; its probability is 0
     if (t >= ctx) s_voff[tid] = s_voff[0];
