@@ -156,6 +156,9 @@ __global__ __launch_bounds__(1024) void residual_norm_split_v2_kernel(const floa
     __shared__ float red[16];
     const int m = blockIdx.x, tid = threadIdx.x, i = 2 * tid;
     float2* hr = (float2*)(h + (size_t)m * D);
+    // the norm weights of this thread's pair, requested with the sums' operands
+    // (at a pair index clamped into the row; without weights the load reads h)
+    const float2 wv = *(const float2*)(w ? w + min(i, D - 2) : h);
     float2 v = make_float2(0.f, 0.f);
     if (i < D) {
         v = hr[tid];
@@ -185,8 +188,8 @@ __global__ __launch_bounds__(1024) void residual_norm_split_v2_kernel(const floa
     const float r = 1.0f / sqrtf(ss / (float)D + eps);
     if (i < D) {
         const size_t e = (size_t)m * D + i;
-        split_bf16(__fmul_rn(__fmul_rn(v.x, r), w[i]), &xh[e], &xl[e]);
-        split_bf16(__fmul_rn(__fmul_rn(v.y, r), w[i + 1]), &xh[e + 1], &xl[e + 1]);
+        split_bf16(__fmul_rn(__fmul_rn(v.x, r), wv.x), &xh[e], &xl[e]);
+        split_bf16(__fmul_rn(__fmul_rn(v.y, r), wv.y), &xh[e + 1], &xl[e + 1]);
     }
 }
 
@@ -194,7 +197,7 @@ static int launch_residual_norm_split(const float* part, int S, size_t slice, fl
                                       uint16_t* xh, uint16_t* xl, int rows, hipStream_t s) {
     QH_REQUIRE(D <= 8192, QRAF_HIP_ERR_INVALID, "residual/norm: hidden size %d > 8192", D);
     if (D % 2 == 0 && D <= 2048 && (S <= 8 || S == 16) && (S == 0 || slice % 2 == 0) && (((uintptr_t)h) & 7) == 0 &&
-        (((uintptr_t)part) & 7) == 0) {
+        (((uintptr_t)part) & 7) == 0 && (((uintptr_t)w) & 7) == 0) {
 #define QH_RN2(Sv) hipLaunchKernelGGL(residual_norm_split_v2_kernel<Sv>, dim3(rows), dim3(1024), 0, s, part, slice, h, w, \
                                       D, eps, xh, xl)
         switch (S) {
