@@ -1537,7 +1537,7 @@ int launch_attention(const float* q, const void* kc, const void* vc, uint32_t kv
 // a rotated pair of a q or k head, or one v element.  qkv may be S slices
 // (GEMM split-K partials) of `slice` floats, summed in slice order.
 // ----------------------------------------------------------------------------
-template <typename KT>
+template <typename KT, int SC>
 __global__ void rope_append_kernel(const float* __restrict__ qkv, const float* __restrict__ bias, int H, int Hkv,
                                    int hd, const int32_t* __restrict__ pos, const float* __restrict__ rope,
                                    float* __restrict__ q_out, KT* __restrict__ kc, KT* __restrict__ vc,
@@ -1549,43 +1549,58 @@ __global__ void rope_append_kernel(const float* __restrict__ qkv, const float* _
          w += (size_t)gridDim.x * blockDim.x) {
     const int s = (int)(w / per), e = (int)(w % per);
     const size_t rbase = (size_t)s * row;
-    auto ld = [&](int i) { return sum_slices(qkv, S, slice, rbase + i); };
+    // SC: the slice count as a constant (0: S at run time)
+    auto ld = [&](int i) {
+        if (SC > 0) {
+            float t[SC > 0 ? SC : 1];
+#pragma unroll
+            for (int u = 0; u < SC; u++) t[u] = qkv[(size_t)u * slice + rbase + i];
+            float acc = t[0];
+#pragma unroll
+            for (int u = 1; u < SC; u++) acc += t[u];
+            return acc;
+        }
+        return sum_slices(qkv, S, slice, rbase + i);
+    };
+    // Every operand is requested before any is waited for, except what needs
+    // the position (its page and rotation): work element e is the rotated
+    // pair (i0, i0 + 1) of the q|k part, or one v element (i0 = i1).
+    const bool rot = e < (qd + kvd) / 2;
+    const int i0 = rot ? 2 * e : qd + kvd + (e - (qd + kvd) / 2);
+    const int i1 = rot ? i0 + 1 : i0;
     const int p = pos[s];
+    float a = ld(i0), b = ld(i1);
+    const float* bp = bias ? bias : qkv;  // without a bias these loads read qkv and are not used
+    const float ba = bp[bias ? i0 : 0], bb = bp[bias ? i1 : 0];
     const int page = page_table[(size_t)s * max_pages + p / page_size], off = p % page_size;
-    const float* cs = rope + (size_t)p * hd;  // (cos, sin) of pair i/2 at [i], [i+1]
+    const int i = rot ? i0 % hd : 0;  // even index inside the head
+    const float* cs = rope + (size_t)p * hd + i;  // (cos, sin) of pair i/2
+    const float c = cs[0], sn = cs[1];
     // pairs (i, i+1) of q heads, then k heads: rotate; v: copy.  Products are
     // rounded separately (no FMA contraction), as the reference's scalar code.
-    {
-        if (e < (qd + kvd) / 2) {
-            const int i0 = 2 * e;  // element index in [0, qd + kvd)
-            const int i = i0 % hd;   // even index inside the head
-            float a = ld(i0), b = ld(i0 + 1);
-            if (bias) {
-                a = __fadd_rn(a, bias[i0]);
-                b = __fadd_rn(b, bias[i0 + 1]);
-            }
-            const float c = cs[i], sn = cs[i + 1];
-            const float ra = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn));
-            const float rb = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, c));
-            if (i0 < qd) {
-                q_out[(size_t)s * qd + i0] = ra;
-                q_out[(size_t)s * qd + i0 + 1] = rb;
-            } else {
-                const int kh = (i0 - qd) / hd;
-                KT* dst = kc + (((size_t)page * Hkv + kh) * page_size + off) * hd + i;
-                dst[0] = (KT)ra;
-                dst[1] = (KT)rb;
-            }
+    if (bias) {
+        a = __fadd_rn(a, ba);
+        b = __fadd_rn(b, bb);
+    }
+    if (rot) {
+        const float ra = __fsub_rn(__fmul_rn(a, c), __fmul_rn(b, sn));
+        const float rb = __fadd_rn(__fmul_rn(a, sn), __fmul_rn(b, c));
+        if (i0 < qd) {
+            q_out[(size_t)s * qd + i0] = ra;
+            q_out[(size_t)s * qd + i0 + 1] = rb;
         } else {
-            const int j = e - (qd + kvd) / 2;  // v element
-            float v = ld(qd + kvd + j);
-            if (bias) v = __fadd_rn(v, bias[qd + kvd + j]);
-            const int vh = j / hd;
-            if (sizeof(KT) == 4)
-                vc[(((size_t)page * Hkv + vh) * page_size + off) * hd + j % hd] = (KT)v;
-            else  // fp16 pages keep V dimension-major
-                vc[(((size_t)page * Hkv + vh) * hd + j % hd) * page_size + off] = (KT)v;
+            const int kh = (i0 - qd) / hd;
+            KT* dst = kc + (((size_t)page * Hkv + kh) * page_size + off) * hd + i;
+            dst[0] = (KT)ra;
+            dst[1] = (KT)rb;
         }
+    } else {
+        const int j = i0 - (qd + kvd);  // v element
+        const int vh = j / hd;
+        if (sizeof(KT) == 4)
+            vc[(((size_t)page * Hkv + vh) * page_size + off) * hd + j % hd] = (KT)a;
+        else  // fp16 pages keep V dimension-major
+            vc[(((size_t)page * Hkv + vh) * hd + j % hd) * page_size + off] = (KT)a;
     }
     }
 }
@@ -1683,14 +1698,25 @@ int launch_rope_append(const float* qkv, const float* bias, int n, int H, int Hk
     }
     const size_t work = (size_t)n * ((H * hd + Hkv * hd) / 2 + Hkv * hd);
     const int grid = (int)std::min<size_t>((work + 255) / 256, 4096);
-    if (kv_dtype == DT_F32)
-        hipLaunchKernelGGL(rope_append_kernel<float>, dim3(grid), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos, rope,
-                           q_out, (float*)kc, (float*)vc, page_table, max_pages, page_size, n, S, slice);
-    else if (kv_dtype == DT_F16)
-        hipLaunchKernelGGL(rope_append_kernel<_Float16>, dim3(grid), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos,
-                           rope, q_out, (_Float16*)kc, (_Float16*)vc, page_table, max_pages, page_size, n, S, slice);
-    else
-        return set_error(QRAF_HIP_ERR_DTYPE, "rope_append: KV dtype %u", kv_dtype);
+    if (kv_dtype != DT_F32 && kv_dtype != DT_F16) return set_error(QRAF_HIP_ERR_DTYPE, "rope_append: KV dtype %u", kv_dtype);
+#define QH_RA(KTv, SCv)                                                                                              \
+    hipLaunchKernelGGL((rope_append_kernel<KTv, SCv>), dim3(grid), dim3(256), 0, st, qkv, bias, H, Hkv, hd, pos, rope, \
+                       q_out, (KTv*)kc, (KTv*)vc, page_table, max_pages, page_size, n, S, slice)
+#define QH_RA_S(KTv)                  \
+    switch (S) {                      \
+        case 1: QH_RA(KTv, 1); break; \
+        case 2: QH_RA(KTv, 2); break; \
+        case 4: QH_RA(KTv, 4); break; \
+        case 8: QH_RA(KTv, 8); break; \
+        default: QH_RA(KTv, 0); break; \
+    }
+    if (kv_dtype == DT_F32) {
+        QH_RA_S(float)
+    } else {
+        QH_RA_S(_Float16)
+    }
+#undef QH_RA_S
+#undef QH_RA
     QH_CHECK_HIP(hipGetLastError());
     return QRAF_HIP_OK;
 }
